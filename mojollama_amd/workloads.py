@@ -1,0 +1,100 @@
+"""Seeded synthetic weights and activations with the distributions and
+shapes of the benchmark configurations (raw GGUF block bytes, as the
+reference's caller hands them over: TE:459-480).
+
+Distributions:
+  * fp16 block scales d / dmin: |N(0,1)| * 0.01, rounded to fp16 (RNE)
+  * Q8_0 quants: int8 uniform in [-127, 127]
+  * Q4_K / Q5_K / Q4_0 / Q4_1 / Q5_0 packed fields: uniform random bytes
+    (iid uniform 6-bit scales/mins and 4-bit quants)
+  * Q6_K: uniform ql/qh bytes, int8 sub-scales uniform in [-32, 31]
+  * MXFP4: uniform nibble bytes, E8M0 exponent 127 + U{-8..0}
+  * fp32 routers N(0, 0.02^2); activations N(0, 1)
+"""
+import numpy as np
+
+QT_F32, QT_Q4_0, QT_Q4_1, QT_Q5_0, QT_Q8_0 = 0, 2, 3, 6, 8
+QT_Q4_K, QT_Q5_K, QT_Q6_K, QT_MXFP4 = 12, 13, 14, 39
+
+# GGUF code -> (elements per block, bytes per block)   (QK:26-37, TE:24-25)
+BLOCK = {QT_F32: (1, 4), QT_Q4_0: (32, 18), QT_Q4_1: (32, 20), QT_Q5_0: (32, 22),
+         QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_Q5_K: (256, 176), QT_Q6_K: (256, 210),
+         QT_MXFP4: (32, 17)}
+
+
+def row_bytes(qt, n_cols):
+    be, bb = BLOCK[qt]
+    return n_cols // be * bb
+
+
+def _f16_scales(rng, n):
+    return (np.abs(rng.standard_normal(n)) * 0.01).astype(np.float16).view(np.uint8).reshape(n, 2)
+
+
+def gen_weights(rng, qt, n_rows, n_cols):
+    """Raw GGUF-order bytes for an n_rows x n_cols matrix of type qt."""
+    if qt == QT_F32:
+        return (rng.standard_normal((n_rows, n_cols)) * 0.02).astype(np.float32).view(np.uint8).ravel()
+    be, bb = BLOCK[qt]
+    nb = n_rows * (n_cols // be)
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    if qt == QT_Q8_0:
+        blk[:, 0:2] = _f16_scales(rng, nb)
+        blk[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+    elif qt in (QT_Q4_0, QT_Q5_0):
+        blk[:, 0:2] = _f16_scales(rng, nb)
+    elif qt in (QT_Q4_1, QT_Q4_K, QT_Q5_K):
+        blk[:, 0:2] = _f16_scales(rng, nb)
+        blk[:, 2:4] = _f16_scales(rng, nb)
+    elif qt == QT_Q6_K:
+        blk[:, 192:208] = rng.integers(-32, 32, size=(nb, 16), dtype=np.int8).view(np.uint8)
+        blk[:, 208:210] = _f16_scales(rng, nb)
+    elif qt == QT_MXFP4:
+        blk[:, 16] = (127 + rng.integers(-8, 1, size=nb)).astype(np.uint8)
+    return np.ascontiguousarray(blk.ravel())
+
+
+def gen_x(rng, B, n_cols, bf16=False):
+    """fp32 activations ~ N(0,1); bf16=True rounds them to bf16 (RNE) and back."""
+    x = rng.standard_normal((B, n_cols)).astype(np.float32)
+    if bf16:
+        u = x.view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+        x = u.astype(np.uint32).view(np.float32)
+    return np.ascontiguousarray(x)
+
+
+def gen_router(rng, E, N):
+    return (rng.standard_normal((E, N)) * 0.02).astype(np.float32)
+
+
+# ---------------------------------------------------------- configurations
+
+# TinyLlama-1.1B Q4_K_M matmul set (per layer) + lm_head.
+TINYLLAMA_LAYERS = 22
+TINYLLAMA_MATS = [  # name, rows, cols, qt
+    ("q", 2048, 2048, QT_Q4_K), ("k", 256, 2048, QT_Q4_K), ("v", 256, 2048, QT_Q4_K),
+    ("o", 2048, 2048, QT_Q4_K), ("gate", 5632, 2048, QT_Q4_K), ("up", 5632, 2048, QT_Q4_K),
+    ("down", 2048, 5632, QT_Q6_K)]
+TINYLLAMA_LM_HEAD = ("lm_head", 32000, 2048, QT_Q6_K)
+
+# MoE layer shapes.
+GPTOSS = dict(N=2880, E=32, K=4, M=2880, qt_gate=QT_MXFP4, qt_up=QT_MXFP4, qt_down=QT_MXFP4)
+QWEN3 = dict(N=2048, E=128, K=8, M=768, qt_gate=QT_Q4_K, qt_up=QT_Q4_K, qt_down=QT_Q6_K)
+
+
+def skewed_tokens(rng, router_w, T, n_hot=8, frac=0.25):
+    """Hidden states for the Qwen3 skewed-routing case: a seeded unit direction
+    u is added (x0.5) to the router rows of n_hot seeded experts, and (x16) to
+    a seeded `frac` of the tokens, which pushes those tokens onto the hot set.
+    Returns (x [T,N], router_w_skewed [E,N], hot_experts, hot_tokens)."""
+    E, N = router_w.shape
+    u = rng.standard_normal(N).astype(np.float32)
+    u /= np.linalg.norm(u)
+    hot = np.sort(rng.choice(E, size=n_hot, replace=False))
+    rw = router_w.copy()
+    rw[hot] += 0.5 * u
+    x = rng.standard_normal((T, N)).astype(np.float32)
+    hot_tok = np.sort(rng.choice(T, size=int(T * frac), replace=False))
+    x[hot_tok] += 16.0 * u
+    return np.ascontiguousarray(x), np.ascontiguousarray(rw), hot, hot_tok

@@ -1,0 +1,233 @@
+"""ctypes bindings for the test oracle.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py import this module, and only as the checker.
+
+Two libraries:
+  * ``Oracle``   — liboracle.so, our scalar C restatement (oracle.c).
+  * ``RefLib``   — _ref/libref.so, the reference's own C compiled in place
+                   from /root/reference by oracle/Makefile (absent when the
+                   reference tree is absent and nothing was built).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref.so")
+
+# Semantic ids (enum orc_sem in oracle.h; the GPU library uses the same numbers).
+F32, Q4_0, Q4_1, Q5_0_F32, Q5_0_Q8, Q8_0, Q4_K_GGML, Q4_K_Q8 = range(8)
+Q5_K_GGML, Q5_K_CE, Q6_K_GGML, Q6_K_LOWNIB, Q6_K_SEQ, MXFP4, MXFP4_CLAMP, MXFP4_Q8 = range(8, 16)
+SEM_NAMES = ["F32", "Q4_0", "Q4_1", "Q5_0_F32", "Q5_0_Q8", "Q8_0", "Q4_K_GGML", "Q4_K_Q8",
+             "Q5_K_GGML", "Q5_K_CE", "Q6_K_GGML", "Q6_K_LOWNIB", "Q6_K_SEQ", "MXFP4",
+             "MXFP4_CLAMP", "MXFP4_Q8"]
+
+_cf = ctypes.POINTER(ctypes.c_float)
+_cu = ctypes.POINTER(ctypes.c_uint8)
+_ci = ctypes.c_int
+
+
+def fp(a):
+    return a.ctypes.data_as(_cf)
+
+
+def up(a):
+    return a.ctypes.data_as(_cu)
+
+
+def ip(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+
+def build():
+    """Compile liboracle.so (and _ref/libref.so where the reference is present)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            build()
+        lib = ctypes.CDLL(path)
+        lib.orc_gemv.argtypes = [_ci, _cu, _cf, _cf, _ci, _ci, _ci]
+        lib.orc_gemv.restype = None
+        lib.orc_dequant_row.argtypes = [_ci, _cu, _cf, _ci]
+        lib.orc_dequant_row.restype = _ci
+        lib.orc_quantize_row_q8_0.argtypes = [_cf, _cu, _ci]
+        lib.orc_quantize_row_q8_0.restype = _ci
+        lib.orc_block_elems.argtypes = [_ci]
+        lib.orc_block_elems.restype = _ci
+        lib.orc_block_bytes.argtypes = [_ci]
+        lib.orc_block_bytes.restype = _ci
+        lib.orc_sem_for.argtypes = [_ci, _ci]
+        lib.orc_sem_for.restype = _ci
+        lib.orc_route.argtypes = [_cf, _cf, _ci, _ci, _ci, _ci, _ci, ctypes.POINTER(ctypes.c_int), _cf]
+        lib.orc_route.restype = None
+        lib.orc_moe_ffn_stride.argtypes = [_ci, _ci, _ci, _ci]
+        lib.orc_moe_ffn_stride.restype = ctypes.c_long
+        lib.orc_moe_ffn_token.argtypes = [_cf, _cu, _cu, _cu, _ci, _ci, _ci, _ci, _ci, _ci, _ci, _cf, _cf]
+        lib.orc_moe_ffn_token.restype = None
+        lib.orc_moe_forward_token.argtypes = [ctypes.POINTER(_cu)] * 3 + [_cf, _ci, _ci, _ci, _ci, _ci,
+                                              ctypes.POINTER(ctypes.c_int), _cf, _ci, _ci, _cf]
+        lib.orc_moe_forward_token.restype = None
+        lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        lib.orc_f32_to_f16.restype = ctypes.c_uint16
+        lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        lib.orc_f16_to_f32.restype = ctypes.c_float
+        self.lib = lib
+
+    def block_elems(self, sem):
+        return self.lib.orc_block_elems(sem)
+
+    def block_bytes(self, sem):
+        return self.lib.orc_block_bytes(sem)
+
+    def row_bytes(self, sem, n_cols):
+        return n_cols // self.block_elems(sem) * self.block_bytes(sem)
+
+    def sem_for(self, entry, qt):
+        return self.lib.orc_sem_for(entry, qt)
+
+    def gemv(self, sem, W, x, n_rows, n_cols, B=1):
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(B * n_rows, dtype=np.float32)
+        self.lib.orc_gemv(sem, up(W), fp(x), fp(out), n_rows, n_cols, B)
+        return out.reshape(B, n_rows)
+
+    def dequant(self, sem, W, n_rows, n_cols):
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        rb = self.row_bytes(sem, n_cols)
+        out = np.zeros((n_rows, n_cols), dtype=np.float32)
+        for r in range(n_rows):
+            rc = self.lib.orc_dequant_row(sem, up(W[r * rb:(r + 1) * rb]), fp(out[r]), n_cols)
+            if rc != 0:
+                raise ValueError(f"semantic {SEM_NAMES[sem]} has no fp32 weight")
+        return out
+
+    def quantize_q8_0(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        q = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+        self.lib.orc_quantize_row_q8_0(fp(x), up(q), x.size)
+        return q
+
+    def route(self, router_w, x, K, renorm):
+        router_w = np.ascontiguousarray(router_w, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        E, N = router_w.shape
+        T = x.size // N
+        idx = np.zeros((T, K), dtype=np.int32)
+        w = np.zeros((T, K), dtype=np.float32)
+        self.lib.orc_route(fp(router_w), fp(x), T, N, E, K, int(renorm), ip(idx), fp(w))
+        return idx, w
+
+    def moe_ffn_stride(self, which, qt, N, M):
+        return self.lib.orc_moe_ffn_stride(which, qt, N, M)
+
+    def moe_ffn_token(self, router_w, gate, upw, down, qts, N, E, K, M, x):
+        out = np.zeros(N, dtype=np.float32)
+        self.lib.orc_moe_ffn_token(fp(np.ascontiguousarray(router_w, dtype=np.float32)), up(gate), up(upw),
+                                   up(down), qts[0], qts[1], qts[2], N, E, K, M,
+                                   fp(np.ascontiguousarray(x, dtype=np.float32)), fp(out))
+        return out
+
+    def moe_forward_token(self, gates, ups, downs, x, n_ff, n_embd, qts, top_idx, top_w, has_q8=True):
+        arr = ctypes.POINTER(ctypes.c_uint8) * len(gates)
+        g = arr(*[up(a) for a in gates])
+        u = arr(*[up(a) for a in ups])
+        d = arr(*[up(a) for a in downs])
+        out = np.zeros(n_embd, dtype=np.float32)
+        ti = np.ascontiguousarray(top_idx, dtype=np.int32)
+        tw = np.ascontiguousarray(top_w, dtype=np.float32)
+        self.lib.orc_moe_forward_token(g, u, d, fp(np.ascontiguousarray(x, dtype=np.float32)), n_ff, n_embd,
+                                       qts[0], qts[1], qts[2], ip(ti), fp(tw), len(ti), int(has_q8), fp(out))
+        return out
+
+
+class RefLib:
+    """The reference's own C (combined like combined_engine.so), by its exported names."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        so = ctypes.CDLL(path)
+        # Signatures as bound by the reference's caller (TE:251-392) and declared in CE/QK.
+        so.quant_matmul_omp.argtypes = [_cu, _cf, _cf, _ci, _ci, _ci]
+        so.quant_matmul_omp.restype = None
+        for name in ("q4_0_batch_matmul", "q8_0_batch_matmul", "q4_k_batch_matmul",
+                     "q6_k_batch_matmul", "q5_k_batch_matmul", "mxfp4_batch_matmul"):
+            f = getattr(so, name)
+            f.argtypes = [_cu, _cf, _cf, _ci, _ci, _ci]
+            f.restype = None
+        so.f32_matmul_omp.argtypes = [_cf, _cf, _cf, _ci, _ci]
+        so.f32_matmul_omp.restype = None
+        so.quantize_row_q8_0.argtypes = [_cf, _cu, _ci]
+        so.quantize_row_q8_0.restype = _ci
+        for name in ("q4_k_dequantize_row", "q6_k_dequantize_row", "q5_k_dequantize_row",
+                     "q8_0_dequantize_row"):
+            f = getattr(so, name)
+            f.argtypes = [_cu, _cf, _ci]
+            f.restype = None
+        so.batch_qkv_omp.argtypes = [_cu, _cu, _cu, _cf, _cf, _cf, _cf, _ci, _ci, _ci, _ci, _ci, _ci, _ci]
+        so.batch_qkv_omp.restype = None
+        so.batch_gate_up_omp.argtypes = [_cu, _cu, _cf, _cf, _cf, _ci, _ci, _ci, _ci, _ci]
+        so.batch_gate_up_omp.restype = None
+        so.moe_forward_omp.argtypes = [ctypes.POINTER(_cu)] * 3 + [_cf, _ci, _ci, _ci, _ci, _ci,
+                                       ctypes.POINTER(ctypes.c_int), _cf, _ci, _cf, _cf, _cu]
+        so.moe_forward_omp.restype = None
+        so.set_num_threads.argtypes = [_ci]
+        so.set_num_threads.restype = None
+        so.get_max_threads.argtypes = []
+        so.get_max_threads.restype = _ci
+        self.so = so
+
+    def quant_matmul(self, W, x, n_rows, n_cols, qt, out=None):
+        out = np.zeros(n_rows, dtype=np.float32) if out is None else out
+        self.so.quant_matmul_omp(up(W), fp(np.ascontiguousarray(x, dtype=np.float32)), fp(out), n_rows, n_cols, qt)
+        return out
+
+    def batch_matmul(self, name, W, x, n_rows, n_cols, B):
+        out = np.zeros(B * n_rows, dtype=np.float32)
+        getattr(self.so, name)(up(W), fp(np.ascontiguousarray(x, dtype=np.float32)), fp(out), n_rows, n_cols, B)
+        return out.reshape(B, n_rows)
+
+    def quantize_q8_0(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        q = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+        self.so.quantize_row_q8_0(fp(x), up(q), x.size)
+        return q
+
+    def moe_forward(self, gates, ups, downs, x, n_ff, n_embd, qts, top_idx, top_w, with_q8=True):
+        arr = ctypes.POINTER(ctypes.c_uint8) * len(gates)
+        g = arr(*[up(a) for a in gates])
+        u = arr(*[up(a) for a in ups])
+        d = arr(*[up(a) for a in downs])
+        K = len(top_idx)
+        out = np.zeros(n_embd, dtype=np.float32)
+        buf = np.zeros(3 * K * n_ff, dtype=np.float32)
+        q8 = np.zeros(K * n_ff * 34 // 32 + 64, dtype=np.uint8)
+        ti = np.ascontiguousarray(top_idx, dtype=np.int32)
+        tw = np.ascontiguousarray(top_w, dtype=np.float32)
+        self.so.moe_forward_omp(g, u, d, fp(np.ascontiguousarray(x, dtype=np.float32)), n_ff, n_embd,
+                                qts[0], qts[1], qts[2], ip(ti), fp(tw), K, fp(out), fp(buf),
+                                up(q8) if with_q8 else ctypes.cast(None, _cu))
+        return out
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
+
+
+def norm_err(got, ref):
+    """max|got-ref| / max|ref|: the normalised max error used for every tolerance."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.max(np.abs(ref)) if ref.size else 0.0
+    num = np.max(np.abs(got - ref)) if ref.size else 0.0
+    if den == 0.0:
+        return float(num)
+    return float(num / den)

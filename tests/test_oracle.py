@@ -1,0 +1,292 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Three independent pins:
+  1. golden vectors written by the reference's own compiled C (tests/golden);
+  2. the live reference build oracle/_ref/libref.so on fresh inputs, where it
+     was built (skipped otherwise);
+  3. properties the mathematics fixes (closed forms, linearity, batching,
+     zero scales, semantic distinctness, quantisation bounds).
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mojollama_amd import workloads as W
+
+TOL = 1e-5       # oracle (double accumulation) vs reference (fp32 AVX2)
+
+
+def crc(*arrays):
+    c = 0
+    for a in arrays:
+        c = zlib.crc32(np.ascontiguousarray(a).view(np.uint8).tobytes(), c)
+    return c
+
+
+# ------------------------------------------------------------ 1. golden
+
+@pytest.mark.parametrize("qt", [0, 2, 3, 6, 8, 12, 13, 14, 39])
+def test_golden_quant_matmul(orc, golden, qt):
+    g = golden(f"qmm_{qt}.npz")
+    sem = orc.sem_for(0, qt)
+    got = orc.gemv(sem, g["W"], g["x"], int(g["n_rows"]), int(g["n_cols"]), 1)[0]
+    assert O.norm_err(got, g["out"]) < TOL
+
+
+@pytest.mark.parametrize("name,qt", [("q4_0", 2), ("q8_0", 8), ("q4_k", 12), ("q6_k", 14),
+                                     ("q5_k", 13), ("mxfp4", 39)])
+@pytest.mark.parametrize("B", [1, 3, 5])
+def test_golden_batch_matmul(orc, golden, name, qt, B):
+    g = golden(f"bmm_{name}_B{B}.npz")
+    sem = orc.sem_for(1, qt)
+    got = orc.gemv(sem, g["W"], g["x"], int(g["n_rows"]), int(g["n_cols"]), B)
+    assert O.norm_err(got, g["out"]) < TOL
+
+
+def test_golden_mxfp4_scale_edges(orc, golden):
+    g = golden("edge_mxfp4.npz")
+    R, C = int(g["n_rows"]), int(g["n_cols"])
+    got = orc.gemv(O.MXFP4_CLAMP, g["W"], g["x"], R, C, 1)[0]
+    assert np.all(np.isfinite(g["out_clamp"]))
+    assert O.norm_err(got, g["out_clamp"]) < TOL
+    got = orc.gemv(O.MXFP4, g["W"], g["x"], R, C, 1)[0]
+    ref = g["out_noclamp"]
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = np.isfinite(ref)
+    if fin.any():
+        assert O.norm_err(got[fin], ref[fin]) < TOL
+
+
+def test_golden_quantize_q8_0_bitexact(orc, golden):
+    g = golden("q8_0.npz")
+    assert np.array_equal(orc.quantize_q8_0(g["x"]), g["q8"])
+
+
+@pytest.mark.parametrize("name,sem", [("q4_k", O.Q4_K_GGML), ("q6_k", O.Q6_K_GGML),
+                                      ("q5_k", O.Q5_K_GGML), ("q8_0", O.Q8_0)])
+def test_golden_dequantize_row(orc, golden, name, sem):
+    g = golden(f"deq_{name}.npz")
+    got = orc.dequant(sem, g["W"], 1, 1024)[0]
+    assert O.norm_err(got, g["out"]) < 1e-6
+
+
+def test_golden_batch_qkv_and_gate_up(orc, golden):
+    g = golden("batch_qkv.npz")
+    for w, o, rows, qt in ((g["Wq"], g["oq"], 32, 12), (g["Wk"], g["ok"], 16, 14), (g["Wv"], g["ov"], 16, 8)):
+        got = orc.gemv(orc.sem_for(2, qt), w, g["x"], rows, 512, 1)[0]
+        assert O.norm_err(got, o) < TOL
+    g = golden("batch_gate_up.npz")
+    for w, o, qt in ((g["Wg"], g["og"], 39), (g["Wu"], g["ou"], 2)):
+        got = orc.gemv(orc.sem_for(2, qt), w, g["x"], 32, 512, 1)[0]
+        assert O.norm_err(got, o) < TOL
+
+
+@pytest.mark.parametrize("tag", ["qwen", "gptoss"])
+def test_golden_moe_forward(orc, golden, tag):
+    g = golden(f"moe_forward_{tag}.npz")
+    got = orc.moe_forward_token(list(g["gates"]), list(g["ups"]), list(g["downs"]), g["x"],
+                                int(g["n_ff"]), int(g["n_embd"]), tuple(int(v) for v in g["qts"]),
+                                g["top_idx"], g["top_w"])
+    assert O.norm_err(got, g["out"]) < 1e-4
+
+
+@pytest.mark.parametrize("tag", ["q4k", "mxfp4"])
+def test_golden_moe_ffn(orc, golden, tag):
+    g = golden(f"moe_ffn_{tag}.npz")
+    N, E, K, M = (int(g[k]) for k in ("N", "E", "K", "M"))
+    for t in range(g["x"].shape[0]):
+        got = orc.moe_ffn_token(g["router"], g["gate"], g["up"], g["down"], tuple(int(v) for v in g["qts"]),
+                                N, E, K, M, g["x"][t])
+        assert O.norm_err(got, g["out"][t]) < 1e-4
+
+
+@pytest.mark.parametrize("tag", ["gptoss", "qwen3"])
+def test_golden_route_selection_bitexact(orc, golden, tag):
+    g = golden(f"route_sel_{tag}.npz")
+    N, E, K, T = (int(g[k]) for k in ("N", "E", "K", "T"))
+    r2 = np.random.default_rng(int(g["seed"]))
+    router = W.gen_router(r2, E, N)
+    xs = W.gen_x(r2, T, N)
+    assert crc(router, xs) == int(g["crc"]), "numpy RNG stream changed: regenerate fixtures"
+    idx, w = orc.route(router, xs, K, renorm=False)
+    sel = np.zeros((T, E), np.uint8)
+    for t in range(T):
+        sel[t, idx[t]] = 1
+    assert np.array_equal(sel, g["sel"])
+    # the probe's output is p_e * D_t at the selected experts (same D_t for all e)
+    ratio = g["ffn"][np.arange(T)[:, None], idx] / w
+    assert np.all(np.abs(ratio / ratio[:, :1] - 1.0) < 1e-5)
+
+
+# ----------------------------------------------------- 2. live reference
+
+@pytest.fixture(scope="module")
+def ref():
+    if not O.ref_available():
+        pytest.skip("oracle/_ref/libref.so not built (reference tree absent)")
+    r = O.RefLib()
+    r.so.set_num_threads(2)
+    return r
+
+
+@pytest.mark.parametrize("qt", [0, 2, 3, 6, 8, 12, 13, 14, 39])
+def test_live_quant_matmul(orc, ref, qt):
+    rng = np.random.default_rng(100 + qt)
+    R, C = 40, 2048
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, 1, C)
+    assert O.norm_err(orc.gemv(orc.sem_for(0, qt), w, x, R, C, 1)[0], ref.quant_matmul(w, x, R, C, qt)) < TOL
+
+
+@pytest.mark.parametrize("name,qt", [("q4_0", 2), ("q8_0", 8), ("q4_k", 12), ("q6_k", 14),
+                                     ("q5_k", 13), ("mxfp4", 39)])
+def test_live_batch_matmul(orc, ref, name, qt):
+    rng = np.random.default_rng(200 + qt)
+    R, C, B = 24, 2816 if qt not in (12, 13, 14) else 2816 // 256 * 256, 4
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, B, C)
+    got = orc.gemv(orc.sem_for(1, qt), w, x, R, C, B)
+    assert O.norm_err(got, ref.batch_matmul(name + "_batch_matmul", w, x, R, C, B)) < TOL
+
+
+def test_live_quantize_q8_0(orc, ref):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(1 << 16) * np.exp(rng.uniform(-8, 8, 1 << 16))).astype(np.float32)
+    assert np.array_equal(orc.quantize_q8_0(x), ref.quantize_q8_0(x))
+
+
+def test_live_moe_forward_null_q8_scratch_differs_only_for_mxfp4_down(orc, ref):
+    # With prealloc_q8 == NULL the reference still runs a Q6_K down projection.
+    rng = np.random.default_rng(9)
+    n_embd, n_ff = 256, 256
+    gates = [W.gen_weights(rng, 12, n_ff, n_embd) for _ in range(2)]
+    ups = [W.gen_weights(rng, 12, n_ff, n_embd) for _ in range(2)]
+    downs = [W.gen_weights(rng, 14, n_embd, n_ff) for _ in range(2)]
+    x = W.gen_x(rng, 1, n_embd)[0]
+    ti, tw = np.array([1, 0], np.int32), np.array([0.6, 0.4], np.float32)
+    a = ref.moe_forward(gates, ups, downs, x, n_ff, n_embd, (12, 12, 14), ti, tw, with_q8=False)
+    b = orc.moe_forward_token(gates, ups, downs, x, n_ff, n_embd, (12, 12, 14), ti, tw, has_q8=False)
+    assert O.norm_err(b, a) < 1e-4
+
+
+# ------------------------------------------------ 3. mathematical pins
+
+def _np_decode_q8_0(w, R, C):
+    b = w.reshape(R, C // 32, 34)
+    d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    q = b[:, :, 2:].view(np.int8).astype(np.float32)
+    return (q * d).reshape(R, C)
+
+
+def _np_decode_mxfp4(w, R, C, clamp):
+    b = w.reshape(R, C // 32, 17)
+    s = (b[:, :, 16].astype(np.uint32) << 23).view(np.float32)
+    if clamp:
+        s = np.minimum(s, np.float32(1e20))
+    lo = (b[:, :, :16] & 15).astype(np.int32)
+    hi = (b[:, :, :16] >> 4).astype(np.int32)
+    v = np.stack([lo, hi], axis=-1).reshape(R, C // 32, 32)
+    v = np.where(v >= 8, v - 16, v).astype(np.float32)
+    return (v * s[:, :, None]).reshape(R, C)
+
+
+def test_closed_form_q8_0_and_mxfp4_are_dense_gemv(orc):
+    rng = np.random.default_rng(1)
+    R, C, B = 33, 640, 3
+    x = W.gen_x(rng, B, C)
+    w = W.gen_weights(rng, 8, R, C)
+    dense = x.astype(np.float64) @ _np_decode_q8_0(w, R, C).T.astype(np.float64)
+    assert O.norm_err(orc.gemv(O.Q8_0, w, x, R, C, B), dense) < 1e-6
+    w = W.gen_weights(rng, 39, R, C)
+    for sem, clamp in ((O.MXFP4, False), (O.MXFP4_CLAMP, True)):
+        dense = x.astype(np.float64) @ _np_decode_mxfp4(w, R, C, clamp).T.astype(np.float64)
+        assert O.norm_err(orc.gemv(sem, w, x, R, C, B), dense) < 1e-6
+
+
+FP32_SEMS = [O.F32, O.Q4_0, O.Q4_1, O.Q5_0_F32, O.Q8_0, O.Q4_K_GGML, O.Q5_K_GGML, O.Q5_K_CE,
+             O.Q6_K_GGML, O.Q6_K_LOWNIB, O.Q6_K_SEQ, O.MXFP4, O.MXFP4_CLAMP]
+SEM_QT = {O.F32: 0, O.Q4_0: 2, O.Q4_1: 3, O.Q5_0_F32: 6, O.Q5_0_Q8: 6, O.Q8_0: 8, O.Q4_K_GGML: 12,
+          O.Q4_K_Q8: 12, O.Q5_K_GGML: 13, O.Q5_K_CE: 13, O.Q6_K_GGML: 14, O.Q6_K_LOWNIB: 14,
+          O.Q6_K_SEQ: 14, O.MXFP4: 39, O.MXFP4_CLAMP: 39, O.MXFP4_Q8: 39}
+
+
+@pytest.mark.parametrize("sem", FP32_SEMS)
+def test_linearity_and_batching(orc, sem):
+    rng = np.random.default_rng(50 + sem)
+    R, C = 20, 512
+    w = W.gen_weights(rng, SEM_QT[sem], R, C)
+    x = W.gen_x(rng, 4, C)
+    y = orc.gemv(sem, w, x, R, C, 4)
+    for b in range(4):
+        assert np.array_equal(orc.gemv(sem, w, x[b], R, C, 1)[0], y[b])
+    y01 = orc.gemv(sem, w, x[0] + 2.0 * x[1], R, C, 1)[0]
+    assert O.norm_err(y01, y[0] + 2.0 * y[1]) < 1e-5
+
+
+@pytest.mark.parametrize("sem", [s for s in range(16) if s != O.F32])
+def test_zero_scales_give_zero(orc, sem):
+    rng = np.random.default_rng(5)
+    R, C = 8, 512
+    qt = SEM_QT[sem]
+    w = W.gen_weights(rng, qt, R, C)
+    be, bb = W.BLOCK[qt]
+    blk = w.reshape(-1, bb)
+    zero_fields = {2: [(0, 2)], 3: [(0, 4)], 6: [(0, 2)], 8: [(0, 2)], 12: [(0, 4)], 13: [(0, 4)],
+                   14: [(208, 210)], 39: [(16, 17)]}[qt]
+    for a, b in zero_fields:
+        blk[:, a:b] = 0
+    if qt == 3:
+        pass  # Q4_1: w = n*d + m with d = m = 0
+    y = orc.gemv(sem, w, W.gen_x(rng, 1, C), R, C, 1)
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("family", [(O.Q6_K_GGML, O.Q6_K_LOWNIB, O.Q6_K_SEQ), (O.Q5_K_GGML, O.Q5_K_CE),
+                                    (O.Q4_K_GGML, O.Q4_K_Q8), (O.MXFP4, O.MXFP4_Q8), (O.Q5_0_F32, O.Q5_0_Q8)])
+def test_semantic_variants_are_distinguishable(orc, family):
+    """A variant mix-up must fail a parity check: variants of one quant type
+    disagree by far more than any tolerance on random data (the Q8-x variants
+    differ by the activation quantisation, still well above 1e-3)."""
+    rng = np.random.default_rng(3)
+    R, C = 16, 512
+    w = W.gen_weights(rng, SEM_QT[family[0]], R, C)
+    x = W.gen_x(rng, 1, C)
+    ys = [orc.gemv(s, w, x, R, C, 1)[0] for s in family]
+    for i in range(len(ys)):
+        for j in range(i + 1, len(ys)):
+            assert O.norm_err(ys[i], ys[j]) > 3e-3
+
+
+def test_quantize_q8_0_bounds(orc):
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(4096) * 5).astype(np.float32)
+    q = orc.quantize_q8_0(x).reshape(-1, 34)
+    d = q[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    v = q[:, 2:].view(np.int8).astype(np.float32)
+    assert np.max(np.abs(v)) <= 127
+    amax = np.abs(x.reshape(-1, 32)).max(1)
+    dd = amax / np.float32(127.0)
+    # values are quantised with the fp32 scale; the stored fp16 scale is that rounded
+    err = np.abs(x.reshape(-1, 32) - v * dd[:, None])
+    assert np.all(err <= dd[:, None] * 0.5 * (1 + 1e-5))
+    assert np.all(np.abs(d - dd) <= np.abs(dd) * 2.0 ** -11)
+
+
+def test_route_properties(orc):
+    rng = np.random.default_rng(6)
+    E, N, K, T = 32, 256, 4, 16
+    rw = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, T, N)
+    i0, w0 = orc.route(rw, x, K, renorm=False)
+    i1, w1 = orc.route(rw, x, K, renorm=True)
+    assert np.array_equal(i0, i1)                       # renorm does not change the selection
+    assert np.all(np.diff(w0, axis=1) <= 0)             # descending
+    assert np.allclose(w1.sum(1), 1.0, atol=1e-6)
+    logits = x.astype(np.float64) @ rw.T.astype(np.float64)
+    top = np.argsort(-logits, axis=1, kind="stable")[:, :K]
+    assert np.array_equal(np.sort(top, 1), np.sort(i0, 1))
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    assert np.allclose(np.take_along_axis(p, i0, 1), w0, rtol=1e-5)

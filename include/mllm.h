@@ -1,0 +1,129 @@
+/* mllm.h — C ABI of libmllm_gpu.so, the MI355X (gfx950) implementation of
+ * a730/MojoLlama's quantised-matmul + MoE-FFN hot path.
+ *
+ * Part 1 declares drop-in replacements for the reference engine's exported
+ * symbols, with identical names, argument lists and meaning, so a caller that
+ * binds them through ctypes (turbo_engine_v7_moe.py, "TE") can load this
+ * library in place of its combined_engine.so.  Weights and activations are
+ * host pointers as in the reference; results are in the caller's buffers when
+ * the call returns.  Reference files:
+ *   QK = src/mojollama/kernels/quant_kernels_omp.c
+ *   CE = src/mojollama/kernels/cengine_batch_instr.c
+ *   TE = src/mojollama/kernels/turbo_engine_v7_moe.py
+ *
+ * Part 2 declares device-pointer entry points (mllm_*) that take inputs already
+ * resident in HBM and queue work on a caller stream (hipStream_t passed as
+ * void*; NULL = the default stream).
+ *
+ * Errors: no entry point aborts.  A failure is logged once to stderr and kept
+ * for mllm_last_error(); drop-in calls leave the output untouched on an
+ * unknown quant code (as the reference's dispatch does, QK:1385-1386);
+ * mllm_* calls return -1.
+ */
+#ifndef MLLM_H
+#define MLLM_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLLM_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------ Part 1: drop-in */
+
+/* QK:1355-1388 quant_matmul_omp — out[n_rows] = W x for one token.  quant_type is
+ * the GGUF code: 0 F32, 2 Q4_0, 3 Q4_1, 6 Q5_0, 8 Q8_0, 12 Q4_K, 13 Q5_K,
+ * 14 Q6_K, 39 MXFP4; bound by TE:251-252. */
+MLLM_API void quant_matmul_omp(const uint8_t *W, const float *x, float *out, int n_rows, int n_cols, int quant_type);
+
+/* QK:884-913 f32_matmul_omp; bound by TE:253-254. */
+MLLM_API void f32_matmul_omp(const float *W, const float *x, float *out, int n_rows, int n_cols);
+
+/* CE:68,216,256,316,381,435 — B-batched GEMV, out[b*n_rows + r]. */
+MLLM_API void q4_0_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+MLLM_API void q8_0_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+MLLM_API void q4_k_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+MLLM_API void q6_k_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+MLLM_API void q5_k_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+MLLM_API void mxfp4_batch_matmul(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B);
+
+/* QK:1139-1183 batch_qkv_omp and QK:1186-1222 batch_gate_up_omp (TE:255-258). */
+MLLM_API void batch_qkv_omp(const uint8_t *Wq, const uint8_t *Wk, const uint8_t *Wv, const float *x, float *out_q,
+                            float *out_k, float *out_v, int nq, int nk, int nv, int n_cols, int qtype_q, int qtype_k,
+                            int qtype_v);
+MLLM_API void batch_gate_up_omp(const uint8_t *Wg, const uint8_t *Wu, const float *x, float *out_gate, float *out_up,
+                                int ng, int nu, int n_cols, int qtype_g, int qtype_u);
+
+/* QK:1406-1455 quantize_row_q8_0 — bit-exact; returns n_cols/32. */
+MLLM_API int quantize_row_q8_0(const float *x, uint8_t *q8, int n_cols);
+
+/* QK:762-878 *_dequantize_row (TE:389-392 binds the Q6_K/Q4_K ones). */
+MLLM_API void q4_k_dequantize_row(const uint8_t *W, float *out, int n_values);
+MLLM_API void q5_k_dequantize_row(const uint8_t *W, float *out, int n_values);
+MLLM_API void q6_k_dequantize_row(const uint8_t *W, float *out, int n_values);
+MLLM_API void q8_0_dequantize_row(const uint8_t *W, float *out, int n_values);
+
+/* QK:2066-2250 moe_forward_omp (TE:363-377, called at TE:2067).  Combine order
+ * is k order (the reference's OpenMP atomic has no fixed order); prealloc_buf
+ * is not written; an MXFP4 down projection with prealloc_q8 == NULL yields a
+ * zero down term and an error (the reference dereferences NULL there). */
+MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, const uint8_t **down_raw,
+                              const float *x_norm, int n_ff_expert, int n_embd, int qt_gate, int qt_up, int qt_down,
+                              const int *top_indices, const float *top_weights, int top_k, float *combined,
+                              float *prealloc_buf, uint8_t *prealloc_q8);
+
+/* CE:591-665 moe_ffn — `c` is the engine's BC struct (CE:536-589); fields read:
+ * N, n_experts, n_experts_per_tok, moe_intermediate, w_gate_inp, w_gate_exps,
+ * w_up_exps, w_down_exps, gate/up/down_exp_quant.  Writes N floats to ffn_buf
+ * (the last token's result when B > 1, as in the reference); gate_buf/up_buf
+ * are not used as scratch. */
+MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up_buf, float *ffn_buf, int B);
+
+/* QK:1029-1030: accepted and ignored / number of compute units. */
+MLLM_API void set_num_threads(int n);
+MLLM_API int get_max_threads(void);
+
+/* Symbols TE binds unconditionally that lie outside this path (TE:263-311,
+ * TE:397-408): log once and return without touching any buffer. */
+MLLM_API void ssm_layer_fused(void);
+MLLM_API void qwen36_batch_forward(void);
+MLLM_API void ssm_decode_step(void);
+
+MLLM_API const char *mllm_last_error(void);
+MLLM_API void mllm_cache_clear(void);
+
+/* ------------------------------------------------------ Part 2: device pointers */
+
+/* Semantic ids (mllm_sem in mojollama_amd/csrc/mllm_common.h) for a reference
+ * entry point: 0 quant_matmul_omp, 1 *_batch_matmul, 2 batch_qkv/gate_up rows,
+ * 3 moe_forward_omp gate/up, 4 moe_forward_omp down.  -1: reference no-op. */
+MLLM_API int mllm_sem_for(int entry, int quant_type);
+
+/* Byte sizes of a raw GGUF matrix and of its packed device layout. */
+MLLM_API long mllm_raw_size(int sem, int n_rows, int n_cols);
+MLLM_API long mllm_packed_size(int sem, int n_rows, int n_cols);
+
+/* Repack raw GGUF blocks (device) into the packed layout (256-byte aligned). */
+MLLM_API int mllm_pack(int sem, const void *raw_dev, void *packed_dev, int n_rows, int n_cols, void *stream);
+
+/* out[b][r] = row r of W applied to x[b], b < B (any B), under semantic `sem`.
+ * Q8_0-activation semantics need `workspace` of mllm_gemv_workspace_size bytes. */
+MLLM_API long mllm_gemv_workspace_size(int sem, int n_cols, int B);
+MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
+                       int B, void *workspace, void *stream);
+
+/* quantize_row_q8_0 over T rows. */
+MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *q8_dev, void *stream);
+
+/* Routing of T tokens: router_t is the [N][E] transpose of the fp32 router. */
+MLLM_API int mllm_route(const float *router_t_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
+                        int *idx_dev, float *w_dev, void *stream);
+
+/* fp32 weights of a packed matrix (fp32-weight semantics only). */
+MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_cols, float *out_dev, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,703 @@
+// capi.hip — the C ABI of libmllm_gpu.
+//
+// Two faces:
+//   * drop-in entry points with the reference engine's names and signatures
+//     (host pointers in, results in the caller's host buffers on return), so
+//     the reference's ctypes caller can load this library instead of its
+//     combined_engine.so;
+//   * mllm_* device-pointer entry points (inputs already in HBM, work queued
+//     on a caller stream) used by the benchmarks and by callers that keep
+//     activations on the GPU.
+//
+// Drop-in calls upload each weight matrix once, keyed by its host pointer,
+// into the packed plane layout (weights are immutable for an engine's
+// lifetime, TE:461-463; mllm_cache_clear() drops the cache).  Each calling
+// thread gets its own HIP stream and staging buffers, so concurrent calls
+// from ctypes threads (which release the GIL) do not share state.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+#include "gemv.h"
+#include "mllm.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+std::mutex g_log_mu;
+std::map<std::string, int> g_logged;
+
+void set_error(const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    std::lock_guard<std::mutex> lk(g_log_mu);
+    if (g_logged[buf]++ == 0) fprintf(stderr, "[mllm_gpu] %s\n", buf);
+}
+
+#define HIP_OK(expr)                                                                                  \
+    do {                                                                                              \
+        hipError_t e_ = (expr);                                                                       \
+        if (e_ != hipSuccess) {                                                                       \
+            set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__);    \
+            return -1;                                                                                \
+        }                                                                                             \
+    } while (0)
+
+// ----------------------------------------------------------- entry → semantic
+// Which semantic a reference entry point gives each GGUF code.
+enum { ENT_QMM = 0, ENT_BMM = 1, ENT_ROWS = 2, ENT_MOE_GU = 3, ENT_MOE_DOWN = 4 };
+
+int sem_for(int entry, int qt)
+{
+    switch (entry) {
+    case ENT_QMM:  // quant_matmul_omp QK:1355-1388
+        switch (qt) {
+        case 0: return SEM_F32; case 2: return SEM_Q4_0; case 3: return SEM_Q4_1; case 6: return SEM_Q5_0_Q8;
+        case 8: return SEM_Q8_0; case 12: return SEM_Q4_K_Q8; case 13: return SEM_Q5_K_GGML;
+        case 14: return SEM_Q6_K_LOWNIB; case 39: return SEM_MXFP4;
+        }
+        return -1;
+    case ENT_BMM:  // *_batch_matmul CE:68,216,256,316,381,435
+        switch (qt) {
+        case 2: return SEM_Q4_0; case 8: return SEM_Q8_0; case 12: return SEM_Q4_K_GGML; case 13: return SEM_Q5_K_CE;
+        case 14: return SEM_Q6_K_SEQ; case 39: return SEM_MXFP4_CLAMP;
+        }
+        return -1;
+    case ENT_ROWS:  // batch_qkv_omp / batch_gate_up_omp via matmul_row_range QK:1095-1222
+        switch (qt) {
+        case 2: return SEM_Q4_0; case 3: return SEM_Q4_1; case 6: return SEM_Q5_0_F32; case 8: return SEM_Q8_0;
+        case 12: return SEM_Q4_K_Q8; case 13: return SEM_Q5_K_GGML; case 14: return SEM_Q6_K_LOWNIB;
+        case 39: return SEM_MXFP4;
+        }
+        return -1;
+    case ENT_MOE_GU:  // moe_forward_omp gate/up when not both MXFP4, QK:2114-2152
+        switch (qt) {
+        case 12: return SEM_Q4_K_Q8; case 14: return SEM_Q6_K_LOWNIB; case 2: return SEM_Q4_0;
+        case 3: return SEM_Q4_1; case 6: return SEM_Q5_0_Q8;
+        }
+        return -1;
+    case ENT_MOE_DOWN:  // moe_forward_omp down QK:2192-2245 (Q4_K down yields zeros there)
+        switch (qt) {
+        case 39: return SEM_MXFP4_Q8; case 14: return SEM_Q6_K_LOWNIB; case 2: return SEM_Q4_0;
+        case 6: return SEM_Q5_0_F32;
+        }
+        return -1;
+    }
+    return -1;
+}
+
+long raw_row_bytes(int ly, int n_cols)
+{
+    if (ly == LY_F32) return (long)n_cols * 4;
+    mllm_layout_desc L = mllm_layout_info(ly);
+    return (long)(n_cols / L.block_elems) * L.block_bytes;
+}
+
+// ----------------------------------------------------------------- device context
+struct dev_buf {
+    void *p = nullptr;
+    size_t n = 0;
+    int ensure(size_t bytes)
+    {
+        if (bytes <= n) return 0;
+        if (p) (void)hipFree(p);
+        p = nullptr; n = 0;
+        size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
+        if (hipMalloc(&p, want) != hipSuccess) { p = nullptr; return -1; }
+        n = want;
+        return 0;
+    }
+};
+
+struct host_buf {
+    void *p = nullptr;
+    size_t n = 0;
+    int ensure(size_t bytes)
+    {
+        if (bytes <= n) return 0;
+        if (p) (void)hipHostFree(p);
+        p = nullptr; n = 0;
+        size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
+        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) { p = nullptr; return -1; }
+        n = want;
+        return 0;
+    }
+};
+
+// Per-thread state: stream plus staging/scratch buffers.  Freed only at
+// process end (a thread's buffers are reused by its later calls).
+struct thread_ctx {
+    hipStream_t st = nullptr;
+    int device = -1;
+    dev_buf d_in, d_out, d_scr, d_tab;
+    host_buf h_in, h_out;
+    int init()
+    {
+        if (st) return 0;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) { set_error("no HIP device"); return -1; }
+        if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) {
+            set_error("hipStreamCreate failed");
+            st = nullptr;
+            return -1;
+        }
+        device = dev;
+        return 0;
+    }
+};
+thread_local thread_ctx t_ctx;
+
+// Weight cache: (host pointer, layout, rows, cols) -> packed device copy.
+struct wkey {
+    const void *host;
+    int ly, rows, cols;
+    bool operator<(const wkey &o) const
+    {
+        return std::tie(host, ly, rows, cols) < std::tie(o.host, o.ly, o.rows, o.cols);
+    }
+};
+struct wentry {
+    uint8_t *dev = nullptr;
+    long bytes = 0;
+    mllm_packed view;
+};
+std::mutex g_cache_mu;
+std::map<wkey, wentry> g_cache;
+std::map<std::tuple<const void *, int, int>, float *> g_router_cache;  // (host, E, N) -> transposed [N][E]
+
+// Upload + pack a raw host matrix (once).  Returns its packed view.
+int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
+{
+    wkey k{host, ly, rows, cols};
+    {
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        auto it = g_cache.find(k);
+        if (it != g_cache.end()) { view = it->second.view; return 0; }
+    }
+    thread_ctx &c = t_ctx;
+    const long raw = raw_row_bytes(ly, cols) * rows;
+    const long packed = ly == LY_F32 ? (raw > 0 ? raw : 256) : mllm_packed_bytes(ly, rows, cols, nullptr);
+    wentry e;
+    e.bytes = packed;
+    HIP_OK(hipMalloc(&e.dev, packed));
+    void *tmp = nullptr;
+    if (raw > 0) {
+        if (hipMalloc(&tmp, raw) != hipSuccess) { (void)hipFree(e.dev); set_error("hipMalloc(raw %ld) failed", raw); return -1; }
+        hipError_t r = hipMemcpyAsync(tmp, host, raw, hipMemcpyHostToDevice, c.st);
+        if (r == hipSuccess) r = mllm_launch_pack(ly, (const uint8_t *)tmp, e.dev, rows, cols, c.st);
+        if (r == hipSuccess) r = hipStreamSynchronize(c.st);
+        (void)hipFree(tmp);
+        if (r != hipSuccess) { (void)hipFree(e.dev); set_error("weight upload failed: %s", hipGetErrorString(r)); return -1; }
+    }
+    e.view = mllm_packed_view(ly, e.dev, rows, cols);
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto ins = g_cache.emplace(k, e);
+    if (!ins.second) (void)hipFree(e.dev);  // another thread uploaded it first
+    view = ins.first->second.view;
+    return 0;
+}
+
+// Router [E][N] fp32 on the host -> device copy transposed to [N][E] (cached).
+int get_router(const float *host, int E, int N, const float **dev_out)
+{
+    auto key = std::make_tuple((const void *)host, E, N);
+    {
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        auto it = g_router_cache.find(key);
+        if (it != g_router_cache.end()) { *dev_out = it->second; return 0; }
+    }
+    std::vector<float> t((size_t)E * N);
+    for (int e = 0; e < E; e++)
+        for (int i = 0; i < N; i++) t[(size_t)i * E + e] = host[(size_t)e * N + i];
+    float *d = nullptr;
+    HIP_OK(hipMalloc(&d, t.size() * 4));
+    HIP_OK(hipMemcpy(d, t.data(), t.size() * 4, hipMemcpyHostToDevice));
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto ins = g_router_cache.emplace(key, d);
+    if (!ins.second) (void)hipFree(d);
+    *dev_out = ins.first->second;
+    return 0;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Scratch layout for the Q8_0 activation pack of T rows x n_cols.
+struct xq_bufs {
+    int8_t *q; float *d; float *s4; int *sq;
+};
+size_t xq_bytes(long T, int n_cols)
+{
+    const long nb = n_cols / 32;
+    return align256(T * nb * 32) + 3 * align256(T * nb * 4);
+}
+xq_bufs xq_carve(void *base, long T, int n_cols)
+{
+    const long nb = n_cols / 32;
+    uint8_t *p = (uint8_t *)base;
+    xq_bufs b;
+    b.q = (int8_t *)p; p += align256(T * nb * 32);
+    b.d = (float *)p; p += align256(T * nb * 4);
+    b.s4 = (float *)p; p += align256(T * nb * 4);
+    b.sq = (int *)p;
+    return b;
+}
+
+// Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data.
+int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_rows, int n_cols, int B,
+             void *scratch, hipStream_t st)
+{
+    const bool q8 = mllm_sem_uses_q8(sem);
+    xq_bufs xb{};
+    if (q8) {
+        xb = xq_carve(scratch, B, n_cols);
+        HIP_OK(mllm_launch_quantize_q8_0(x, B, n_cols, nullptr, xb.q, xb.d, xb.s4, xb.sq, st));
+    }
+    for (int b0 = 0; b0 < B; b0 += 8) {
+        mllm_gemv_args a{};
+        a.W = W;
+        a.x = x + (long)b0 * n_cols;
+        a.ldx = n_cols;
+        a.out = out + (long)b0 * n_rows;
+        a.ldo = n_rows;
+        a.n_rows = n_rows; a.n_cols = n_cols; a.B = B - b0 < 8 ? B - b0 : 8;
+        if (q8) {
+            const long nb = n_cols / 32;
+            a.xq = {xb.q + (long)b0 * n_cols, xb.d + b0 * nb, xb.s4 + b0 * nb, xb.sq + b0 * nb};
+        }
+        HIP_OK(mllm_launch_gemv(sem, a, 1, st));
+    }
+    return 0;
+}
+
+// Drop-in GEMV: host W/x/out, B tokens.
+int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows, int n_cols, int B)
+{
+    if (n_rows <= 0 || B <= 0) return 0;
+    thread_ctx &c = t_ctx;
+    if (c.init()) return -1;
+    const int ly = mllm_sem_layout(sem);
+    mllm_packed view;
+    if (get_weight(W, ly, n_rows, n_cols, view)) return -1;
+    const size_t xbytes = (size_t)B * n_cols * 4, obytes = (size_t)B * n_rows * 4;
+    if (c.d_in.ensure(xbytes) || c.d_out.ensure(obytes) || c.h_in.ensure(xbytes) || c.h_out.ensure(obytes) ||
+        c.d_scr.ensure(xq_bytes(B, n_cols))) {
+        set_error("staging allocation failed");
+        return -1;
+    }
+    memcpy(c.h_in.p, x, xbytes);
+    HIP_OK(hipMemcpyAsync(c.d_in.p, c.h_in.p, xbytes, hipMemcpyHostToDevice, c.st));
+    if (run_gemv(sem, view, (const float *)c.d_in.p, (float *)c.d_out.p, n_rows, n_cols, B, c.d_scr.p, c.st)) return -1;
+    HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
+    HIP_OK(hipStreamSynchronize(c.st));
+    memcpy(out, c.h_out.p, obytes);
+    return 0;
+}
+
+int layout_for_qt_bmm(int qt)
+{
+    int s = sem_for(ENT_BMM, qt);
+    return s < 0 ? -1 : mllm_sem_layout(s);
+}
+
+// moe_ffn (CE:591-665) reads these fields of the engine's BC struct (x86-64 offsets of CE:536-589).
+enum { BC_N = 4, BC_NE = 224, BC_NK = 228, BC_M = 232, BC_ROUTER = 240, BC_GATE = 248, BC_UP = 256, BC_DOWN = 264,
+       BC_QG = 272, BC_QU = 276, BC_QD = 280 };
+
+template <class T> static T bc_field(const void *c, int off)
+{
+    T v;
+    memcpy(&v, (const uint8_t *)c + off, sizeof v);
+    return v;
+}
+
+// moe_ffn's expert strides (CE:593-605): gate/up default to the Q4_K size and
+// down to the Q6_K size; only codes 12/13/14/39 change them.
+static long moe_ffn_stride(int which, int qt, int N, int M)
+{
+    if (which < 2) {
+        long s = (long)M * (N / 256) * 144;
+        if (qt == 13) s = (long)M * (N / 256) * 176;
+        if (qt == 14) s = (long)M * (N / 256) * 210;
+        if (qt == 39) s = (long)M * (N / 32) * 17;
+        return s;
+    }
+    long s = (long)N * (M / 256) * 210;
+    if (qt == 12) s = (long)N * (M / 256) * 144;
+    if (qt == 13) s = (long)N * (M / 256) * 176;
+    if (qt == 39) s = (long)N * (M / 32) * 17;
+    return s;
+}
+
+} // namespace
+
+// =============================================================== drop-in ABI
+extern "C" {
+
+MLLM_API void quant_matmul_omp(const uint8_t *W, const float *x, float *out, int n_rows, int n_cols, int quant_type)
+{
+    const int sem = sem_for(ENT_QMM, quant_type);
+    if (sem < 0) { set_error("quant_matmul_omp: unknown quant type %d (output untouched)", quant_type); return; }
+    host_gemv(sem, W, x, out, n_rows, n_cols, 1);
+}
+
+MLLM_API void f32_matmul_omp(const float *W, const float *x, float *out, int n_rows, int n_cols)
+{
+    host_gemv(SEM_F32, (const uint8_t *)W, x, out, n_rows, n_cols, 1);
+}
+
+#define MLLM_BMM(name, qt)                                                                           \
+    MLLM_API void name(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B)     \
+    {                                                                                                \
+        host_gemv(sem_for(ENT_BMM, qt), W, x, out, n_rows, nc, B);                                 \
+    }
+MLLM_BMM(q4_0_batch_matmul, 2)
+MLLM_BMM(q8_0_batch_matmul, 8)
+MLLM_BMM(q4_k_batch_matmul, 12)
+MLLM_BMM(q6_k_batch_matmul, 14)
+MLLM_BMM(q5_k_batch_matmul, 13)
+MLLM_BMM(mxfp4_batch_matmul, 39)
+#undef MLLM_BMM
+
+MLLM_API void batch_qkv_omp(const uint8_t *Wq, const uint8_t *Wk, const uint8_t *Wv, const float *x, float *out_q,
+                            float *out_k, float *out_v, int nq, int nk, int nv, int n_cols, int qtype_q, int qtype_k,
+                            int qtype_v)
+{
+    const uint8_t *Ws[3] = {Wq, Wk, Wv};
+    float *outs[3] = {out_q, out_k, out_v};
+    const int ns[3] = {nq, nk, nv}, qts[3] = {qtype_q, qtype_k, qtype_v};
+    for (int i = 0; i < 3; i++) {
+        const int sem = sem_for(ENT_ROWS, qts[i]);
+        if (sem < 0) { set_error("batch_qkv_omp: unknown quant type %d", qts[i]); continue; }
+        host_gemv(sem, Ws[i], x, outs[i], ns[i], n_cols, 1);
+    }
+}
+
+MLLM_API void batch_gate_up_omp(const uint8_t *Wg, const uint8_t *Wu, const float *x, float *out_gate, float *out_up,
+                                int ng, int nu, int n_cols, int qtype_g, int qtype_u)
+{
+    const int sg = sem_for(ENT_ROWS, qtype_g), su = sem_for(ENT_ROWS, qtype_u);
+    if (sg >= 0) host_gemv(sg, Wg, x, out_gate, ng, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_g);
+    if (su >= 0) host_gemv(su, Wu, x, out_up, nu, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_u);
+}
+
+MLLM_API int quantize_row_q8_0(const float *x, uint8_t *q8, int n_cols)
+{
+    const int nb = n_cols / 32;
+    if (nb <= 0) return nb;
+    thread_ctx &c = t_ctx;
+    if (c.init()) return nb;
+    const size_t xb = (size_t)n_cols * 4, qb = (size_t)nb * 34;
+    if (c.d_in.ensure(xb) || c.d_out.ensure(qb) || c.h_in.ensure(xb) || c.h_out.ensure(qb)) { set_error("staging allocation failed"); return nb; }
+    memcpy(c.h_in.p, x, xb);
+    if (hipMemcpyAsync(c.d_in.p, c.h_in.p, xb, hipMemcpyHostToDevice, c.st) != hipSuccess ||
+        mllm_launch_quantize_q8_0((const float *)c.d_in.p, 1, n_cols, (uint8_t *)c.d_out.p, nullptr, nullptr, nullptr,
+                                  nullptr, c.st) != hipSuccess ||
+        hipMemcpyAsync(c.h_out.p, c.d_out.p, qb, hipMemcpyDeviceToHost, c.st) != hipSuccess ||
+        hipStreamSynchronize(c.st) != hipSuccess) {
+        set_error("quantize_row_q8_0 failed");
+        return nb;
+    }
+    memcpy(q8, c.h_out.p, qb);
+    return nb;
+}
+
+// *_dequantize_row (QK:762-878): the ggml definitions, rounded as the reference rounds them.
+static void dequant_row(int sem, const uint8_t *W, float *out, int n_values)
+{
+    if (n_values <= 0) return;
+    thread_ctx &c = t_ctx;
+    if (c.init()) return;
+    mllm_packed view;
+    if (get_weight(W, mllm_sem_layout(sem), 1, n_values, view)) return;
+    const size_t ob = (size_t)n_values * 4;
+    if (c.d_out.ensure(ob) || c.h_out.ensure(ob)) { set_error("staging allocation failed"); return; }
+    if (mllm_launch_dequant(sem, view, 1, n_values, (float *)c.d_out.p, c.st) != 0) return;
+    if (hipMemcpyAsync(c.h_out.p, c.d_out.p, ob, hipMemcpyDeviceToHost, c.st) != hipSuccess ||
+        hipStreamSynchronize(c.st) != hipSuccess) { set_error("dequantize_row failed"); return; }
+    memcpy(out, c.h_out.p, ob);
+}
+MLLM_API void q4_k_dequantize_row(const uint8_t *W, float *out, int n_values) { dequant_row(SEM_Q4_K_GGML, W, out, n_values); }
+MLLM_API void q5_k_dequantize_row(const uint8_t *W, float *out, int n_values) { dequant_row(SEM_Q5_K_GGML, W, out, n_values); }
+MLLM_API void q6_k_dequantize_row(const uint8_t *W, float *out, int n_values) { dequant_row(SEM_Q6_K_GGML, W, out, n_values); }
+MLLM_API void q8_0_dequantize_row(const uint8_t *W, float *out, int n_values) { dequant_row(SEM_Q8_0, W, out, n_values); }
+
+MLLM_API void set_num_threads(int n) { (void)n; }
+MLLM_API int get_max_threads(void)
+{
+    int dev = 0, cus = 1;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    return cus;
+}
+
+// moe_forward_omp (QK:2066-2250): caller-supplied routing; gate/up per
+// type, SiLU clamped to +-80, down per type (MXFP4 through Q8_0(h)), and
+// combined[row] = sum_k w_k * down_k in k order (the reference sums with
+// an OpenMP atomic in no fixed order).  prealloc_buf is not written.
+MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, const uint8_t **down_raw,
+                              const float *x_norm, int n_ff_expert, int n_embd, int qt_gate, int qt_up, int qt_down,
+                              const int *top_indices, const float *top_weights, int top_k, float *combined,
+                              float *prealloc_buf, uint8_t *prealloc_q8)
+{
+    (void)prealloc_buf;
+    if (top_k <= 0 || n_embd <= 0) return;
+    if (top_k > 64) { set_error("moe_forward_omp: top_k %d > 64", top_k); return; }
+    thread_ctx &c = t_ctx;
+    if (c.init()) return;
+    const bool pair_mx = qt_gate == 39 && qt_up == 39;  // QK:2094
+    const int sg = pair_mx ? SEM_MXFP4 : sem_for(ENT_MOE_GU, qt_gate);
+    const int su = pair_mx ? SEM_MXFP4 : sem_for(ENT_MOE_GU, qt_up);
+    int sd = sem_for(ENT_MOE_DOWN, qt_down);
+    if (qt_down == 39 && !prealloc_q8) {
+        set_error("moe_forward_omp: MXFP4 down projection needs prealloc_q8 (the reference dereferences NULL); down treated as zero");
+        sd = -1;
+    }
+    const int K = top_k, F = n_ff_expert, N = n_embd;
+    // tables of the selected experts' packed views: [0,K) gate, [K,2K) up, [2K,3K) down
+    std::vector<mllm_packed> tab(3 * K);
+    for (int k = 0; k < K; k++) {
+        const int e = top_indices[k];
+        if (sg >= 0 && get_weight(gate_raw[e], mllm_sem_layout(sg), F, N, tab[k])) return;
+        if (su >= 0 && get_weight(up_raw[e], mllm_sem_layout(su), F, N, tab[K + k])) return;
+        if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k])) return;
+    }
+    // device scratch: x | g[K][F] | u[K][F] | h[K][F] | dn[K][N] | w[K] | xq(x) | xq(h)
+    size_t o_x = 0, o_g = align256(o_x + N * 4), o_u = align256(o_g + (size_t)K * F * 4),
+           o_h = align256(o_u + (size_t)K * F * 4), o_dn = align256(o_h + (size_t)K * F * 4),
+           o_w = align256(o_dn + (size_t)K * N * 4), o_xq = align256(o_w + K * 4),
+           o_hq = align256(o_xq + xq_bytes(1, N)), total = align256(o_hq + xq_bytes(K, F));
+    if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
+        c.h_in.ensure(N * 4 + K * 4 + tab.size() * sizeof(mllm_packed)) || c.h_out.ensure(N * 4)) {
+        set_error("moe_forward_omp: scratch allocation failed");
+        return;
+    }
+    uint8_t *S = (uint8_t *)c.d_scr.p;
+    float *dx = (float *)(S + o_x), *dg = (float *)(S + o_g), *du = (float *)(S + o_u), *dh = (float *)(S + o_h),
+          *ddn = (float *)(S + o_dn), *dw = (float *)(S + o_w);
+    uint8_t *hin = (uint8_t *)c.h_in.p;
+    memcpy(hin, x_norm, N * 4);
+    memcpy(hin + N * 4, top_weights, K * 4);
+    memcpy(hin + N * 4 + K * 4, tab.data(), tab.size() * sizeof(mllm_packed));
+    mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
+    hipStream_t st = c.st;
+#define CK(expr) do { if ((expr) != hipSuccess) { set_error("moe_forward_omp: %s failed", #expr); return; } } while (0)
+    CK(hipMemcpyAsync(dx, hin, N * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(dw, hin + N * 4, K * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(dtab, hin + N * 4 + K * 4, tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
+    xq_bufs xqx = xq_carve(S + o_xq, 1, N), xqh = xq_carve(S + o_hq, K, F);
+    if (mllm_sem_uses_q8(sg) || mllm_sem_uses_q8(su))
+        CK(mllm_launch_quantize_q8_0(dx, 1, N, nullptr, xqx.q, xqx.d, xqx.s4, xqx.sq, st));
+    auto gu = [&](int sem, const mllm_packed *t, float *out) -> hipError_t {
+        if (sem < 0) return hipMemsetAsync(out, 0, (size_t)K * F * 4, st);
+        mllm_gemv_args a{};
+        a.table = t; a.x = dx; a.x_job_stride = 0; a.ldx = N;
+        a.out = out; a.out_job_stride = F; a.ldo = F;
+        a.n_rows = F; a.n_cols = N; a.B = 1;
+        a.xq = {xqx.q, xqx.d, xqx.s4, xqx.sq};
+        return mllm_launch_gemv(sem, a, K, st);
+    };
+    CK(gu(sg, dtab, dg));
+    CK(gu(su, dtab + K, du));
+    CK(mllm_launch_silu_mul(dg, du, dh, (long)K * F, 1, st));
+    if (sd < 0) {
+        CK(hipMemsetAsync(ddn, 0, (size_t)K * N * 4, st));
+    } else {
+        if (mllm_sem_uses_q8(sd)) CK(mllm_launch_quantize_q8_0(dh, K, F, nullptr, xqh.q, xqh.d, xqh.s4, xqh.sq, st));
+        mllm_gemv_args a{};
+        a.table = dtab + 2 * K; a.x = dh; a.x_job_stride = F; a.ldx = F;
+        a.out = ddn; a.out_job_stride = N; a.ldo = N;
+        a.n_rows = N; a.n_cols = F; a.B = 1;
+        a.xq = {xqh.q, xqh.d, xqh.s4, xqh.sq};
+        CK(mllm_launch_gemv(sd, a, K, st));
+    }
+    CK(mllm_launch_combine(ddn, dw, 1, K, N, dx, 0, st));
+    CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
+    CK(hipStreamSynchronize(st));
+#undef CK
+    memcpy(combined, c.h_out.p, N * 4);
+}
+
+MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up_buf, float *ffn_buf, int B)
+{
+    (void)gate_buf; (void)up_buf;
+    if (B <= 0) return;
+    const int N = bc_field<int>(c, BC_N), E = bc_field<int>(c, BC_NE), K = bc_field<int>(c, BC_NK),
+              M = bc_field<int>(c, BC_M);
+    const int qts[3] = {bc_field<int>(c, BC_QG), bc_field<int>(c, BC_QU), bc_field<int>(c, BC_QD)};
+    const float *router = bc_field<const float **>(c, BC_ROUTER)[l];
+    const uint8_t *bases[3] = {bc_field<const uint8_t **>(c, BC_GATE)[l], bc_field<const uint8_t **>(c, BC_UP)[l],
+                               bc_field<const uint8_t **>(c, BC_DOWN)[l]};
+    // With B > 1 the reference clears ffn_buf per token, so only the last token's result survives (CE:610-643).
+    mllm_moe_ffn_dev_tokens(router, bases, qts, N, E, K, M, x + (long)(B - 1) * N, ffn_buf, 1);
+}
+
+// Out-of-path symbols the reference caller binds unconditionally (TE:263-311,397-408).
+MLLM_API void ssm_layer_fused(void) { set_error("ssm_layer_fused is outside this library's scope (no-op)"); }
+MLLM_API void qwen36_batch_forward(void) { set_error("qwen36_batch_forward is outside this library's scope (no-op)"); }
+MLLM_API void ssm_decode_step(void) { set_error("ssm_decode_step is outside this library's scope (no-op)"); }
+
+MLLM_API const char *mllm_last_error(void) { return g_last_error.c_str(); }
+
+MLLM_API void mllm_cache_clear(void)
+{
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    (void)hipDeviceSynchronize();
+    for (auto &kv : g_cache) (void)hipFree(kv.second.dev);
+    g_cache.clear();
+    for (auto &kv : g_router_cache) (void)hipFree(kv.second);
+    g_router_cache.clear();
+}
+
+// ====================================================== device-pointer ABI
+MLLM_API int mllm_sem_for(int entry, int quant_type) { return sem_for(entry, quant_type); }
+
+MLLM_API long mllm_packed_size(int sem, int n_rows, int n_cols)
+{
+    if (sem < 0 || sem >= SEM_COUNT || n_rows < 0 || n_cols < 0) return -1;
+    const int ly = mllm_sem_layout(sem);
+    if (ly == LY_F32) return (long)n_rows * n_cols * 4;
+    return mllm_packed_bytes(ly, n_rows, n_cols, nullptr);
+}
+
+MLLM_API long mllm_raw_size(int sem, int n_rows, int n_cols)
+{
+    if (sem < 0 || sem >= SEM_COUNT) return -1;
+    return raw_row_bytes(mllm_sem_layout(sem), n_cols) * n_rows;
+}
+
+MLLM_API int mllm_pack(int sem, const void *raw_dev, void *packed_dev, int n_rows, int n_cols, void *stream)
+{
+    if (sem < 0 || sem >= SEM_COUNT) { set_error("mllm_pack: bad semantic %d", sem); return -1; }
+    HIP_OK(mllm_launch_pack(mllm_sem_layout(sem), (const uint8_t *)raw_dev, (uint8_t *)packed_dev, n_rows, n_cols,
+                            (hipStream_t)stream));
+    return 0;
+}
+
+MLLM_API long mllm_gemv_workspace_size(int sem, int n_cols, int B)
+{
+    return mllm_sem_uses_q8(sem) ? (long)xq_bytes(B, n_cols) : 0;
+}
+
+MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
+                       int B, void *workspace, void *stream)
+{
+    if (sem < 0 || sem >= SEM_COUNT) { set_error("mllm_gemv: bad semantic %d", sem); return -1; }
+    if (((uintptr_t)x_dev & 15) || ((uintptr_t)packed_dev & 255)) { set_error("mllm_gemv: misaligned pointer"); return -1; }
+    if (mllm_sem_uses_q8(sem) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
+    mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
+    return run_gemv(sem, view, x_dev, out_dev, n_rows, n_cols, B, workspace, (hipStream_t)stream);
+}
+
+MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *q8_dev, void *stream)
+{
+    HIP_OK(mllm_launch_quantize_q8_0(x_dev, T, n_cols, q8_dev, nullptr, nullptr, nullptr, nullptr, (hipStream_t)stream));
+    return 0;
+}
+
+MLLM_API int mllm_route(const float *router_t_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
+                        int *idx_dev, float *w_dev, void *stream)
+{
+    hipError_t r = mllm_launch_route(router_t_dev, x_dev, T, N, E, K, renorm, idx_dev, w_dev, (hipStream_t)stream);
+    if (r != hipSuccess) { set_error("mllm_route: %s (E<=256, K<=16 required)", hipGetErrorString(r)); return -1; }
+    return 0;
+}
+
+MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_cols, float *out_dev, void *stream)
+{
+    mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
+    return mllm_launch_dequant(sem, view, n_rows, n_cols, out_dev, (hipStream_t)stream);
+}
+
+} // extern "C"
+
+// ---------------------------------------------------------- moe_ffn engine
+// Decode MoE for T tokens with moe_ffn semantics (A11): C routing without
+// renormalisation, quant_matmul_omp semantics per expert, unclamped SiLU,
+// ffn = fma(p_k, down_k, ffn) in k order.  Experts are addressed at
+// base + e*stride exactly as CE:593-605 computes them.
+int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], const int qts[3], int N, int E, int K,
+                            int M, const float *x_host, float *out_host, int T)
+{
+    thread_ctx &c = t_ctx;
+    if (c.init()) return -1;
+    const int sems[3] = {sem_for(ENT_QMM, qts[0]), sem_for(ENT_QMM, qts[1]), sem_for(ENT_QMM, qts[2])};
+    if (sems[0] < 0 || sems[1] < 0 || sems[2] < 0) {
+        // the reference's quant_matmul_omp leaves buffers untouched for unknown codes; we zero the output
+        set_error("moe_ffn: unknown expert quant type (%d,%d,%d)", qts[0], qts[1], qts[2]);
+        memset(out_host, 0, (size_t)N * T * 4);
+        return -1;
+    }
+    if (K > 16 || E > 256) { set_error("moe_ffn: E<=256 and K<=16 required"); return -1; }
+    // per-expert packed views, cached per (layer tensor, expert)
+    std::vector<mllm_packed> tab(3 * (size_t)E);
+    for (int w = 0; w < 3; w++) {
+        const long stride = moe_ffn_stride(w, qts[w], N, M);
+        const int rows = w < 2 ? M : N, cols = w < 2 ? N : M;
+        for (int e = 0; e < E; e++)
+            if (get_weight(bases[w] + (long)e * stride, mllm_sem_layout(sems[w]), rows, cols, tab[(size_t)w * E + e])) return -1;
+    }
+    const float *rt = nullptr;
+    if (get_router(router, E, N, &rt)) return -1;
+    // scratch: x[T][N] | idx[T][K] | w[T][K] | g,u,h [T*K][M] | dn [T*K][N] | out[T][N] | xq(x) | xq(h)
+    const size_t TK = (size_t)T * K;
+    size_t o_x = 0, o_i = align256(o_x + (size_t)T * N * 4), o_w = align256(o_i + TK * 4), o_g = align256(o_w + TK * 4),
+           o_u = align256(o_g + TK * M * 4), o_h = align256(o_u + TK * M * 4), o_dn = align256(o_h + TK * M * 4),
+           o_o = align256(o_dn + TK * N * 4), o_xq = align256(o_o + (size_t)T * N * 4),
+           o_hq = align256(o_xq + xq_bytes(T, N)), total = align256(o_hq + xq_bytes(TK, M));
+    if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
+        c.h_in.ensure((size_t)T * N * 4) || c.h_out.ensure((size_t)T * N * 4)) {
+        set_error("moe_ffn: scratch allocation failed");
+        return -1;
+    }
+    uint8_t *S = (uint8_t *)c.d_scr.p;
+    float *dx = (float *)(S + o_x), *dwt = (float *)(S + o_w), *dg = (float *)(S + o_g), *du = (float *)(S + o_u),
+          *dh = (float *)(S + o_h), *ddn = (float *)(S + o_dn), *dout = (float *)(S + o_o);
+    int *didx = (int *)(S + o_i);
+    mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
+    hipStream_t st = c.st;
+    memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
+    HIP_OK(hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st));
+    HIP_OK(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
+    HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, st));
+    xq_bufs xqx = xq_carve(S + o_xq, T, N), xqh = xq_carve(S + o_hq, (long)TK, M);
+    if (mllm_sem_uses_q8(sems[0]) || mllm_sem_uses_q8(sems[1]))
+        HIP_OK(mllm_launch_quantize_q8_0(dx, T, N, nullptr, xqx.q, xqx.d, xqx.s4, xqx.sq, st));
+    for (int t = 0; t < T; t++) {
+        for (int w = 0; w < 2; w++) {
+            mllm_gemv_args a{};
+            a.table = dtab + (size_t)w * E; a.idx = didx + (size_t)t * K;
+            a.x = dx + (size_t)t * N; a.x_job_stride = 0; a.ldx = N;
+            a.out = (w == 0 ? dg : du) + (size_t)t * K * M; a.out_job_stride = M; a.ldo = M;
+            a.n_rows = M; a.n_cols = N; a.B = 1;
+            const long nb = N / 32;
+            a.xq = {xqx.q + (size_t)t * N, xqx.d + t * nb, xqx.s4 + t * nb, xqx.sq + t * nb};
+            HIP_OK(mllm_launch_gemv(sems[w], a, K, st));
+        }
+    }
+    HIP_OK(mllm_launch_silu_mul(dg, du, dh, (long)TK * M, 0, st));
+    if (mllm_sem_uses_q8(sems[2])) HIP_OK(mllm_launch_quantize_q8_0(dh, (int)TK, M, nullptr, xqh.q, xqh.d, xqh.s4, xqh.sq, st));
+    for (int t = 0; t < T; t++) {
+        mllm_gemv_args a{};
+        a.table = dtab + 2 * (size_t)E; a.idx = didx + (size_t)t * K;
+        a.x = dh + (size_t)t * K * M; a.x_job_stride = M; a.ldx = M;
+        a.out = ddn + (size_t)t * K * N; a.out_job_stride = N; a.ldo = N;
+        a.n_rows = N; a.n_cols = M; a.B = 1;
+        const long nb = M / 32;
+        a.xq = {xqh.q + (size_t)t * K * M, xqh.d + t * K * nb, xqh.s4 + t * K * nb, xqh.sq + t * K * nb};
+        HIP_OK(mllm_launch_gemv(sems[2], a, K, st));
+    }
+    HIP_OK(mllm_launch_combine(ddn, dwt, T, K, N, dout, 1, st));
+    HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
+    HIP_OK(hipStreamSynchronize(st));
+    memcpy(out_host, c.h_out.p, (size_t)T * N * 4);
+    return 0;
+}

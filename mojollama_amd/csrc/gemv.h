@@ -1,0 +1,57 @@
+// gemv.h — host-side launch interfaces of the kernels in libmllm_gpu.
+#pragma once
+#include <hip/hip_runtime.h>
+#include "mllm_common.h"
+
+// One decode GEMV launch.  A "job" is one matrix-vector product; blockIdx.y
+// walks the jobs.  Matrix of job j: `W` when `table` is null, otherwise
+// table[idx ? idx[j] : j] (device arrays).  x / out of job j start at
+// x + j*x_job_stride / out + j*out_job_stride (elements); token b of a job
+// reads x + b*ldx and writes out + b*ldo.
+struct mllm_gemv_args {
+    mllm_packed W;
+    const mllm_packed *table;
+    const int *idx;
+    const float *x;
+    long x_job_stride;
+    int ldx;
+    float *out;
+    long out_job_stride;
+    int ldo;
+    int n_rows, n_cols, B;
+    mllm_xq xq;   // Q8_0 activation pack (Q8 semantics only); job/token strides follow x's
+};
+
+hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStream_t st);
+
+// Repack raw GGUF blocks (device) into the plane layout `ly`.
+hipError_t mllm_launch_pack(int ly, const uint8_t *raw, uint8_t *packed, int n_rows, int n_cols, hipStream_t st);
+mllm_packed mllm_packed_view(int ly, const uint8_t *packed, int n_rows, int n_cols);
+
+// quantize_row_q8_0 over T rows of n_cols floats (QK:1406-1455), bit-exact.
+// Writes the raw 34-byte blocks to q8_raw (if non-null) and the activation
+// pack (q / d / s4 / sq) to the xq arrays (if non-null).
+hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t *q8_raw,
+                                     int8_t *xq_q, float *xq_d, float *xq_s4, int *xq_sq, hipStream_t st);
+
+// Router: logits by a sequential fp32 FMA chain (CE:614-618), softmax with
+// expf, insertion top-k with strict '>' (CE:628-638), optional renormalise
+// (GO:88-92).  router_t is the router transposed to [N][E].
+hipError_t mllm_launch_route(const float *router_t, const float *x, int T, int N, int E, int K, int renorm,
+                             int *top_idx, float *top_w, hipStream_t st);
+
+// h[i] = silu(g[i]) * u[i] (clamp g to +-80 when clamp != 0), i < n.
+hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st);
+
+// out[t][i] = sum_k (in k order) w[t][k] * d[t][k][i]; fused selects fmaf (moe_ffn CE:662) or
+// add-of-product (moe_forward_omp QK:2243-2244).
+hipError_t mllm_launch_combine(const float *d, const float *w, int T, int K, int N, float *out, int fused,
+                               hipStream_t st);
+
+// fp32 rows of a packed matrix under a fp32-weight semantic; returns 0 or -1
+// (semantic without an fp32 weight form, or launch failure).
+int mllm_launch_dequant(int sem, const mllm_packed &W, int n_rows, int n_cols, float *out, hipStream_t st);
+
+// moe_ffn engine for T tokens (host activations in/out); see capi.hip.
+int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], const int qts[3], int N, int E, int K,
+                            int M, const float *x_host, float *out_host, int T);

@@ -1,0 +1,178 @@
+"""ctypes bindings of libmllm_gpu.so.
+
+``load_kernels()`` binds the drop-in symbols with exactly the ``argtypes``
+the reference's Python engine uses for its C library
+(src/mojollama/kernels/turbo_engine_v7_moe.py:_load_kernels, TE:240-392), so
+engine code written against that library runs unchanged on this one.
+
+``DeviceOps`` wraps the mllm_* device-pointer entry points for torch tensors
+already on the GPU (the benchmark and batched paths).
+
+There is no CPU fallback: if the library is missing or cannot be loaded,
+``load_kernels()`` raises.
+"""
+import ctypes
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmllm_gpu.so")
+
+cf = ctypes.POINTER(ctypes.c_float)
+cu = ctypes.POINTER(ctypes.c_uint8)
+ci = ctypes.c_int
+cvp = ctypes.c_void_p
+
+# Semantic ids (mllm_sem, mojollama_amd/csrc/mllm_common.h).
+F32, Q4_0, Q4_1, Q5_0_F32, Q5_0_Q8, Q8_0, Q4_K_GGML, Q4_K_Q8 = range(8)
+Q5_K_GGML, Q5_K_CE, Q6_K_GGML, Q6_K_LOWNIB, Q6_K_SEQ, MXFP4, MXFP4_CLAMP, MXFP4_Q8 = range(8, 16)
+SEM_NAMES = ["F32", "Q4_0", "Q4_1", "Q5_0_F32", "Q5_0_Q8", "Q8_0", "Q4_K_GGML", "Q4_K_Q8",
+             "Q5_K_GGML", "Q5_K_CE", "Q6_K_GGML", "Q6_K_LOWNIB", "Q6_K_SEQ", "MXFP4",
+             "MXFP4_CLAMP", "MXFP4_Q8"]
+# Reference entry points, for mllm_sem_for().
+ENT_QMM, ENT_BMM, ENT_ROWS, ENT_MOE_GU, ENT_MOE_DOWN = range(5)
+
+
+def build(verbose=False):
+    """Compile libmllm_gpu.so for gfx950 in-tree (hipcc)."""
+    r = subprocess.run(["make", "-s", "-C", os.path.join(HERE, "csrc")], capture_output=not verbose, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("libmllm_gpu build failed:\n" + (r.stdout or "") + (r.stderr or ""))
+
+
+_LIB = None
+
+
+def load_kernels(path=LIB_PATH):
+    """Load the library and bind the reference engine's symbols (TE:251-392) plus mllm_*."""
+    global _LIB
+    if _LIB is not None and path == LIB_PATH:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run mojollama_amd.kernels.build() (needs hipcc)")
+    so = ctypes.CDLL(path)
+    # --- as bound by TE:251-261, 363-377, 389-392
+    so.quant_matmul_omp.argtypes = [cu, cf, cf, ci, ci, ci]
+    so.quant_matmul_omp.restype = None
+    so.f32_matmul_omp.argtypes = [cf, cf, cf, ci, ci]
+    so.f32_matmul_omp.restype = None
+    # QK:1139-1145 takes three quant types (TE:255 lists only two: its third is dropped there)
+    so.batch_qkv_omp.argtypes = [cu, cu, cu, cf, cf, cf, cf, ci, ci, ci, ci, ci, ci, ci]
+    so.batch_qkv_omp.restype = None
+    so.batch_gate_up_omp.argtypes = [cu, cu, cf, cf, cf, ci, ci, ci, ci, ci]
+    so.batch_gate_up_omp.restype = None
+    so.set_num_threads.argtypes = [ci]
+    so.set_num_threads.restype = None
+    so.moe_forward_omp.argtypes = [ctypes.POINTER(cu), ctypes.POINTER(cu), ctypes.POINTER(cu), cf, ci, ci,
+                                   ci, ci, ci, ctypes.POINTER(ctypes.c_int), cf, ci, cf, cf, cu]
+    so.moe_forward_omp.restype = None
+    for name in ("q6_k_dequantize_row", "q4_k_dequantize_row", "q5_k_dequantize_row", "q8_0_dequantize_row"):
+        getattr(so, name).argtypes = [cu, cf, ci]
+        getattr(so, name).restype = None
+    # --- the engine's other kernel entry points (CE:68-534, 591; QK:1406, 1029)
+    for name in ("q4_0_batch_matmul", "q8_0_batch_matmul", "q4_k_batch_matmul", "q6_k_batch_matmul",
+                 "q5_k_batch_matmul", "mxfp4_batch_matmul"):
+        getattr(so, name).argtypes = [cu, cf, cf, ci, ci, ci]
+        getattr(so, name).restype = None
+    so.moe_ffn.argtypes = [cvp, ci, cf, cf, cf, cf, ci]
+    so.moe_ffn.restype = None
+    so.quantize_row_q8_0.argtypes = [cf, cu, ci]
+    so.quantize_row_q8_0.restype = ci
+    so.get_max_threads.argtypes = []
+    so.get_max_threads.restype = ci
+    so.mllm_last_error.argtypes = []
+    so.mllm_last_error.restype = ctypes.c_char_p
+    so.mllm_cache_clear.argtypes = []
+    so.mllm_cache_clear.restype = None
+    # --- device-pointer API
+    so.mllm_sem_for.argtypes = [ci, ci]
+    so.mllm_sem_for.restype = ci
+    so.mllm_raw_size.argtypes = [ci, ci, ci]
+    so.mllm_raw_size.restype = ctypes.c_long
+    so.mllm_packed_size.argtypes = [ci, ci, ci]
+    so.mllm_packed_size.restype = ctypes.c_long
+    so.mllm_pack.argtypes = [ci, cvp, cvp, ci, ci, cvp]
+    so.mllm_pack.restype = ci
+    so.mllm_gemv_workspace_size.argtypes = [ci, ci, ci]
+    so.mllm_gemv_workspace_size.restype = ctypes.c_long
+    so.mllm_gemv.argtypes = [ci, cvp, cvp, cvp, ci, ci, ci, cvp, cvp]
+    so.mllm_gemv.restype = ci
+    so.mllm_quantize_q8_0.argtypes = [cvp, ci, ci, cvp, cvp]
+    so.mllm_quantize_q8_0.restype = ci
+    so.mllm_route.argtypes = [cvp, cvp, ci, ci, ci, ci, ci, cvp, cvp, cvp]
+    so.mllm_route.restype = ci
+    so.mllm_dequant.argtypes = [ci, cvp, ci, ci, cvp, cvp]
+    so.mllm_dequant.restype = ci
+    if path == LIB_PATH:
+        _LIB = so
+    return so
+
+
+def last_error(so=None):
+    so = so or load_kernels()
+    return so.mllm_last_error().decode()
+
+
+class DeviceOps:
+    """mllm_* calls on torch tensors that live on the current GPU."""
+
+    def __init__(self, so=None):
+        import torch
+        self.torch = torch
+        self.so = so or load_kernels()
+
+    def _stream(self):
+        return ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {last_error(self.so)}")
+
+    def pack(self, sem, raw_dev, n_rows, n_cols):
+        """raw GGUF bytes (uint8 tensor on GPU) -> packed uint8 tensor."""
+        torch = self.torch
+        n = self.so.mllm_packed_size(sem, n_rows, n_cols)
+        packed = torch.empty(n, dtype=torch.uint8, device=raw_dev.device)
+        self._check(self.so.mllm_pack(sem, raw_dev.data_ptr(), packed.data_ptr(), n_rows, n_cols, self._stream()),
+                    "mllm_pack")
+        return packed
+
+    def workspace(self, sem, n_cols, B, device):
+        n = self.so.mllm_gemv_workspace_size(sem, n_cols, B)
+        return self.torch.empty(max(n, 256), dtype=self.torch.uint8, device=device) if n > 0 else None
+
+    def gemv(self, sem, packed, x, n_rows, n_cols, out=None, ws=None):
+        torch = self.torch
+        B = x.numel() // n_cols
+        if out is None:
+            out = torch.empty((B, n_rows), dtype=torch.float32, device=x.device)
+        if ws is None:
+            ws = self.workspace(sem, n_cols, B, x.device)
+        self._check(self.so.mllm_gemv(sem, packed.data_ptr(), x.data_ptr(), out.data_ptr(), n_rows, n_cols, B,
+                                      ws.data_ptr() if ws is not None else None, self._stream()), "mllm_gemv")
+        return out
+
+    def quantize_q8_0(self, x, n_cols):
+        torch = self.torch
+        T = x.numel() // n_cols
+        q8 = torch.empty(T * (n_cols // 32) * 34, dtype=torch.uint8, device=x.device)
+        self._check(self.so.mllm_quantize_q8_0(x.data_ptr(), T, n_cols, q8.data_ptr(), self._stream()),
+                    "mllm_quantize_q8_0")
+        return q8
+
+    def route(self, router_t, x, K, renorm):
+        torch = self.torch
+        N, E = router_t.shape
+        T = x.numel() // N
+        idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+        w = torch.empty((T, K), dtype=torch.float32, device=x.device)
+        self._check(self.so.mllm_route(router_t.data_ptr(), x.data_ptr(), T, N, E, K, int(renorm), idx.data_ptr(),
+                                       w.data_ptr(), self._stream()), "mllm_route")
+        return idx, w
+
+    def dequant(self, sem, packed, n_rows, n_cols):
+        torch = self.torch
+        out = torch.empty((n_rows, n_cols), dtype=torch.float32, device=packed.device)
+        self._check(self.so.mllm_dequant(sem, packed.data_ptr(), n_rows, n_cols, out.data_ptr(), self._stream()),
+                    "mllm_dequant")
+        return out

@@ -169,23 +169,49 @@ struct wkey {
 struct wentry {
     uint8_t *dev = nullptr;
     long bytes = 0;
+    uint64_t fp = 0;
     mllm_packed view;
 };
 std::mutex g_cache_mu;
 std::map<wkey, wentry> g_cache;
+std::vector<uint8_t *> g_retired;  // replaced device copies, freed by mllm_cache_clear()
+
+// Fingerprint of a host buffer: 64 words sampled across it.  A cache hit
+// whose fingerprint changed (the caller freed a matrix and a new one landed
+// at the same address) re-uploads instead of using stale weights.
+uint64_t fingerprint(const void *p, long n)
+{
+    const uint8_t *b = (const uint8_t *)p;
+    uint64_t h = 1469598103934665603ull ^ (uint64_t)n;
+    if (n <= 0) return h;
+    for (int i = 0; i < 64; i++) {
+        long off = (long)((__int128)n * i / 64);
+        uint64_t w = 0;
+        memcpy(&w, b + off, (size_t)(n - off < 8 ? n - off : 8));
+        h = (h ^ w) * 1099511628211ull;
+    }
+    uint64_t w = 0;
+    memcpy(&w, b + (n >= 8 ? n - 8 : 0), (size_t)(n >= 8 ? 8 : n));
+    return (h ^ w) * 1099511628211ull;
+}
 std::map<std::tuple<const void *, int, int>, float *> g_router_cache;  // (host, E, N) -> transposed [N][E]
 
 // Upload + pack a raw host matrix (once).  Returns its packed view.
 int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
 {
     wkey k{host, ly, rows, cols};
+    const long raw = raw_row_bytes(ly, cols) * rows;
+    const uint64_t fpr = fingerprint(host, raw);
     {
         std::lock_guard<std::mutex> lk(g_cache_mu);
         auto it = g_cache.find(k);
-        if (it != g_cache.end()) { view = it->second.view; return 0; }
+        if (it != g_cache.end()) {
+            if (it->second.fp == fpr) { view = it->second.view; return 0; }
+            g_retired.push_back(it->second.dev);
+            g_cache.erase(it);
+        }
     }
     thread_ctx &c = t_ctx;
-    const long raw = raw_row_bytes(ly, cols) * rows;
     const long packed = ly == LY_F32 ? (raw > 0 ? raw : 256) : mllm_packed_bytes(ly, rows, cols, nullptr);
     wentry e;
     e.bytes = packed;
@@ -200,6 +226,7 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
         if (r != hipSuccess) { (void)hipFree(e.dev); set_error("weight upload failed: %s", hipGetErrorString(r)); return -1; }
     }
     e.view = mllm_packed_view(ly, e.dev, rows, cols);
+    e.fp = fpr;
     std::lock_guard<std::mutex> lk(g_cache_mu);
     auto ins = g_cache.emplace(k, e);
     if (!ins.second) (void)hipFree(e.dev);  // another thread uploaded it first
@@ -553,6 +580,8 @@ MLLM_API void mllm_cache_clear(void)
     (void)hipDeviceSynchronize();
     for (auto &kv : g_cache) (void)hipFree(kv.second.dev);
     g_cache.clear();
+    for (uint8_t *p : g_retired) (void)hipFree(p);
+    g_retired.clear();
     for (auto &kv : g_router_cache) (void)hipFree(kv.second);
     g_router_cache.clear();
 }

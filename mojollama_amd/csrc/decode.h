@@ -1,194 +1,317 @@
 // decode.h — device-side block decoders for every semantic, on the packed
 // plane layout of mllm_common.h.
 //
-// Unit of work: a "chunk" of 32 weights of one row, split into two runs of
-// 16 that each have one scale s and offset o (w = s*q + o, q integer-valued),
-// and whose activations sit at 16 consecutive element offsets x0.. / x1...
-// A lane loads one chunk with one or two 16-byte loads from the bulk plane
-// plus its scales, and decodes it in registers.
+// Unit of work: a "chunk" of 32 weights of one row.  A chunk is two runs of
+// 16 weights; run r has one scale s_r, one offset o_r and an integer bias
+// b, and its activations sit at 16 consecutive element offsets starting at
+// x_r.  The weights are w = s_r * (u - b) + o_r, where the unsigned codes u
+// (0..255) arrive packed four to a dword (U[0..3] run 0, U[4..7] run 1) so
+// that one v_cvt_f32_ubyteN converts each, and a dot product needs
+//     sum_i w_i x_i = s_r * sum_i u_i x_i + (o_r - s_r * b) * sum_i x_i.
+// Byte t of U[j] holds element code_pos<SEM>(j, t) of its run: in order for
+// formats that keep a run's elements in one nibble half ("SEQ": Q8_0, Q4_0,
+// Q4_1, Q4_K, Q5_K ggml, Q6_K ggml), interleaved for formats that put
+// elements 2i and 2i+1 in the two nibbles of byte i ("ILV": MXFP4, Q5_0,
+// the engine's Q5_K, Q6_K sequential).
+//
+// fetch<SEM>() issues the global loads of one chunk (one or two 16-byte
+// loads from the bulk plane plus the block scales), codes<SEM>() decodes them
+// in registers; callers fetch several rows before decoding any so the loads
+// are in flight together.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "mllm_common.h"
 
 #define MLLM_DEV __device__ __forceinline__
 
-MLLM_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+MLLM_DEV float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 // E8M0 byte -> float with bits (E << 23)  (QK:542, CE:449): 0 -> 0.0, 255 -> +inf.
 MLLM_DEV float e8m0f(uint32_t e) { return __uint_as_float(e << 23); }
 
-// 6-bit (scale, min) pair j of a K-quant scale array (get_scale_min_k4 QK:62-71).
-MLLM_DEV void k4_pair(int j, const uint8_t *q, int &sc, int &m)
-{
-    if (j < 4) { sc = q[j] & 63; m = q[j + 4] & 63; }
-    else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        m  = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+// Loads through the global address space: generic (flat) loads would share
+// the LDS wait counter and serialise the weight stream behind LDS reads.
+#define MLLM_GLOBAL __attribute__((address_space(1)))
+typedef unsigned int mllm_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mllm_u32x2 __attribute__((ext_vector_type(2)));
+typedef float mllm_f32x4 __attribute__((ext_vector_type(4)));
+template <class T> struct gld_impl {
+    static MLLM_DEV T load(const void *p) { return *(const MLLM_GLOBAL T *)p; }
+};
+template <> struct gld_impl<uint4> {
+    static MLLM_DEV uint4 load(const void *p)
+    {
+        const mllm_u32x4 v = *(const MLLM_GLOBAL mllm_u32x4 *)p;
+        return make_uint4(v.x, v.y, v.z, v.w);
     }
+};
+template <> struct gld_impl<uint2> {
+    static MLLM_DEV uint2 load(const void *p)
+    {
+        const mllm_u32x2 v = *(const MLLM_GLOBAL mllm_u32x2 *)p;
+        return make_uint2(v.x, v.y);
+    }
+};
+template <> struct gld_impl<float4> {
+    static MLLM_DEV float4 load(const void *p)
+    {
+        const mllm_f32x4 v = *(const MLLM_GLOBAL mllm_f32x4 *)p;
+        return make_float4(v.x, v.y, v.z, v.w);
+    }
+};
+template <class T> MLLM_DEV T gld(const void *p) { return gld_impl<T>::load(p); }
+
+// Streamed weight bytes: read once per pass, so loaded non-temporally.
+MLLM_DEV uint4 ld16(const uint8_t *p)
+{
+    const mllm_u32x4 v = __builtin_nontemporal_load((const MLLM_GLOBAL mllm_u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+MLLM_DEV uint4 ld16c(const uint8_t *p) { return gld<uint4>(p); }
+
+template <int SEM> struct sem_traits {
+    static constexpr bool kKQuant = (SEM == SEM_Q4_K_GGML || SEM == SEM_Q4_K_Q8 || SEM == SEM_Q5_K_GGML ||
+                                     SEM == SEM_Q5_K_CE || SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB ||
+                                     SEM == SEM_Q6_K_SEQ);
+    static constexpr int kBlockElems = kKQuant ? 256 : 32;
+    static constexpr int kChunksPerBlock = kBlockElems / 32;
+    // element order of the codes: interleaved nibbles
+    static constexpr bool kIlv = (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP || SEM == SEM_Q5_0_F32 ||
+                                  SEM == SEM_Q5_K_CE || SEM == SEM_Q6_K_SEQ);
+    static constexpr int kBias = (SEM == SEM_Q8_0) ? 128 : (SEM == SEM_Q4_0 || SEM == SEM_MXFP4 ||
+                                  SEM == SEM_MXFP4_CLAMP) ? 8 : (SEM == SEM_Q5_0_F32) ? 16 :
+                                 (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB || SEM == SEM_Q6_K_SEQ) ? 32 : 0;
+    // weights carry an offset term o (Q4_1 min, K-quant mins) besides the bias
+    static constexpr bool kOffset = (SEM == SEM_Q4_1 || SEM == SEM_Q4_K_GGML || SEM == SEM_Q5_K_GGML ||
+                                     SEM == SEM_Q5_K_CE);
+};
+
+// Element offset (0..15) within its run of byte t of code word U[j].
+template <int SEM>
+__host__ __device__ constexpr int code_pos(int j, int t)
+{
+    return sem_traits<SEM>::kIlv ? 8 * ((j & 3) >> 1) + 2 * t + (j & 1) : 4 * (j & 3) + t;
 }
 
-MLLM_DEV uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+struct raw_chunk {
+    uint4 a;      // bulk quant bytes of the chunk
+    uint4 b;      // second bulk piece (Q8_0 upper half, qh bytes)
+    uint4 m;      // block metadata (K-quant scales)
+    uint32_t d;   // scalar scale bits / scale bytes
+};
 
-struct mllm_chunk {
-    float q[32];
-    float s0, s1, o0, o1;
+struct chunk_codes {
+    uint32_t U[8];
+    float s0, s1, o0, o1;   // w = s*(u - bias) + o
     int x0, x1;
 };
 
-template <int SEM> struct sem_traits {
-    static constexpr int kBlockElems = (SEM == SEM_Q4_K_GGML || SEM == SEM_Q4_K_Q8 || SEM == SEM_Q5_K_GGML ||
-                                        SEM == SEM_Q5_K_CE || SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB ||
-                                        SEM == SEM_Q6_K_SEQ) ? 256 : 32;
-    static constexpr int kChunksPerBlock = kBlockElems / 32;
-    static constexpr bool kHasOffset = (SEM == SEM_Q4_1 || SEM == SEM_Q4_K_GGML || SEM == SEM_Q5_K_GGML ||
-                                        SEM == SEM_Q5_K_CE);
-};
+// K-quant metadata as packed by k_pack: [d:16 | dmin:16] [sc6 x 8 : 48 bits] [m6 x 8 : 48 bits]
+// (the 6-bit pairs of get_scale_min_k4, QK:62-71, laid out for shift extraction).
+// 32 bits of the 64-bit value hi:lo starting at bit sh (0 <= sh < 32): v_alignbit_b32.
+MLLM_DEV uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t sh) { return __builtin_amdgcn_alignbit(hi, lo, sh); }
 
-MLLM_DEV void bytes16(uint4 v, uint8_t b[16])
+MLLM_DEV void kq_pairs(const uint4 &m, int j0, int &s_a, int &m_a, int &s_b, int &m_b)
 {
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 16; i++) b[i] = (w[i >> 2] >> (8 * (i & 3))) & 0xFF;
+    // S occupies bits [0, 48) of m.y:m.z, M bits [48, 96) of m.y:m.z:m.w.
+    // 32-bit funnel shifts only: 64-bit shifts would need register pairs.
+    const int so = 6 * j0, mo = 48 + 6 * j0;              // so < 48, 48 <= mo < 96
+    const uint32_t sv = so < 32 ? funnel(m.z, m.y, so) : (m.z >> (so - 32));
+    const uint32_t mv = mo < 64 ? funnel(m.w, m.z, mo - 32) : (m.w >> (mo - 64));
+    s_a = sv & 63; s_b = (sv >> 6) & 63;
+    m_a = mv & 63; m_b = (mv >> 6) & 63;
 }
 
-// Decode chunk c (0 <= c < chunks per row) of row `row`; nb = blocks per row.
 template <int SEM>
-MLLM_DEV void load_chunk(const mllm_packed &P, int nb, int row, int c, mllm_chunk &k)
+MLLM_DEV void fetch(const mllm_packed &P, int nb, int row, int c, raw_chunk &r)
 {
     constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
     const int blk = c / CPB, cc = c % CPB;
     const long bi = (long)row * nb + blk;
-    k.o0 = k.o1 = 0.0f;
-    uint8_t b[16];
     if constexpr (SEM == SEM_Q8_0) {
-        // CE:216-253 / QK:376-416: w = d * q
-        const uint8_t *qs = P.p[0] + bi * 32;
-        uint8_t b2[16];
-        bytes16(ld16(qs), b);
-        bytes16(ld16(qs + 16), b2);
-        float d = h2f(*reinterpret_cast<const uint16_t *>(P.p[1] + bi * 2));
+        r.a = ld16(P.p[0] + bi * 32);
+        r.b = ld16(P.p[0] + bi * 32 + 16);
+        r.d = gld<uint16_t>(P.p[1] + bi * 2);
+    } else if constexpr (SEM == SEM_Q4_0) {
+        r.a = ld16(P.p[0] + bi * 16);
+        r.d = gld<uint16_t>(P.p[1] + bi * 2);
+    } else if constexpr (SEM == SEM_Q4_1) {
+        r.a = ld16(P.p[0] + bi * 16);
+        r.d = gld<uint32_t>(P.p[1] + bi * 4);
+    } else if constexpr (SEM == SEM_Q5_0_F32) {
+        r.a = ld16(P.p[0] + bi * 16);
+        r.b.x = gld<uint32_t>(P.p[1] + bi * 4);
+        r.d = gld<uint16_t>(P.p[2] + bi * 2);
+    } else if constexpr (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP) {
+        r.a = ld16(P.p[0] + bi * 16);
+        r.d = gld<uint8_t>(P.p[1] + bi);
+    } else if constexpr (SEM == SEM_Q4_K_GGML) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * cc);
+        r.m = ld16c(P.p[1] + bi * 16);
+    } else if constexpr (SEM == SEM_Q5_K_GGML) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * cc);
+        r.b = ld16c(P.p[1] + bi * 32 + 16 * (cc & 1));
+        r.m = ld16c(P.p[2] + bi * 16);
+    } else if constexpr (SEM == SEM_Q5_K_CE) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * cc);
+        r.b.x = gld<uint32_t>(P.p[1] + bi * 32 + 4 * cc);
+        r.m = ld16c(P.p[2] + bi * 16);
+    } else if constexpr (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB) {
+        const int h = cc >> 2, q1 = (cc >> 1) & 1, lh = cc & 1;
+        r.a = ld16(P.p[0] + bi * 128 + 16 * cc);
+        r.b = ld16c(P.p[1] + bi * 64 + 32 * h + 16 * lh);
+        const uint8_t *sc = P.p[2] + bi * 16 + 8 * h + lh + 2 * q1;
+        r.m.x = gld<uint8_t>(sc);
+        r.m.y = gld<uint8_t>(sc + 4);
+        r.d = gld<uint16_t>(P.p[3] + bi * 2);
+    } else if constexpr (SEM == SEM_Q6_K_SEQ) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * cc);
+        const uint2 q = gld<uint2>(P.p[1] + bi * 64 + 8 * cc);
+        r.b.x = q.x; r.b.y = q.y;
+        r.m.x = gld<uint16_t>(P.p[2] + bi * 16 + 2 * cc);
+        r.d = gld<uint16_t>(P.p[3] + bi * 2);
+    }
+}
+
+// Spread bit k of each of four elements (positions e0, e0+2, e0+4, e0+6 of
+// `bits`) into bit 4 of the four bytes of a dword (ILV element order).
+MLLM_DEV uint32_t ilv_bit4(uint32_t bits, int e0)
+{
+    const uint32_t v = bits >> e0;
+    return ((v & 1u) << 4) | ((v & 4u) << 10) | ((v & 16u) << 16) | ((v & 64u) << 22);
+}
+
+template <int SEM>
+MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
+{
+    constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
+    const int blk = c / CPB, cc = c % CPB;
+    const uint32_t A[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    const uint32_t L4 = 0x0F0F0F0Fu;
+    k.o0 = k.o1 = 0.0f;
+    if constexpr (SEM == SEM_Q8_0) {
+        // CE:216-253 / QK:376-416: w = d*q; u = q + 128
+        const uint32_t Bv[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
-        for (int i = 0; i < 16; i++) { k.q[i] = (float)(int8_t)b[i]; k.q[16 + i] = (float)(int8_t)b2[i]; }
-        k.s0 = k.s1 = d;
+        for (int j = 0; j < 4; j++) { k.U[j] = A[j] ^ 0x80808080u; k.U[4 + j] = Bv[j] ^ 0x80808080u; }
+        k.s0 = k.s1 = h2f(r.d);
         k.x0 = 32 * blk; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_Q4_0 || SEM == SEM_Q4_1) {
-        // QK:77-117: low nibble -> element k, high -> 16+k; Q4_0 w = (n-8)d, Q4_1 w = n d + m
-        bytes16(ld16(P.p[0] + bi * 16), b);
-        const int bias = (SEM == SEM_Q4_0) ? 8 : 0;
+        // QK:77-117: low nibble -> element k, high nibble -> 16+k; Q4_0 w = (n-8)d, Q4_1 w = n d + m
 #pragma unroll
-        for (int i = 0; i < 16; i++) { k.q[i] = (float)((b[i] & 15) - bias); k.q[16 + i] = (float)((b[i] >> 4) - bias); }
-        if constexpr (SEM == SEM_Q4_0) {
-            k.s0 = k.s1 = h2f(*reinterpret_cast<const uint16_t *>(P.p[1] + bi * 2));
-        } else {
-            uint32_t dm = *reinterpret_cast<const uint32_t *>(P.p[1] + bi * 4);
-            k.s0 = k.s1 = h2f(dm & 0xFFFF);
-            k.o0 = k.o1 = h2f(dm >> 16);
-        }
+        for (int j = 0; j < 4; j++) { k.U[j] = A[j] & L4; k.U[4 + j] = (A[j] >> 4) & L4; }
+        k.s0 = k.s1 = h2f(r.d & 0xFFFF);
+        if constexpr (SEM == SEM_Q4_1) k.o0 = k.o1 = h2f(r.d >> 16);
         k.x0 = 32 * blk; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_Q5_0_F32) {
         // QK:1245-1266: element e = nibble (e&1) of ql[e/2] | bit e of qh << 4, minus 16
-        bytes16(ld16(P.p[0] + bi * 16), b);
-        uint32_t qh = *reinterpret_cast<const uint32_t *>(P.p[1] + bi * 4);
+        const uint32_t qh = r.b.x;
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            int v = ((b[e >> 1] >> ((e & 1) * 4)) & 15) | (((qh >> e) & 1) << 4);
-            k.q[e] = (float)(v - 16);
+        for (int m = 0; m < 4; m++) {
+            k.U[2 * m] = (A[m] & L4) | ilv_bit4(qh, 8 * m);
+            k.U[2 * m + 1] = ((A[m] >> 4) & L4) | ilv_bit4(qh, 8 * m + 1);
         }
-        k.s0 = k.s1 = h2f(*reinterpret_cast<const uint16_t *>(P.p[2] + bi * 2));
+        k.s0 = k.s1 = h2f(r.d);
         k.x0 = 32 * blk; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP) {
-        // QK:485-627, CE:427-534: element e = sext4(nibble (e&1) of q[e/2]); w = v * 2^(E-127)
-        bytes16(ld16(P.p[0] + bi * 16), b);
-        float s = e8m0f(P.p[1][bi]);
-        if constexpr (SEM == SEM_MXFP4_CLAMP) s = fminf(s, 1e20f);
+        // QK:485-627, CE:427-534: element e = sext4(nibble (e&1) of q[e/2]); w = v * 2^(E-127);
+        // u = n ^ 8 = v + 8.
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            int n = (b[e >> 1] >> ((e & 1) * 4)) & 15;
-            k.q[e] = (float)(n >= 8 ? n - 16 : n);
+        for (int m = 0; m < 4; m++) {
+            const uint32_t w = A[m] ^ 0x88888888u;
+            k.U[2 * m] = w & L4;
+            k.U[2 * m + 1] = (w >> 4) & L4;
         }
+        float s = e8m0f(r.d);
+        if constexpr (SEM == SEM_MXFP4_CLAMP) s = fminf(s, 1e20f);
         k.s0 = k.s1 = s;
         k.x0 = 32 * blk; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_Q4_K_GGML || SEM == SEM_Q5_K_GGML) {
         // CE:255-313 / QK:830-866: chunk cc = qs[16cc..16cc+16) of group g = cc/2, half h = cc&1:
         // low nibbles -> elements 64g+16h+i (pair 2g), high -> 64g+32+16h+i (pair 2g+1).
         const int g = cc >> 1, h = cc & 1;
-        bytes16(ld16(P.p[0] + bi * 128 + 16 * cc), b);
-        const uint8_t *meta = P.p[SEM == SEM_Q4_K_GGML ? 1 : 2] + bi * 16;
-        uint4 mv = ld16(meta);
-        uint8_t mb[16];
-        bytes16(mv, mb);
-        float d = h2f(mv.x & 0xFFFF), dmin = h2f(mv.x >> 16);
-        int s1, m1, s2, m2;
-        k4_pair(2 * g, mb + 4, s1, m1);
-        k4_pair(2 * g + 1, mb + 4, s2, m2);
-        if constexpr (SEM == SEM_Q4_K_GGML) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) { k.q[i] = (float)(b[i] & 15); k.q[16 + i] = (float)(b[i] >> 4); }
-        } else {
-            uint8_t qh[16];
-            bytes16(ld16(P.p[1] + bi * 32 + 16 * h), qh);
+        for (int j = 0; j < 4; j++) { k.U[j] = A[j] & L4; k.U[4 + j] = (A[j] >> 4) & L4; }
+        if constexpr (SEM == SEM_Q5_K_GGML) {
+            const uint32_t Q[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                k.q[i] = (float)((b[i] & 15) + (((qh[i] >> (2 * g)) & 1) << 4));
-                k.q[16 + i] = (float)((b[i] >> 4) + (((qh[i] >> (2 * g + 1)) & 1) << 4));
+            for (int j = 0; j < 4; j++) {
+                k.U[j] |= ((Q[j] >> (2 * g)) & 0x01010101u) << 4;
+                k.U[4 + j] |= ((Q[j] >> (2 * g + 1)) & 0x01010101u) << 4;
             }
         }
+        int s1, m1, s2, m2;
+        kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
+        const float d = h2f(r.m.x & 0xFFFF), dmin = h2f(r.m.x >> 16);
         k.s0 = d * (float)s1; k.o0 = -(dmin * (float)m1);
         k.s1 = d * (float)s2; k.o1 = -(dmin * (float)m2);
         k.x0 = 256 * blk + 64 * g + 16 * h;
         k.x1 = k.x0 + 32;
     } else if constexpr (SEM == SEM_Q5_K_CE) {
         // CE:380-425: sequential; element e = nibble (e&1) of ql[e/2] | bit (e&7) of qh[e/8] << 4, pair e/32.
-        bytes16(ld16(P.p[0] + bi * 128 + 16 * cc), b);
-        uint32_t qh = *reinterpret_cast<const uint32_t *>(P.p[1] + bi * 32 + 4 * cc);
-        uint4 mv = ld16(P.p[2] + bi * 16);
-        uint8_t mb[16];
-        bytes16(mv, mb);
-        float d = h2f(mv.x & 0xFFFF), dmin = h2f(mv.x >> 16);
-        int s, m;
-        k4_pair(cc, mb + 4, s, m);
+        const uint32_t qh = r.b.x;
 #pragma unroll
-        for (int e = 0; e < 32; e++)
-            k.q[e] = (float)(((b[e >> 1] >> ((e & 1) * 4)) & 15) | (((qh >> e) & 1) << 4));
-        k.s0 = k.s1 = d * (float)s;
-        k.o0 = k.o1 = -(dmin * (float)m);
+        for (int m = 0; m < 4; m++) {
+            k.U[2 * m] = (A[m] & L4) | ilv_bit4(qh, 8 * m);
+            k.U[2 * m + 1] = ((A[m] >> 4) & L4) | ilv_bit4(qh, 8 * m + 1);
+        }
+        int s1, m1, s2, m2;
+        kq_pairs(r.m, cc, s1, m1, s2, m2);
+        const float d = h2f(r.m.x & 0xFFFF), dmin = h2f(r.m.x >> 16);
+        k.s0 = k.s1 = d * (float)s1;
+        k.o0 = k.o1 = -(dmin * (float)m1);
         k.x0 = 256 * blk + 32 * cc; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB) {
         // QK:762-800 (ggml) and QK:1778-1812 (low nibble for quadrants 2,3):
         // chunk cc = ql[16cc..), half h = cc/4, quadrant pair q1 = (cc/2)&1, l-half lh = cc&1.
         const int h = cc >> 2, q1 = (cc >> 1) & 1, lh = cc & 1;
-        bytes16(ld16(P.p[0] + bi * 128 + 16 * cc), b);
-        uint8_t qh[16];
-        bytes16(ld16(P.p[1] + bi * 64 + 32 * h + 16 * lh), qh);
-        const int8_t *sc = reinterpret_cast<const int8_t *>(P.p[2] + bi * 16);
-        float d = h2f(*reinterpret_cast<const uint16_t *>(P.p[3] + bi * 2));
+        const uint32_t Q[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            int lo = b[i] & 15;
-            int hi = (SEM == SEM_Q6_K_LOWNIB) ? lo : (b[i] >> 4);
-            k.q[i] = (float)((lo | (((qh[i] >> (2 * q1)) & 3) << 4)) - 32);
-            k.q[16 + i] = (float)((hi | (((qh[i] >> (2 * q1 + 4)) & 3) << 4)) - 32);
+        for (int j = 0; j < 4; j++) {
+            const uint32_t lo = A[j] & L4;
+            const uint32_t hi = (SEM == SEM_Q6_K_LOWNIB) ? lo : ((A[j] >> 4) & L4);
+            k.U[j] = lo | (((Q[j] >> (2 * q1)) & 0x03030303u) << 4);
+            k.U[4 + j] = hi | (((Q[j] >> (2 * q1 + 4)) & 0x03030303u) << 4);
         }
-        k.s0 = d * (float)sc[8 * h + lh + 2 * q1];
-        k.s1 = d * (float)sc[8 * h + lh + 2 * q1 + 4];
+        const float d = h2f(r.d);
+        k.s0 = d * (float)(int8_t)r.m.x;
+        k.s1 = d * (float)(int8_t)r.m.y;
         k.x0 = 256 * blk + 128 * h + 32 * q1 + 16 * lh;
         k.x1 = k.x0 + 64;
     } else if constexpr (SEM == SEM_Q6_K_SEQ) {
         // CE:315-378: element e = nibble (e&1) of ql[e/2] | ((qh[e/4] >> 2(e&3)) & 3) << 4, minus 32; scale sc[e/16].
-        bytes16(ld16(P.p[0] + bi * 128 + 16 * cc), b);
-        uint2 qv = *reinterpret_cast<const uint2 *>(P.p[1] + bi * 64 + 8 * cc);
-        const int8_t *sc = reinterpret_cast<const int8_t *>(P.p[2] + bi * 16);
-        float d = h2f(*reinterpret_cast<const uint16_t *>(P.p[3] + bi * 2));
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            uint32_t qw = (e < 16) ? qv.x : qv.y;
-            int up = (qw >> (2 * (e & 15))) & 3;
-            k.q[e] = (float)((((b[e >> 1] >> ((e & 1) * 4)) & 15) | (up << 4)) - 32);
+        for (int m = 0; m < 4; m++) {
+            const uint32_t qw = (m < 2) ? r.b.x : r.b.y;
+            const int base = 8 * (m & 1);               // element offset within the 16 covered by qw
+            uint32_t ue = 0, uo = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                ue |= ((qw >> (2 * (base + 2 * t))) & 3u) << (8 * t + 4);
+                uo |= ((qw >> (2 * (base + 2 * t + 1))) & 3u) << (8 * t + 4);
+            }
+            k.U[2 * m] = (A[m] & L4) | ue;
+            k.U[2 * m + 1] = ((A[m] >> 4) & L4) | uo;
         }
-        k.s0 = d * (float)sc[2 * cc];
-        k.s1 = d * (float)sc[2 * cc + 1];
+        const float d = h2f(r.d);
+        k.s0 = d * (float)(int8_t)(r.m.x & 0xFF);
+        k.s1 = d * (float)(int8_t)(r.m.x >> 8);
         k.x0 = 256 * blk + 32 * cc; k.x1 = k.x0 + 16;
     }
+}
+
+// Byte t of w as a float: one v_cvt_f32_ubyte{t} (the compiler's own
+// lowering of the shift-and-mask takes a v_bfe_u32 plus a conversion).
+MLLM_DEV float ubyte_f(uint32_t w, int t)
+{
+    float r;
+    switch (t) {
+    case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w)); break;
+    case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w)); break;
+    case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w)); break;
+    default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w)); break;
+    }
+    return r;
 }
 
 // ---------------------------------------------------------------- Q8_0-activation semantics
@@ -202,71 +325,81 @@ template <int SEM> struct q8_traits {
 
 MLLM_DEV int dot4_i8(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
-// Value of chunk c of `row` against token b's Q8_0 activation (xq offset already applied).
 template <int SEM>
-MLLM_DEV float q8_chunk_dot(const mllm_packed &P, int nb, int row, int c, const mllm_xq &xq, long tok_q, long tok_b)
+MLLM_DEV void q8_fetch(const mllm_packed &P, int nb, int row, int c, raw_chunk &r)
 {
     if constexpr (SEM == SEM_Q4_K_Q8) {
-        // dot_q4_k_q8_0 QK:1647-1735: integer term over k < 16 of each sub-block, no Q8 scale;
-        // min term dmin * sum_j d8_j (sum q8[0..8) + sum q8[16..24)).
         const int sb = c >> 2, g = c & 3;
         const long bi = (long)row * nb + sb;
-        uint4 w = ld16(P.p[0] + bi * 128 + 32 * g);
-        uint4 mv = ld16(P.p[1] + bi * 16);
-        uint8_t mb[16];
-        bytes16(mv, mb);
-        float d = h2f(mv.x & 0xFFFF), dmin = h2f(mv.x >> 16);
-        int s1, m1, s2, m2;
-        k4_pair(2 * g, mb + 4, s1, m1);
-        k4_pair(2 * g + 1, mb + 4, s2, m2);
-        const int jlo = 8 * sb + 2 * g, jhi = jlo + 1;
-        uint4 qlo = *reinterpret_cast<const uint4 *>(xq.q + tok_q + 32L * jlo);
-        uint4 qhi = *reinterpret_cast<const uint4 *>(xq.q + tok_q + 32L * jhi);
+        r.a = ld16(P.p[0] + bi * 128 + 32 * g);
+        r.m = ld16c(P.p[1] + bi * 16);
+    } else if constexpr (SEM == SEM_MXFP4_Q8) {
+        const long bi = (long)row * nb + c;
+        r.a = ld16(P.p[0] + bi * 16);
+        r.d = gld<uint8_t>(P.p[1] + bi);
+    } else {
+        const long bi = (long)row * nb + c;
+        r.a = ld16(P.p[0] + bi * 16);
+        r.b.x = gld<uint32_t>(P.p[1] + bi * 4);
+        r.d = gld<uint16_t>(P.p[2] + bi * 2);
+    }
+}
+
+// Value of one chunk against a token's Q8_0 activation: q = its 32 (Q4_K: the
+// two 16-byte halves at the chunk's sub-blocks) int8 quants, d8 its scale(s),
+// s4 the Q4_K min-term sums.
+//   Q4_K_Q8  (dot_q4_k_q8_0 QK:1647-1735): d * sum_j sc_j sum_{k<16} nib q8 - dmin * (s4_lo + s4_hi)
+//   MXFP4_Q8 (mxfp4_row_dot_q8 QK:629-678): clamp(2^(E-127) d8, +-1e20) * sum v q8
+//   Q5_0_Q8  (dot_q5_0_q8_0 QK:1268-1320): d5 * d8 * sum v q8
+template <int SEM>
+MLLM_DEV float q8_dot(const raw_chunk &r, int c, const uint4 &qa, const uint4 &qb, float d8, float s4sum)
+{
+    if constexpr (SEM == SEM_Q4_K_Q8) {
+        const int g = c & 3;
         const uint32_t M = 0x0F0F0F0Fu;
         int dlo = 0, dhi = 0;
-        dlo = dot4_i8(w.x & M, qlo.x, dlo); dlo = dot4_i8(w.y & M, qlo.y, dlo);
-        dlo = dot4_i8(w.z & M, qlo.z, dlo); dlo = dot4_i8(w.w & M, qlo.w, dlo);
-        dhi = dot4_i8((w.x >> 4) & M, qhi.x, dhi); dhi = dot4_i8((w.y >> 4) & M, qhi.y, dhi);
-        dhi = dot4_i8((w.z >> 4) & M, qhi.z, dhi); dhi = dot4_i8((w.w >> 4) & M, qhi.w, dhi);
-        float mins = xq.s4[tok_b + jlo] + xq.s4[tok_b + jhi];
-        return d * (float)(s1 * dlo + s2 * dhi) - dmin * mins;
+        dlo = dot4_i8(r.a.x & M, qa.x, dlo); dlo = dot4_i8(r.a.y & M, qa.y, dlo);
+        dlo = dot4_i8(r.a.z & M, qa.z, dlo); dlo = dot4_i8(r.a.w & M, qa.w, dlo);
+        dhi = dot4_i8((r.a.x >> 4) & M, qb.x, dhi); dhi = dot4_i8((r.a.y >> 4) & M, qb.y, dhi);
+        dhi = dot4_i8((r.a.z >> 4) & M, qb.z, dhi); dhi = dot4_i8((r.a.w >> 4) & M, qb.w, dhi);
+        int s1, m1, s2, m2;
+        kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
+        const float d = h2f(r.m.x & 0xFFFF), dmin = h2f(r.m.x >> 16);
+        return d * (float)(s1 * dlo + s2 * dhi) - dmin * s4sum;
     } else if constexpr (SEM == SEM_MXFP4_Q8) {
-        // mxfp4_row_dot_q8 QK:629-678: cs = clamp(2^(E-127) * d8, +-1e20); cs * sum v*q8.
-        const long bi = (long)row * nb + c;
-        uint4 w = ld16(P.p[0] + bi * 16);
-        float cs = e8m0f(P.p[1][bi]) * xq.d[tok_b + c];
+        float cs = e8m0f(r.d) * d8;
         cs = fminf(fmaxf(cs, -1e20f), 1e20f);
-        const int8_t *q = xq.q + tok_q + 32L * c;
-        uint4 qa = *reinterpret_cast<const uint4 *>(q), qb = *reinterpret_cast<const uint4 *>(q + 16);
-        uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-        uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint32_t wv[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         int acc = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            // bytes 4i..4i+3 hold elements 8i..8i+7 (low nibble even, high nibble odd).
-            // Nibble n scaled by 16 is a valid int8 (16*sext4(n)) when placed in the high half of a byte.
-            uint32_t lo16 = (wv[i] << 4) & 0xF0F0F0F0u;   // 16 * even elements
-            uint32_t hi16 = wv[i] & 0xF0F0F0F0u;          // 16 * odd elements
-            uint32_t qe = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x06040200u); // even q8 bytes
-            uint32_t qo = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x07050301u); // odd q8 bytes
+            // bytes 4i..4i+3 hold elements 8i..8i+7 (low nibble even, high nibble odd); a nibble
+            // placed in the high half of a byte is the int8 16*sext4(n).
+            const uint32_t lo16 = (wv[i] << 4) & 0xF0F0F0F0u;
+            const uint32_t hi16 = wv[i] & 0xF0F0F0F0u;
+            const uint32_t qe = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x06040200u);  // even q8 bytes
+            const uint32_t qo = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x07050301u);  // odd q8 bytes
             acc = dot4_i8(lo16, qe, acc);
             acc = dot4_i8(hi16, qo, acc);
         }
         return cs * (float)(acc >> 4);
     } else {
-        // dot_q5_0_q8_0 QK:1268-1320: d5 * d8 * sum v * q8
-        const long bi = (long)row * nb + c;
-        uint8_t b[16];
-        bytes16(ld16(P.p[0] + bi * 16), b);
-        uint32_t qh = *reinterpret_cast<const uint32_t *>(P.p[1] + bi * 4);
-        float d5 = h2f(*reinterpret_cast<const uint16_t *>(P.p[2] + bi * 2));
-        const int8_t *q = xq.q + tok_q + 32L * c;
+        const uint32_t qh = r.b.x;
+        const uint32_t wv[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         int acc = 0;
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            int v = (((b[e >> 1] >> ((e & 1) * 4)) & 15) | (((qh >> e) & 1) << 4)) - 16;
-            acc += v * (int)q[e];
+        for (int i = 0; i < 4; i++) {
+            // elements 8i..8i+7: v = (nibble | qh bit << 4) - 16; as bytes u = v + 16 in [0,31]
+            const uint32_t ue = (wv[i] & 0x0F0F0F0Fu) | ilv_bit4(qh, 8 * i);
+            const uint32_t uo = ((wv[i] >> 4) & 0x0F0F0F0Fu) | ilv_bit4(qh, 8 * i + 1);
+            const uint32_t qe = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x06040200u);
+            const uint32_t qo = __builtin_amdgcn_perm(qv[2 * i + 1], qv[2 * i], 0x07050301u);
+            acc = dot4_i8(ue, qe, acc);
+            acc = dot4_i8(uo, qo, acc);
+            acc -= 16 * (dot4_i8(0x01010101u, qe, 0) + dot4_i8(0x01010101u, qo, 0));
         }
-        return d5 * xq.d[tok_b + c] * (float)acc;
+        return h2f(r.d) * d8 * (float)acc;
     }
 }

@@ -19,6 +19,7 @@ struct mllm_gemv_args {
     long out_job_stride;
     int ldo;
     int n_rows, n_cols, B;
+    int k_tile;   // activation elements staged in LDS per pass (set by the launcher)
     mllm_xq xq;   // Q8_0 activation pack (Q8 semantics only); job/token strides follow x's
 };
 

@@ -8,25 +8,36 @@ namespace {
 
 // ------------------------------------------------------------------ repack
 // Source byte offsets of each plane inside a raw GGUF block.
-struct pack_src { int n; int off[5]; int len[5]; int plane[5]; int dst[5]; };
+struct pack_src { int n; int off[4]; int len[4]; int plane[4]; };
 
 __host__ __device__ pack_src pack_plan(int ly)
 {
     switch (ly) {
-    case LY_Q4_0: return {2, {2, 0}, {16, 2}, {0, 1}, {0, 0}};
-    case LY_Q4_1: return {2, {4, 0}, {16, 4}, {0, 1}, {0, 0}};
-    case LY_Q5_0: return {3, {6, 2, 0}, {16, 4, 2}, {0, 1, 2}, {0, 0, 0}};
-    case LY_Q8_0: return {2, {2, 0}, {32, 2}, {0, 1}, {0, 0}};
-    case LY_Q4_K: return {2, {16, 0}, {128, 16}, {0, 1}, {0, 0}};
+    case LY_Q4_0: return {2, {2, 0}, {16, 2}, {0, 1}};
+    case LY_Q4_1: return {2, {4, 0}, {16, 4}, {0, 1}};
+    case LY_Q5_0: return {3, {6, 2, 0}, {16, 4, 2}, {0, 1, 2}};
+    case LY_Q8_0: return {2, {2, 0}, {32, 2}, {0, 1}};
+    // K-quant meta planes get d, dmin here; the scale pairs are re-laid below.
+    case LY_Q4_K: return {2, {16, 0}, {128, 4}, {0, 1}};
     // block_q5_K (ggml, QK:211-246): d dmin scales[12] qh[32] qs[128]
-    case LY_Q5_K_GGML: return {3, {48, 16, 0}, {128, 32, 16}, {0, 1, 2}, {0, 0, 0}};
+    case LY_Q5_K_GGML: return {3, {48, 16, 0}, {128, 32, 4}, {0, 1, 2}};
     // the engine's block_q5_K (CE:46-52): d dmin qh[32] ql[128] scales[12]
-    case LY_Q5_K_CE: return {4, {36, 4, 0, 164}, {128, 32, 4, 12}, {0, 1, 2, 2}, {0, 0, 0, 4}};
+    case LY_Q5_K_CE: return {3, {36, 4, 0}, {128, 32, 4}, {0, 1, 2}};
     // block_q6_K (CE:34-39): ql[128] qh[64] scales[16] d
-    case LY_Q6_K: return {4, {0, 128, 192, 208}, {128, 64, 16, 2}, {0, 1, 2, 3}, {0, 0, 0, 0}};
-    case LY_MXFP4: return {2, {0, 16}, {16, 1}, {0, 1}, {0, 0}};
+    case LY_Q6_K: return {4, {0, 128, 192, 208}, {128, 64, 16, 2}, {0, 1, 2, 3}};
+    case LY_MXFP4: return {2, {0, 16}, {16, 1}, {0, 1}};
     }
-    return {0, {0}, {0}, {0}, {0}};
+    return {0, {0}, {0}, {0}};
+}
+
+// 6-bit (scale, min) pair j of a K-quant scale array (get_scale_min_k4 QK:62-71).
+__device__ void k4_pair(int j, const uint8_t *q, uint32_t &sc, uint32_t &m)
+{
+    if (j < 4) { sc = q[j] & 63; m = q[j + 4] & 63; }
+    else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m  = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
 }
 
 __global__ void k_pack(int ly, const uint8_t *__restrict__ raw, uint8_t *__restrict__ packed, long nblk,
@@ -40,8 +51,23 @@ __global__ void k_pack(int ly, const uint8_t *__restrict__ raw, uint8_t *__restr
     const uint8_t *src = raw + i * L.block_bytes;
     for (int s = 0; s < ps.n; s++) {
         const int p = ps.plane[s];
-        uint8_t *dst = packed + offs[p] + i * L.plane_bytes[p] + ps.dst[s];
+        uint8_t *dst = packed + offs[p] + i * L.plane_bytes[p];
         for (int j = 0; j < ps.len[s]; j++) dst[j] = src[ps.off[s] + j];
+    }
+    if (ly == LY_Q4_K || ly == LY_Q5_K_GGML || ly == LY_Q5_K_CE) {
+        // meta = [d | dmin] [sc_0..7 as 6-bit fields, 48 bits] [m_0..7, 48 bits]
+        const uint8_t *sc = src + (ly == LY_Q5_K_CE ? 164 : 4);
+        uint64_t S = 0, M = 0;
+        for (int j = 0; j < 8; j++) {
+            uint32_t a, b;
+            k4_pair(j, sc, a, b);
+            S |= (uint64_t)a << (6 * j);
+            M |= (uint64_t)b << (6 * j);
+        }
+        uint32_t *meta = reinterpret_cast<uint32_t *>(packed + offs[ly == LY_Q4_K ? 1 : 2] + i * 16);
+        meta[1] = (uint32_t)S;
+        meta[2] = (uint32_t)(S >> 32) | ((uint32_t)M << 16);
+        meta[3] = (uint32_t)(M >> 16);
     }
 }
 

@@ -50,6 +50,13 @@ def load_kernels(path=LIB_PATH):
         return _LIB
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} is not built: run mojollama_amd.kernels.build() (needs hipcc)")
+    # PyTorch-ROCm ships its own libamdhip64.so.7 and links it by another name.
+    # Loading torch first makes this library bind to that same runtime, so one
+    # HIP runtime serves both (and torch streams are valid handles here).
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     so = ctypes.CDLL(path)
     # --- as bound by TE:251-261, 363-377, 389-392
     so.quant_matmul_omp.argtypes = [cu, cf, cf, ci, ci, ci]

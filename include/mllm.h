@@ -123,6 +123,31 @@ MLLM_API int mllm_route(const float *router_t_dev, const float *x_dev, int T, in
 /* fp32 weights of a packed matrix (fp32-weight semantics only). */
 MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_cols, float *out_dev, void *stream);
 
+/* ------------------------------------------------------- MoE layer, T tokens */
+
+/* A prepared MoE layer: per-expert packed weights (device pointers, arrays of E
+ * entries on the host) with the reference's GGUF codes, and the router
+ * transposed to [N][E] (device).  Per token the layer computes what
+ * moe_forward_omp (QK:2066-2250) computes when fed the C routing of moe_ffn
+ * (CE:606-638), renormalised when `renorm` (GO:88-92): gate/up per type,
+ * SiLU with the gate clamped to +-80, down per type, k-order combine.
+ * T > 8 tokens run the batched path (GPU bucketing by expert, grouped MFMA
+ * GEMMs); T <= 8 the decode GEMVs. */
+typedef struct mllm_moe_layer mllm_moe_layer;
+MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
+                                          const void *const *gate_packed, const void *const *up_packed,
+                                          const void *const *down_packed, const float *router_t_dev, int renorm);
+MLLM_API void mllm_moe_release(mllm_moe_layer *layer);
+MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *layer, int T);
+/* out[T][N]; idx_out/w_out (optional, device [T][K]) receive the routing. */
+MLLM_API int mllm_moe_forward(const mllm_moe_layer *layer, const float *x, int T, float *out, void *workspace,
+                              long ws_bytes, int *idx_out, float *w_out, void *stream);
+/* The stable expert bucketing on its own: entries idx[TK] over E experts ->
+ * off[E+1], perm[pos] = entry, pos_of[entry] = pos (-1 for idx < 0), and
+ * tiles = 3 arrays of (TK/64 + E + 1) ints (expert, begin, end) + count. */
+MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm, int *pos_of, int *tiles,
+                             void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,7 @@
 #include <string>
 #include <tuple>
 #include <vector>
+#include "gemm.h"
 #include "gemv.h"
 #include "mllm.h"
 
@@ -288,6 +289,18 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
     if (q8) {
         xb = xq_carve(scratch, B, n_cols);
         HIP_OK(mllm_launch_quantize_q8_0(x, B, n_cols, nullptr, xb.q, xb.d, xb.s4, xb.sq, st));
+    }
+    if (B > 8 && mllm_qgemm_supported(sem)) {
+        // prefill / batched: quantised-weight MFMA GEMM over the B tokens
+        qgemm_args g{};
+        g.W = W;
+        g.x = x; g.ldx = n_cols;
+        if (q8) g.xq = {xb.q, xb.d, xb.s4, xb.sq};
+        g.out = out; g.ldo = n_rows;
+        g.n_rows = n_rows; g.n_cols = n_cols; g.n_entries = B;
+        const int xm = sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_F32;
+        HIP_OK(mllm_launch_qgemm(sem, xm, false, g, 0, st));
+        return 0;
     }
     for (int b0 = 0; b0 < B; b0 += 8) {
         mllm_gemv_args a{};

@@ -1,0 +1,582 @@
+// gemv_impl.h — decode GEMV kernels for batch 1..8 on gfx950 (instantiated per
+// semantic in gemv_*.hip so the library compiles in parallel).
+//
+// out[b][row] = sum_k w[row][k] * x[b][k] for one weight matrix, or for a list
+// of "jobs" (expert matrices picked through a device-side index array, as the
+// MoE layer needs).  The path is HBM-bound, so the kernel is built around the
+// weight stream:
+//   * a workgroup (4 wave64s) first copies its activations into LDS (padded by
+//     16 bytes every 256 so the lanes' 16-float reads fall in distinct banks),
+//     tiling K when B*K does not fit in 48 KB;
+//   * a wave owns R rows per group of LPR lanes; the lanes of a group walk the
+//     row's 32-weight chunks, so one wave-wide load reads consecutive 16-byte
+//     pieces of a row; a lane issues the loads of all R rows before decoding;
+//   * chunks decode to byte codes converted with v_cvt_f32_ubyte and are
+//     accumulated in fp32 (per-run scale and offset applied once per run);
+//   * lane groups reduce with DPP row operations and two cross-row swaps.
+#pragma once
+#include <algorithm>
+#include "decode.h"
+#include "gemv.h"
+
+namespace mllm_gemv {
+
+constexpr int kLdsFloats = 12288;   // 48 KB of activations per workgroup
+
+template <int W>
+MLLM_DEV float group_sum(float v)
+{
+    // Sum over aligned groups of W lanes; every lane of the group ends with the total.
+    if constexpr (W >= 2)  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); // quad_perm 1,0,3,2
+    if constexpr (W >= 4)  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)); // quad_perm 2,3,0,1
+    if constexpr (W >= 8)  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+    if constexpr (W >= 16) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
+    if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+MLLM_DEV void resolve_job(const mllm_gemv_args &a, int job, mllm_packed &W)
+{
+    if (a.table) {
+        int e = a.idx ? a.idx[job] : job;
+        W = a.table[e < 0 ? 0 : e];
+    } else {
+        W = a.W;
+    }
+}
+
+// padded LDS index of tile-relative element i
+MLLM_DEV int xpad(int i) { return i + ((i >> 6) << 2); }
+
+// Copy x[b][k0 .. k0+kn) for b < B into LDS (stride xs floats per token).
+MLLM_DEV void stage_x(float *lds, int xs, const float *__restrict__ x, int ldx, int B, int k0, int kn)
+{
+    const int tid = threadIdx.x;
+    if ((ldx & 3) == 0) {
+        const int n4 = kn >> 2;
+        for (int i = tid; i < B * n4; i += blockDim.x) {
+            const int b = i / n4, e = (i - b * n4) << 2;
+            const float4 v = gld<float4>(x + (long)b * ldx + k0 + e);
+            *reinterpret_cast<float4 *>(lds + b * xs + xpad(e)) = v;
+        }
+    } else {
+        for (int i = tid; i < B * kn; i += blockDim.x) {
+            const int b = i / kn, e = i - b * kn;
+            lds[b * xs + xpad(e)] = gld<float>(x + (long)b * ldx + k0 + e);
+        }
+    }
+}
+
+MLLM_DEV void lds_run16(const float *p, float v[16])
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 f = reinterpret_cast<const float4 *>(p)[q];
+        v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+    }
+}
+
+MLLM_DEV float sum16(const float v[16])
+{
+    float a = (v[0] + v[1]) + (v[2] + v[3]), b = (v[4] + v[5]) + (v[6] + v[7]);
+    float c = (v[8] + v[9]) + (v[10] + v[11]), d = (v[12] + v[13]) + (v[14] + v[15]);
+    return (a + b) + (c + d);
+}
+
+// sum over one run of u_i * x_i; U points at the run's four code words
+template <int SEM>
+MLLM_DEV float run_dot(const uint32_t *U, const float xv[16])
+{
+    float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float u = ubyte_f(U[j], t);
+            if (t & 1) p1 = fmaf(u, xv[code_pos<SEM>(j, t)], p1);
+            else p0 = fmaf(u, xv[code_pos<SEM>(j, t)], p0);
+        }
+    return p0 + p1;
+}
+
+// Contribution of one decoded chunk to one token.
+template <int SEM>
+MLLM_DEV float chunk_value(const chunk_codes &k, const float x0[16], const float x1[16], float sx0, float sx1)
+{
+    constexpr float bias = (float)sem_traits<SEM>::kBias;
+    constexpr bool need_sum = sem_traits<SEM>::kBias != 0 || sem_traits<SEM>::kOffset;
+    float t = fmaf(k.s0, run_dot<SEM>(k.U, x0), k.s1 * run_dot<SEM>(k.U + 4, x1));
+    if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), sx0, fmaf(fmaf(-k.s1, bias, k.o1), sx1, t));
+    if (!isfinite(t)) {
+        // inf/NaN somewhere (scale or activation): weigh each element as the reference
+        // does (w = s*q first), so that a zero code times an infinite scale gives NaN.
+        t = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float w0 = fmaf(k.s0, ubyte_f(k.U[j], q) - bias, k.o0);
+                const float w1 = fmaf(k.s1, ubyte_f(k.U[4 + j], q) - bias, k.o1);
+                t = fmaf(w0, x0[code_pos<SEM>(j, q)], t);
+                t = fmaf(w1, x1[code_pos<SEM>(j, q)], t);
+            }
+    }
+    return t;
+}
+
+// Add chunk c of R rows (already fetched into raw) to acc, activations from
+// LDS (tile starting at element k0, token stride xs floats).
+template <int SEM, int BM, int R>
+MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const float *xl, int xs, int k0, int B, float (&acc)[R][BM])
+{
+    constexpr bool need_sum = sem_traits<SEM>::kBias != 0 || sem_traits<SEM>::kOffset;
+    chunk_codes k;
+    if constexpr (BM == 1) {
+        // activations once per chunk, reused by the R rows
+        codes<SEM>(raw[0], c, k);
+        float xv0[16], xv1[16];
+        lds_run16(xl + xpad(k.x0 - k0), xv0);
+        lds_run16(xl + xpad(k.x1 - k0), xv1);
+        const float sx0 = need_sum ? sum16(xv0) : 0.f, sx1 = need_sum ? sum16(xv1) : 0.f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (r) codes<SEM>(raw[r], c, k);
+            acc[r][0] += chunk_value<SEM>(k, xv0, xv1, sx0, sx1);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            codes<SEM>(raw[r], c, k);
+#pragma unroll
+            for (int b = 0; b < BM; b++) {
+                if (b < B) {
+                    float xv0[16], xv1[16];
+                    lds_run16(xl + b * xs + xpad(k.x0 - k0), xv0);
+                    lds_run16(xl + b * xs + xpad(k.x1 - k0), xv1);
+                    const float sx0 = need_sum ? sum16(xv0) : 0.f, sx1 = need_sum ? sum16(xv1) : 0.f;
+                    acc[r][b] += chunk_value<SEM>(k, xv0, xv1, sx0, sx1);
+                }
+            }
+        }
+    }
+}
+
+// fp32-activation semantics, K tiled through LDS (used when B*K does not fit)
+template <int SEM, int BM, int R, int LPR>
+__global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
+{
+    extern __shared__ float xl[];
+    constexpr int BE = sem_traits<SEM>::kBlockElems, CPB = sem_traits<SEM>::kChunksPerBlock;
+    const int job = blockIdx.y;
+    mllm_packed W;
+    resolve_job(a, job, W);
+    const float *__restrict__ x = a.x + job * a.x_job_stride;
+    float *__restrict__ out = a.out + job * a.out_job_stride;
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane / LPR, sl = lane % LPR;
+    const int row0 = ((blockIdx.x * 4 + wave) * (64 / LPR) + grp) * R;
+    const int nb = a.n_cols / BE;
+    const int kused = nb * BE;
+    const int B = a.B;
+    const int KT = a.k_tile, xs = KT + (KT >> 4);
+
+    float acc[R][BM];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
+
+    for (int k0 = 0; k0 < kused; k0 += KT) {
+        const int kn = min(KT, kused - k0);
+        if (k0) __syncthreads();
+        stage_x(xl, xs, x, a.ldx, B, k0, kn);
+        __syncthreads();
+        const int c_end = (k0 + kn) / BE * CPB;
+        for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
+            raw_chunk raw[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) fetch<SEM>(W, nb, min(row0 + r, a.n_rows - 1), c, raw[r]);
+            accumulate<SEM, BM, R>(raw, c, xl, xs, k0, B, acc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int b = 0; b < BM; b++) {
+            const float v = group_sum<LPR>(acc[r][b]);
+            const int row = row0 + r;
+            if (sl == 0 && row < a.n_rows && b < B) out[(long)b * a.ldo + row] = v;
+        }
+    }
+}
+
+// Add chunk c of R rows to acc against the Q8_0 activation staged in LDS
+// (per token: quant bytes padded 16 B per 256, then KT/32 scales, KT/32 min sums).
+template <int SEM, int BM, int R>
+MLLM_DEV void accumulate_q8(const raw_chunk (&raw)[R], int c, const float *xl, int tstride, int qstride, int KT,
+                            int k0, int B, float (&acc)[R][BM])
+{
+    const uint8_t *lq = reinterpret_cast<const uint8_t *>(xl);
+    // tile-relative 32-block indices of the chunk's two 16-byte activation pieces
+    int ja, jb, qoa, qob;
+    if constexpr (SEM == SEM_Q4_K_Q8) {
+        ja = 8 * (c >> 2) + 2 * (c & 3) - k0 / 32; jb = ja + 1;
+        qoa = 32 * ja; qob = 32 * jb;
+    } else {
+        ja = jb = c - k0 / 32;
+        qoa = 32 * ja; qob = qoa + 16;
+    }
+#pragma unroll
+    for (int b = 0; b < BM; b++) {
+        if (b < B) {
+            const uint8_t *tq = lq + b * tstride * 4;
+            const float *tf = xl + b * tstride + qstride / 4;
+            const uint4 qa = *reinterpret_cast<const uint4 *>(tq + qoa + ((qoa >> 8) << 4));
+            const uint4 qb = *reinterpret_cast<const uint4 *>(tq + qob + ((qob >> 8) << 4));
+            const float d8 = tf[ja];
+            const float s4 = tf[KT / 32 + ja] + tf[KT / 32 + jb];
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r][b] += q8_dot<SEM>(raw[r], c, qa, qb, d8, s4);
+        }
+    }
+}
+
+// Copy the Q8_0 activation pack of tokens b < B, elements [k0, k0+kn), into LDS.
+MLLM_DEV void stage_q8(float *xl, const mllm_xq &xq, long q_job, long b_job, int ldx, int B, int KT, int tstride,
+                       int qstride, int k0, int kn)
+{
+    uint8_t *lq = reinterpret_cast<uint8_t *>(xl);
+    const int n16 = kn >> 4, nbk = kn >> 5;
+    for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
+        const int b = i / n16, e = (i - b * n16) << 4;
+        const uint4 v = gld<uint4>(xq.q + q_job + (long)b * (ldx / 32) * 32 + k0 + e);
+        *reinterpret_cast<uint4 *>(lq + b * tstride * 4 + e + ((e >> 8) << 4)) = v;
+    }
+    for (int i = threadIdx.x; i < B * nbk; i += blockDim.x) {
+        const int b = i / nbk, j = i - b * nbk;
+        const long src = b_job + (long)b * (ldx / 32) + k0 / 32 + j;
+        float *tb = xl + b * tstride + qstride / 4;
+        tb[j] = gld<float>(xq.d + src);
+        tb[KT / 32 + j] = gld<float>(xq.s4 + src);
+    }
+}
+
+// Q8_0-activation semantics: the quantised activation (int8 quants, decoded
+// scales, Q4_K min-term sums) is staged in LDS the same way.
+template <int SEM, int BM, int R, int LPR>
+__global__ __launch_bounds__(256) void k_gemv_q8(mllm_gemv_args a)
+{
+    extern __shared__ float xl[];
+    constexpr int BE = q8_traits<SEM>::kBlockElems, CPB = q8_traits<SEM>::kChunksPerBlock;
+    const int job = blockIdx.y;
+    mllm_packed W;
+    resolve_job(a, job, W);
+    float *__restrict__ out = a.out + job * a.out_job_stride;
+    const long q_job = job * a.x_job_stride;          // elements
+    const long b_job = job * (a.x_job_stride / 32);   // 32-blocks
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane / LPR, sl = lane % LPR;
+    const int row0 = ((blockIdx.x * 4 + wave) * (64 / LPR) + grp) * R;
+    const int nb = a.n_cols / BE;
+    const int kused = nb * BE;
+    const int B = a.B;
+    const int KT = a.k_tile;
+    // LDS per token: KT quant bytes (+16 B per 256), then KT/32 scales and KT/32 min sums
+    const int qstride = KT + (KT >> 4);
+    const int tstride = qstride / 4 + 2 * (KT / 32);   // in floats
+
+    float acc[R][BM];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
+
+    for (int k0 = 0; k0 < kused; k0 += KT) {
+        const int kn = min(KT, kused - k0);
+        if (k0) __syncthreads();
+        stage_q8(xl, a.xq, q_job, b_job, a.ldx, B, KT, tstride, qstride, k0, kn);
+        __syncthreads();
+        const int c_end = (k0 + kn) / BE * CPB;
+        for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
+            raw_chunk raw[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) q8_fetch<SEM>(W, nb, min(row0 + r, a.n_rows - 1), c, raw[r]);
+            accumulate_q8<SEM, BM, R>(raw, c, xl, tstride, qstride, KT, k0, B, acc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int b = 0; b < BM; b++) {
+            const float v = group_sum<LPR>(acc[r][b]);
+            const int row = row0 + r;
+            if (sl == 0 && row < a.n_rows && b < B) out[(long)b * a.ldo + row] = v;
+        }
+    }
+}
+
+// Persistent variant used whenever all of x fits in LDS: a workgroup stages
+// x once, then its waves walk row groups (stride = all waves of the grid),
+// prefetching the next step's weight chunks while the current step computes,
+// so every lane keeps two rounds of 16-byte loads in flight.  A step is one
+// pass of the lane group over LPR chunks of its R rows; the last step of a
+// row group reduces and writes it.  Q8 selects the Q8_0-activation form.
+template <int SEM, bool Q8> struct gemv_geom {
+    static constexpr int BE = Q8 ? q8_traits<SEM>::kBlockElems : sem_traits<SEM>::kBlockElems;
+    static constexpr int CPB = Q8 ? q8_traits<SEM>::kChunksPerBlock : sem_traits<SEM>::kChunksPerBlock;
+};
+
+template <int SEM, bool Q8, int BM, int R, int LPR>
+__global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
+{
+    extern __shared__ float xl[];
+    constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
+    constexpr int RPW = (64 / LPR) * R;                 // rows per wave and step
+    const int job = blockIdx.y;
+    mllm_packed W;
+    resolve_job(a, job, W);
+    float *__restrict__ out = a.out + job * a.out_job_stride;
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane / LPR, sl = lane % LPR;
+    const int nb = a.n_cols / BE, kused = nb * BE, nch = nb * CPB;
+    const int iters = (nch + LPR - 1) / LPR;
+    const int nrg = (a.n_rows + RPW - 1) / RPW;
+    const int wstride = gridDim.x * 4;
+    const int rg0 = blockIdx.x * 4 + wave;
+    const int B = a.B;
+    // LDS geometry (whole K staged): fp32 x, or the Q8_0 pack
+    const int KT = (kused + 255) / 256 * 256;
+    const int xs = KT + (KT >> 4);
+    const int qstride = KT + (KT >> 4), tstride = qstride / 4 + 2 * (KT / 32);
+
+    // A step is (row group rg, chunk pass it); the next step advances it, then rg.
+    auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) {
+        const int c = min(it * LPR + sl, nch - 1);
+        const int r0 = rg * RPW + grp * R;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if constexpr (Q8) q8_fetch<SEM>(W, nb, min(r0 + r, a.n_rows - 1), c, buf[r]);
+            else fetch<SEM>(W, nb, min(r0 + r, a.n_rows - 1), c, buf[r]);
+        }
+    };
+    float acc[R][BM];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
+    auto run_step = [&](int rg, int it, const raw_chunk (&buf)[R]) {
+        // a lane past the row's last chunk recomputes the last one and discards it
+        const int c = min(it * LPR + sl, nch - 1);
+        const bool live = it * LPR + sl < nch;
+        float part[R][BM];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int b = 0; b < BM; b++) part[r][b] = 0.0f;
+        if constexpr (Q8) accumulate_q8<SEM, BM, R>(buf, c, xl, tstride, qstride, KT, 0, B, part);
+        else accumulate<SEM, BM, R>(buf, c, xl, xs, 0, B, part);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int b = 0; b < BM; b++) acc[r][b] += live ? part[r][b] : 0.0f;
+        if (it == iters - 1) {
+            const int r0 = rg * RPW + grp * R;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int b = 0; b < BM; b++) {
+                    const float v = group_sum<LPR>(acc[r][b]);
+                    acc[r][b] = 0.0f;
+                    if (sl == 0 && r0 + r < a.n_rows && b < B) out[(long)b * a.ldo + r0 + r] = v;
+                }
+            }
+        }
+    };
+    auto advance = [&](int &rg, int &it) {
+        if (++it == iters) { it = 0; rg += wstride; }
+    };
+
+    // Every prefetch is issued unconditionally (clamped to the last row group):
+    // with the same loads outstanding on every path, the compiler waits only
+    // for the older buffer instead of draining all loads.
+    raw_chunk bufA[R], bufB[R];
+    int rg = rg0, it = 0;
+    fetch_step(min(rg, nrg - 1), it, bufA);
+    if constexpr (Q8) {
+        stage_q8(xl, a.xq, job * a.x_job_stride, job * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride, 0,
+                 kused);
+    } else {
+        stage_x(xl, xs, a.x + job * a.x_job_stride, a.ldx, B, 0, kused);
+    }
+    __syncthreads();
+    if (rg >= nrg) return;
+    for (;;) {
+        int rg1 = rg, it1 = it;
+        advance(rg1, it1);
+        fetch_step(min(rg1, nrg - 1), it1, bufB);
+        run_step(rg, it, bufA);
+        if (rg1 >= nrg) break;
+        int rg2 = rg1, it2 = it1;
+        advance(rg2, it2);
+        fetch_step(min(rg2, nrg - 1), it2, bufA);
+        run_step(rg1, it1, bufB);
+        if (rg2 >= nrg) break;
+        rg = rg2; it = it2;
+    }
+}
+
+// f32_matmul_omp (QK:884-913): plain fp32 rows, any n_cols.
+template <int BM>
+__global__ __launch_bounds__(256) void k_gemv_f32(mllm_gemv_args a)
+{
+    const int job = blockIdx.y;
+    const float *Wf = reinterpret_cast<const float *>(a.table ? a.table[a.idx ? a.idx[job] : job].p[0] : a.W.p[0]);
+    const float *x = a.x + job * a.x_job_stride;
+    float *out = a.out + job * a.out_job_stride;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= a.n_rows) return;
+    const float *w = Wf + (long)row * a.n_cols;
+    float acc[BM];
+#pragma unroll
+    for (int b = 0; b < BM; b++) acc[b] = 0.f;
+    for (int i = lane; i < a.n_cols; i += 64) {
+        float wv = w[i];
+#pragma unroll
+        for (int b = 0; b < BM; b++)
+            if (b < a.B) acc[b] = fmaf(wv, x[(long)b * a.ldx + i], acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < BM; b++) {
+        float v = group_sum<64>(acc[b]);
+        if (lane == 0 && b < a.B) out[(long)b * a.ldo + row] = v;
+    }
+}
+
+// Dequantise rows to fp32 the way the reference's *_dequantize_row functions
+// round: w = fl(s*q) + o, two roundings (QK:762-878).
+template <int SEM>
+__global__ __launch_bounds__(256) void k_dequant(mllm_packed W, int n_rows, int n_cols, float *__restrict__ out)
+{
+    constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
+    constexpr int bias = sem_traits<SEM>::kBias;
+    const int nb = n_cols / sem_traits<SEM>::kBlockElems, nch = nb * CPB;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n_rows * nch) return;
+    const int row = (int)(i / nch), c = (int)(i % nch);
+    raw_chunk raw;
+    fetch<SEM>(W, nb, row, c, raw);
+    chunk_codes k;
+    codes<SEM>(raw, c, k);
+    float *o = out + (long)row * n_cols;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float q0 = (float)((int)((k.U[j] >> (8 * t)) & 0xFF) - bias);
+            const float q1 = (float)((int)((k.U[4 + j] >> (8 * t)) & 0xFF) - bias);
+            o[k.x0 + code_pos<SEM>(j, t)] = __fadd_rn(__fmul_rn(k.s0, q0), k.o0);
+            o[k.x1 + code_pos<SEM>(j, t)] = __fadd_rn(__fmul_rn(k.s1, q1), k.o1);
+        }
+}
+
+template <int SEM>
+hipError_t launch_dequant(const mllm_packed &W, int n_rows, int n_cols, float *out, hipStream_t st)
+{
+    const long n = (long)n_rows * (n_cols / sem_traits<SEM>::kBlockElems) * sem_traits<SEM>::kChunksPerBlock;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_dequant<SEM>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, W, n_rows, n_cols, out);
+    return hipGetLastError();
+}
+
+inline int device_cus()
+{
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+constexpr size_t kPersistentLds = 72 * 1024;
+
+template <int SEM, int BM>
+void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
+{
+    constexpr bool Q8 = mllm_sem_uses_q8(SEM);
+    constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
+    const int kused = a.n_cols / BE * BE;
+    const int nch = kused / BE * CPB;
+    constexpr int R = (BM <= 2) ? 4 : 2;
+    // lanes per row: enough chunks per lane to keep every lane busy on short rows
+    auto waste = [&](int lpr) { int it = (nch + lpr - 1) / lpr; return (double)(it * lpr - nch) / (it * lpr); };
+    int lpr = 64;
+    if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;
+    if (nch < 32 || (lpr == 32 && waste(32) > waste(16) + 0.05)) lpr = 16;
+    const int rows_per_wg = 4 * (64 / lpr) * R;
+    const int wg_needed = (a.n_rows + rows_per_wg - 1) / rows_per_wg;
+
+    // whole-K staging for the persistent kernel
+    const int ktp = (kused + 255) / 256 * 256;
+    const size_t lds_p = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * (ktp + ktp / 16) * 4;
+    if (lds_p <= kPersistentLds) {
+        const int per_cu = lds_p <= 40 * 1024 ? 3 : 2;
+        const int wgs = std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs)));
+        dim3 grid(wgs, n_jobs);
+        if (lpr == 64) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64>), grid, dim3(256), lds_p, st, a);
+        else if (lpr == 32) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 32>), grid, dim3(256), lds_p, st, a);
+        else hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 16>), grid, dim3(256), lds_p, st, a);
+        return;
+    }
+    // K tiled through 48 KB of LDS
+    int kt = Q8 ? (kLdsFloats * 4 * 4 / (BM * 5 * 4 + BM)) / 256 * 256 : (kLdsFloats / BM) / 256 * 256;
+    if (kt > kused) kt = (kused + 255) / 256 * 256;
+    if (kt < 256) kt = 256;
+    a.k_tile = kt;
+    const size_t lds = Q8 ? (size_t)BM * (kt + kt / 16 + 8 * (kt / 32)) : (size_t)BM * (kt + kt / 16) * 4;
+    dim3 grid(wg_needed, n_jobs);
+    if constexpr (Q8) {
+        if (lpr == 64) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 64>), grid, dim3(256), lds, st, a);
+        else if (lpr == 32) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 32>), grid, dim3(256), lds, st, a);
+        else hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 16>), grid, dim3(256), lds, st, a);
+    } else {
+        if (lpr == 64) hipLaunchKernelGGL((k_gemv<SEM, BM, R, 64>), grid, dim3(256), lds, st, a);
+        else if (lpr == 32) hipLaunchKernelGGL((k_gemv<SEM, BM, R, 32>), grid, dim3(256), lds, st, a);
+        else hipLaunchKernelGGL((k_gemv<SEM, BM, R, 16>), grid, dim3(256), lds, st, a);
+    }
+}
+
+// Launch the GEMV of one semantic for B = a.B (1..8).
+template <int SEM>
+void launch_sem_any_b(const mllm_gemv_args &a, int n_jobs, hipStream_t st)
+{
+    if (a.B == 1) launch_sem<SEM, 1>(a, n_jobs, st);
+    else if (a.B == 2) launch_sem<SEM, 2>(a, n_jobs, st);
+    else if (a.B <= 4) launch_sem<SEM, 4>(a, n_jobs, st);
+    else launch_sem<SEM, 8>(a, n_jobs, st);
+}
+
+// Per-semantic entry points, defined in gemv_*.hip.
+template <int SEM> void gemv_sem(const mllm_gemv_args &a, int n_jobs, hipStream_t st);
+template <int SEM> hipError_t dequant_sem(const mllm_packed &W, int n_rows, int n_cols, float *out, hipStream_t st);
+
+#define MLLM_GEMV_INSTANTIATE(SEM)                                                                   \
+    template <> void gemv_sem<SEM>(const mllm_gemv_args &a, int n_jobs, hipStream_t st)              \
+    {                                                                                                \
+        launch_sem_any_b<SEM>(a, n_jobs, st);                                                        \
+    }
+#define MLLM_DEQUANT_INSTANTIATE(SEM)                                                                \
+    template <> hipError_t dequant_sem<SEM>(const mllm_packed &W, int n_rows, int n_cols, float *out, \
+                                            hipStream_t st)                                          \
+    {                                                                                                \
+        return launch_dequant<SEM>(W, n_rows, n_cols, out, st);                                      \
+    }
+
+} // namespace mllm_gemv

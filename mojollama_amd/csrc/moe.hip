@@ -1,0 +1,363 @@
+// moe.hip — the MoE FFN layer for T tokens on device data.
+//
+// Semantics per token are those of moe_forward_omp (QK:2066-2250) fed by the
+// C routing of moe_ffn (CE:606-638), renormalised as GO:88-92 /
+// CE:1148-1152 when asked: gate/up per quant type (an MXFP4 pair in fp32,
+// Q4_K through the Q8_0-activation dot), SiLU with the gate clamped to +-80,
+// down per type (MXFP4 through Q8_0(h)), combined[n] = sum_k w_k * down_k in
+// k order.
+//
+// Batched flow (T > 8 tokens):
+//   route -> stable bucketing of the T*K (token, slot) entries by expert on
+//   the GPU -> grouped MFMA GEMM gate+up with the SiLU product in its
+//   epilogue (bucket order) -> grouped MFMA GEMM down -> per-token combine
+//   in k order through the inverse permutation.
+// Decode flow (T <= 8): the same stages with the decode GEMV kernels, one job
+// per (token, slot), no bucketing.
+#include <string.h>
+#include <algorithm>
+#include <vector>
+#include "gemm.h"
+#include "gemv.h"
+#include "mllm.h"
+
+namespace {
+
+constexpr int kTileEntries = 64;   // entries per grouped-GEMM work tile (gemm.hip TM)
+
+// Stable bucketing of entries i = t*K + k by expert idx[i], in one workgroup:
+// block histograms -> exclusive scan in (expert, block) order -> each block
+// places its entries in order.  perm[pos] = i, pos_of[i] = pos (or -1 for a
+// negative expert id), bucket offsets off[0..E], and the list of work tiles
+// (<= kTileEntries consecutive positions of one expert).
+__global__ __launch_bounds__(256) void k_bucket(const int *__restrict__ idx, int TK, int E, int CH,
+                                                int *__restrict__ off, int *__restrict__ perm,
+                                                int *__restrict__ pos_of, int *__restrict__ tile_expert,
+                                                int *__restrict__ tile_begin, int *__restrict__ tile_end,
+                                                int *__restrict__ n_tiles)
+{
+    extern __shared__ int hist[];   // [NB][E]
+    const int NB = (TK + CH - 1) / CH;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < NB * E; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    if (tid < NB) {
+        const int i1 = min(TK, (tid + 1) * CH);
+        for (int i = tid * CH; i < i1; i++) {
+            const int e = idx[i];
+            if (e >= 0 && e < E) hist[tid * E + e]++;
+        }
+    }
+    __syncthreads();
+    __shared__ int tot[257];
+    if (tid < E) {
+        int s = 0;
+        for (int b = 0; b < NB; b++) s += hist[b * E + tid];
+        tot[tid] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int e = 0; e < E; e++) { const int c = tot[e]; tot[e] = run; off[e] = run; run += c; }
+        off[E] = run;
+        tot[E] = run;
+    }
+    __syncthreads();
+    if (tid < E) {
+        int run = tot[tid];
+        for (int b = 0; b < NB; b++) { const int c = hist[b * E + tid]; hist[b * E + tid] = run; run += c; }
+    }
+    __syncthreads();
+    if (tid < NB) {
+        const int i1 = min(TK, (tid + 1) * CH);
+        for (int i = tid * CH; i < i1; i++) {
+            const int e = idx[i];
+            if (e >= 0 && e < E) {
+                const int pos = hist[tid * E + e]++;
+                perm[pos] = i;
+                pos_of[i] = pos;
+            } else {
+                pos_of[i] = -1;
+            }
+        }
+    }
+    if (tid == 0) {
+        int nt = 0;
+        for (int e = 0; e < E; e++) {
+            const int b = tot[e], c = (e + 1 < E ? tot[e + 1] : tot[E]) - b;
+            for (int s = 0; s < c; s += kTileEntries) {
+                tile_expert[nt] = e;
+                tile_begin[nt] = b + s;
+                tile_end[nt] = b + min(c, s + kTileEntries);
+                nt++;
+            }
+        }
+        *n_tiles = nt;
+    }
+}
+
+// Token row of bucket position p: perm[p] / K.
+__global__ void k_entry_tokens(const int *__restrict__ perm, int TK, int K, int *__restrict__ tok)
+{
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p < TK) tok[p] = perm[p] / K;
+}
+
+// out[t][n] = sum over k (in order) of w[t][k] * dn[pos_of[t*K+k]][n], as
+// moe_forward_omp's combined[row] += top_weight * dot (QK:2243-2244).
+__global__ void k_combine_pos(const float *__restrict__ dn, const float *__restrict__ w,
+                              const int *__restrict__ pos_of, int K, int N, float *__restrict__ out)
+{
+    const int t = blockIdx.y;
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) {
+        const int pos = pos_of[t * K + k];
+        if (pos >= 0) acc += w[t * K + k] * dn[(long)pos * N + n];
+    }
+    out[(long)t * N + n] = acc;
+}
+
+size_t a256(size_t n) { return (n + 255) / 256 * 256; }
+
+size_t xq_size(long rows, int n_cols)
+{
+    const long nb = n_cols / 32;
+    return a256(rows * nb * 32) + 3 * a256(rows * nb * 4);
+}
+
+mllm_xq xq_at(uint8_t *p, long rows, int n_cols, int8_t **q, float **d, float **s4, int **sq)
+{
+    const long nb = n_cols / 32;
+    *q = (int8_t *)p; p += a256(rows * nb * 32);
+    *d = (float *)p; p += a256(rows * nb * 4);
+    *s4 = (float *)p; p += a256(rows * nb * 4);
+    *sq = (int *)p;
+    return mllm_xq{*q, *d, *s4, *sq};
+}
+
+int sem_gu_of(int qt_gate, int qt_up, int which)
+{
+    if (qt_gate == 39 && qt_up == 39) return SEM_MXFP4;          // QK:2094
+    const int qt = which == 0 ? qt_gate : qt_up;
+    switch (qt) {                                                 // QK:2114-2152
+    case 12: return SEM_Q4_K_Q8; case 14: return SEM_Q6_K_LOWNIB; case 2: return SEM_Q4_0;
+    case 3: return SEM_Q4_1; case 6: return SEM_Q5_0_Q8;
+    }
+    return -1;
+}
+
+int sem_down_of(int qt)
+{
+    switch (qt) {                                                 // QK:2192-2245
+    case 39: return SEM_MXFP4_Q8; case 14: return SEM_Q6_K_LOWNIB; case 2: return SEM_Q4_0; case 6: return SEM_Q5_0_F32;
+    }
+    return -1;
+}
+
+int xmode_of(int sem)
+{
+    return sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_F32;
+}
+
+} // namespace
+
+struct mllm_moe_layer {
+    int N, M, E, K, renorm;
+    int sem_g, sem_u, sem_d;
+    const float *router_t;
+    mllm_packed *tab;   // device: [E] gate, [E] up, [E] down
+};
+
+struct moe_ws {
+    int *idx, *off, *perm, *pos_of, *tok, *tile_expert, *tile_begin, *tile_end, *n_tiles;
+    float *w, *g, *u, *h, *dn;
+    uint8_t *xq_x, *xq_h;
+};
+
+static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *base)
+{
+    const size_t TK = (size_t)T * L.K;
+    const size_t max_tiles = TK / kTileEntries + L.E + 1;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t at = o; o += a256(bytes); return base ? base + at : nullptr; };
+    moe_ws s;
+    s.idx = (int *)take(TK * 4);
+    s.w = (float *)take(TK * 4);
+    s.off = (int *)take((L.E + 1) * 4);
+    s.perm = (int *)take(TK * 4);
+    s.pos_of = (int *)take(TK * 4);
+    s.tok = (int *)take(TK * 4);
+    s.tile_expert = (int *)take(max_tiles * 4);
+    s.tile_begin = (int *)take(max_tiles * 4);
+    s.tile_end = (int *)take(max_tiles * 4);
+    s.n_tiles = (int *)take(4);
+    s.g = (float *)take(TK * L.M * 4);
+    s.u = (float *)take(TK * L.M * 4);
+    s.h = (float *)take(TK * L.M * 4);
+    s.dn = (float *)take(TK * L.N * 4);
+    s.xq_x = take(xq_size(T, L.N));
+    s.xq_h = take(xq_size((long)TK, L.M));
+    if (w) *w = s;
+    return o;
+}
+
+extern "C" {
+
+MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
+                                          const void *const *gate_packed, const void *const *up_packed,
+                                          const void *const *down_packed, const float *router_t_dev, int renorm)
+{
+    if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0) return nullptr;
+    mllm_moe_layer *L = new mllm_moe_layer;
+    L->N = N; L->M = M; L->E = E; L->K = K; L->renorm = renorm;
+    L->sem_g = sem_gu_of(qt_gate, qt_up, 0);
+    L->sem_u = sem_gu_of(qt_gate, qt_up, 1);
+    L->sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);     // Q4_K down: the reference adds zeros
+    L->router_t = router_t_dev;
+    std::vector<mllm_packed> tab(3 * (size_t)E);
+    for (int e = 0; e < E; e++) {
+        if (L->sem_g >= 0) tab[e] = mllm_packed_view(mllm_sem_layout(L->sem_g), (const uint8_t *)gate_packed[e], M, N);
+        if (L->sem_u >= 0) tab[E + e] = mllm_packed_view(mllm_sem_layout(L->sem_u), (const uint8_t *)up_packed[e], M, N);
+        if (L->sem_d >= 0) tab[2 * E + e] = mllm_packed_view(mllm_sem_layout(L->sem_d), (const uint8_t *)down_packed[e], N, M);
+    }
+    if (hipMalloc(&L->tab, tab.size() * sizeof(mllm_packed)) != hipSuccess ||
+        hipMemcpy(L->tab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess) {
+        delete L;
+        return nullptr;
+    }
+    return L;
+}
+
+MLLM_API void mllm_moe_release(mllm_moe_layer *L)
+{
+    if (!L) return;
+    (void)hipFree(L->tab);
+    delete L;
+}
+
+MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *L, int T)
+{
+    return L ? (long)moe_ws_layout(*L, T, nullptr, nullptr) : -1;
+}
+
+// x [T][N] fp32 -> out [T][N]; also returns the routing (idx/w [T][K]) in the workspace.
+MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
+                              long ws_bytes, int *idx_out, float *w_out, void *stream)
+{
+    if (!L || T <= 0) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (ws_bytes < (long)moe_ws_layout(*L, T, nullptr, nullptr)) return -1;
+    moe_ws s;
+    moe_ws_layout(*L, T, &s, (uint8_t *)workspace);
+    const int N = L->N, M = L->M, E = L->E, K = L->K, TK = T * K;
+#define CK(e) do { if ((e) != hipSuccess) return -1; } while (0)
+    CK(mllm_launch_route(L->router_t, x, T, N, E, K, L->renorm, s.idx, s.w, st));
+    if (L->sem_g < 0 || L->sem_u < 0) return -1;   // reference-zero gate/up types are not served here
+    int8_t *q; float *d, *s4; int *sq;
+    const mllm_xq xqx = xq_at(s.xq_x, T, N, &q, &d, &s4, &sq);
+    if (mllm_sem_uses_q8(L->sem_g) || mllm_sem_uses_q8(L->sem_u))
+        CK(mllm_launch_quantize_q8_0(x, T, N, nullptr, q, d, s4, sq, st));
+    int8_t *hq; float *hd, *hs4; int *hsq;
+    const mllm_xq xqh = xq_at(s.xq_h, TK, M, &hq, &hd, &hs4, &hsq);
+
+    const bool batched = T > 8 && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
+                         (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d));
+    if (batched) {
+        // histogram blocks: at most 256 blocks and 64 KB of LDS
+        int nb_max = std::min(256, 16384 / E);
+        const int ch = (TK + nb_max - 1) / nb_max;
+        const int nb = (TK + ch - 1) / ch;
+        hipLaunchKernelGGL(k_bucket, dim3(1), dim3(256), (size_t)nb * E * 4, st, s.idx, TK, E, ch, s.off, s.perm,
+                           s.pos_of, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles);
+        CK(hipGetLastError());
+        hipLaunchKernelGGL(k_entry_tokens, dim3((TK + 255) / 256), dim3(256), 0, st, s.perm, TK, K, s.tok);
+        CK(hipGetLastError());
+        const int max_tiles = TK / kTileEntries + E + 1;
+        // gate + up (+ SiLU) in bucket order
+        qgemm_args a{};
+        a.table = L->tab; a.table2 = L->tab + E;
+        a.x = x; a.ldx = N; a.xq = xqx;
+        a.row_of = s.tok;
+        a.n_rows = M; a.n_cols = N;
+        a.tile_expert = s.tile_expert; a.tile_begin = s.tile_begin; a.tile_end = s.tile_end; a.n_tiles = s.n_tiles;
+        a.clamp_silu = 1;
+        if (L->sem_g == L->sem_u) {
+            a.out = s.h; a.ldo = M;
+            CK(mllm_launch_qgemm(L->sem_g, xmode_of(L->sem_g), true, a, max_tiles, st));
+        } else {
+            a.out = s.g; a.ldo = M;
+            CK(mllm_launch_qgemm(L->sem_g, xmode_of(L->sem_g), false, a, max_tiles, st));
+            a.table = L->tab + E; a.out = s.u;
+            CK(mllm_launch_qgemm(L->sem_u, xmode_of(L->sem_u), false, a, max_tiles, st));
+            CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
+        }
+        // down, rows of h already in bucket order
+        if (L->sem_d >= 0) {
+            if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
+            qgemm_args b{};
+            b.table = L->tab + 2 * E;
+            b.x = s.h; b.ldx = M; b.xq = xqh;
+            b.out = s.dn; b.ldo = N;
+            b.n_rows = N; b.n_cols = M;
+            b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;
+            CK(mllm_launch_qgemm(L->sem_d, xmode_of(L->sem_d), false, b, max_tiles, st));
+        } else {
+            CK(hipMemsetAsync(s.dn, 0, (size_t)TK * N * 4, st));
+        }
+        hipLaunchKernelGGL(k_combine_pos, dim3((N + 255) / 256, T), dim3(256), 0, st, s.dn, s.w, s.pos_of, K, N, out);
+        CK(hipGetLastError());
+    } else {
+        // decode: per token, one GEMV job per routing slot (expert picked on the device)
+        for (int t = 0; t < T; t++) {
+            for (int wch = 0; wch < 2; wch++) {
+                mllm_gemv_args a{};
+                a.table = L->tab + (size_t)wch * E; a.idx = s.idx + (size_t)t * K;
+                a.x = x + (size_t)t * N; a.x_job_stride = 0; a.ldx = N;
+                a.out = (wch == 0 ? s.g : s.u) + (size_t)t * K * M; a.out_job_stride = M; a.ldo = M;
+                a.n_rows = M; a.n_cols = N; a.B = 1;
+                const long nb = N / 32;
+                a.xq = {q + (size_t)t * nb * 32, d + t * nb, s4 + t * nb, sq + t * nb};
+                CK(mllm_launch_gemv(wch == 0 ? L->sem_g : L->sem_u, a, K, st));
+            }
+        }
+        CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
+        if (L->sem_d >= 0) {
+            if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
+            for (int t = 0; t < T; t++) {
+                mllm_gemv_args a{};
+                a.table = L->tab + 2 * (size_t)E; a.idx = s.idx + (size_t)t * K;
+                a.x = s.h + (size_t)t * K * M; a.x_job_stride = M; a.ldx = M;
+                a.out = s.dn + (size_t)t * K * N; a.out_job_stride = N; a.ldo = N;
+                a.n_rows = N; a.n_cols = M; a.B = 1;
+                const long nb = M / 32;
+                a.xq = {hq + (size_t)t * K * nb * 32, hd + (size_t)t * K * nb, hs4 + (size_t)t * K * nb,
+                        hsq + (size_t)t * K * nb};
+                CK(mllm_launch_gemv(L->sem_d, a, K, st));
+            }
+        } else {
+            CK(hipMemsetAsync(s.dn, 0, (size_t)TK * N * 4, st));
+        }
+        CK(mllm_launch_combine(s.dn, s.w, T, K, N, out, 0, st));
+    }
+    if (idx_out) CK(hipMemcpyAsync(idx_out, s.idx, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
+    if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
+#undef CK
+    return 0;
+}
+
+// Bucketing alone (for tests): perm/pos_of/off of the entries idx [TK] over E experts.
+MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm, int *pos_of, int *tiles, void *stream)
+{
+    if (E <= 0 || E > 256 || TK <= 0) return -1;
+    const int max_tiles = TK / kTileEntries + E + 1;
+    int nb_max = std::min(256, 16384 / E);
+    const int ch = (TK + nb_max - 1) / nb_max;
+    const int nb = (TK + ch - 1) / ch;
+    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(256), (size_t)nb * E * 4, (hipStream_t)stream, idx, TK, E, ch, off,
+                       perm, pos_of, tiles, tiles + max_tiles, tiles + 2 * max_tiles, tiles + 3 * max_tiles);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+} // extern "C"

@@ -110,6 +110,17 @@ def load_kernels(path=LIB_PATH):
     so.mllm_route.restype = ci
     so.mllm_dequant.argtypes = [ci, cvp, ci, ci, cvp, cvp]
     so.mllm_dequant.restype = ci
+    so.mllm_moe_prepare.argtypes = [ci, ci, ci, ci, ci, ci, ci, ctypes.POINTER(cvp), ctypes.POINTER(cvp),
+                                    ctypes.POINTER(cvp), cvp, ci]
+    so.mllm_moe_prepare.restype = cvp
+    so.mllm_moe_release.argtypes = [cvp]
+    so.mllm_moe_release.restype = None
+    so.mllm_moe_workspace_size.argtypes = [cvp, ci]
+    so.mllm_moe_workspace_size.restype = ctypes.c_long
+    so.mllm_moe_forward.argtypes = [cvp, cvp, ci, cvp, cvp, ctypes.c_long, cvp, cvp, cvp]
+    so.mllm_moe_forward.restype = ci
+    so.mllm_moe_bucket.argtypes = [cvp, ci, ci, cvp, cvp, cvp, cvp, cvp]
+    so.mllm_moe_bucket.restype = ci
     if path == LIB_PATH:
         _LIB = so
     return so
@@ -183,3 +194,70 @@ class DeviceOps:
         self._check(self.so.mllm_dequant(sem, packed.data_ptr(), n_rows, n_cols, out.data_ptr(), self._stream()),
                     "mllm_dequant")
         return out
+
+    # ------------------------------------------------------------ MoE layer
+    def moe_prepare(self, qts, N, M, E, K, gates, ups, downs, router, renorm):
+        """gates/ups/downs: per-expert raw GGUF uint8 tensors (GPU) in the
+        reference's layout; router: fp32 [E][N] (GPU).  Returns a MoELayer."""
+        return MoELayer(self, qts, N, M, E, K, gates, ups, downs, router, renorm)
+
+    def moe_bucket(self, idx, E):
+        """Stable bucketing of entries idx (int32 GPU, flat) over E experts."""
+        torch = self.torch
+        TK = idx.numel()
+        max_tiles = TK // 64 + E + 1
+        off = torch.empty(E + 1, dtype=torch.int32, device=idx.device)
+        perm = torch.empty(TK, dtype=torch.int32, device=idx.device)
+        pos_of = torch.empty(TK, dtype=torch.int32, device=idx.device)
+        tiles = torch.empty(3 * max_tiles + 1, dtype=torch.int32, device=idx.device)
+        self._check(self.so.mllm_moe_bucket(idx.data_ptr(), TK, E, off.data_ptr(), perm.data_ptr(), pos_of.data_ptr(),
+                                            tiles.data_ptr(), self._stream()), "mllm_moe_bucket")
+        n = int(tiles[3 * max_tiles].item())
+        return off, perm, pos_of, (tiles[:n], tiles[max_tiles:max_tiles + n], tiles[2 * max_tiles:2 * max_tiles + n])
+
+
+class MoELayer:
+    """A prepared MoE layer (mllm_moe_prepare) holding its packed expert weights."""
+
+    def __init__(self, ops, qts, N, M, E, K, gates, ups, downs, router, renorm):
+        torch = ops.torch
+        self.ops, self.N, self.M, self.E, self.K = ops, N, M, E, K
+        sg = ops.so.mllm_sem_for(ENT_MOE_GU, qts[0]) if not (qts[0] == 39 and qts[1] == 39) else MXFP4
+        su = ops.so.mllm_sem_for(ENT_MOE_GU, qts[1]) if not (qts[0] == 39 and qts[1] == 39) else MXFP4
+        sd = ops.so.mllm_sem_for(ENT_MOE_DOWN, qts[2])
+        self.gp = [ops.pack(sg, g, M, N) for g in gates]
+        self.up = [ops.pack(su, u, M, N) for u in ups]
+        self.dp = [ops.pack(sd, d, N, M) for d in downs] if sd >= 0 else [self.gp[0]] * E
+        self.router_t = router.t().contiguous()
+        arr = ctypes.c_void_p * E
+        self.h = ops.so.mllm_moe_prepare(qts[0], qts[1], qts[2], N, M, E, K,
+                                         arr(*[t.data_ptr() for t in self.gp]), arr(*[t.data_ptr() for t in self.up]),
+                                         arr(*[t.data_ptr() for t in self.dp]), self.router_t.data_ptr(), int(renorm))
+        if not self.h:
+            raise RuntimeError("mllm_moe_prepare failed")
+        self._ws = None
+
+    def workspace(self, T):
+        n = self.ops.so.mllm_moe_workspace_size(self.h, T)
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = self.ops.torch.empty(n, dtype=self.ops.torch.uint8, device=self.router_t.device)
+        return self._ws
+
+    def forward(self, x, out=None, idx=None, w=None):
+        torch = self.ops.torch
+        T = x.numel() // self.N
+        if out is None:
+            out = torch.empty((T, self.N), dtype=torch.float32, device=x.device)
+        ws = self.workspace(T)
+        self.ops._check(self.ops.so.mllm_moe_forward(self.h, x.data_ptr(), T, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                     idx.data_ptr() if idx is not None else None,
+                                                     w.data_ptr() if w is not None else None, self.ops._stream()),
+                        "mllm_moe_forward")
+        return out
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.ops.so.mllm_moe_release(self.h)
+        except Exception:
+            pass

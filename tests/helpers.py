@@ -38,6 +38,16 @@ class BCView:
 GEMV_TOL = 2e-5
 # moe outputs chain three GEMVs and a SiLU; expf differs from glibc by <= 1 ulp.
 MOE_TOL = 1e-4
+# moe_forward_omp requantises the SiLU output h to Q8_0 before an MXFP4 down
+# projection (QK:2166-2189, mxfp4_row_dot_q8).  Any fp32 summation-order
+# difference in h (the reference's own AVX order vs ours) flips a few Q8 codes
+# by one step, and one flip moves that token's output by about
+# 3 / (127 * sqrt(M)) ~ 4e-4 of its max: the bound there is the north star's 1e-3.
+MOE_Q8H_TOL = 1e-3
+
+
+def moe_tol(qts):
+    return MOE_Q8H_TOL if qts[2] == 39 else MOE_TOL
 
 
 def fp(a):

@@ -1,0 +1,79 @@
+"""GPU parity of the quantised-weight MFMA GEMM (prefill / batched path of
+*_batch_matmul and mllm_gemv for B > 8) against the oracle.
+
+Tolerance GEMM_TOL: weights and fp32 activations enter the MFMA as bf16
+hi+lo pairs (about 16 significant bits each, products accumulated in fp32),
+so the normalised max error is ~1e-5; any decode or layout mistake costs
+> 3e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import fp, up
+from mojollama_amd import kernels as K
+from mojollama_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+GEMM_TOL = 5e-5
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return K.load_kernels()
+
+
+@pytest.fixture(scope="module")
+def dev(lib):
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return K.DeviceOps(lib)
+
+
+def bmm(lib, name, w, x, R, C, B):
+    out = np.full(B * R, np.nan, np.float32)
+    getattr(lib, name + "_batch_matmul")(up(w), fp(np.ascontiguousarray(x, np.float32)), fp(out), R, C, B)
+    return out.reshape(B, R)
+
+
+@pytest.mark.parametrize("name,qt", [("q4_0", 2), ("q8_0", 8), ("q4_k", 12), ("q6_k", 14), ("q5_k", 13),
+                                     ("mxfp4", 39)])
+@pytest.mark.parametrize("B", [9, 64, 130])
+def test_batch_matmul_gemm_vs_oracle(lib, orc, name, qt, B):
+    rng = np.random.default_rng(300 + qt + B)
+    R, C = 200, 512
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, B, C)
+    got = bmm(lib, name, w, x, R, C, B)
+    assert O.norm_err(got, orc.gemv(orc.sem_for(1, qt), w, x, R, C, B)) < GEMM_TOL
+
+
+@pytest.mark.parametrize("sem", [K.Q4_0, K.Q4_1, K.Q5_0_F32, K.Q8_0, K.Q4_K_GGML, K.Q4_K_Q8, K.Q5_K_GGML, K.Q5_K_CE,
+                                 K.Q6_K_GGML, K.Q6_K_LOWNIB, K.Q6_K_SEQ, K.MXFP4, K.MXFP4_CLAMP, K.MXFP4_Q8])
+def test_device_gemm_every_semantic(dev, orc, sem):
+    import torch
+    qt = {K.Q4_0: 2, K.Q4_1: 3, K.Q5_0_F32: 6, K.Q8_0: 8, K.Q4_K_GGML: 12, K.Q4_K_Q8: 12, K.Q5_K_GGML: 13,
+          K.Q5_K_CE: 13, K.Q6_K_GGML: 14, K.Q6_K_LOWNIB: 14, K.Q6_K_SEQ: 14, K.MXFP4: 39, K.MXFP4_CLAMP: 39,
+          K.MXFP4_Q8: 39}[sem]
+    rng = np.random.default_rng(700 + sem)
+    R, C, B = 130, 768 if W.BLOCK[qt][0] == 256 else 800, 70
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, B, C)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy()
+    assert O.norm_err(got, orc.gemv(sem, w, x, R, C, B)) < GEMM_TOL, K.SEM_NAMES[sem]
+
+
+@pytest.mark.parametrize("name,qt,R,C,M", [("q4_k", 12, 5632, 2048, 128), ("q6_k", 14, 2048, 5632, 128),
+                                           ("q4_k", 12, 5632, 2048, 1280)])
+def test_prefill_config_shapes(lib, orc, name, qt, R, C, M):
+    """the full matrices with bf16-valued activations, checked on a row subset."""
+    rng = np.random.default_rng(R + M)
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, M, C, bf16=True)
+    got = bmm(lib, name, w, x, R, C, M)
+    rows = 256
+    rb = W.row_bytes(qt, C)
+    ref = orc.gemv(orc.sem_for(1, qt), w[:rows * rb], x[:64], rows, C, 64)
+    assert O.norm_err(got[:64, :rows], ref) < GEMM_TOL
+    assert np.all(np.isfinite(got))

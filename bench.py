@@ -39,6 +39,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU reference timing")
+    ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     return ap.parse_args()
 
 
@@ -144,6 +145,119 @@ def cpu_reference(layers_np, lm_np, B, passes=5):
             "ms_per_pass": round(med * 1e3, 3)}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(torch, dev, args):
+    """configs[2]: Q4_K gate/up 5632x2048 and Q6_K down 2048x5632 at M in {128, 512, 1280}
+    bf16-valued activations, *_batch_matmul semantics, through the MFMA GEMM."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    out = {}
+    mats = {"gate_q4k": (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048), "down_q6k": (K.Q6_K_SEQ, W.QT_Q6_K, 2048, 5632)}
+    for name, (sem, qt, R, C) in mats.items():
+        raw = W.gen_weights_torch(gen, qt, R, C)
+        packed = dev.pack(sem, raw, R, C)
+        for M in (128, 512, 1280):
+            x = torch.randn(M, C, device="cuda", generator=gen).bfloat16().float()
+            o = torch.empty(M, R, device="cuda")
+            ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o), max(5, args.steps), args.warmup)
+            flops = 2.0 * R * C * M
+            out[f"{name}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                   "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+            print(f"[bench] prefill {name} M={M}: {ms * 1e3:.1f} us, {out[f'{name}_M{M}']['TFLOP/s']} TFLOP/s",
+                  file=sys.stderr, flush=True)
+    return out
+
+
+def moe_cfg(tag):
+    return dict(W.GPTOSS) if tag == "gptoss" else dict(W.QWEN3)
+
+
+def bench_moe(torch, dev, args, tag, with_cpu, sizes=(1, 1280)):
+    """one MoE FFN layer (all experts resident) at decode
+    batch 1 and at 10 x 128 = 1280 tokens; tokens/s = tokens / layer time."""
+    c = moe_cfg(tag)
+    N, E, Kk, M = c["N"], c["E"], c["K"], c["M"]
+    qts = (c["qt_gate"], c["qt_up"], c["qt_down"])
+    renorm = 1
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4 if tag == "gptoss" else 5)
+    if tag == "gptoss":
+        # fused gate/up tensor per expert (5760 x 2880): gate = rows [0, M), up = rows [M, 2M)
+        rb = W.row_bytes(qts[0], N)
+        fused = [W.gen_weights_torch(gen, qts[0], 2 * M, N) for _ in range(E)]
+        gates = [f[:M * rb] for f in fused]
+        ups = [f[M * rb:] for f in fused]
+    else:
+        gates = [W.gen_weights_torch(gen, qts[0], M, N) for _ in range(E)]
+        ups = [W.gen_weights_torch(gen, qts[1], M, N) for _ in range(E)]
+    downs = [W.gen_weights_torch(gen, qts[2], N, M) for _ in range(E)]
+    rng = np.random.default_rng(7)
+    router_np = W.gen_router(rng, E, N)
+    T = max(sizes)
+    if tag == "qwen3":
+        x_np, router_np, hot, _ = W.skewed_tokens(rng, router_np, T)
+    else:
+        x_np = W.gen_x(rng, T, N)
+    router = torch.from_numpy(router_np).cuda()
+    layer = dev.moe_prepare(qts, N, M, E, Kk, gates, ups, downs, router, renorm)
+    x = torch.from_numpy(x_np).cuda()
+    res = {}
+    wbytes_expert = sum(W.row_bytes(q, cols) * rows for q, rows, cols in ((qts[0], M, N), (qts[1], M, N), (qts[2], N, M)))
+    for Tn in sizes:
+        xs = x[:Tn].contiguous()
+        o = torch.empty(Tn, N, device="cuda")
+        layer.workspace(Tn)
+        ms = time_region(torch, lambda: layer.forward(xs, out=o), max(5, args.steps), args.warmup)
+        idx = torch.empty(Tn, Kk, dtype=torch.int32, device="cuda")
+        layer.forward(xs, idx=idx)
+        n_exp = int(torch.unique(idx).numel())
+        flops = 2.0 * Tn * Kk * (3 * M * N) + 2.0 * Tn * N * E
+        nbytes = n_exp * wbytes_expert + E * N * 4 + 2 * Tn * N * 4
+        r = {"us": round(ms * 1e3, 1), "tokens/s": round(Tn / (ms * 1e-3), 1), "experts_touched": n_exp,
+             "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2)}
+        if Tn == 1:
+            r["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        else:
+            r["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+        res[f"T{Tn}"] = r
+        print(f"[bench] MoE {tag} T={Tn}: {ms * 1e3:.1f} us, {r['tokens/s']} tokens/s", file=sys.stderr, flush=True)
+    if with_cpu:
+        res["cpu_baseline"] = cpu_moe_reference(tag, qts, N, M, E, Kk, gates, ups, downs, router_np, x_np)
+    del layer
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_moe_reference(tag, qts, N, M, E, Kk, gates, ups, downs, router_np, x_np, n_tok=16):
+    """The reference's moe_forward_omp (oracle/_ref, AVX2 + OpenMP) per token with
+    the renormalised C routing, on the first n_tok tokens of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    if not O.ref_available():
+        return None
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    ref = O.RefLib()
+    ref.so.set_num_threads(cores)
+    orc = O.Oracle()
+    idx, w = orc.route(router_np, x_np[:n_tok], Kk, renorm=True)
+    need = sorted(set(int(e) for e in idx.ravel()))
+    host = {e: (gates[e].cpu().numpy(), ups[e].cpu().numpy(), downs[e].cpu().numpy()) for e in need}
+    dummy = host[need[0]]
+    g = [host.get(e, dummy)[0] for e in range(E)]
+    u = [host.get(e, dummy)[1] for e in range(E)]
+    d = [host.get(e, dummy)[2] for e in range(E)]
+    ref.moe_forward(g, u, d, x_np[0], M, N, qts, idx[0], w[0])   # warm-up
+    t0 = time.perf_counter()
+    for t in range(n_tok):
+        ref.moe_forward(g, u, d, x_np[t], M, N, qts, idx[t], w[t])
+    dt = time.perf_counter() - t0
+    return {"value": round(n_tok / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "reference",
+            "sample": f"moe_forward_omp (oracle/_ref) on {n_tok} tokens of the {tag} workload, C routing "
+                      f"(renormalised top-{Kk}) precomputed, {cores} OpenMP threads"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -218,6 +332,12 @@ def main():
         if cpu:
             print(f"[bench] CPU reference: {cpu['value']} GB/s on {cpu['cores']} threads", file=sys.stderr, flush=True)
 
+    extra = {}
+    if not args.no_extra:
+        extra["configs2_prefill_gemm"] = bench_prefill(torch, dev, args)
+        extra["configs3_gptoss_moe"] = bench_moe(torch, dev, args, "gptoss", with_cpu=not args.no_cpu)
+        extra["configs4_qwen3_moe"] = bench_moe(torch, dev, args, "qwen3", with_cpu=not args.no_cpu)
+
     ms1, gbs1 = results[1]
     line = {
         "metric": "quant GEMV HBM GB/s (% of peak) + MoE-FFN layer tokens/s, batch 1 and 10",
@@ -243,6 +363,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": f"k_gemv_p<Q4_K_GGML,B=1> fused gate+up 11264x2048 ({gu_bytes:,} algorithmic B/launch)"},
         "cpu_baseline": cpu,
+        "extra": extra,
     }
     print(json.dumps(line), flush=True)
 

@@ -116,8 +116,15 @@ MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, floa
 /* quantize_row_q8_0 over T rows. */
 MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *q8_dev, void *stream);
 
-/* Routing of T tokens: router_t is the [N][E] transpose of the fp32 router. */
-MLLM_API int mllm_route(const float *router_t_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
+/* Routing layout of an fp32 router [E][N] (row e = expert e's weights, as the
+ * reference's w_gate_inp): element (i, e) at ((i/4)*E + e)*4 + i%4, rows from N
+ * up to a multiple of 32 zero; mllm_router_packed_size bytes. */
+MLLM_API long mllm_router_packed_size(int N, int E);
+MLLM_API int mllm_router_pack(const float *router_dev, int N, int E, float *out_dev, void *stream);
+
+/* Routing of T tokens (CE:606-638; renormalised top-K weights when `renorm`):
+ * router_p in the routing layout, x [T][N] -> idx/w [T][K].  E <= 256, K <= 16. */
+MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
                         int *idx_dev, float *w_dev, void *stream);
 
 /* fp32 weights of a packed matrix (fp32-weight semantics only). */
@@ -126,8 +133,9 @@ MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_col
 /* ------------------------------------------------------- MoE layer, T tokens */
 
 /* A prepared MoE layer: per-expert packed weights (device pointers, arrays of E
- * entries on the host) with the reference's GGUF codes, and the router
- * transposed to [N][E] (device).  Per token the layer computes what
+ * entries on the host) with the reference's GGUF codes, and the fp32 router
+ * [E][N] (device; the layer keeps its own copy in the routing layout, so the
+ * caller may free it after the call).  Per token the layer computes what
  * moe_forward_omp (QK:2066-2250) computes when fed the C routing of moe_ffn
  * (CE:606-638), renormalised when `renorm` (GO:88-92): gate/up per type,
  * SiLU with the gate clamped to +-80, down per type, k-order combine.
@@ -136,7 +144,7 @@ MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_col
 typedef struct mllm_moe_layer mllm_moe_layer;
 MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
                                           const void *const *gate_packed, const void *const *up_packed,
-                                          const void *const *down_packed, const float *router_t_dev, int renorm);
+                                          const void *const *down_packed, const float *router_dev, int renorm);
 MLLM_API void mllm_moe_release(mllm_moe_layer *layer);
 MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *layer, int T);
 /* out[T][N]; idx_out/w_out (optional, device [T][K]) receive the routing. */

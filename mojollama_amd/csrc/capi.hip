@@ -195,7 +195,7 @@ uint64_t fingerprint(const void *p, long n)
     memcpy(&w, b + (n >= 8 ? n - 8 : 0), (size_t)(n >= 8 ? 8 : n));
     return (h ^ w) * 1099511628211ull;
 }
-std::map<std::tuple<const void *, int, int>, float *> g_router_cache;  // (host, E, N) -> transposed [N][E]
+std::map<std::tuple<const void *, int, int>, float *> g_router_cache;  // (host, E, N) -> routing layout
 
 // Upload + pack a raw host matrix (once).  Returns its packed view.
 int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
@@ -235,7 +235,9 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
     return 0;
 }
 
-// Router [E][N] fp32 on the host -> device copy transposed to [N][E] (cached).
+// Router [E][N] fp32 on the host -> device copy in the routing layout
+// (mllm_router_pack: element (i, e) at ((i/4)*E + e)*4 + i%4, zero pad
+// rows), cached.
 int get_router(const float *host, int E, int N, const float **dev_out)
 {
     auto key = std::make_tuple((const void *)host, E, N);
@@ -244,9 +246,9 @@ int get_router(const float *host, int E, int N, const float **dev_out)
         auto it = g_router_cache.find(key);
         if (it != g_router_cache.end()) { *dev_out = it->second; return 0; }
     }
-    std::vector<float> t((size_t)E * N);
+    std::vector<float> t((size_t)mllm_router_packed_floats(N, E), 0.0f);
     for (int e = 0; e < E; e++)
-        for (int i = 0; i < N; i++) t[(size_t)i * E + e] = host[(size_t)e * N + i];
+        for (int i = 0; i < N; i++) t[((size_t)(i >> 2) * E + e) * 4 + (i & 3)] = host[(size_t)e * N + i];
     float *d = nullptr;
     HIP_OK(hipMalloc(&d, t.size() * 4));
     HIP_OK(hipMemcpy(d, t.data(), t.size() * 4, hipMemcpyHostToDevice));
@@ -645,10 +647,22 @@ MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *
     return 0;
 }
 
-MLLM_API int mllm_route(const float *router_t_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
+MLLM_API long mllm_router_packed_size(int N, int E)
+{
+    return (N > 0 && E > 0) ? mllm_router_packed_floats(N, E) * 4 : -1;
+}
+
+MLLM_API int mllm_router_pack(const float *router_dev, int N, int E, float *out_dev, void *stream)
+{
+    hipError_t r = mllm_launch_router_pack(router_dev, N, E, out_dev, (hipStream_t)stream);
+    if (r != hipSuccess) { set_error("mllm_router_pack: %s", hipGetErrorString(r)); return -1; }
+    return 0;
+}
+
+MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
                         int *idx_dev, float *w_dev, void *stream)
 {
-    hipError_t r = mllm_launch_route(router_t_dev, x_dev, T, N, E, K, renorm, idx_dev, w_dev, (hipStream_t)stream);
+    hipError_t r = mllm_launch_route(router_p_dev, x_dev, T, N, E, K, renorm, idx_dev, w_dev, (hipStream_t)stream);
     if (r != hipSuccess) { set_error("mllm_route: %s (E<=256, K<=16 required)", hipGetErrorString(r)); return -1; }
     return 0;
 }

@@ -38,6 +38,8 @@ hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t 
 // Router: logits by a sequential fp32 FMA chain (CE:614-618), softmax with
 // expf, insertion top-k with strict '>' (CE:628-638), optional renormalise
 // (GO:88-92).  router_t is the router transposed to [N][E].
+long mllm_router_packed_floats(int N, int E);
+hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out, hipStream_t st);
 hipError_t mllm_launch_route(const float *router_t, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, hipStream_t st);
 

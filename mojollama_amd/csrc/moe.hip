@@ -166,7 +166,7 @@ int xmode_of(int sem)
 struct mllm_moe_layer {
     int N, M, E, K, renorm;
     int sem_g, sem_u, sem_d;
-    const float *router_t;
+    float *router_p;    // device, routing layout (mllm_router_pack), owned
     mllm_packed *tab;   // device: [E] gate, [E] up, [E] down
 };
 
@@ -207,7 +207,7 @@ extern "C" {
 
 MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
                                           const void *const *gate_packed, const void *const *up_packed,
-                                          const void *const *down_packed, const float *router_t_dev, int renorm)
+                                          const void *const *down_packed, const float *router_dev, int renorm)
 {
     if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0) return nullptr;
     mllm_moe_layer *L = new mllm_moe_layer;
@@ -215,16 +215,21 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
     L->sem_g = sem_gu_of(qt_gate, qt_up, 0);
     L->sem_u = sem_gu_of(qt_gate, qt_up, 1);
     L->sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);     // Q4_K down: the reference adds zeros
-    L->router_t = router_t_dev;
+    L->router_p = nullptr;
+    L->tab = nullptr;
     std::vector<mllm_packed> tab(3 * (size_t)E);
     for (int e = 0; e < E; e++) {
         if (L->sem_g >= 0) tab[e] = mllm_packed_view(mllm_sem_layout(L->sem_g), (const uint8_t *)gate_packed[e], M, N);
         if (L->sem_u >= 0) tab[E + e] = mllm_packed_view(mllm_sem_layout(L->sem_u), (const uint8_t *)up_packed[e], M, N);
         if (L->sem_d >= 0) tab[2 * E + e] = mllm_packed_view(mllm_sem_layout(L->sem_d), (const uint8_t *)down_packed[e], N, M);
     }
+    const size_t rbytes = (size_t)mllm_router_packed_floats(N, E) * sizeof(float);
     if (hipMalloc(&L->tab, tab.size() * sizeof(mllm_packed)) != hipSuccess ||
-        hipMemcpy(L->tab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess) {
-        delete L;
+        hipMemcpy(L->tab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMalloc(&L->router_p, rbytes) != hipSuccess ||
+        mllm_launch_router_pack(router_dev, N, E, L->router_p, nullptr) != hipSuccess ||
+        hipStreamSynchronize(nullptr) != hipSuccess) {
+        mllm_moe_release(L);
         return nullptr;
     }
     return L;
@@ -233,7 +238,8 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
 MLLM_API void mllm_moe_release(mllm_moe_layer *L)
 {
     if (!L) return;
-    (void)hipFree(L->tab);
+    if (L->tab) (void)hipFree(L->tab);
+    if (L->router_p) (void)hipFree(L->router_p);
     delete L;
 }
 
@@ -253,7 +259,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     moe_ws_layout(*L, T, &s, (uint8_t *)workspace);
     const int N = L->N, M = L->M, E = L->E, K = L->K, TK = T * K;
 #define CK(e) do { if ((e) != hipSuccess) return -1; } while (0)
-    CK(mllm_launch_route(L->router_t, x, T, N, E, K, L->renorm, s.idx, s.w, st));
+    CK(mllm_launch_route(L->router_p, x, T, N, E, K, L->renorm, s.idx, s.w, st));
     if (L->sem_g < 0 || L->sem_u < 0) return -1;   // reference-zero gate/up types are not served here
     int8_t *q; float *d, *s4; int *sq;
     const mllm_xq xqx = xq_at(s.xq_x, T, N, &q, &d, &s4, &sq);

@@ -135,49 +135,240 @@ __global__ void k_quantize_q8_0(const float *__restrict__ x, int T, int n_cols, 
 // match the reference's except where the two roundings straddle a midpoint.
 __device__ __forceinline__ float expf_cr(float v) { return (float)exp((double)v); }
 
-// One workgroup per token; thread e computes logit e as a sequential FMA
-// chain over i = 0..N-1 (CE:614-618 compiles to scalar vfmadd231ss), then
-// thread 0 runs the softmax and insertion top-k exactly as CE:620-638.
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_t, const float *__restrict__ x,
-                                               int N, int E, int K, int renorm, int *__restrict__ top_idx,
-                                               float *__restrict__ top_w)
+// Softmax and insertion top-k (CE:620-638) of the logits of TW tokens held in
+// LDS as p[tw * PS + e], PS = route_pitch(E): max by strict '>' from p[0],
+// exp element-wise, sequential sum, x 1/(sum+1e-10), then the top-K of the
+// strict-'>' insertion in index order, optionally renormalised by the
+// sequential sum of the K weights.  That insertion keeps a stable descending
+// order (an element goes after every earlier one that is >= it) and never
+// takes a NaN, so element j lands at slot rank(j) = #{j' : p[j'] > p[j]} +
+// #{j' < j : p[j'] == p[j]} when that is < K -- computed here one thread per
+// element.  Slots no element reaches keep (-1, -1e30), as the reference's
+// initial list does.  Needs route_finish_floats(TW, E) floats at p.
+__host__ __device__ constexpr int route_pitch(int E) { return (E + 3) / 4 * 4 + 4; }
+__host__ __device__ constexpr int route_finish_floats(int TW, int E) { return TW * route_pitch(E) + 2 * TW + 32 * TW; }
+
+__device__ __forceinline__ void route_finish(float *p, int TW, int t0, int T, int E, int K, int renorm,
+                                             int *__restrict__ top_idx, float *__restrict__ top_w)
 {
-    __shared__ float p[256];
+    const int PS = route_pitch(E);
+    float *s_mx = p + TW * PS, *s_inv = s_mx + TW, *s_v = s_inv + TW;
+    int *s_i = reinterpret_cast<int *>(s_v + 16 * TW);
+    const int tid = threadIdx.x;
+    for (int q = tid; q < 16 * TW; q += blockDim.x) { s_v[q] = -1e30f; s_i[q] = -1; }
+    if (tid < TW) {
+        const float *pt = p + tid * PS;
+        float mx = pt[0];
+        for (int j = 1; j < E; j++) if (pt[j] > mx) mx = pt[j];
+        s_mx[tid] = mx;
+    }
+    __syncthreads();
+    for (int q = tid; q < TW * E; q += blockDim.x) {
+        const int tw = q / E, j = q - tw * E;
+        p[tw * PS + j] = expf_cr(p[tw * PS + j] - s_mx[tw]);
+    }
+    __syncthreads();
+    if (tid < TW) {
+        const float *pt = p + tid * PS;
+        float sum = 0.0f;                        // sequential, as CE:624
+        for (int j = 0; j < E; j++) sum += pt[j];
+        s_inv[tid] = 1.0f / (sum + 1e-10f);
+    }
+    __syncthreads();
+    for (int q = tid; q < TW * E; q += blockDim.x) {
+        const int tw = q / E, j = q - tw * E;
+        p[tw * PS + j] *= s_inv[tw];
+    }
+    __syncthreads();
+    for (int q = tid; q < TW * E; q += blockDim.x) {
+        const int tw = q / E, j = q - tw * E;
+        const float *pt = p + tw * PS;
+        const float v = pt[j];
+        if (v != v) continue;                    // NaN: never inserted
+        int r = 0;
+        for (int jj = 0; jj < E; jj++) {
+            const float u = pt[jj];
+            r += (u > v) || (u == v && jj < j);
+        }
+        if (r < K) { s_v[tw * 16 + r] = v; s_i[tw * 16 + r] = j; }
+    }
+    __syncthreads();
+    if (tid >= TW || t0 + tid >= T) return;
+    const int t = t0 + tid;
+    float r = 1.0f;
+    if (renorm) {
+        float sw = 0.0f;
+        for (int k = 0; k < K; k++) sw += s_v[tid * 16 + k];
+        r = 1.0f / (sw + 1e-10f);
+    }
+    for (int k = 0; k < K; k++) {
+        top_idx[(long)t * K + k] = s_i[tid * 16 + k];
+        top_w[(long)t * K + k] = renorm ? s_v[tid * 16 + k] * r : s_v[tid * 16 + k];
+    }
+}
+
+// Router layout for routing: element (i, e) of the [E][N] router (row e =
+// expert e's weights over the N inputs) sits at ((i/4)*E + e)*4 + i%4 --
+// four consecutive inputs of one expert are 16 contiguous bytes, and a run
+// of rows is one contiguous block.  Rows from N up to a multiple of 32 are 0.
+constexpr int kRouteRowPad = 32;
+
+__global__ void k_router_pack(const float *__restrict__ router, int N, int E, float *__restrict__ out)
+{
+    const long n4 = (long)((N + kRouteRowPad - 1) / kRouteRowPad) * (kRouteRowPad / 4) * E;
+    const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n4) return;
+    const int i4 = (int)(q / E), e = (int)(q - (long)i4 * E);
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = 4 * i4 + j;
+        v[j] = i < N ? router[(long)e * N + i] : 0.0f;
+    }
+    reinterpret_cast<float4 *>(out)[q] = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Routing logits: logit[t][e] is a sequential fp32 FMA chain over i = 0..N-1
+// (CE:614-618 compiles to scalar vfmadd231ss).  Thread (g, e) of a workgroup,
+// g < G token groups of TT tokens, runs the TT chains of expert e for its
+// group's tokens side by side (independent chains overlap their latency).
+// The workgroup streams KC-row chunks of the packed router (contiguous) and
+// of its TW = G*TT tokens' x (as [token][KC+4]) through two LDS buffers,
+// loading chunk c+1 into registers while chunk c is consumed.  Rows run to
+// N rounded up to 32: the router's pad rows are zero and so is x there, and
+// fma(0, 0, d) == d, so every chunk is whole 32-step batches.  A lane reads
+// four steps of its chain with one ds_read_b128 (router lanes contiguous, x
+// a broadcast), 16 steps per batch, two register sets so the next batch's
+// reads are in flight during this batch's FMAs.  x slots use a power-of-two
+// row pitch 2^lgq >= KC/4 so a slot's (token, column) is a shift and a mask.
+// Needs N % 4 == 0, KC % 32 == 0, KC*E/4 <= 256*PF and TW << lgq <= 256*XS,
+// and route_slack(E) floats of LDS past the two buffers.
+__host__ __device__ constexpr int route_slack(int E) { return 16 * E + 16; }
+template <int TT, int PF, int XS>
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_p, const float *__restrict__ x,
+                                               int T, int N, int E, int K, int renorm, int KC, int G, int lgq,
+                                               int *__restrict__ top_idx, float *__restrict__ top_w)
+{
+    extern __shared__ float4 lds4[];
+    float *lds = reinterpret_cast<float *>(lds4);
+    const int TW = G * TT, KCR = KC + 4;
+    const int per = KC * E + TW * KCR;           // floats per buffer (multiple of 4)
+    const int NP = (N + kRouteRowPad - 1) / kRouteRowPad * kRouteRowPad;
+    const int t0 = blockIdx.x * TW;
+    const int tid = threadIdx.x;
+    const int g = tid / E, e = tid - g * E;
+    const int nch = (NP + KC - 1) / KC;
+    const int qmask = (1 << lgq) - 1;
+    float4 pr[PF], px[XS];
+
+    auto load_chunk = [&](int c) {
+        const int i0 = c * KC, kq = min(KC, NP - i0) >> 2, kv = min(KC, N - i0) >> 2;
+        const float4 *src = reinterpret_cast<const float4 *>(router_p + (long)i0 * E);
+        const int nr4 = kq * E;
+#pragma unroll
+        for (int s = 0; s < PF; s++) {
+            const int j = tid + s * 256;
+            if (j < nr4) pr[s] = gld<float4>(src + j);
+        }
+#pragma unroll
+        for (int s = 0; s < XS; s++) {
+            const int q = tid + s * 256, tw = q >> lgq, ii = q & qmask;
+            px[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (tw < TW && ii < kv && t0 + tw < T) px[s] = gld<float4>(x + (long)(t0 + tw) * N + i0 + 4 * ii);
+        }
+    };
+    auto store_chunk = [&](int c) {
+        float4 *rb = lds4 + (c & 1) * (per >> 2), *xb = rb + ((KC * E) >> 2);
+        const int kq = min(KC, NP - c * KC) >> 2;
+        const int nr4 = kq * E;
+#pragma unroll
+        for (int s = 0; s < PF; s++) {
+            const int j = tid + s * 256;
+            if (j < nr4) rb[j] = pr[s];
+        }
+#pragma unroll
+        for (int s = 0; s < XS; s++) {
+            const int q = tid + s * 256, tw = q >> lgq, ii = q & qmask;
+            if (tw < TW && ii < kq) xb[tw * (KCR >> 2) + ii] = px[s];
+        }
+    };
+
+    float dot[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) dot[tt] = 0.0f;
+    load_chunk(0);
+    store_chunk(0);
+    for (int c = 0; c < nch; c++) {
+        if (c + 1 < nch) load_chunk(c + 1);
+        __syncthreads();                         // chunk c stored by every thread
+        const int kc = min(KC, NP - c * KC);     // multiple of 32
+        if (g < G) {
+            const float *rr = lds + (c & 1) * per + 4 * e;           // + (i/4)*4E
+            const float *xr = lds + (c & 1) * per + KC * E + g * TT * KCR;
+            auto ldb = [&](int i0, float4(&r)[4], float4(&xx)[TT][4]) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    r[q] = *reinterpret_cast<const float4 *>(rr + (i0 + 4 * q) * E);
+#pragma unroll
+                    for (int tt = 0; tt < TT; tt++) xx[tt][q] = *reinterpret_cast<const float4 *>(xr + tt * KCR + i0 + 4 * q);
+                }
+            };
+            auto fmb = [&](const float4(&r)[4], const float4(&xx)[TT][4]) {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+#pragma unroll
+                    for (int tt = 0; tt < TT; tt++) {
+                        dot[tt] = fmaf(xx[tt][q].x, r[q].x, dot[tt]);
+                        dot[tt] = fmaf(xx[tt][q].y, r[q].y, dot[tt]);
+                        dot[tt] = fmaf(xx[tt][q].z, r[q].z, dot[tt]);
+                        dot[tt] = fmaf(xx[tt][q].w, r[q].w, dot[tt]);
+                    }
+            };
+            // The read of batch i0 + 32 after the last batch is not used; it stays
+            // inside the allocation (route_slack(E) floats past the two buffers).
+            float4 ra[4], rb2[4], xa[TT][4], xb2[TT][4];
+            ldb(0, ra, xa);
+            // Scheduling barriers keep each batch's reads issued ahead of the
+            // previous batch's FMAs (the scheduler would sink them to their uses).
+            for (int i0 = 0; i0 < kc; i0 += 32) {
+                ldb(i0 + 16, rb2, xb2);
+                __builtin_amdgcn_sched_barrier(0);
+                fmb(ra, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                ldb(i0 + 32, ra, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                fmb(rb2, xb2);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // buffer (c+1)&1 was last read in iteration c-1, before this iteration's barrier
+        if (c + 1 < nch) store_chunk(c + 1);
+    }
+    __syncthreads();                             // every chain done: LDS reused for the logits
+    float *p = lds;
+    if (g < G)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) p[(g * TT + tt) * route_pitch(E) + e] = dot[tt];
+    __syncthreads();
+    route_finish(p, TW, t0, T, E, K, renorm, top_idx, top_w);
+}
+
+// Any N: one workgroup per token reading the packed router straight from
+// global memory, same chain order.
+__global__ __launch_bounds__(256) void k_route_any(const float *__restrict__ router_p, const float *__restrict__ x,
+                                                   int T, int N, int E, int K, int renorm,
+                                                   int *__restrict__ top_idx, float *__restrict__ top_w)
+{
+    __shared__ float p[route_finish_floats(1, 256)];
     const int t = blockIdx.x, e = threadIdx.x;
-    const float *xt = x + (long)t * N;
     if (e < E) {
+        const float *xt = x + (long)t * N;
         float dot = 0.0f;
-        for (int i = 0; i < N; i++) dot = fmaf(xt[i], router_t[(long)i * E + e], dot);
+        for (int i = 0; i < N; i++) dot = fmaf(xt[i], router_p[((long)(i >> 2) * E + e) * 4 + (i & 3)], dot);
         p[e] = dot;
     }
     __syncthreads();
-    if (e != 0) return;
-    float mx = p[0];
-    for (int j = 1; j < E; j++) if (p[j] > mx) mx = p[j];
-    float sum = 0.0f;
-    for (int j = 0; j < E; j++) { p[j] = expf_cr(p[j] - mx); sum += p[j]; }
-    const float inv = 1.0f / (sum + 1e-10f);
-    for (int j = 0; j < E; j++) p[j] *= inv;
-    float tv[16];
-    int ti[16];
-    for (int k = 0; k < K; k++) { tv[k] = -1e30f; ti[k] = -1; }
-    for (int j = 0; j < E; j++) {
-        const float v = p[j];
-        for (int k = 0; k < K; k++) {
-            if (v > tv[k]) {
-                for (int k2 = K - 1; k2 > k; k2--) { tv[k2] = tv[k2 - 1]; ti[k2] = ti[k2 - 1]; }
-                tv[k] = v; ti[k] = j;
-                break;
-            }
-        }
-    }
-    if (renorm) {
-        float s = 0.0f;
-        for (int k = 0; k < K; k++) s += tv[k];
-        const float r = 1.0f / (s + 1e-10f);
-        for (int k = 0; k < K; k++) tv[k] *= r;
-    }
-    for (int k = 0; k < K; k++) { top_idx[(long)t * K + k] = ti[k]; top_w[(long)t * K + k] = tv[k]; }
+    route_finish(p, 1, t, T, E, K, renorm, top_idx, top_w);
 }
 
 // ---------------------------------------------------------------- MoE glue
@@ -242,13 +433,56 @@ hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t 
     return hipGetLastError();
 }
 
-hipError_t mllm_launch_route(const float *router_t, const float *x, int T, int N, int E, int K, int renorm,
+long mllm_router_packed_floats(int N, int E)
+{
+    return (long)((N + kRouteRowPad - 1) / kRouteRowPad) * kRouteRowPad * E;
+}
+
+hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out, hipStream_t st)
+{
+    if (N <= 0 || E <= 0) return hipErrorInvalidValue;
+    const long n4 = mllm_router_packed_floats(N, E) / 4;
+    hipLaunchKernelGGL(k_router_pack, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, router, N, E, out);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, hipStream_t st)
 {
-    if (E > 256 || K > 16 || K > E || T <= 0) return hipErrorInvalidValue;
-    const int threads = (E + 63) / 64 * 64;
-    hipLaunchKernelGGL(k_route, dim3(T), dim3(threads), 0, st, router_t, x, N, E, K, renorm, top_idx, top_w);
-    return hipGetLastError();
+    if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || T <= 0 || N <= 0) return hipErrorInvalidValue;
+    const bool vec = (N % 4) == 0 && ((uintptr_t)router_p % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    if (!vec) {
+        hipLaunchKernelGGL(k_route_any, dim3(T), dim3(256), 0, st, router_p, x, T, N, E, K, renorm, top_idx, top_w);
+        return hipGetLastError();
+    }
+    // T <= 8: a workgroup per token (latency).  More: token groups over the
+    // idle lanes and four tokens per thread.
+    auto go = [&](auto tt_c, auto pf_c, auto xs_c, int G) {
+        constexpr int TT = decltype(tt_c)::value, PF = decltype(pf_c)::value, XS = decltype(xs_c)::value;
+        const int TW = G * TT;
+        const int NP = (N + kRouteRowPad - 1) / kRouteRowPad * kRouteRowPad;
+        int KC = 4 * 256 * PF / E / 32 * 32;          // router slots fit
+        KC = KC < NP ? KC : NP;
+        int lgq = 0;
+        for (;;) {                                     // x slots fit
+            lgq = 0;
+            while ((1 << lgq) < KC / 4) lgq++;
+            if ((TW << lgq) <= 256 * XS || KC <= 32) break;
+            KC -= 32;
+        }
+        if (KC < 32 || (TW << lgq) > 256 * XS) return hipErrorInvalidValue;
+        const size_t fl = 2 * ((size_t)KC * E + (size_t)TW * (KC + 4)) + route_slack(E);
+        const size_t fin = (size_t)route_finish_floats(TW, E);
+        const size_t lds = (fl > fin ? fl : fin) * sizeof(float);
+        hipLaunchKernelGGL((k_route<TT, PF, XS>), dim3((T + TW - 1) / TW), dim3(256), lds, st, router_p, x, T, N, E,
+                           K, renorm, KC, G, lgq, top_idx, top_w);
+        return hipGetLastError();
+    };
+    using I = std::integral_constant<int, 1>;
+    if (T <= 8) return go(I{}, std::integral_constant<int, 16>{}, I{}, 1);
+    int G = 256 / E;
+    G = G > 8 ? 8 : G;
+    return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}, G);
 }
 
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st)

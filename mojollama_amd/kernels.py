@@ -106,6 +106,10 @@ def load_kernels(path=LIB_PATH):
     so.mllm_gemv.restype = ci
     so.mllm_quantize_q8_0.argtypes = [cvp, ci, ci, cvp, cvp]
     so.mllm_quantize_q8_0.restype = ci
+    so.mllm_router_packed_size.argtypes = [ci, ci]
+    so.mllm_router_packed_size.restype = ctypes.c_long
+    so.mllm_router_pack.argtypes = [cvp, ci, ci, cvp, cvp]
+    so.mllm_router_pack.restype = ci
     so.mllm_route.argtypes = [cvp, cvp, ci, ci, ci, ci, ci, cvp, cvp, cvp]
     so.mllm_route.restype = ci
     so.mllm_dequant.argtypes = [ci, cvp, ci, ci, cvp, cvp]
@@ -178,13 +182,24 @@ class DeviceOps:
                     "mllm_quantize_q8_0")
         return q8
 
-    def route(self, router_t, x, K, renorm):
+    def router_pack(self, router):
+        """fp32 router [E][N] (device) -> the routing layout (mllm_router_pack)."""
         torch = self.torch
-        N, E = router_t.shape
+        E, N = router.shape
+        out = torch.empty(self.so.mllm_router_packed_size(N, E) // 4, dtype=torch.float32, device=router.device)
+        self._check(self.so.mllm_router_pack(router.data_ptr(), N, E, out.data_ptr(), self._stream()),
+                    "mllm_router_pack")
+        return out
+
+    def route(self, router, x, K, renorm, packed=None):
+        """Top-K routing of x [T][N] by the fp32 router [E][N] (device)."""
+        torch = self.torch
+        E, N = router.shape
+        rp = self.router_pack(router) if packed is None else packed
         T = x.numel() // N
         idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
         w = torch.empty((T, K), dtype=torch.float32, device=x.device)
-        self._check(self.so.mllm_route(router_t.data_ptr(), x.data_ptr(), T, N, E, K, int(renorm), idx.data_ptr(),
+        self._check(self.so.mllm_route(rp.data_ptr(), x.data_ptr(), T, N, E, K, int(renorm), idx.data_ptr(),
                                        w.data_ptr(), self._stream()), "mllm_route")
         return idx, w
 
@@ -228,11 +243,11 @@ class MoELayer:
         self.gp = [ops.pack(sg, g, M, N) for g in gates]
         self.up = [ops.pack(su, u, M, N) for u in ups]
         self.dp = [ops.pack(sd, d, N, M) for d in downs] if sd >= 0 else [self.gp[0]] * E
-        self.router_t = router.t().contiguous()
+        self.router = router.contiguous()
         arr = ctypes.c_void_p * E
         self.h = ops.so.mllm_moe_prepare(qts[0], qts[1], qts[2], N, M, E, K,
                                          arr(*[t.data_ptr() for t in self.gp]), arr(*[t.data_ptr() for t in self.up]),
-                                         arr(*[t.data_ptr() for t in self.dp]), self.router_t.data_ptr(), int(renorm))
+                                         arr(*[t.data_ptr() for t in self.dp]), self.router.data_ptr(), int(renorm))
         if not self.h:
             raise RuntimeError("mllm_moe_prepare failed")
         self._ws = None
@@ -240,7 +255,7 @@ class MoELayer:
     def workspace(self, T):
         n = self.ops.so.mllm_moe_workspace_size(self.h, T)
         if self._ws is None or self._ws.numel() < n:
-            self._ws = self.ops.torch.empty(n, dtype=self.ops.torch.uint8, device=self.router_t.device)
+            self._ws = self.ops.torch.empty(n, dtype=self.ops.torch.uint8, device=self.router.device)
         return self._ws
 
     def forward(self, x, out=None, idx=None, w=None):

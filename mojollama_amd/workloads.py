@@ -98,3 +98,29 @@ def skewed_tokens(rng, router_w, T, n_hot=8, frac=0.25):
     hot_tok = np.sort(rng.choice(T, size=int(T * frac), replace=False))
     x[hot_tok] += 16.0 * u
     return np.ascontiguousarray(x), np.ascontiguousarray(rw), hot, hot_tok
+
+
+def gen_weights_torch(gen, qt, n_rows, n_cols, device="cuda"):
+    """gen_weights' distributions drawn on the GPU with a torch Generator (for
+    the large benchmark tensors; the parity tests use the numpy generator)."""
+    import torch
+    be, bb = BLOCK[qt]
+    nb = n_rows * (n_cols // be)
+    blk = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=device, generator=gen)
+
+    def f16_scales(n):
+        return (torch.randn(n, device=device, generator=gen).abs() * 0.01).half().view(torch.uint8).view(n, 2)
+    if qt == QT_Q8_0:
+        blk[:, 0:2] = f16_scales(nb)
+        blk[:, 2:] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
+    elif qt in (QT_Q4_0, QT_Q5_0):
+        blk[:, 0:2] = f16_scales(nb)
+    elif qt in (QT_Q4_1, QT_Q4_K, QT_Q5_K):
+        blk[:, 0:2] = f16_scales(nb)
+        blk[:, 2:4] = f16_scales(nb)
+    elif qt == QT_Q6_K:
+        blk[:, 192:208] = torch.randint(-32, 32, (nb, 16), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
+        blk[:, 208:210] = f16_scales(nb)
+    elif qt == QT_MXFP4:
+        blk[:, 16] = (127 + torch.randint(-8, 1, (nb,), device=device, generator=gen)).to(torch.uint8)
+    return blk.reshape(-1)

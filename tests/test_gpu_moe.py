@@ -93,15 +93,18 @@ def test_golden_route_selection_bitexact(lib, golden, tag):
     assert O.norm_err(ffn, g["ffn"]) < MOE_TOL
 
 
-@pytest.mark.parametrize("E,N,Kk,renorm", [(32, 2880, 4, 0), (128, 2048, 8, 1), (8, 256, 2, 0)])
-def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm):
+@pytest.mark.parametrize("T", [3, 300])
+@pytest.mark.parametrize("E,N,Kk,renorm", [(32, 2880, 4, 0), (128, 2048, 8, 1), (8, 256, 2, 0), (256, 512, 16, 1),
+                                           (6, 250, 2, 1), (36, 2884, 4, 0), (30, 1000, 3, 0)])
+def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm, T):
+    """Both streamed variants (T <= 8, token groups), the any-shape fallback
+    (N not a multiple of 4) and a ragged last chunk (N % 8 == 4)."""
     import torch
-    rng = np.random.default_rng(E + N)
-    T = 300
+    rng = np.random.default_rng(E + N + T)
     rw = W.gen_router(rng, E, N)
     x = W.gen_x(rng, T, N)
     ri, rwt = orc.route(rw, x, Kk, renorm)
-    idx, wt = dev.route(torch.from_numpy(np.ascontiguousarray(rw.T)).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
+    idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
     assert np.array_equal(idx.cpu().numpy(), ri)
     assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
 
@@ -232,3 +235,40 @@ def test_moe_layer_qwen3_shape_skewed(dev, orc):
     """Qwen3-30B-A3B expert shapes (N = 2048, M = 768, Q4_K/Q6_K, top-8 renormalised), skewed routing."""
     got, ref = _moe_case(dev, orc, (12, 12, 14), N=2048, M=768, E=32, Kk=8, T=40, renorm=1, seed=5, skew=True)
     assert O.norm_err(got, ref) < MOE_TOL
+
+
+@pytest.mark.parametrize("E,N", [(32, 2880), (5, 9)])
+def test_router_pack_layout(dev, E, N):
+    """mllm_router_pack: element (i, e) at ((i/4)*E + e)*4 + i%4, rows from N up
+    to a multiple of 32 zero."""
+    import torch
+    rng = np.random.default_rng(N)
+    rw = W.gen_router(rng, E, N)
+    got = dev.router_pack(torch.from_numpy(rw).cuda()).cpu().numpy()
+    N4 = (N + 31) // 32 * 32
+    want = np.zeros((N4, E), np.float32)
+    want[:N] = rw.T
+    want = want.reshape(N4 // 4, 4, E).transpose(0, 2, 1).reshape(-1)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("T", [2, 40])
+@pytest.mark.parametrize("renorm", [0, 1])
+def test_device_route_exact_ties(dev, orc, T, renorm):
+    """Experts with identical router rows have bit-identical probabilities; the
+    reference's strict '>' insertion keeps the lower index first, and so must
+    the device routing."""
+    import torch
+    rng = np.random.default_rng(11 + T)
+    E, N, Kk = 32, 512, 4
+    rw = W.gen_router(rng, E, N)
+    rw[3] *= 6.0
+    rw[7] = rw[3]
+    rw[20] = rw[3]
+    rw[9] = rw[1]
+    x = W.gen_x(rng, T, N)
+    ri, rwt = orc.route(rw, x, Kk, renorm)
+    assert any((1 in r and 9 in r) or (3 in r and 7 in r) for r in ri.tolist()), "fixture lost its ties"
+    idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6

@@ -350,7 +350,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (Q4_K/Q6_K weights decoded in registers, fp32 FMA accumulate)",
+        "dtype": "f32 (fp32 activations as three int8 digit planes, int32 dot4 per 16-weight run, fp32 scales and accumulation)",
         "data": "synthetic (BASELINE.json distributions, seeded)",
         "config": {"workload": "configs[1] TinyLlama-1.1B Q4_K_M matmul set (22 layers + lm_head), decode B=1, "
                                "*_batch_matmul semantics, qkv and gate/up fused per layer (89 launches per pass)",

@@ -181,7 +181,9 @@ MLLM_DEV uint32_t ilv_bit4(uint32_t bits, int e0)
     return ((v & 1u) << 4) | ((v & 4u) << 10) | ((v & 16u) << 16) | ((v & 64u) << 22);
 }
 
-template <int SEM>
+// SIGNED_Q8: Q8_0 codes are left as the signed quant bytes (bias 0) instead of
+// q + 128, for the integer-dot GEMV.
+template <int SEM, bool SIGNED_Q8 = false>
 MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
 {
     constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
@@ -192,8 +194,9 @@ MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
     if constexpr (SEM == SEM_Q8_0) {
         // CE:216-253 / QK:376-416: w = d*q; u = q + 128
         const uint32_t Bv[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t flip = SIGNED_Q8 ? 0u : 0x80808080u;
 #pragma unroll
-        for (int j = 0; j < 4; j++) { k.U[j] = A[j] ^ 0x80808080u; k.U[4 + j] = Bv[j] ^ 0x80808080u; }
+        for (int j = 0; j < 4; j++) { k.U[j] = A[j] ^ flip; k.U[4 + j] = Bv[j] ^ flip; }
         k.s0 = k.s1 = h2f(r.d);
         k.x0 = 32 * blk; k.x1 = k.x0 + 16;
     } else if constexpr (SEM == SEM_Q4_0 || SEM == SEM_Q4_1) {

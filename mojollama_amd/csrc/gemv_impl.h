@@ -5,14 +5,14 @@
 // of "jobs" (expert matrices picked through a device-side index array, as the
 // MoE layer needs).  The path is HBM-bound, so the kernel is built around the
 // weight stream:
-//   * a workgroup (4 wave64s) first copies its activations into LDS (padded by
-//     16 bytes every 256 so the lanes' 16-float reads fall in distinct banks),
-//     tiling K when B*K does not fit in 48 KB;
+//   * a workgroup (4 wave64s) first stages its activations into LDS, tiling
+//     K when B*K does not fit in 48 KB;
 //   * a wave owns R rows per group of LPR lanes; the lanes of a group walk the
 //     row's 32-weight chunks, so one wave-wide load reads consecutive 16-byte
 //     pieces of a row; a lane issues the loads of all R rows before decoding;
-//   * chunks decode to byte codes converted with v_cvt_f32_ubyte and are
-//     accumulated in fp32 (per-run scale and offset applied once per run);
+//   * fp32 activations are staged as three int8 digit planes per 16-element
+//     group (see "activation digits"), so a run of 16 byte codes costs 12
+//     v_dot4_i32_i8 and the per-run scale and offset are applied once in fp32;
 //   * lane groups reduce with DPP row operations and two cross-row swaps.
 #pragma once
 #include <algorithm>
@@ -46,116 +46,242 @@ MLLM_DEV void resolve_job(const mllm_gemv_args &a, int job, mllm_packed &W)
     }
 }
 
-// padded LDS index of tile-relative element i
-MLLM_DEV int xpad(int i) { return i + ((i >> 6) << 2); }
+// ---------------------------------------------------------------- activation digits
+//
+// fp32-activation semantics run their dot products on integers.  Each
+// 16-element group of x is written as P * (d0 + d1/2^7 + d2/2^14) with P a
+// power of two (P >= max|x|/126, so |d0| <= 127) and d1, d2 in [-64, 64]:
+// all of it exact in fp32 except the discarded remainder, below 2^-15 of P,
+// i.e. within ~5e-7 of the group's largest element.  A run of 16 weight codes
+// u then dots each digit plane with v_dot4_i32_i8 (exact in int32), and
+//   sum_i (s*(u_i - bias) + o) * x_i = s*P*(I0 + I1/2^7 + I2/2^14) + (o - s*bias) * sum_i x_i.
+// LDS per token: three digit planes of PL = KT + KT/16 bytes (16 bytes of
+// padding per 256, so the lanes' 16-byte reads spread over the banks), then
+// a float2 record (P, sum x) per group.  Digit bytes are stored in the
+// format's code order (byte t of word j holds element code_pos(j, t)), so a
+// code word and a digit word line up byte for byte.  A group holding an inf
+// or NaN gets P = NaN: every row then falls to the per-element path below
+// and comes out NaN.
+MLLM_DEV int dpad(int i) { return i + ((i >> 8) << 4); }
 
-// Copy x[b][k0 .. k0+kn) for b < B into LDS (stride xs floats per token).
-MLLM_DEV void stage_x(float *lds, int xs, const float *__restrict__ x, int ldx, int B, int k0, int kn)
+struct digit_geom {
+    int PL;        // bytes per digit plane
+    int tstride;   // bytes per token (16-byte multiple)
+};
+
+__host__ __device__ inline digit_geom digit_geom_for(int KT)
 {
-    const int tid = threadIdx.x;
-    if ((ldx & 3) == 0) {
-        const int n4 = kn >> 2;
-        for (int i = tid; i < B * n4; i += blockDim.x) {
-            const int b = i / n4, e = (i - b * n4) << 2;
-            const float4 v = gld<float4>(x + (long)b * ldx + k0 + e);
-            *reinterpret_cast<float4 *>(lds + b * xs + xpad(e)) = v;
-        }
-    } else {
-        for (int i = tid; i < B * kn; i += blockDim.x) {
-            const int b = i / kn, e = i - b * kn;
-            lds[b * xs + xpad(e)] = gld<float>(x + (long)b * ldx + k0 + e);
-        }
-    }
+    digit_geom g;
+    g.PL = KT + (KT >> 4);
+    g.tstride = (3 * g.PL + 8 * (KT >> 4) + 15) & ~15;
+    return g;
 }
 
-MLLM_DEV void lds_run16(const float *p, float v[16])
+// Staging is split in two so that a workgroup can issue its activation loads
+// ahead of its first weight loads (loads complete in order, so x then does
+// not wait behind the weights) and turn them into digits while the weights
+// are in flight.  Each thread takes half-groups of 8 elements (kStageSlots
+// per pass); the two halves of a group sit in adjacent lanes and exchange
+// their max and sum over DPP.
+constexpr int kStageSlots = 4;
+
+struct x_stage {
+    float4 v[kStageSlots][2];
+};
+
+MLLM_DEV void stage_load(x_stage &st, const float *__restrict__ x, int ldx, int B, int k0, int kn, int pass)
 {
+    const int nh = kn >> 3;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float4 f = reinterpret_cast<const float4 *>(p)[q];
-        v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+    for (int q = 0; q < kStageSlots; q++) {
+        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
+        if (idx < B * nh) {
+            const int b = idx / nh, h = idx - b * nh;
+            const float *src = x + (long)b * ldx + k0 + 8 * h;
+            if ((ldx & 3) == 0) {
+                st.v[q][0] = gld<float4>(src);
+                st.v[q][1] = gld<float4>(src + 4);
+            } else {
+                st.v[q][0] = make_float4(gld<float>(src), gld<float>(src + 1), gld<float>(src + 2), gld<float>(src + 3));
+                st.v[q][1] = make_float4(gld<float>(src + 4), gld<float>(src + 5), gld<float>(src + 6), gld<float>(src + 7));
+            }
+        }
     }
 }
 
-MLLM_DEV float sum16(const float v[16])
+// Value of the partner lane (lane ^ 1).
+MLLM_DEV float lane_pair(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); }
+
+// Byte 0 of a, b, c, d packed into one word (a lowest).
+MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 {
-    float a = (v[0] + v[1]) + (v[2] + v[3]), b = (v[4] + v[5]) + (v[6] + v[7]);
-    float c = (v[8] + v[9]) + (v[10] + v[11]), d = (v[12] + v[13]) + (v[14] + v[15]);
-    return (a + b) + (c + d);
+    const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // [a0, b0, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x04000c0cu);   // [0, 0, c0, d0]
+    return lo | hi;
 }
 
-// sum over one run of u_i * x_i; U points at the run's four code words
 template <int SEM>
-MLLM_DEV float run_dot(const uint32_t *U, const float xv[16])
+MLLM_DEV void stage_store(const x_stage &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass)
 {
-    float p0 = 0.f, p1 = 0.f;
+    const int nh = kn >> 3;
+    constexpr float M = 12582912.0f;   // 1.5 * 2^23: t = y + M holds rne(y) in its low mantissa bits
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int q = 0; q < kStageSlots; q++) {
+        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
+        if (idx >= B * nh) continue;       // B * nh is even: both halves of a group take the same path
+        const int b = idx / nh, h = idx - b * nh, g = h >> 1, half = h & 1;
+        const float v[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
+                            st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
+        float m = 0.0f, sum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const float u = ubyte_f(U[j], t);
-            if (t & 1) p1 = fmaf(u, xv[code_pos<SEM>(j, t)], p1);
-            else p0 = fmaf(u, xv[code_pos<SEM>(j, t)], p0);
+        for (int e = 0; e < 8; e++) { m = fmaxf(m, fabsf(v[e])); sum += v[e]; }
+        m = fmaxf(m, lane_pair(m));
+        sum += lane_pair(sum);
+        const bool bad = !isfinite(sum);
+        // P = 2^E with |x| / P < 64: E from m's exponent field
+        const int E = (int)((__float_as_uint(m) >> 23) & 0xFF) - 132;
+        uint32_t t[3][8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float y = ldexpf(v[e], -E);          // exact (|y| < 64)
+            const float t0 = y + M, r0 = y - (t0 - M);
+            const float t1 = fmaf(r0, 128.0f, M), r1 = fmaf(r0, 128.0f, M - t1);
+            const float t2 = fmaf(r1, 128.0f, M);
+            t[0][e] = __float_as_uint(t0); t[1][e] = __float_as_uint(t1); t[2][e] = __float_as_uint(t2);
         }
-    return p0 + p1;
+        // this half's 8 elements are words 2*half, 2*half+1 of the group
+        uint8_t *tb = lds + b * dg.tstride;
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            // word jj of this half holds, in both code orders, its elements code_pos(jj, 0..3)
+            uint32_t w[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+                w[jj] = pack_b0(t[p][code_pos<SEM>(jj, 0)], t[p][code_pos<SEM>(jj, 1)], t[p][code_pos<SEM>(jj, 2)],
+                                t[p][code_pos<SEM>(jj, 3)]);
+            *reinterpret_cast<uint2 *>(tb + p * dg.PL + dpad(16 * g) + 8 * half) = make_uint2(w[0], w[1]);
+        }
+        if (half == 0) {
+            const float P = bad ? __int_as_float(0x7FC00000) : ldexpf(1.0f, E);
+            reinterpret_cast<float2 *>(tb + 3 * dg.PL)[g] = make_float2(P, bad ? P : sum);
+        }
+    }
+}
+
+// Stage tokens b < B, elements [k0, k0+kn), as digits; load_first = a pass-0
+// load already issued by the caller.
+template <int SEM>
+MLLM_DEV void stage_digits(x_stage &st, bool load_first, uint8_t *lds, const digit_geom &dg,
+                           const float *__restrict__ x, int ldx, int B, int k0, int kn)
+{
+    const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
+    for (int pass = 0; pass < passes; pass++) {
+        if (pass || !load_first) stage_load(st, x, ldx, B, k0, kn, pass);
+        stage_store<SEM>(st, lds, dg, B, kn, pass);
+    }
+}
+
+// The digit words of the run starting at tile-relative element e.
+struct run_digits {
+    uint32_t w[3][4];
+    float P, sum;
+};
+
+MLLM_DEV void load_run(const uint8_t *tb, const digit_geom &dg, int e, run_digits &r)
+{
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(tb + p * dg.PL + dpad(e));
+        r.w[p][0] = q.x; r.w[p][1] = q.y; r.w[p][2] = q.z; r.w[p][3] = q.w;
+    }
+    const float2 rec = reinterpret_cast<const float2 *>(tb + 3 * dg.PL)[e >> 4];
+    r.P = rec.x;
+    r.sum = rec.y;
+}
+
+template <int SEM> constexpr int digit_bias() { return SEM == SEM_Q8_0 ? 0 : sem_traits<SEM>::kBias; }
+
+// Code t of word U as a value (Q8_0 codes are signed bytes here).
+template <int SEM>
+MLLM_DEV float code_f(uint32_t U, int t)
+{
+    if constexpr (SEM == SEM_Q8_0) return (float)(int8_t)((U >> (8 * t)) & 0xFF);
+    else return ubyte_f(U, t);
+}
+
+// sum over one run of u_i * x_i in units of P: I0 + I1/2^7 + I2/2^14.
+MLLM_DEV float run_idot(const uint32_t *U, const run_digits &x)
+{
+    int I[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        int acc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot4((int)U[j], (int)x.w[p][j], acc, false);
+        I[p] = acc;
+    }
+    return fmaf((float)I[2], 0x1p-14f, fmaf((float)I[1], 0x1p-7f, (float)I[0]));
 }
 
 // Contribution of one decoded chunk to one token.
 template <int SEM>
-MLLM_DEV float chunk_value(const chunk_codes &k, const float x0[16], const float x1[16], float sx0, float sx1)
+MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run_digits &x1)
 {
-    constexpr float bias = (float)sem_traits<SEM>::kBias;
-    constexpr bool need_sum = sem_traits<SEM>::kBias != 0 || sem_traits<SEM>::kOffset;
-    float t = fmaf(k.s0, run_dot<SEM>(k.U, x0), k.s1 * run_dot<SEM>(k.U + 4, x1));
-    if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), sx0, fmaf(fmaf(-k.s1, bias, k.o1), sx1, t));
+    constexpr int ibias = digit_bias<SEM>();
+    constexpr float bias = (float)ibias;
+    constexpr bool need_sum = ibias != 0 || sem_traits<SEM>::kOffset;
+    float t = fmaf(k.s0 * x0.P, run_idot(k.U, x0), (k.s1 * x1.P) * run_idot(k.U + 4, x1));
+    if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), x0.sum, fmaf(fmaf(-k.s1, bias, k.o1), x1.sum, t));
     if (!isfinite(t)) {
-        // inf/NaN somewhere (scale or activation): weigh each element as the reference
-        // does (w = s*q first), so that a zero code times an infinite scale gives NaN.
+        // inf/NaN somewhere (scale, activation or an overflowing partial): weigh each
+        // element as the reference does (w = s*q first, then w*x), x rebuilt from its digits.
         t = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float w0 = fmaf(k.s0, ubyte_f(k.U[j], q) - bias, k.o0);
-                const float w1 = fmaf(k.s1, ubyte_f(k.U[4 + j], q) - bias, k.o1);
-                t = fmaf(w0, x0[code_pos<SEM>(j, q)], t);
-                t = fmaf(w1, x1[code_pos<SEM>(j, q)], t);
+                const float w0 = fmaf(k.s0, code_f<SEM>(k.U[j], q) - bias, k.o0);
+                const float w1 = fmaf(k.s1, code_f<SEM>(k.U[4 + j], q) - bias, k.o1);
+                const float e0 = fmaf((float)(int8_t)(x0.w[2][j] >> (8 * q)), 0x1p-14f,
+                                      fmaf((float)(int8_t)(x0.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x0.w[0][j] >> (8 * q))));
+                const float e1 = fmaf((float)(int8_t)(x1.w[2][j] >> (8 * q)), 0x1p-14f,
+                                      fmaf((float)(int8_t)(x1.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x1.w[0][j] >> (8 * q))));
+                t = fmaf(w0, x0.P * e0, t);
+                t = fmaf(w1, x1.P * e1, t);
             }
     }
     return t;
 }
 
-// Add chunk c of R rows (already fetched into raw) to acc, activations from
-// LDS (tile starting at element k0, token stride xs floats).
+// Add chunk c of R rows (already fetched into raw) to acc, activation digits
+// from LDS (tile starting at element k0).
 template <int SEM, int BM, int R>
-MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const float *xl, int xs, int k0, int B, float (&acc)[R][BM])
+MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const uint8_t *xl, const digit_geom &dg, int k0, int B,
+                         float (&acc)[R][BM])
 {
-    constexpr bool need_sum = sem_traits<SEM>::kBias != 0 || sem_traits<SEM>::kOffset;
     chunk_codes k;
     if constexpr (BM == 1) {
-        // activations once per chunk, reused by the R rows
-        codes<SEM>(raw[0], c, k);
-        float xv0[16], xv1[16];
-        lds_run16(xl + xpad(k.x0 - k0), xv0);
-        lds_run16(xl + xpad(k.x1 - k0), xv1);
-        const float sx0 = need_sum ? sum16(xv0) : 0.f, sx1 = need_sum ? sum16(xv1) : 0.f;
+        // activation digits once per chunk, reused by the R rows
+        codes<SEM, true>(raw[0], c, k);
+        run_digits x0, x1;
+        load_run(xl, dg, k.x0 - k0, x0);
+        load_run(xl, dg, k.x1 - k0, x1);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            if (r) codes<SEM>(raw[r], c, k);
-            acc[r][0] += chunk_value<SEM>(k, xv0, xv1, sx0, sx1);
+            if (r) codes<SEM, true>(raw[r], c, k);
+            acc[r][0] += chunk_value<SEM>(k, x0, x1);
         }
     } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            codes<SEM>(raw[r], c, k);
+            codes<SEM, true>(raw[r], c, k);
 #pragma unroll
             for (int b = 0; b < BM; b++) {
                 if (b < B) {
-                    float xv0[16], xv1[16];
-                    lds_run16(xl + b * xs + xpad(k.x0 - k0), xv0);
-                    lds_run16(xl + b * xs + xpad(k.x1 - k0), xv1);
-                    const float sx0 = need_sum ? sum16(xv0) : 0.f, sx1 = need_sum ? sum16(xv1) : 0.f;
-                    acc[r][b] += chunk_value<SEM>(k, xv0, xv1, sx0, sx1);
+                    run_digits x0, x1;
+                    load_run(xl + b * dg.tstride, dg, k.x0 - k0, x0);
+                    load_run(xl + b * dg.tstride, dg, k.x1 - k0, x1);
+                    acc[r][b] += chunk_value<SEM>(k, x0, x1);
                 }
             }
         }
@@ -166,7 +292,8 @@ MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const float *xl, int 
 template <int SEM, int BM, int R, int LPR>
 __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
 {
-    extern __shared__ float xl[];
+    extern __shared__ uint4 xl4[];
+    uint8_t *xl = reinterpret_cast<uint8_t *>(xl4);
     constexpr int BE = sem_traits<SEM>::kBlockElems, CPB = sem_traits<SEM>::kChunksPerBlock;
     const int job = blockIdx.y;
     mllm_packed W;
@@ -180,7 +307,8 @@ __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
     const int nb = a.n_cols / BE;
     const int kused = nb * BE;
     const int B = a.B;
-    const int KT = a.k_tile, xs = KT + (KT >> 4);
+    const int KT = a.k_tile;
+    const digit_geom dg = digit_geom_for(KT);
 
     float acc[R][BM];
 #pragma unroll
@@ -191,14 +319,15 @@ __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
     for (int k0 = 0; k0 < kused; k0 += KT) {
         const int kn = min(KT, kused - k0);
         if (k0) __syncthreads();
-        stage_x(xl, xs, x, a.ldx, B, k0, kn);
+        x_stage xst;
+        stage_digits<SEM>(xst, false, xl, dg, x, a.ldx, B, k0, kn);
         __syncthreads();
         const int c_end = (k0 + kn) / BE * CPB;
         for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
             raw_chunk raw[R];
 #pragma unroll
             for (int r = 0; r < R; r++) fetch<SEM>(W, nb, min(row0 + r, a.n_rows - 1), c, raw[r]);
-            accumulate<SEM, BM, R>(raw, c, xl, xs, k0, B, acc);
+            accumulate<SEM, BM, R>(raw, c, xl, dg, k0, B, acc);
         }
     }
 #pragma unroll
@@ -348,13 +477,13 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     const int wstride = gridDim.x * 4;
     const int rg0 = blockIdx.x * 4 + wave;
     const int B = a.B;
-    // LDS geometry (whole K staged): fp32 x, or the Q8_0 pack
+    // LDS geometry (whole K staged): activation digits, or the Q8_0 pack
     const int KT = (kused + 255) / 256 * 256;
-    const int xs = KT + (KT >> 4);
+    const digit_geom dg = digit_geom_for(KT);
     const int qstride = KT + (KT >> 4), tstride = qstride / 4 + 2 * (KT / 32);
 
     // A step is (row group rg, chunk pass it); the next step advances it, then rg.
-    auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) {
+    auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) __attribute__((always_inline)) {
         const int c = min(it * LPR + sl, nch - 1);
         const int r0 = rg * RPW + grp * R;
 #pragma unroll
@@ -368,7 +497,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
-    auto run_step = [&](int rg, int it, const raw_chunk (&buf)[R]) {
+    auto run_step = [&](int rg, int it, const raw_chunk (&buf)[R]) __attribute__((always_inline)) {
         // a lane past the row's last chunk recomputes the last one and discards it
         const int c = min(it * LPR + sl, nch - 1);
         const bool live = it * LPR + sl < nch;
@@ -378,7 +507,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 #pragma unroll
             for (int b = 0; b < BM; b++) part[r][b] = 0.0f;
         if constexpr (Q8) accumulate_q8<SEM, BM, R>(buf, c, xl, tstride, qstride, KT, 0, B, part);
-        else accumulate<SEM, BM, R>(buf, c, xl, xs, 0, B, part);
+        else accumulate<SEM, BM, R>(buf, c, reinterpret_cast<const uint8_t *>(xl), dg, 0, B, part);
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -396,7 +525,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             }
         }
     };
-    auto advance = [&](int &rg, int &it) {
+    auto advance = [&](int &rg, int &it) __attribute__((always_inline)) {
         if (++it == iters) { it = 0; rg += wstride; }
     };
 
@@ -405,12 +534,17 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     // for the older buffer instead of draining all loads.
     raw_chunk bufA[R], bufB[R];
     int rg = rg0, it = 0;
-    fetch_step(min(rg, nrg - 1), it, bufA);
     if constexpr (Q8) {
+        fetch_step(min(rg, nrg - 1), it, bufA);
         stage_q8(xl, a.xq, job * a.x_job_stride, job * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride, 0,
                  kused);
     } else {
-        stage_x(xl, xs, a.x + job * a.x_job_stride, a.ldx, B, 0, kused);
+        // activation loads first, then the weights; the digits are computed while the weights are in flight
+        x_stage xst;
+        const float *xj = a.x + job * a.x_job_stride;
+        stage_load(xst, xj, a.ldx, B, 0, kused, 0);
+        fetch_step(min(rg, nrg - 1), it, bufA);
+        stage_digits<SEM>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, a.ldx, B, 0, kused);
     }
     __syncthreads();
     if (rg >= nrg) return;
@@ -514,18 +648,25 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
     const int kused = a.n_cols / BE * BE;
     const int nch = kused / BE * CPB;
-    constexpr int R = (BM <= 2) ? 4 : 2;
-    // lanes per row: enough chunks per lane to keep every lane busy on short rows
+    // Batch 1: one row per lane group and 16-32 lanes per row (3-6 chunks per
+    // lane) measured fastest on MI355X across the TinyLlama/GPT-OSS shapes;
+    // larger batches reuse each chunk's decode over R rows x B tokens.
+    constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
     auto waste = [&](int lpr) { int it = (nch + lpr - 1) / lpr; return (double)(it * lpr - nch) / (it * lpr); };
     int lpr = 64;
-    if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;
-    if (nch < 32 || (lpr == 32 && waste(32) > waste(16) + 0.05)) lpr = 16;
+    if (BM == 1) {
+        lpr = nch <= 96 ? 16 : nch <= 192 ? 32 : 64;
+    } else {
+        // lanes per row: enough chunks per lane to keep every lane busy on short rows
+        if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;
+        if (nch < 32 || (lpr == 32 && waste(32) > waste(16) + 0.05)) lpr = 16;
+    }
     const int rows_per_wg = 4 * (64 / lpr) * R;
     const int wg_needed = (a.n_rows + rows_per_wg - 1) / rows_per_wg;
 
     // whole-K staging for the persistent kernel
     const int ktp = (kused + 255) / 256 * 256;
-    const size_t lds_p = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * (ktp + ktp / 16) * 4;
+    const size_t lds_p = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
     if (lds_p <= kPersistentLds) {
         const int per_cu = lds_p <= 40 * 1024 ? 3 : 2;
         const int wgs = std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs)));
@@ -536,11 +677,12 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
         return;
     }
     // K tiled through 48 KB of LDS
-    int kt = Q8 ? (kLdsFloats * 4 * 4 / (BM * 5 * 4 + BM)) / 256 * 256 : (kLdsFloats / BM) / 256 * 256;
+    // digits: 3.6875 bytes per element and token (3 planes + 1/16 padding each + 8-byte record per 16)
+    int kt = Q8 ? (kLdsFloats * 4 * 4 / (BM * 5 * 4 + BM)) / 256 * 256 : (kLdsFloats * 4 * 16 / (BM * 59)) / 256 * 256;
     if (kt > kused) kt = (kused + 255) / 256 * 256;
     if (kt < 256) kt = 256;
     a.k_tile = kt;
-    const size_t lds = Q8 ? (size_t)BM * (kt + kt / 16 + 8 * (kt / 32)) : (size_t)BM * (kt + kt / 16) * 4;
+    const size_t lds = Q8 ? (size_t)BM * (kt + kt / 16 + 8 * (kt / 32)) : (size_t)BM * digit_geom_for(kt).tstride;
     dim3 grid(wg_needed, n_jobs);
     if constexpr (Q8) {
         if (lpr == 64) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 64>), grid, dim3(256), lds, st, a);

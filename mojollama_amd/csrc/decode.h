@@ -84,6 +84,12 @@ template <int SEM> struct sem_traits {
     // weights carry an offset term o (Q4_1 min, K-quant mins) besides the bias
     static constexpr bool kOffset = (SEM == SEM_Q4_1 || SEM == SEM_Q4_K_GGML || SEM == SEM_Q5_K_GGML ||
                                      SEM == SEM_Q5_K_CE);
+    // raw GGUF bytes per 32 weights (rounded), for launch-shape choices
+    static constexpr int kBytesPer32 = (SEM == SEM_Q8_0) ? 34 : (SEM == SEM_Q4_1) ? 20 :
+                                       (SEM == SEM_Q5_0_F32 || SEM == SEM_Q5_0_Q8 || SEM == SEM_Q5_K_GGML ||
+                                        SEM == SEM_Q5_K_CE) ? 22 :
+                                       (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB || SEM == SEM_Q6_K_SEQ) ? 26 :
+                                       (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP || SEM == SEM_MXFP4_Q8) ? 17 : 18;
 };
 
 // Element offset (0..15) within its run of byte t of code word U[j].

@@ -648,14 +648,16 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
     const int kused = a.n_cols / BE * BE;
     const int nch = kused / BE * CPB;
-    // Batch 1: one row per lane group and 16-32 lanes per row (3-6 chunks per
-    // lane) measured fastest on MI355X across the TinyLlama/GPT-OSS shapes;
-    // larger batches reuse each chunk's decode over R rows x B tokens.
+    // Batch 1: one row per lane group, 16 lanes per row up to ~1.8 KB of row
+    // bytes and 32 up to ~5 KB, measured fastest on MI355X across the
+    // TinyLlama/GPT-OSS shapes; larger batches reuse each chunk's decode over
+    // R rows x B tokens.
     constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
     auto waste = [&](int lpr) { int it = (nch + lpr - 1) / lpr; return (double)(it * lpr - nch) / (it * lpr); };
     int lpr = 64;
     if (BM == 1) {
-        lpr = nch <= 96 ? 16 : nch <= 192 ? 32 : 64;
+        const long row_bytes = (long)kused / 32 * sem_traits<SEM>::kBytesPer32;
+        lpr = row_bytes <= 1800 ? 16 : row_bytes <= 5000 ? 32 : 64;
     } else {
         // lanes per row: enough chunks per lane to keep every lane busy on short rows
         if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;

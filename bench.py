@@ -161,7 +161,8 @@ def bench_prefill(torch, dev, args):
         for M in (128, 512, 1280):
             x = torch.randn(M, C, device="cuda", generator=gen).bfloat16().float()
             o = torch.empty(M, R, device="cuda")
-            ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o), max(5, args.steps), args.warmup)
+            ws = dev.workspace(sem, C, M, x.device, R)
+            ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o, ws=ws), max(5, args.steps), args.warmup)
             flops = 2.0 * R * C * M
             out[f"{name}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
                                    "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}

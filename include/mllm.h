@@ -108,8 +108,9 @@ MLLM_API long mllm_packed_size(int sem, int n_rows, int n_cols);
 MLLM_API int mllm_pack(int sem, const void *raw_dev, void *packed_dev, int n_rows, int n_cols, void *stream);
 
 /* out[b][r] = row r of W applied to x[b], b < B (any B), under semantic `sem`.
- * Q8_0-activation semantics need `workspace` of mllm_gemv_workspace_size bytes. */
-MLLM_API long mllm_gemv_workspace_size(int sem, int n_cols, int B);
+ * Q8_0-activation semantics, and B > 8 (run as an MFMA GEMM over split bf16
+ * activation planes), need `workspace` of mllm_gemv_workspace_size bytes. */
+MLLM_API long mllm_gemv_workspace_size(int sem, int n_rows, int n_cols, int B);
 MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
                        int B, void *workspace, void *stream);
 

@@ -282,6 +282,24 @@ xq_bufs xq_carve(void *base, long T, int n_cols)
     return b;
 }
 
+// The GEMM's activation mode for a semantic.
+int gemm_xmode(int sem) { return sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_PLANES; }
+
+// B > 8 tokens run the MFMA GEMM; fp32-activation semantics then need split planes.
+bool uses_planes(int sem, int B) { return B > 8 && mllm_qgemm_supported(sem) && gemm_xmode(sem) == XM_PLANES; }
+size_t planes_bytes(int sem, long rows, int n_cols)
+{
+    return align256((size_t)act_nplanes(sem) * act_planes_elems(rows, n_cols) * 2) + align256(rows * 4);
+}
+
+// Scratch of run_gemv: Q8_0 activation pack, split planes, split-K partials.
+size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
+{
+    const bool gemm = B > 8 && mllm_qgemm_supported(sem);
+    return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0) +
+           (gemm ? align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4) : 0);
+}
+
 // Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data.
 int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_rows, int n_cols, int B,
              void *scratch, hipStream_t st)
@@ -296,12 +314,21 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
         // prefill / batched: quantised-weight MFMA GEMM over the B tokens
         qgemm_args g{};
         g.W = W;
-        g.x = x; g.ldx = n_cols;
         if (q8) g.xq = {xb.q, xb.d, xb.s4, xb.sq};
+        if (uses_planes(sem, B)) {
+            uint8_t *pb = (uint8_t *)scratch + (q8 ? xq_bytes(B, n_cols) : 0);
+            const long pe = act_planes_elems(B, n_cols);
+            int *lo_nz = (int *)(pb + align256((size_t)act_nplanes(sem) * pe * 2));
+            HIP_OK(mllm_launch_act_split(x, n_cols, B, n_cols, act_nplanes(sem), (__bf16 *)pb, pe, lo_nz, st));
+            g.xp = {(const __bf16 *)pb, pe, act_planes_ld(n_cols), lo_nz};
+        }
         g.out = out; g.ldo = n_rows;
         g.n_rows = n_rows; g.n_cols = n_cols; g.n_entries = B;
-        const int xm = sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_F32;
-        HIP_OK(mllm_launch_qgemm(sem, xm, false, g, 0, st));
+        g.ksplit = mllm_qgemm_ksplit(sem, n_rows, n_cols, B);
+        if (g.ksplit > 1)
+            g.part = (float *)((uint8_t *)scratch + (q8 ? xq_bytes(B, n_cols) : 0) +
+                               (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0));
+        HIP_OK(mllm_launch_qgemm(sem, gemm_xmode(sem), false, g, 0, st));
         return 0;
     }
     for (int b0 = 0; b0 < B; b0 += 8) {
@@ -332,7 +359,7 @@ int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows,
     if (get_weight(W, ly, n_rows, n_cols, view)) return -1;
     const size_t xbytes = (size_t)B * n_cols * 4, obytes = (size_t)B * n_rows * 4;
     if (c.d_in.ensure(xbytes) || c.d_out.ensure(obytes) || c.h_in.ensure(xbytes) || c.h_out.ensure(obytes) ||
-        c.d_scr.ensure(xq_bytes(B, n_cols))) {
+        c.d_scr.ensure(gemv_scratch_bytes(sem, n_rows, n_cols, B))) {
         set_error("staging allocation failed");
         return -1;
     }
@@ -626,9 +653,9 @@ MLLM_API int mllm_pack(int sem, const void *raw_dev, void *packed_dev, int n_row
     return 0;
 }
 
-MLLM_API long mllm_gemv_workspace_size(int sem, int n_cols, int B)
+MLLM_API long mllm_gemv_workspace_size(int sem, int n_rows, int n_cols, int B)
 {
-    return mllm_sem_uses_q8(sem) ? (long)xq_bytes(B, n_cols) : 0;
+    return (long)gemv_scratch_bytes(sem, n_rows, n_cols, B);
 }
 
 MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
@@ -636,7 +663,7 @@ MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, floa
 {
     if (sem < 0 || sem >= SEM_COUNT) { set_error("mllm_gemv: bad semantic %d", sem); return -1; }
     if (((uintptr_t)x_dev & 15) || ((uintptr_t)packed_dev & 255)) { set_error("mllm_gemv: misaligned pointer"); return -1; }
-    if (mllm_sem_uses_q8(sem) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
+    if (gemv_scratch_bytes(sem, n_rows, n_cols, B) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
     mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
     return run_gemv(sem, view, x_dev, out_dev, n_rows, n_cols, B, workspace, (hipStream_t)stream);
 }

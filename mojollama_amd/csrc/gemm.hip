@@ -8,16 +8,17 @@
 // NA bf16 planes (w = w0 + w1 + w2, each plane the bf16 rounding of what the
 // previous ones leave; three planes carry all 24 bits of a float); the
 // activations into NB planes.  v_mfma_f32_16x16x32_bf16 accumulates the
-// products wi*bj with i + j <= 2 in fp32, i.e. every term down to 2^-16 of
-// the leading one.  Operands exact in one bf16 use one plane: MXFP4 weights
-// (int4 times a power of two) and Q8_0 quants; their partners then get
-// three, which makes those products exact to fp32.  Everything else uses
-// two planes each (normalised error ~1e-5).
+// products wi*bj in fp32.  Operands exact in one bf16 use one plane: MXFP4
+// weights (int4 times a power of two) and Q8_0 quants; their partners then
+// get three, which makes those products exact to fp32.  Everything else uses
+// two planes each and the three leading products (normalised error ~5e-6).
 //
 // Tiling.  Workgroup = 4 wave64s, tile TN (128, or 64 when gate and up share
 // it) rows x 64 entries, K staged KE columns at a time; a wave owns 32 rows
 // x (64 or 32) entries = 2 x JT MFMA 16x16 outputs.  LDS rows are padded by
-// 16 bytes so the 16 lanes reading one k-slice hit distinct banks.
+// 16 bytes so the 16 lanes reading one k-slice hit distinct banks.  Global
+// loads run two K-steps ahead of the MFMAs (register double buffer).
+#include <algorithm>
 #include "decode.h"
 #include "gemm.h"
 
@@ -26,17 +27,30 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int TM = 64;   // entries per tile
-
 template <int SEM, int XM> struct gemm_cfg {
     static constexpr bool A4 = (SEM == SEM_Q4_K_Q8);
     static constexpr bool WEXACT = (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP || SEM == SEM_MXFP4_Q8);
     static constexpr int NA = WEXACT ? 1 : (A4 ? 3 : 2);
-    static constexpr int NB = (XM == XM_Q8) ? 1 : (NA == 1 ? 3 : 2);
+    static constexpr int NB = (XM == XM_Q8) ? 1 : (XM == XM_PLANES && !WEXACT) ? 2 : 3;
     // K columns per step: A4 keeps only the 32 columns its dot reads of each 64
     static constexpr int KS = 64;
     static constexpr int KE = A4 ? 32 : 64;
     static constexpr int LDA = KE + 8;
+    // products w_i * b_j taken: i + j <= MAXT.  Two planes each: the three leading
+    // terms (the dropped w1*b1 is ~2^-16 of the product, below the two-plane
+    // truncation itself).  One exact plane against three, or three against
+    // exact quants: all three.
+    static constexpr int MAXT = (NA == 2 && NB == 2) ? 1 : 2;
+};
+
+// Tile of TN weight rows x TM_ entries; 4 waves in a WR x WE grid, each owning
+// IT x JT MFMA 16x16 outputs.
+template <bool DUAL, int TM_> struct tile_cfg {
+    static constexpr int TN = DUAL ? 64 : 128;
+    static constexpr int WR = (TN == 128 && TM_ == 64) ? 4 : 2;
+    static constexpr int WE = 4 / WR;
+    static constexpr int IT = TN / WR / 16;
+    static constexpr int JT = TM_ / WE / 16;
 };
 
 MLLM_DEV void put16(__bf16 *dst, const float (&v)[16])
@@ -91,23 +105,87 @@ MLLM_DEV void chunk_weights(const raw_chunk &raw, int c, float (&w0)[16], float 
     x1 = k.x1;
 }
 
-// Stage weight rows [n0, n0+TN_) x the step's columns into LDS planes
-// (plane p at A + p*TN_*LDA).  For Q4_K_Q8 also each row's dmin.
+// ---------------------------------------------------------------- staging
+//
+// A K-step's operands are fetched from global memory into registers two
+// steps ahead of their use (fetch_*), then decoded, split into bf16 planes and
+// stored to LDS (put_*).  Every fetch is issued unconditionally -- indices past
+// the matrix are clamped to valid ones and put_* writes zeros for them -- so
+// the number of loads in flight is the same on every path and the compiler's
+// waits cover only the older step.
+
+// Weight tasks per row and step: Q4_K_Q8 one chunk; MXFP4_Q8 two 32-blocks;
+// otherwise the two chunks covering the 64 columns, or four for the ggml
+// Q6_K orders whose chunks put their two runs 64 columns apart.
+template <int SEM, int XM> struct wtask {
+    static constexpr bool SPLIT = (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB);
+    static constexpr int NT = gemm_cfg<SEM, XM>::A4 ? 1 : (SEM == SEM_MXFP4_Q8) ? 2 : SPLIT ? 4 : 2;
+};
+
+template <int SEM, int XM, int TN_> struct wraw {
+    static constexpr int WT = (TN_ * wtask<SEM, XM>::NT + 255) / 256;
+    raw_chunk r[WT];
+};
+
+// Row, chunk index and validity of task t (t may exceed the task count: clamped, invalid).
 template <int SEM, int XM, int TN_>
-MLLM_DEV void stage_weights(const mllm_packed &W, int n_rows, int nb, int n0, int k0, __bf16 *A, float *dmin_l)
+MLLM_DEV void wtask_at(int t, int n_rows, int nb, int n0, int k0, int &rr, int &sub, int &row, int &c, bool &valid)
+{
+    using C = gemm_cfg<SEM, XM>;
+    constexpr int NT = wtask<SEM, XM>::NT, NTOT = TN_ * NT;
+    valid = t < NTOT;
+    t = min(t, NTOT - 1);
+    rr = t / NT;
+    sub = t % NT;
+    row = min(n0 + rr, n_rows - 1);
+    if constexpr (C::A4) {
+        c = k0 / 64;
+    } else if constexpr (SEM == SEM_MXFP4_Q8) {
+        c = k0 / 32 + sub;
+        if (c >= nb) { valid = false; c = nb - 1; }
+    } else {
+        constexpr int CPB = sem_traits<SEM>::kChunksPerBlock, BE = sem_traits<SEM>::kBlockElems;
+        const int q = (k0 % 256) / 64;
+        if constexpr (BE == 256) {
+            c = (k0 / 256) * CPB + (wtask<SEM, XM>::SPLIT ? 4 * (q >> 1) + sub : 2 * q + sub);
+        } else {
+            c = k0 / 32 + sub;
+            if (c >= nb) { valid = false; c = nb - 1; }   // past the last block of an odd block count
+        }
+    }
+}
+
+template <int SEM, int XM, int TN_>
+MLLM_DEV void fetch_w(const mllm_packed &W, int n_rows, int nb, int n0, int k0, wraw<SEM, XM, TN_> &wr)
+{
+#pragma unroll
+    for (int i = 0; i < wraw<SEM, XM, TN_>::WT; i++) {
+        int rr, sub, row, c;
+        bool valid;
+        wtask_at<SEM, XM, TN_>(threadIdx.x + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
+        if constexpr (mllm_sem_uses_q8(SEM)) q8_fetch<SEM>(W, nb, row, c, wr.r[i]);
+        else fetch<SEM>(W, nb, row, c, wr.r[i]);
+    }
+}
+
+// Decode the fetched weight tasks into LDS planes (plane p at A + p*TN_*LDA);
+// for Q4_K_Q8 also each row's dmin.
+template <int SEM, int XM, int TN_>
+MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, int k0, __bf16 *A, float *dmin_l)
 {
     using C = gemm_cfg<SEM, XM>;
     constexpr int LDA = C::LDA, NA = C::NA, PS = TN_ * C::LDA;
-    const int tid = threadIdx.x;
-    if constexpr (C::A4) {
-        // dot_q4_k_q8_0 (QK:1647-1735): the integer term reads k < 16 of each 32-element sub-block;
-        // group g of a super-block holds sub-blocks 2g (low nibbles) and 2g+1 (high nibbles).
-        // Step columns: 0..15 = sub-block 2g, 16..31 = sub-block 2g+1, weight d*sc_j*nib.
-        if (tid < TN_) {
-            const int row = min(n0 + tid, n_rows - 1);
-            const int c = k0 / 64;
-            raw_chunk r;
-            q8_fetch<SEM>(W, nb, row, c, r);
+#pragma unroll
+    for (int i = 0; i < wraw<SEM, XM, TN_>::WT; i++) {
+        int rr, sub, row, c;
+        bool valid;
+        wtask_at<SEM, XM, TN_>(threadIdx.x + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
+        if (threadIdx.x + 256 * i >= TN_ * wtask<SEM, XM>::NT) continue;   // clamped duplicate
+        const raw_chunk &r = wr.r[i];
+        if constexpr (C::A4) {
+            // dot_q4_k_q8_0 (QK:1647-1735): the integer term reads k < 16 of each 32-element
+            // sub-block; group g of a super-block holds sub-blocks 2g (low nibbles) and 2g+1
+            // (high nibbles).  Step columns: 0..15 = sub-block 2g, 16..31 = 2g+1, w = d*sc_j*nib.
             const int g = c & 3;
             int s1, m1, s2, m2;
             kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
@@ -116,62 +194,41 @@ MLLM_DEV void stage_weights(const mllm_packed &W, int n_rows, int nb, int n0, in
             const uint32_t Aw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
             float lo[16], hi[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                lo[i] = ds1 * (float)((Aw[i >> 2] >> (8 * (i & 3))) & 15);
-                hi[i] = ds2 * (float)((Aw[i >> 2] >> (8 * (i & 3) + 4)) & 15);
+            for (int e = 0; e < 16; e++) {
+                lo[e] = ds1 * (float)((Aw[e >> 2] >> (8 * (e & 3))) & 15);
+                hi[e] = ds2 * (float)((Aw[e >> 2] >> (8 * (e & 3) + 4)) & 15);
             }
-            put16_planes<NA>(A, PS, tid * LDA, lo);
-            put16_planes<NA>(A, PS, tid * LDA + 16, hi);
-            if (dmin_l) dmin_l[tid] = h2f(r.m.x >> 16);
-        }
-    } else if constexpr (SEM == SEM_MXFP4_Q8) {
-        // mxfp4_row_dot_q8 (QK:629-678) with the token's Q8 scale moved to the activation side:
-        // w = sext4(n) * 2^(E-127), exact in bf16.
-        for (int t = tid; t < TN_ * 2; t += blockDim.x) {
-            const int rr = t >> 1, cc = t & 1;
-            const int row = min(n0 + rr, n_rows - 1);
-            const int c = k0 / 32 + cc;
+            put16_planes<NA>(A, PS, rr * LDA, lo);
+            put16_planes<NA>(A, PS, rr * LDA + 16, hi);
+            if (dmin_l) dmin_l[rr] = h2f(r.m.x >> 16);
+        } else if constexpr (SEM == SEM_MXFP4_Q8) {
+            // mxfp4_row_dot_q8 (QK:629-678) with the token's Q8 scale moved to the activation
+            // side: w = sext4(n) * 2^(E-127), exact in bf16.
             float v0[16], v1[16];
-            if (c < nb) {
-                raw_chunk r;
-                q8_fetch<SEM>(W, nb, row, c, r);
-                const float s = e8m0f(r.d);
+            if (valid) {
+                const float sc = e8m0f(r.d);
                 const uint32_t Aw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
                 for (int e = 0; e < 32; e++) {
                     const int n = (Aw[e >> 3] >> (4 * (e & 7))) & 15;
-                    const float w = (float)(n >= 8 ? n - 16 : n) * s;
+                    const float w = (float)(n >= 8 ? n - 16 : n) * sc;
                     if (e < 16) v0[e] = w; else v1[e - 16] = w;
                 }
-            } else {   // past the last block of an odd block count
+            } else {
                 zero16(v0); zero16(v1);
             }
-            put16_planes<NA>(A, PS, rr * LDA + 32 * cc, v0);
-            put16_planes<NA>(A, PS, rr * LDA + 32 * cc + 16, v1);
-        }
-    } else {
-        constexpr int CPB = sem_traits<SEM>::kChunksPerBlock, BE = sem_traits<SEM>::kBlockElems;
-        // Chunks touching columns [k0, k0+64): 32-element blocks -> two whole chunks; K-quants ->
-        // chunks 2q, 2q+1 of the super-block's quarter q, except the ggml Q6_K orders, whose chunks
-        // put their two runs 64 columns apart: four chunks, one run each.
-        constexpr bool SPLIT = (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB);
-        constexpr int NT = SPLIT ? 4 : 2;
-        const int q = (k0 % 256) / 64;
-        for (int t = tid; t < TN_ * NT; t += blockDim.x) {
-            const int rr = t / NT, sub = t % NT;
-            const int row = min(n0 + rr, n_rows - 1);
-            int c;
-            if constexpr (BE == 256) c = (k0 / 256) * CPB + (SPLIT ? 4 * (q >> 1) + sub : 2 * q + sub);
-            else c = k0 / 32 + sub;
-            if (BE == 32 && c >= nb) {   // past the last block of an odd block count: zero columns
+            put16_planes<NA>(A, PS, rr * LDA + 32 * sub, v0);
+            put16_planes<NA>(A, PS, rr * LDA + 32 * sub + 16, v1);
+        } else {
+            constexpr bool SPLIT = wtask<SEM, XM>::SPLIT;
+            if (!valid) {   // past the last block of an odd block count: zero columns
                 float z[16];
                 zero16(z);
                 put16_planes<NA>(A, PS, rr * LDA + 32 * sub, z);
                 put16_planes<NA>(A, PS, rr * LDA + 32 * sub + 16, z);
                 continue;
             }
-            raw_chunk r;
-            fetch<SEM>(W, nb, row, c, r);
+            const int q = (k0 % 256) / 64;
             float w0[16], w1[16];
             int x0, x1;
             chunk_weights<SEM>(r, c, w0, w1, x0, x1);
@@ -181,29 +238,72 @@ MLLM_DEV void stage_weights(const mllm_packed &W, int n_rows, int nb, int n0, in
     }
 }
 
-// Stage the activations of the tile's entries for the step into LDS planes
-// (plane p at Bp + p*TM*LDA).  Columns past kused stay zero.
-template <int SEM, int XM>
-MLLM_DEV void stage_acts(const qgemm_args &a, const int *ent_row, int n_ent, int k0, int kused, __bf16 *Bp,
-                         float *tsum_l)
+// Activation task of thread tid.  XM_PLANES: TM_/32 16-byte pieces per plane
+// (entry q/8, columns 8*(q%8) .. +8 of the step, q = tid + 256*i); Q4_K_Q8:
+// entry tid/2, part tid&1 (16 quants of one sub-block, k < 16); other Q8
+// forms: entry tid/4, 16 columns at (tid&3)*16.
+template <int TM_, int NB> struct araw {
+    static constexpr int NP = TM_ / 32;
+    uint4 p[NB][NP];
+    uint4 q;
+    float s0, s1;
+};
+
+template <int SEM, int XM, int TM_>
+MLLM_DEV void fetch_a(const qgemm_args &a, const int *ent_row, int n_ent, int k0, int kused,
+                      araw<TM_, gemm_cfg<SEM, XM>::NB> &ar)
 {
     using C = gemm_cfg<SEM, XM>;
-    constexpr int LDA = C::LDA, NB = C::NB, PS = TM * C::LDA;
     const int tid = threadIdx.x;
     const long nbk = a.n_cols / 32;
+    if constexpr (XM == XM_PLANES) {
+        // rows past n_ent read row ent_row[] = 0; their columns are never stored
+#pragma unroll
+        for (int i = 0; i < araw<TM_, C::NB>::NP; i++) {
+            const int q = tid + 256 * i, er = q >> 3, c8 = q & 7;
+            const __bf16 *src = a.xp.base + (long)ent_row[er] * a.xp.ldp + k0 + 8 * c8;
+#pragma unroll
+            for (int p = 0; p < C::NB; p++) ar.p[p][i] = gld<uint4>(reinterpret_cast<const uint4 *>(src + p * a.xp.plane));
+        }
+    } else if constexpr (C::A4) {
+        const int er = min(tid >> 1, TM_ - 1), part = tid & 1;
+        const long row = ent_row[min(er, n_ent - 1)];
+        ar.q = gld<uint4>(a.xq.q + row * (nbk * 32) + k0 + 32 * part);
+        ar.s0 = gld<float>(a.xq.s4 + row * nbk + k0 / 32);
+        ar.s1 = gld<float>(a.xq.s4 + row * nbk + k0 / 32 + 1);
+    } else {
+        const int er = min(tid >> 2, TM_ - 1), seg = min((tid & 3) * 16, kused - k0 - 16);
+        const long row = ent_row[min(er, n_ent - 1)];
+        ar.q = gld<uint4>(a.xq.q + row * (nbk * 32) + k0 + seg);
+        if constexpr (XM == XM_Q8D) ar.s0 = gld<float>(a.xq.d + row * nbk + (k0 + seg) / 32);
+    }
+}
+
+// Store the step's activation planes (plane p at Bp + p*TM_*LDA); Q8 columns past
+// kused and entries past n_ent are zero.
+template <int SEM, int XM, int TM_>
+MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k0, int kused, __bf16 *Bp,
+                    float *tsum_l)
+{
+    using C = gemm_cfg<SEM, XM>;
+    constexpr int LDA = C::LDA, NB = C::NB, PS = TM_ * C::LDA;
+    const int tid = threadIdx.x;
     float v[16];
-    if constexpr (C::A4) {
-        // columns 0..15: q8 of sub-block k0/32, k < 16; 16..31: sub-block k0/32 + 1, k < 16
-        if (tid < 2 * TM) {
+    if constexpr (XM == XM_PLANES) {
+#pragma unroll
+        for (int i = 0; i < araw<TM_, NB>::NP; i++) {
+            const int q = tid + 256 * i, er = q >> 3, c8 = q & 7;
+#pragma unroll
+            for (int p = 0; p < NB; p++) *reinterpret_cast<uint4 *>(Bp + p * PS + er * LDA + 8 * c8) = ar.p[p][i];
+        }
+    } else if constexpr (C::A4) {
+        if (tid < 2 * TM_) {
             const int er = tid >> 1, part = tid & 1;
             if (er < n_ent) {
-                const long row = ent_row[er];
-                const uint4 q = gld<uint4>(a.xq.q + row * (nbk * 32) + k0 + 32 * part);
-                const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+                const uint32_t Q[4] = {ar.q.x, ar.q.y, ar.q.z, ar.q.w};
 #pragma unroll
                 for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)((Q[i >> 2] >> (8 * (i & 3))) & 0xFF);
-                if (part == 0 && tsum_l)   // Q4_K min term of the step's two sub-blocks
-                    tsum_l[er] = gld<float>(a.xq.s4 + row * nbk + k0 / 32) + gld<float>(a.xq.s4 + row * nbk + k0 / 32 + 1);
+                if (part == 0 && tsum_l) tsum_l[er] = ar.s0 + ar.s1;   // Q4_K min term of the step's two sub-blocks
             } else {
                 zero16(v);
                 if (part == 0 && tsum_l) tsum_l[er] = 0.0f;
@@ -211,42 +311,29 @@ MLLM_DEV void stage_acts(const qgemm_args &a, const int *ent_row, int n_ent, int
             put16_planes<NB>(Bp, PS, er * LDA + 16 * part, v);
         }
     } else {
-        // 4 threads per entry row, 16 columns each
-        const int er = tid >> 2, seg = (tid & 3) * 16;
-        if (er < n_ent && k0 + seg < kused) {
-            const long row = ent_row[er];
-            if constexpr (XM == XM_F32) {
-                const float *src = a.x + row * a.ldx + k0 + seg;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 f = gld<float4>(src + 4 * q);
-                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-                }
-            } else {
-                const uint4 q = gld<uint4>(a.xq.q + row * (nbk * 32) + k0 + seg);
-                const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
-                float d8 = 1.0f;
-                if constexpr (XM == XM_Q8D) d8 = gld<float>(a.xq.d + row * nbk + (k0 + seg) / 32);
+        if (tid < 4 * TM_) {
+            const int er = tid >> 2, seg = (tid & 3) * 16;
+            if (er < n_ent && k0 + seg < kused) {
+                const uint32_t Q[4] = {ar.q.x, ar.q.y, ar.q.z, ar.q.w};
+                const float d8 = (XM == XM_Q8D) ? ar.s0 : 1.0f;
 #pragma unroll
                 for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)((Q[i >> 2] >> (8 * (i & 3))) & 0xFF) * d8;
+            } else {
+                zero16(v);
             }
-        } else {
-            zero16(v);
+            put16_planes<NB>(Bp, PS, er * LDA + seg, v);
         }
-        put16_planes<NB>(Bp, PS, er * LDA + seg, v);
     }
 }
 
-template <int SEM, int XM, bool DUAL>
-__global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
+template <int SEM, int XM, bool DUAL, int TM>
+__global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
 {
     using C = gemm_cfg<SEM, XM>;
-    constexpr int NA = C::NA, NB = C::NB, LDA = C::LDA, KE = C::KE, KS = C::KS;
+    using G = tile_cfg<DUAL, TM>;
+    constexpr int NA = C::NA, NB = C::NB, LDA = C::LDA, KE = C::KE, KS = C::KS, MAXT = C::MAXT;
     // 128 weight rows per tile, 64 when gate and up share the tile (LDS budget)
-    constexpr int TN = DUAL ? 64 : 128;
-    constexpr int RG = TN / 32;              // 32-row groups per tile
-    constexpr int EG = 4 / RG;               // entry groups
-    constexpr int JT = TM / 16 / EG;         // 16-entry MFMA tiles per wave
+    constexpr int TN = G::TN, IT = G::IT, JT = G::JT;
     __shared__ __attribute__((aligned(16))) __bf16 s_a[NA * TN * LDA];
     __shared__ __attribute__((aligned(16))) __bf16 s_u[DUAL ? NA * TN * LDA : 8];
     __shared__ __attribute__((aligned(16))) __bf16 s_b[NB * TM * LDA];
@@ -272,32 +359,60 @@ __global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
         if constexpr (DUAL) W2 = a.W2;
     }
     const int n_ent = p1 - p0;
+    if (n_ent <= 0) return;
     const int n0 = blockIdx.x * TN;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (tid < TM) s_row[tid] = tid < n_ent ? (a.row_of ? a.row_of[p0 + tid] : p0 + tid) : 0;
-    __syncthreads();
+    int lo_any = 0;   // some entry's activation is not bf16-exact: the lo plane takes part
+    if (tid < TM) {
+        const int row = tid < n_ent ? (a.row_of ? a.row_of[p0 + tid] : p0 + tid) : 0;
+        s_row[tid] = row;
+        if constexpr (XM == XM_PLANES) lo_any = tid < n_ent && a.xp.lo_nz[row] != 0;
+    }
+    lo_any = __syncthreads_or(lo_any);
 
     const int nb = a.n_cols / BE;
     const int kused = nb * BE;
-    const int wr0 = (wave % RG) * 32, we0 = (wave / RG) * 16 * JT;
-    f32x4 acc[2][JT], acc2[DUAL ? 2 : 1][DUAL ? JT : 1];
+    const int nsteps = (kused + KS - 1) / KS;
+    // K steps of this workgroup: all, or split z of a.ksplit
+    int s_beg = 0, s_end = nsteps;
+    if (a.ksplit > 1) {
+        const int spp = (nsteps + a.ksplit - 1) / a.ksplit;
+        s_beg = min(nsteps, (int)blockIdx.z * spp);
+        s_end = min(nsteps, s_beg + spp);
+    }
+    const int wr0 = (wave % G::WR) * 16 * IT, we0 = (wave / G::WR) * 16 * JT;
+    f32x4 acc[IT][JT], acc2[DUAL ? IT : 1][DUAL ? JT : 1];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < IT; i++)
 #pragma unroll
         for (int j = 0; j < JT; j++) acc[i][j] = f32x4{0, 0, 0, 0};
     if constexpr (DUAL) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < IT; i++)
 #pragma unroll
             for (int j = 0; j < JT; j++) acc2[i][j] = f32x4{0, 0, 0, 0};
     }
+    // activation planes past the first all zero: their products are skipped (uniform per workgroup)
+    const int pb_end = (XM == XM_PLANES && !lo_any) ? 1 : NB;
     const int li = lane & 15, lk = (lane >> 4) * 8;
 
-    for (int k0 = 0; k0 < kused; k0 += KS) {
-        stage_weights<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr);
-        if constexpr (DUAL) stage_weights<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr);
-        stage_acts<SEM, XM>(a, s_row, n_ent, k0, kused, s_b, C::A4 ? s_tsum : nullptr);
-        __syncthreads();
+    struct stepbuf {
+        wraw<SEM, XM, TN> w, u;
+        araw<TM, NB> x;
+    };
+    auto fetch_step = [&](int s, stepbuf &b) __attribute__((always_inline)) {
+        const int k0 = min(s, s_end - 1) * KS;   // past the end: refetch the last step (unused)
+        fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w);
+        if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u);
+        fetch_a<SEM, XM, TM>(a, s_row, n_ent, k0, kused, b.x);
+    };
+    auto put_step = [&](int s, const stepbuf &b) __attribute__((always_inline)) {
+        const int k0 = s * KS;
+        put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr);
+        if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr);
+        put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, C::A4 ? s_tsum : nullptr);
+    };
+    auto mfma_step = [&]() __attribute__((always_inline)) {
         // MFMA 16x16x32: lane l supplies row/entry (l % 16), k = 8*(l/16) .. +8 of a 32-wide slice
 #pragma unroll
         for (int ks = 0; ks < KE; ks += 32) {
@@ -308,29 +423,29 @@ __global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
                 for (int j = 0; j < JT; j++)
                     bv[p][j] = *reinterpret_cast<const bf16x8 *>(s_b + p * TM * LDA + (we0 + 16 * j + li) * LDA + ks + lk);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int ar = (wr0 + 16 * i + li) * LDA + ks + lk;
+            for (int i = 0; i < IT; i++) {
+                const int ar_ = (wr0 + 16 * i + li) * LDA + ks + lk;
                 bf16x8 av[NA];
 #pragma unroll
-                for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_a + p * TN * LDA + ar);
+                for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_a + p * TN * LDA + ar_);
 #pragma unroll
                 for (int j = 0; j < JT; j++)
 #pragma unroll
                     for (int pa = 0; pa < NA; pa++)
 #pragma unroll
                         for (int pb = 0; pb < NB; pb++)
-                            if (pa + pb <= 2)
+                            if (pa + pb <= MAXT && pb < pb_end)
                                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc[i][j], 0, 0, 0);
                 if constexpr (DUAL) {
 #pragma unroll
-                    for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_u + p * TN * LDA + ar);
+                    for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_u + p * TN * LDA + ar_);
 #pragma unroll
                     for (int j = 0; j < JT; j++)
 #pragma unroll
                         for (int pa = 0; pa < NA; pa++)
 #pragma unroll
                             for (int pb = 0; pb < NB; pb++)
-                                if (pa + pb <= 2)
+                                if (pa + pb <= MAXT && pb < pb_end)
                                     acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc2[i][j], 0, 0, 0);
                 }
             }
@@ -339,7 +454,7 @@ __global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
             // min term: acc[row][ent] -= dmin[row] * (d8-weighted q8 sums of the step's two sub-blocks).
             // D layout of a 16x16 output: lane l holds entry (l % 16), rows 4*(l/16) .. +3.
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < IT; i++)
 #pragma unroll
                 for (int j = 0; j < JT; j++) {
                     const float ts = s_tsum[we0 + 16 * j + li];
@@ -351,12 +466,37 @@ __global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
                     }
                 }
         }
+    };
+
+    // two steps in flight: buffer A holds steps s_beg, s_beg+2, ..., B the others
+    if (s_beg < s_end) {
+        stepbuf bA, bB;
+        fetch_step(s_beg, bA);
+        fetch_step(s_beg + 1, bB);
+        put_step(s_beg, bA);
         __syncthreads();
+        for (int s = s_beg;; s += 2) {
+            fetch_step(s + 2, bA);
+            mfma_step();
+            __syncthreads();
+            if (s + 1 >= s_end) break;
+            put_step(s + 1, bB);
+            __syncthreads();
+            fetch_step(s + 3, bB);
+            mfma_step();
+            __syncthreads();
+            if (s + 2 >= s_end) break;
+            put_step(s + 2, bA);
+            __syncthreads();
+        }
     }
 
     // ---- epilogue
+    float *out = a.out;
+    long ldo = a.ldo;
+    if (a.ksplit > 1) { out = a.part + (long)blockIdx.z * a.n_entries * a.n_rows; ldo = a.n_rows; }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < IT; i++)
 #pragma unroll
         for (int j = 0; j < JT; j++) {
             const int ent = we0 + 16 * j + li;
@@ -373,47 +513,142 @@ __global__ __launch_bounds__(256) void k_qgemm(qgemm_args a)
                     if (a.clamp_silu) { g = g < -80.0f ? -80.0f : g; g = g > 80.0f ? 80.0f : g; }
                     r = (g / (1.0f + expf(-g))) * acc2[i][j][v];
                 }
-                a.out[orow * a.ldo + n] = r;
+                out[orow * ldo + n] = r;
             }
         }
 }
 
-template <int SEM, int XM, bool DUAL>
+// out[e][n] = sum over z < ks of part[z][e][n], in order.
+__global__ void k_ksum(const float *__restrict__ part, int ks, long plane, int n_rows, float *__restrict__ out, int ldo)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= plane) return;
+    float v = part[i];
+    for (int z = 1; z < ks; z++) v += part[z * plane + i];
+    const long e = i / n_rows, n = i - e * n_rows;
+    out[e * ldo + n] = v;
+}
+
+template <int SEM, int XM, bool DUAL, int TM>
 hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
 {
-    constexpr int TN = DUAL ? 64 : 128;
-    dim3 grid((a.n_rows + TN - 1) / TN, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM);
+    constexpr int TN = tile_cfg<DUAL, TM>::TN;
+    const int ks = (a.ksplit > 1 && !DUAL && !a.tile_expert && !a.out_row) ? a.ksplit : 1;
+    dim3 grid((a.n_rows + TN - 1) / TN, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
     if (grid.y == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_qgemm<SEM, XM, DUAL>), grid, dim3(256), 0, st, a);
+    qgemm_args b = a;
+    b.ksplit = ks;
+    hipLaunchKernelGGL((k_qgemm<SEM, XM, DUAL, TM>), grid, dim3(256), 0, st, b);
+    if (ks > 1) {
+        const long plane = (long)a.n_entries * a.n_rows;
+        hipLaunchKernelGGL(k_ksum, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part, ks, plane,
+                           a.n_rows, a.out, a.ldo);
+    }
     return hipGetLastError();
 }
 
 } // namespace
 
+// Grouped (expert-tile) launches use the 64-entry tiles the bucketing makes;
+// dense split-plane launches take 128-entry tiles once there are enough
+// entries to fill them.
 hipError_t mllm_launch_qgemm(int sem, int xmode, bool dual, const qgemm_args &a, int max_tiles, hipStream_t st)
 {
-#define QG(S, X)                                                                      \
-    if (sem == S && xmode == X) return dual ? launch<S, X, true>(a, max_tiles, st)    \
-                                            : launch<S, X, false>(a, max_tiles, st);
-    QG(SEM_Q4_0, XM_F32)
-    QG(SEM_Q4_1, XM_F32)
-    QG(SEM_Q5_0_F32, XM_F32)
-    QG(SEM_Q8_0, XM_F32)
-    QG(SEM_Q4_K_GGML, XM_F32)
-    QG(SEM_Q5_K_GGML, XM_F32)
-    QG(SEM_Q5_K_CE, XM_F32)
-    QG(SEM_Q6_K_GGML, XM_F32)
-    QG(SEM_Q6_K_LOWNIB, XM_F32)
-    QG(SEM_Q6_K_SEQ, XM_F32)
-    QG(SEM_MXFP4, XM_F32)
-    QG(SEM_MXFP4_CLAMP, XM_F32)
-    QG(SEM_Q4_K_Q8, XM_Q8)
-    QG(SEM_MXFP4_Q8, XM_Q8D)
-#undef QG
+    const bool wide = !dual && !a.tile_expert && a.n_entries >= 512;
+#define QGP(S)                                                                        \
+    if (sem == S && xmode == XM_PLANES) {                                             \
+        if (dual) return launch<S, XM_PLANES, true, 64>(a, max_tiles, st);            \
+        return wide ? launch<S, XM_PLANES, false, 128>(a, max_tiles, st)              \
+                    : launch<S, XM_PLANES, false, 64>(a, max_tiles, st);              \
+    }
+#define QGQ(S, X)                                                                     \
+    if (sem == S && xmode == X) return dual ? launch<S, X, true, 64>(a, max_tiles, st) \
+                                            : launch<S, X, false, 64>(a, max_tiles, st);
+    QGP(SEM_Q4_0)
+    QGP(SEM_Q4_1)
+    QGP(SEM_Q5_0_F32)
+    QGP(SEM_Q8_0)
+    QGP(SEM_Q4_K_GGML)
+    QGP(SEM_Q5_K_GGML)
+    QGP(SEM_Q5_K_CE)
+    QGP(SEM_Q6_K_GGML)
+    QGP(SEM_Q6_K_LOWNIB)
+    QGP(SEM_Q6_K_SEQ)
+    QGP(SEM_MXFP4)
+    QGP(SEM_MXFP4_CLAMP)
+    QGQ(SEM_Q4_K_Q8, XM_Q8)
+    QGQ(SEM_MXFP4_Q8, XM_Q8D)
+#undef QGP
+#undef QGQ
     return hipErrorInvalidValue;
 }
 
 bool mllm_qgemm_supported(int sem)
 {
     return sem != SEM_F32 && sem != SEM_Q5_0_Q8;
+}
+
+// A dense launch with fewer output tiles than CUs is split along K towards
+// ~512 workgroups, each split keeping at least 16 K steps of 64 columns (the
+// partial sums cost an extra pass over ksplit x entries x rows floats, which
+// does not pay on a launch that already fills the GPU).
+int mllm_qgemm_ksplit(int sem, int n_rows, int n_cols, int n_entries)
+{
+    if (!mllm_qgemm_supported(sem) || n_entries <= 0) return 1;
+    const int tm = (n_entries >= 512 && sem != SEM_Q4_K_Q8 && sem != SEM_MXFP4_Q8) ? 128 : 64;
+    const long tiles = (long)((n_rows + 127) / 128) * ((n_entries + tm - 1) / tm);
+    if (tiles >= 256) return 1;
+    const int steps = (n_cols + 63) / 64;
+    int ks = (int)((512 + tiles - 1) / tiles);
+    ks = std::min(ks, std::max(1, steps / 16));
+    return std::max(1, std::min(ks, 16));
+}
+
+// fp32 rows -> NP bf16 planes (one workgroup per row, 8 columns per thread and
+// pass), zero padded to act_planes_ld(K); lo_nz[row] = a plane past the first
+// has a non-zero element.
+template <int NP>
+__global__ __launch_bounds__(256) void k_act_split(const float *__restrict__ x, int ldx, int K,
+                                                   __bf16 *__restrict__ base, long plane, int ldp, int *lo_nz)
+{
+    const int row = blockIdx.x;
+    const float *xr = x + (long)row * ldx;
+    __bf16 *pr = base + (long)row * ldp;
+    const bool vec = (ldx & 3) == 0 && (K & 7) == 0;
+    int nz = 0;
+    for (int k = 8 * threadIdx.x; k < ldp; k += 8 * blockDim.x) {
+        float v[8];
+        if (vec && k + 8 <= K) {
+            const float4 f0 = gld<float4>(xr + k), f1 = gld<float4>(xr + k + 4);
+            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w; v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = k + e < K ? xr[k + e] : 0.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            bf16x8 h;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                h[e] = (__bf16)v[e];
+                v[e] -= (float)h[e];
+                if (p) nz |= (float)h[e] != 0.0f;
+            }
+            *reinterpret_cast<bf16x8 *>(pr + p * plane + k) = h;
+        }
+    }
+    nz = __syncthreads_or(nz);
+    if (threadIdx.x == 0) lo_nz[row] = nz;
+}
+
+hipError_t mllm_launch_act_split(const float *x, int ldx, int rows, int K, int nplanes, __bf16 *base, long plane,
+                                 int *lo_nz, hipStream_t st)
+{
+    if (rows <= 0) return hipSuccess;
+    if (K <= 0 || ((uintptr_t)base & 15) || (plane & 7) || (nplanes != 2 && nplanes != 3)) return hipErrorInvalidValue;
+    if (nplanes == 2)
+        hipLaunchKernelGGL(k_act_split<2>, dim3(rows), dim3(256), 0, st, x, ldx, K, base, plane, act_planes_ld(K), lo_nz);
+    else
+        hipLaunchKernelGGL(k_act_split<3>, dim3(rows), dim3(256), 0, st, x, ldx, K, base, plane, act_planes_ld(K), lo_nz);
+    return hipGetLastError();
 }

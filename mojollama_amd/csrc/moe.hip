@@ -158,7 +158,7 @@ int sem_down_of(int qt)
 
 int xmode_of(int sem)
 {
-    return sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_F32;
+    return sem == SEM_Q4_K_Q8 ? XM_Q8 : sem == SEM_MXFP4_Q8 ? XM_Q8D : XM_PLANES;
 }
 
 } // namespace
@@ -174,6 +174,8 @@ struct moe_ws {
     int *idx, *off, *perm, *pos_of, *tok, *tile_expert, *tile_begin, *tile_end, *n_tiles;
     float *w, *g, *u, *h, *dn;
     uint8_t *xq_x, *xq_h;
+    __bf16 *xp_x, *xp_h;      // split planes of x [T][N] and h [T*K][M] (batched path)
+    int *lo_x, *lo_h;
 };
 
 static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *base)
@@ -199,6 +201,10 @@ static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *
     s.dn = (float *)take(TK * L.N * 4);
     s.xq_x = take(xq_size(T, L.N));
     s.xq_h = take(xq_size((long)TK, L.M));
+    s.xp_x = (__bf16 *)take(3 * act_planes_elems(T, L.N) * 2);
+    s.xp_h = (__bf16 *)take(3 * act_planes_elems((long)TK, L.M) * 2);
+    s.lo_x = (int *)take((size_t)T * 4);
+    s.lo_h = (int *)take(TK * 4);
     if (w) *w = s;
     return o;
 }
@@ -284,7 +290,14 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
         // gate + up (+ SiLU) in bucket order
         qgemm_args a{};
         a.table = L->tab; a.table2 = L->tab + E;
-        a.x = x; a.ldx = N; a.xq = xqx;
+        a.xq = xqx;
+        if (xmode_of(L->sem_g) == XM_PLANES || xmode_of(L->sem_u) == XM_PLANES) {
+            const long pe = act_planes_elems(T, N);
+            const int np = std::max(xmode_of(L->sem_g) == XM_PLANES ? act_nplanes(L->sem_g) : 2,
+                                    xmode_of(L->sem_u) == XM_PLANES ? act_nplanes(L->sem_u) : 2);
+            CK(mllm_launch_act_split(x, N, T, N, np, s.xp_x, pe, s.lo_x, st));
+            a.xp = {s.xp_x, pe, act_planes_ld(N), s.lo_x};
+        }
         a.row_of = s.tok;
         a.n_rows = M; a.n_cols = N;
         a.tile_expert = s.tile_expert; a.tile_begin = s.tile_begin; a.tile_end = s.tile_end; a.n_tiles = s.n_tiles;
@@ -304,7 +317,12 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
             qgemm_args b{};
             b.table = L->tab + 2 * E;
-            b.x = s.h; b.ldx = M; b.xq = xqh;
+            b.xq = xqh;
+            if (xmode_of(L->sem_d) == XM_PLANES) {
+                const long pe = act_planes_elems((long)TK, M);
+                CK(mllm_launch_act_split(s.h, M, TK, M, act_nplanes(L->sem_d), s.xp_h, pe, s.lo_h, st));
+                b.xp = {s.xp_h, pe, act_planes_ld(M), s.lo_h};
+            }
             b.out = s.dn; b.ldo = N;
             b.n_rows = N; b.n_cols = M;
             b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;

@@ -100,7 +100,7 @@ def load_kernels(path=LIB_PATH):
     so.mllm_packed_size.restype = ctypes.c_long
     so.mllm_pack.argtypes = [ci, cvp, cvp, ci, ci, cvp]
     so.mllm_pack.restype = ci
-    so.mllm_gemv_workspace_size.argtypes = [ci, ci, ci]
+    so.mllm_gemv_workspace_size.argtypes = [ci, ci, ci, ci]
     so.mllm_gemv_workspace_size.restype = ctypes.c_long
     so.mllm_gemv.argtypes = [ci, cvp, cvp, cvp, ci, ci, ci, cvp, cvp]
     so.mllm_gemv.restype = ci
@@ -159,8 +159,8 @@ class DeviceOps:
                     "mllm_pack")
         return packed
 
-    def workspace(self, sem, n_cols, B, device):
-        n = self.so.mllm_gemv_workspace_size(sem, n_cols, B)
+    def workspace(self, sem, n_cols, B, device, n_rows=0):
+        n = self.so.mllm_gemv_workspace_size(sem, n_rows, n_cols, B)
         return self.torch.empty(max(n, 256), dtype=self.torch.uint8, device=device) if n > 0 else None
 
     def gemv(self, sem, packed, x, n_rows, n_cols, out=None, ws=None):
@@ -169,7 +169,7 @@ class DeviceOps:
         if out is None:
             out = torch.empty((B, n_rows), dtype=torch.float32, device=x.device)
         if ws is None:
-            ws = self.workspace(sem, n_cols, B, x.device)
+            ws = self.workspace(sem, n_cols, B, x.device, n_rows)
         self._check(self.so.mllm_gemv(sem, packed.data_ptr(), x.data_ptr(), out.data_ptr(), n_rows, n_cols, B,
                                       ws.data_ptr() if ws is not None else None, self._stream()), "mllm_gemv")
         return out

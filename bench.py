@@ -31,6 +31,10 @@ from mojollama_amd import kernels as K  # noqa: E402
 from mojollama_amd import workloads as W  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel (fused Q4_K gate+up GEMV, B=1) from
+# FETCH_SIZE / WRITE_SIZE counter runs calibrated on a copy of known size:
+# profiles/gemv_gate_up_q4k_traffic.md (commands and raw counter values).
+GATE_UP_TRAFFIC_BYTES = 13266000
 
 
 def parse():
@@ -40,7 +44,32 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU reference timing")
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
+    ap.add_argument("--kernel", choices=("gate_up", "copy"),
+                    help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
+                         "fused Q4_K gate+up GEMV of the roofline, or a 256 MiB device copy to calibrate bytes")
     return ap.parse_args()
+
+
+def kernel_only(torch, dev, which):
+    """50 launches of one kernel, nothing else on the GPU besides set-up."""
+    if which == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        a.fill_(1)
+        torch.cuda.synchronize()
+        for _ in range(50):
+            b.copy_(a)
+    else:
+        rng = np.random.default_rng(2)
+        raw = np.concatenate([W.gen_weights(rng, W.QT_Q4_K, 5632, 2048) for _ in range(2)])
+        m = Matrix(dev, K.Q4_K_GGML, raw, 11264, 2048)
+        x = torch.randn(1, 2048, device="cuda")
+        o = torch.empty(1, 11264, device="cuda")
+        torch.cuda.synchronize()
+        for _ in range(50):
+            dev.gemv(m.sem, m.packed, x, m.rows, m.cols, out=o)
+    torch.cuda.synchronize()
+    print(f"[bench] {which}: 50 launches done", file=sys.stderr, flush=True)
 
 
 class Matrix:
@@ -269,6 +298,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = K.DeviceOps()
     torch.cuda.set_device(0)
+    if args.kernel:
+        kernel_only(torch, dev, args.kernel)
+        return
     rng = np.random.default_rng(2)
     n_layers = W.TINYLLAMA_LAYERS
     print(f"[bench] building {n_layers} TinyLlama layers + lm_head on {gpu_info(torch)}", file=sys.stderr, flush=True)
@@ -361,7 +393,7 @@ def main():
                    "configs0_q8_0_gemv": {"us": round(ms_q8 * 1e3 / len(q8), 3), "GB/s": round(q8_gbs, 1),
                                           "hbm_frac": round(q8_gbs / HBM_PEAK_GBS, 4)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "kernel": f"k_gemv_p<Q4_K_GGML,B=1> fused gate+up 11264x2048 ({gu_bytes:,} algorithmic B/launch)"},
         "cpu_baseline": cpu,
         "extra": extra,

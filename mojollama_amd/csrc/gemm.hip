@@ -31,7 +31,9 @@ template <int SEM, int XM> struct gemm_cfg {
     static constexpr bool A4 = (SEM == SEM_Q4_K_Q8);
     static constexpr bool WEXACT = (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP || SEM == SEM_MXFP4_Q8);
     static constexpr int NA = WEXACT ? 1 : (A4 ? 3 : 2);
-    static constexpr int NB = (XM == XM_Q8) ? 1 : (XM == XM_PLANES && !WEXACT) ? 2 : 3;
+    // Q8_0 quants are exact in one bf16 plane; XM_Q8D applies their block scale
+    // after each 32-column MFMA (one Q8_0 block per k-slice).
+    static constexpr int NB = (XM == XM_Q8 || XM == XM_Q8D) ? 1 : (XM == XM_PLANES && !WEXACT) ? 2 : 3;
     // K columns per step: A4 keeps only the 32 columns its dot reads of each 64
     static constexpr int KS = 64;
     static constexpr int KE = A4 ? 32 : 64;
@@ -39,7 +41,7 @@ template <int SEM, int XM> struct gemm_cfg {
     // products w_i * b_j taken: i + j <= MAXT.  Two planes each: the three leading
     // terms (the dropped w1*b1 is ~2^-16 of the product, below the two-plane
     // truncation itself).  One exact plane against three, or three against
-    // exact quants: all three.
+    // exact quants: all three (one exact plane against exact quants: the one).
     static constexpr int MAXT = (NA == 2 && NB == 2) ? 1 : 2;
 };
 
@@ -313,15 +315,17 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
     } else {
         if (tid < 4 * TM_) {
             const int er = tid >> 2, seg = (tid & 3) * 16;
-            if (er < n_ent && k0 + seg < kused) {
+            const bool live = er < n_ent && k0 + seg < kused;
+            if (live) {
                 const uint32_t Q[4] = {ar.q.x, ar.q.y, ar.q.z, ar.q.w};
-                const float d8 = (XM == XM_Q8D) ? ar.s0 : 1.0f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)((Q[i >> 2] >> (8 * (i & 3))) & 0xFF) * d8;
+                for (int i = 0; i < 16; i++) v[i] = (float)(int8_t)((Q[i >> 2] >> (8 * (i & 3))) & 0xFF);
             } else {
                 zero16(v);
             }
             put16_planes<NB>(Bp, PS, er * LDA + seg, v);
+            // Q8D: block scale of the entry's 32 columns at seg (one writer per block)
+            if (XM == XM_Q8D && tsum_l && (seg & 16) == 0) tsum_l[2 * er + (seg >> 5)] = live ? ar.s0 : 0.0f;
         }
     }
 }
@@ -338,7 +342,9 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
     __shared__ __attribute__((aligned(16))) __bf16 s_u[DUAL ? NA * TN * LDA : 8];
     __shared__ __attribute__((aligned(16))) __bf16 s_b[NB * TM * LDA];
     __shared__ int s_row[TM];
-    __shared__ float s_dmin[C::A4 ? TN : 1], s_dmin2[C::A4 && DUAL ? TN : 1], s_tsum[C::A4 ? TM : 1];
+    // s_tsum: Q4_K_Q8 min-term sums per entry, or Q8D block scales per entry and 32-column half
+    __shared__ float s_dmin[C::A4 ? TN : 1], s_dmin2[C::A4 && DUAL ? TN : 1],
+        s_tsum[C::A4 ? TM : (XM == XM_Q8D ? 2 * TM : 1)];
     constexpr int BE = mllm_sem_uses_q8(SEM) ? q8_traits<SEM>::kBlockElems : sem_traits<SEM>::kBlockElems;
 
     // ---- work tile
@@ -410,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
         const int k0 = s * KS;
         put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr);
         if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr);
-        put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, C::A4 ? s_tsum : nullptr);
+        put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, (C::A4 || XM == XM_Q8D) ? s_tsum : nullptr);
     };
     auto mfma_step = [&]() __attribute__((always_inline)) {
         // MFMA 16x16x32: lane l supplies row/entry (l % 16), k = 8*(l/16) .. +8 of a 32-wide slice
@@ -428,17 +434,16 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
                 bf16x8 av[NA];
 #pragma unroll
                 for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_a + p * TN * LDA + ar_);
+                if constexpr (XM == XM_Q8D) {
+                    // exact block product (MXFP4 weight x Q8_0 quant), then its activation scale
 #pragma unroll
-                for (int j = 0; j < JT; j++)
+                    for (int j = 0; j < JT; j++) {
+                        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0][j], f32x4{0, 0, 0, 0}, 0, 0, 0);
+                        const float sc = s_tsum[2 * (we0 + 16 * j + li) + (ks >> 5)];
 #pragma unroll
-                    for (int pa = 0; pa < NA; pa++)
-#pragma unroll
-                        for (int pb = 0; pb < NB; pb++)
-                            if (pa + pb <= MAXT && pb < pb_end)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc[i][j], 0, 0, 0);
-                if constexpr (DUAL) {
-#pragma unroll
-                    for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_u + p * TN * LDA + ar_);
+                        for (int v = 0; v < 4; v++) acc[i][j][v] = fmaf(sc, d[v], acc[i][j][v]);
+                    }
+                } else {
 #pragma unroll
                     for (int j = 0; j < JT; j++)
 #pragma unroll
@@ -446,7 +451,29 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
 #pragma unroll
                             for (int pb = 0; pb < NB; pb++)
                                 if (pa + pb <= MAXT && pb < pb_end)
-                                    acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc2[i][j], 0, 0, 0);
+                                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc[i][j], 0, 0, 0);
+                }
+                if constexpr (DUAL) {
+#pragma unroll
+                    for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_u + p * TN * LDA + ar_);
+                    if constexpr (XM == XM_Q8D) {
+#pragma unroll
+                        for (int j = 0; j < JT; j++) {
+                            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0][j], f32x4{0, 0, 0, 0}, 0, 0, 0);
+                            const float sc = s_tsum[2 * (we0 + 16 * j + li) + (ks >> 5)];
+#pragma unroll
+                            for (int v = 0; v < 4; v++) acc2[i][j][v] = fmaf(sc, d[v], acc2[i][j][v]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < JT; j++)
+#pragma unroll
+                            for (int pa = 0; pa < NA; pa++)
+#pragma unroll
+                                for (int pb = 0; pb < NB; pb++)
+                                    if (pa + pb <= MAXT && pb < pb_end)
+                                        acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[pa], bv[pb][j], acc2[i][j], 0, 0, 0);
+                    }
                 }
             }
         }

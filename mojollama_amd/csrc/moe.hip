@@ -25,82 +25,98 @@ namespace {
 
 constexpr int kTileEntries = 64;   // entries per grouped-GEMM work tile (gemm.hip TM)
 
-// Stable bucketing of entries i = t*K + k by expert idx[i], in one workgroup:
-// block histograms -> exclusive scan in (expert, block) order -> each block
-// places its entries in order.  perm[pos] = i, pos_of[i] = pos (or -1 for a
-// negative expert id), bucket offsets off[0..E], and the list of work tiles
-// (<= kTileEntries consecutive positions of one expert).
-__global__ __launch_bounds__(256) void k_bucket(const int *__restrict__ idx, int TK, int E, int CH,
-                                                int *__restrict__ off, int *__restrict__ perm,
-                                                int *__restrict__ pos_of, int *__restrict__ tile_expert,
-                                                int *__restrict__ tile_begin, int *__restrict__ tile_end,
-                                                int *__restrict__ n_tiles)
-{
-    extern __shared__ int hist[];   // [NB][E]
-    const int NB = (TK + CH - 1) / CH;
-    const int tid = threadIdx.x;
-    for (int i = tid; i < NB * E; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    if (tid < NB) {
-        const int i1 = min(TK, (tid + 1) * CH);
-        for (int i = tid * CH; i < i1; i++) {
-            const int e = idx[i];
-            if (e >= 0 && e < E) hist[tid * E + e]++;
-        }
-    }
-    __syncthreads();
-    __shared__ int tot[257];
-    if (tid < E) {
-        int s = 0;
-        for (int b = 0; b < NB; b++) s += hist[b * E + tid];
-        tot[tid] = s;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) { const int c = tot[e]; tot[e] = run; off[e] = run; run += c; }
-        off[E] = run;
-        tot[E] = run;
-    }
-    __syncthreads();
-    if (tid < E) {
-        int run = tot[tid];
-        for (int b = 0; b < NB; b++) { const int c = hist[b * E + tid]; hist[b * E + tid] = run; run += c; }
-    }
-    __syncthreads();
-    if (tid < NB) {
-        const int i1 = min(TK, (tid + 1) * CH);
-        for (int i = tid * CH; i < i1; i++) {
-            const int e = idx[i];
-            if (e >= 0 && e < E) {
-                const int pos = hist[tid * E + e]++;
-                perm[pos] = i;
-                pos_of[i] = pos;
-            } else {
-                pos_of[i] = -1;
-            }
-        }
-    }
-    if (tid == 0) {
-        int nt = 0;
-        for (int e = 0; e < E; e++) {
-            const int b = tot[e], c = (e + 1 < E ? tot[e + 1] : tot[E]) - b;
-            for (int s = 0; s < c; s += kTileEntries) {
-                tile_expert[nt] = e;
-                tile_begin[nt] = b + s;
-                tile_end[nt] = b + min(c, s + kTileEntries);
-                nt++;
-            }
-        }
-        *n_tiles = nt;
-    }
-}
+// Stable bucketing of entries i = t*K + k by expert idx[i], in one workgroup of
+// 1024 threads: an LDS histogram, an exclusive scan over experts (bucket
+// offsets off[0..E] and the work-tile list: <= kTileEntries consecutive
+// positions of one expert), then passes of 1024 entries in index order.  An
+// entry's position is its expert's running base + the entries of that expert
+// in earlier waves of the pass + its rank among its wave's equal lanes below
+// it (a 64-step scan of the wave), so the order is the entries' index order
+// without atomics.  perm[pos] = i, pos_of[i] = pos (-1 for an expert id
+// outside [0, E)), tok[pos] = i / K when tok is given.
+constexpr int kBucketThreads = 1024, kBucketWaves = kBucketThreads / 64;
 
-// Token row of bucket position p: perm[p] / K.
-__global__ void k_entry_tokens(const int *__restrict__ perm, int TK, int K, int *__restrict__ tok)
+__global__ __launch_bounds__(1024) void k_bucket(const int *__restrict__ idx, int TK, int E, int K,
+                                                 int *__restrict__ off, int *__restrict__ perm,
+                                                 int *__restrict__ pos_of, int *__restrict__ tok,
+                                                 int *__restrict__ tile_expert, int *__restrict__ tile_begin,
+                                                 int *__restrict__ tile_end, int *__restrict__ n_tiles)
 {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p < TK) tok[p] = perm[p] / K;
+    __shared__ int cnt[256], base[256], tbase[257], scan[256];
+    __shared__ int wcnt[kBucketWaves][256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < 256; e += kBucketThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < TK; i += kBucketThreads) {
+        const int e = idx[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);    // a count: order-free
+    }
+    __syncthreads();
+    // exclusive scans over experts of counts and of tile counts (Hillis-Steele, 256 wide)
+    int c = 0, nt = 0;
+    if (tid < 256) {
+        c = tid < E ? cnt[tid] : 0;
+        nt = (c + kTileEntries - 1) / kTileEntries;
+        scan[tid] = c;
+        tbase[tid] = nt;
+    }
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {
+        int v = 0, w = 0;
+        if (tid < 256 && tid >= d) { v = scan[tid - d]; w = tbase[tid - d]; }
+        __syncthreads();
+        if (tid < 256 && tid >= d) { scan[tid] += v; tbase[tid] += w; }
+        __syncthreads();
+    }
+    if (tid < E) {
+        const int b = scan[tid] - c, tb = tbase[tid] - nt;   // exclusive
+        base[tid] = b;
+        off[tid] = b;
+        for (int t = 0; t < nt; t++) {
+            tile_expert[tb + t] = tid;
+            tile_begin[tb + t] = b + t * kTileEntries;
+            tile_end[tb + t] = b + min(c, (t + 1) * kTileEntries);
+        }
+    }
+    if (tid == E - 1) {
+        off[E] = scan[tid];
+        *n_tiles = tbase[tid];
+    }
+    __syncthreads();
+    for (int p0 = 0; p0 < TK; p0 += kBucketThreads) {
+        const int i = p0 + tid;
+        int e = i < TK ? idx[i] : -1;
+        const bool valid = e >= 0 && e < E;
+        if (!valid) e = -1;
+        // rank among the wave's lanes below with the same expert, and the wave's count of it
+        int rank = 0, tot = 0;
+        for (int j = 0; j < 64; j++) {
+            const int ej = __builtin_amdgcn_readlane(e, j);
+            const int m = ej == e;
+            tot += m;
+            rank += m & (j < lane);
+        }
+        for (int q = tid; q < kBucketWaves * 256; q += kBucketThreads) (&wcnt[0][0])[q] = 0;
+        __syncthreads();
+        if (valid && rank == 0) wcnt[wave][e] = tot;
+        __syncthreads();
+        if (valid) {
+            int pos = base[e] + rank;
+            for (int w = 0; w < wave; w++) pos += wcnt[w][e];
+            perm[pos] = i;
+            pos_of[i] = pos;
+            if (tok) tok[pos] = i / K;
+        } else if (i < TK) {
+            pos_of[i] = -1;
+        }
+        __syncthreads();
+        if (tid < E) {
+            int add = 0;
+            for (int w = 0; w < kBucketWaves; w++) add += wcnt[w][tid];
+            base[tid] += add;
+        }
+        __syncthreads();
+    }
 }
 
 // out[t][n] = sum over k (in order) of w[t][k] * dn[pos_of[t*K+k]][n], as
@@ -277,14 +293,8 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     const bool batched = T > 8 && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
                          (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d));
     if (batched) {
-        // histogram blocks: at most 256 blocks and 64 KB of LDS
-        int nb_max = std::min(256, 16384 / E);
-        const int ch = (TK + nb_max - 1) / nb_max;
-        const int nb = (TK + ch - 1) / ch;
-        hipLaunchKernelGGL(k_bucket, dim3(1), dim3(256), (size_t)nb * E * 4, st, s.idx, TK, E, ch, s.off, s.perm,
-                           s.pos_of, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles);
-        CK(hipGetLastError());
-        hipLaunchKernelGGL(k_entry_tokens, dim3((TK + 255) / 256), dim3(256), 0, st, s.perm, TK, K, s.tok);
+        hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), 0, st, s.idx, TK, E, K, s.off, s.perm, s.pos_of,
+                           s.tok, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles);
         CK(hipGetLastError());
         const int max_tiles = TK / kTileEntries + E + 1;
         // gate + up (+ SiLU) in bucket order
@@ -376,11 +386,8 @@ MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm,
 {
     if (E <= 0 || E > 256 || TK <= 0) return -1;
     const int max_tiles = TK / kTileEntries + E + 1;
-    int nb_max = std::min(256, 16384 / E);
-    const int ch = (TK + nb_max - 1) / nb_max;
-    const int nb = (TK + ch - 1) / ch;
-    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(256), (size_t)nb * E * 4, (hipStream_t)stream, idx, TK, E, ch, off,
-                       perm, pos_of, tiles, tiles + max_tiles, tiles + 2 * max_tiles, tiles + 3 * max_tiles);
+    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), 0, (hipStream_t)stream, idx, TK, E, 1, off, perm,
+                       pos_of, nullptr, tiles, tiles + max_tiles, tiles + 2 * max_tiles, tiles + 3 * max_tiles);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -116,12 +116,12 @@ MLLM_DEV void chunk_weights(const raw_chunk &raw, int c, float (&w0)[16], float 
 // the number of loads in flight is the same on every path and the compiler's
 // waits cover only the older step.
 
-// Weight tasks per row and step: Q4_K_Q8 one chunk; MXFP4_Q8 two 32-blocks;
+// Weight tasks per row and step: Q4_K_Q8 the two 16-weight halves of one chunk; MXFP4_Q8 two 32-blocks;
 // otherwise the two chunks covering the 64 columns, or four for the ggml
 // Q6_K orders whose chunks put their two runs 64 columns apart.
 template <int SEM, int XM> struct wtask {
     static constexpr bool SPLIT = (SEM == SEM_Q6_K_GGML || SEM == SEM_Q6_K_LOWNIB);
-    static constexpr int NT = gemm_cfg<SEM, XM>::A4 ? 1 : (SEM == SEM_MXFP4_Q8) ? 2 : SPLIT ? 4 : 2;
+    static constexpr int NT = gemm_cfg<SEM, XM>::A4 ? 2 : (SEM == SEM_MXFP4_Q8) ? 2 : SPLIT ? 4 : 2;
 };
 
 template <int SEM, int XM, int TN_> struct wraw {
@@ -157,14 +157,18 @@ MLLM_DEV void wtask_at(int t, int n_rows, int nb, int n0, int k0, int &rr, int &
     }
 }
 
+// Task numbering starts at thread `rot` (mod 256): the two matrices of a fused
+// gate+up tile start half a workgroup apart, so their decode lands on
+// different waves when each has at most 128 tasks.
 template <int SEM, int XM, int TN_>
-MLLM_DEV void fetch_w(const mllm_packed &W, int n_rows, int nb, int n0, int k0, wraw<SEM, XM, TN_> &wr)
+MLLM_DEV void fetch_w(const mllm_packed &W, int n_rows, int nb, int n0, int k0, wraw<SEM, XM, TN_> &wr, int rot)
 {
+    const int tt = (threadIdx.x + rot) & 255;
 #pragma unroll
     for (int i = 0; i < wraw<SEM, XM, TN_>::WT; i++) {
         int rr, sub, row, c;
         bool valid;
-        wtask_at<SEM, XM, TN_>(threadIdx.x + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
+        wtask_at<SEM, XM, TN_>(tt + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
         if constexpr (mllm_sem_uses_q8(SEM)) q8_fetch<SEM>(W, nb, row, c, wr.r[i]);
         else fetch<SEM>(W, nb, row, c, wr.r[i]);
     }
@@ -173,36 +177,34 @@ MLLM_DEV void fetch_w(const mllm_packed &W, int n_rows, int nb, int n0, int k0, 
 // Decode the fetched weight tasks into LDS planes (plane p at A + p*TN_*LDA);
 // for Q4_K_Q8 also each row's dmin.
 template <int SEM, int XM, int TN_>
-MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, int k0, __bf16 *A, float *dmin_l)
+MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, int k0, __bf16 *A, float *dmin_l,
+                    int rot)
 {
     using C = gemm_cfg<SEM, XM>;
     constexpr int LDA = C::LDA, NA = C::NA, PS = TN_ * C::LDA;
+    const int tt = (threadIdx.x + rot) & 255;
 #pragma unroll
     for (int i = 0; i < wraw<SEM, XM, TN_>::WT; i++) {
         int rr, sub, row, c;
         bool valid;
-        wtask_at<SEM, XM, TN_>(threadIdx.x + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
-        if (threadIdx.x + 256 * i >= TN_ * wtask<SEM, XM>::NT) continue;   // clamped duplicate
+        wtask_at<SEM, XM, TN_>(tt + 256 * i, n_rows, nb, n0, k0, rr, sub, row, c, valid);
+        if (tt + 256 * i >= TN_ * wtask<SEM, XM>::NT) continue;   // clamped duplicate
         const raw_chunk &r = wr.r[i];
         if constexpr (C::A4) {
             // dot_q4_k_q8_0 (QK:1647-1735): the integer term reads k < 16 of each 32-element
             // sub-block; group g of a super-block holds sub-blocks 2g (low nibbles) and 2g+1
             // (high nibbles).  Step columns: 0..15 = sub-block 2g, 16..31 = 2g+1, w = d*sc_j*nib.
+            // this task: half sub = 0 (sub-block 2g, low nibbles) or 1 (2g+1, high nibbles)
             const int g = c & 3;
             int s1, m1, s2, m2;
             kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
-            const float d = h2f(r.m.x & 0xFFFF);
-            const float ds1 = d * (float)s1, ds2 = d * (float)s2;
+            const float ds = h2f(r.m.x & 0xFFFF) * (float)(sub ? s2 : s1);
             const uint32_t Aw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
-            float lo[16], hi[16];
+            float v[16];
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                lo[e] = ds1 * (float)((Aw[e >> 2] >> (8 * (e & 3))) & 15);
-                hi[e] = ds2 * (float)((Aw[e >> 2] >> (8 * (e & 3) + 4)) & 15);
-            }
-            put16_planes<NA>(A, PS, rr * LDA, lo);
-            put16_planes<NA>(A, PS, rr * LDA + 16, hi);
-            if (dmin_l) dmin_l[rr] = h2f(r.m.x >> 16);
+            for (int e = 0; e < 16; e++) v[e] = ds * (float)((Aw[e >> 2] >> (8 * (e & 3) + 4 * sub)) & 15);
+            put16_planes<NA>(A, PS, rr * LDA + 16 * sub, v);
+            if (dmin_l && sub == 0) dmin_l[rr] = h2f(r.m.x >> 16);
         } else if constexpr (SEM == SEM_MXFP4_Q8) {
             // mxfp4_row_dot_q8 (QK:629-678) with the token's Q8 scale moved to the activation
             // side: w = sext4(n) * 2^(E-127), exact in bf16.
@@ -330,8 +332,21 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
     }
 }
 
+// Workgroups per CU the tile's LDS allows (160 KB per CU), at most 3 (2 for
+// the Q8D form, whose registers do not fit a third); the compiler then
+// budgets registers for that many.
+template <int SEM, int XM, bool DUAL, int TM> constexpr int qgemm_wgs_per_cu()
+{
+    using C = gemm_cfg<SEM, XM>;
+    constexpr int TN = tile_cfg<DUAL, TM>::TN;
+    constexpr int lds = 2 * (C::NA * TN * C::LDA * (DUAL ? 2 : 1) + C::NB * TM * C::LDA) + 4 * TM + 4 * 3 * TN + 8 * TM + 64;
+    constexpr int cap = XM == XM_Q8D ? 2 : 3;
+    constexpr int n = 163840 / lds;
+    return n < 1 ? 1 : n > cap ? cap : n;
+}
+
 template <int SEM, int XM, bool DUAL, int TM>
-__global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
+__global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void k_qgemm(qgemm_args a)
 {
     using C = gemm_cfg<SEM, XM>;
     using G = tile_cfg<DUAL, TM>;
@@ -408,14 +423,14 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(qgemm_args a)
     };
     auto fetch_step = [&](int s, stepbuf &b) __attribute__((always_inline)) {
         const int k0 = min(s, s_end - 1) * KS;   // past the end: refetch the last step (unused)
-        fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w);
-        if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u);
+        fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w, 0);
+        if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u, 128);
         fetch_a<SEM, XM, TM>(a, s_row, n_ent, k0, kused, b.x);
     };
     auto put_step = [&](int s, const stepbuf &b) __attribute__((always_inline)) {
         const int k0 = s * KS;
-        put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr);
-        if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr);
+        put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr, 0);
+        if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr, 128);
         put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, (C::A4 || XM == XM_Q8D) ? s_tsum : nullptr);
     };
     auto mfma_step = [&]() __attribute__((always_inline)) {

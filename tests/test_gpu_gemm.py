@@ -77,3 +77,39 @@ def test_prefill_config_shapes(lib, orc, name, qt, R, C, M):
     ref = orc.gemv(orc.sem_for(1, qt), w[:rows * rb], x[:64], rows, C, 64)
     assert O.norm_err(got[:64, :rows], ref) < GEMM_TOL
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("sem,qt", [(K.Q4_K_GGML, 12), (K.Q6_K_SEQ, 14), (K.MXFP4, 39)])
+@pytest.mark.parametrize("bf16_rows", ["all", "some"])
+def test_gemm_bf16_exact_activations(dev, orc, sem, qt, bf16_rows):
+    """Rows whose activations are exact in bf16 (configs[2]'s prefill inputs) let a
+    tile skip its lower activation planes; a tile holding one fp32 row must not."""
+    import torch
+    rng = np.random.default_rng(900 + qt + len(bf16_rows))
+    R, C, B = 300, 1024, 600          # B >= 512: 128-entry tiles, and split-K off
+    w = W.gen_weights(rng, qt, R, C)
+    x = torch.from_numpy(W.gen_x(rng, B, C)).bfloat16().float().numpy()
+    if bf16_rows == "some":
+        x[::97] = W.gen_x(rng, x[::97].shape[0], C)   # a full-precision row in most tiles
+    raw = torch.from_numpy(w).cuda()
+    packed = dev.pack(sem, raw, R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(np.ascontiguousarray(x)).cuda(), R, C).cpu().numpy()
+    assert O.norm_err(got, orc.gemv(sem, w, x, R, C, B)) < GEMM_TOL
+
+
+@pytest.mark.parametrize("B", [16, 100])
+def test_gemm_split_k_vs_oracle(dev, orc, B):
+    """Few output tiles and a long K: the launch splits K across workgroups and
+    adds the partials in order (deterministic: two runs agree bit for bit)."""
+    import torch
+    rng = np.random.default_rng(950 + B)
+    R, C = 256, 5632
+    w = W.gen_weights(rng, 14, R, C)
+    x = W.gen_x(rng, B, C)
+    raw = torch.from_numpy(w).cuda()
+    packed = dev.pack(K.Q6_K_SEQ, raw, R, C)
+    xt = torch.from_numpy(x).cuda()
+    got1 = dev.gemv(K.Q6_K_SEQ, packed, xt, R, C).cpu().numpy()
+    got2 = dev.gemv(K.Q6_K_SEQ, packed, xt, R, C).cpu().numpy()
+    assert np.array_equal(got1, got2)
+    assert O.norm_err(got1, orc.gemv(K.Q6_K_SEQ, w, x, R, C, B)) < GEMM_TOL

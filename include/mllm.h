@@ -124,9 +124,12 @@ MLLM_API long mllm_router_packed_size(int N, int E);
 MLLM_API int mllm_router_pack(const float *router_dev, int N, int E, float *out_dev, void *stream);
 
 /* Routing of T tokens (CE:606-638; renormalised top-K weights when `renorm`):
- * router_p in the routing layout, x [T][N] -> idx/w [T][K].  E <= 256, K <= 16. */
+ * router_p in the routing layout, x [T][N] -> idx/w [T][K].  E <= 256, K <= 16.
+ * `workspace` (optional, mllm_route_workspace_size bytes) lets T <= 8 tokens
+ * spread over expert slices; NULL runs one workgroup per token. */
+MLLM_API long mllm_route_workspace_size(int T, int E);
 MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
-                        int *idx_dev, float *w_dev, void *stream);
+                        int *idx_dev, float *w_dev, void *workspace, void *stream);
 
 /* fp32 weights of a packed matrix (fp32-weight semantics only). */
 MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_cols, float *out_dev, void *stream);

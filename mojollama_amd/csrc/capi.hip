@@ -686,10 +686,16 @@ MLLM_API int mllm_router_pack(const float *router_dev, int N, int E, float *out_
     return 0;
 }
 
-MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
-                        int *idx_dev, float *w_dev, void *stream)
+MLLM_API long mllm_route_workspace_size(int T, int E)
 {
-    hipError_t r = mllm_launch_route(router_p_dev, x_dev, T, N, E, K, renorm, idx_dev, w_dev, (hipStream_t)stream);
+    return (T > 0 && E > 0) ? mllm_route_workspace_floats(T, E) * 4 : -1;
+}
+
+MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, int N, int E, int K, int renorm,
+                        int *idx_dev, float *w_dev, void *workspace, void *stream)
+{
+    hipError_t r = mllm_launch_route(router_p_dev, x_dev, T, N, E, K, renorm, idx_dev, w_dev, (float *)workspace,
+                                     (hipStream_t)stream);
     if (r != hipSuccess) { set_error("mllm_route: %s (E<=256, K<=16 required)", hipGetErrorString(r)); return -1; }
     return 0;
 }
@@ -750,7 +756,7 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
     HIP_OK(hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st));
     HIP_OK(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
-    HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, st));
+    HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, nullptr, st));
     xq_bufs xqx = xq_carve(S + o_xq, T, N), xqh = xq_carve(S + o_hq, (long)TK, M);
     if (mllm_sem_uses_q8(sems[0]) || mllm_sem_uses_q8(sems[1]))
         HIP_OK(mllm_launch_quantize_q8_0(dx, T, N, nullptr, xqx.q, xqx.d, xqx.s4, xqx.sq, st));

@@ -40,8 +40,10 @@ hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t 
 // (GO:88-92).  router_t is the router transposed to [N][E].
 long mllm_router_packed_floats(int N, int E);
 hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out, hipStream_t st);
-hipError_t mllm_launch_route(const float *router_t, const float *x, int T, int N, int E, int K, int renorm,
-                             int *top_idx, float *top_w, hipStream_t st);
+// logits_ws (optional, mllm_route_workspace_floats floats): lets T <= 8 tokens spread over expert slices.
+long mllm_route_workspace_floats(int T, int E);
+hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
+                             int *top_idx, float *top_w, float *logits_ws, hipStream_t st);
 
 // h[i] = silu(g[i]) * u[i] (clamp g to +-80 when clamp != 0), i < n.
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st);

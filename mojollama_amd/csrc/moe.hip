@@ -192,6 +192,7 @@ struct moe_ws {
     uint8_t *xq_x, *xq_h;
     __bf16 *xp_x, *xp_h;      // split planes of x [T][N] and h [T*K][M] (batched path)
     int *lo_x, *lo_h;
+    float *logits;            // routing logits [T][E] (decode path, expert slices)
 };
 
 static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *base)
@@ -221,6 +222,7 @@ static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *
     s.xp_h = (__bf16 *)take(3 * act_planes_elems((long)TK, L.M) * 2);
     s.lo_x = (int *)take((size_t)T * 4);
     s.lo_h = (int *)take(TK * 4);
+    s.logits = (float *)take((size_t)mllm_route_workspace_floats(T, L.E) * 4);
     if (w) *w = s;
     return o;
 }
@@ -281,7 +283,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     moe_ws_layout(*L, T, &s, (uint8_t *)workspace);
     const int N = L->N, M = L->M, E = L->E, K = L->K, TK = T * K;
 #define CK(e) do { if ((e) != hipSuccess) return -1; } while (0)
-    CK(mllm_launch_route(L->router_p, x, T, N, E, K, L->renorm, s.idx, s.w, st));
+    CK(mllm_launch_route(L->router_p, x, T, N, E, K, L->renorm, s.idx, s.w, s.logits, st));
     if (L->sem_g < 0 || L->sem_u < 0) return -1;   // reference-zero gate/up types are not served here
     int8_t *q; float *d, *s4; int *sq;
     const mllm_xq xqx = xq_at(s.xq_x, T, N, &q, &d, &s4, &sq);

@@ -247,16 +247,20 @@ __host__ __device__ constexpr int route_slack(int E) { return 16 * E + 16; }
 template <int TT, int PF, int XS>
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_p, const float *__restrict__ x,
                                                int T, int N, int E, int K, int renorm, int KC, int G, int lgq,
+                                               int lgES, float *__restrict__ logits,
                                                int *__restrict__ top_idx, float *__restrict__ top_w)
 {
     extern __shared__ float4 lds4[];
     float *lds = reinterpret_cast<float *>(lds4);
+    // experts of this workgroup: all E, or (lgES >= 0) the slice of 2^lgES starting at
+    // blockIdx.y * 2^lgES, whose raw logits go to logits[t][e] for k_route_finish
+    const int ES = lgES >= 0 ? (1 << lgES) : E, e0 = lgES >= 0 ? blockIdx.y * ES : 0;
     const int TW = G * TT, KCR = KC + 4;
-    const int per = KC * E + TW * KCR;           // floats per buffer (multiple of 4)
+    const int per = KC * ES + TW * KCR;          // floats per buffer (multiple of 4)
     const int NP = (N + kRouteRowPad - 1) / kRouteRowPad * kRouteRowPad;
     const int t0 = blockIdx.x * TW;
     const int tid = threadIdx.x;
-    const int g = tid / E, e = tid - g * E;
+    const int g = tid / ES, e = tid - g * ES;
     const int nch = (NP + KC - 1) / KC;
     const int qmask = (1 << lgq) - 1;
     float4 pr[PF], px[XS];
@@ -264,11 +268,12 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
     auto load_chunk = [&](int c) {
         const int i0 = c * KC, kq = min(KC, NP - i0) >> 2, kv = min(KC, N - i0) >> 2;
         const float4 *src = reinterpret_cast<const float4 *>(router_p + (long)i0 * E);
-        const int nr4 = kq * E;
+        const int nr4 = kq * ES;
 #pragma unroll
         for (int s = 0; s < PF; s++) {
             const int j = tid + s * 256;
-            if (j < nr4) pr[s] = gld<float4>(src + j);
+            // slice: row group j >> lgES, expert e0 + (j & (ES-1)) of E (16 bytes each)
+            if (j < nr4) pr[s] = gld<float4>(lgES >= 0 ? src + (long)(j >> lgES) * E + e0 + (j & (ES - 1)) : src + j);
         }
 #pragma unroll
         for (int s = 0; s < XS; s++) {
@@ -278,9 +283,9 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
         }
     };
     auto store_chunk = [&](int c) {
-        float4 *rb = lds4 + (c & 1) * (per >> 2), *xb = rb + ((KC * E) >> 2);
+        float4 *rb = lds4 + (c & 1) * (per >> 2), *xb = rb + ((KC * ES) >> 2);
         const int kq = min(KC, NP - c * KC) >> 2;
-        const int nr4 = kq * E;
+        const int nr4 = kq * ES;
 #pragma unroll
         for (int s = 0; s < PF; s++) {
             const int j = tid + s * 256;
@@ -303,12 +308,12 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
         __syncthreads();                         // chunk c stored by every thread
         const int kc = min(KC, NP - c * KC);     // multiple of 32
         if (g < G) {
-            const float *rr = lds + (c & 1) * per + 4 * e;           // + (i/4)*4E
-            const float *xr = lds + (c & 1) * per + KC * E + g * TT * KCR;
+            const float *rr = lds + (c & 1) * per + 4 * e;           // + (i/4)*4ES
+            const float *xr = lds + (c & 1) * per + KC * ES + g * TT * KCR;
             auto ldb = [&](int i0, float4(&r)[4], float4(&xx)[TT][4]) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    r[q] = *reinterpret_cast<const float4 *>(rr + (i0 + 4 * q) * E);
+                    r[q] = *reinterpret_cast<const float4 *>(rr + (i0 + 4 * q) * ES);
 #pragma unroll
                     for (int tt = 0; tt < TT; tt++) xx[tt][q] = *reinterpret_cast<const float4 *>(xr + tt * KCR + i0 + 4 * q);
                 }
@@ -344,6 +349,13 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
         // buffer (c+1)&1 was last read in iteration c-1, before this iteration's barrier
         if (c + 1 < nch) store_chunk(c + 1);
     }
+    if (logits) {
+        if (g < G)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+                if (t0 + g * TT + tt < T) logits[(long)(t0 + g * TT + tt) * E + e0 + e] = dot[tt];
+        return;
+    }
     __syncthreads();                             // every chain done: LDS reused for the logits
     float *p = lds;
     if (g < G)
@@ -351,6 +363,17 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
         for (int tt = 0; tt < TT; tt++) p[(g * TT + tt) * route_pitch(E) + e] = dot[tt];
     __syncthreads();
     route_finish(p, TW, t0, T, E, K, renorm, top_idx, top_w);
+}
+
+// Softmax and top-K of logits[t][0..E) written by the expert slices of k_route.
+__global__ __launch_bounds__(256) void k_route_finish(const float *__restrict__ logits, int T, int E, int K, int renorm,
+                                                      int *__restrict__ top_idx, float *__restrict__ top_w)
+{
+    __shared__ float p[route_finish_floats(1, 256)];
+    const int t = blockIdx.x;
+    if (threadIdx.x < E) p[threadIdx.x] = logits[(long)t * E + threadIdx.x];
+    __syncthreads();
+    route_finish(p, 1, t, T, E, K, renorm, top_idx, top_w);
 }
 
 // Any N: one workgroup per token reading the packed router straight from
@@ -446,8 +469,10 @@ hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out
     return hipGetLastError();
 }
 
+long mllm_route_workspace_floats(int T, int E) { return (long)T * E; }
+
 hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
-                             int *top_idx, float *top_w, hipStream_t st)
+                             int *top_idx, float *top_w, float *logits_ws, hipStream_t st)
 {
     if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || T <= 0 || N <= 0) return hipErrorInvalidValue;
     const bool vec = (N % 4) == 0 && ((uintptr_t)router_p % 16) == 0 && ((uintptr_t)x % 16) == 0;
@@ -455,13 +480,16 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
         hipLaunchKernelGGL(k_route_any, dim3(T), dim3(256), 0, st, router_p, x, T, N, E, K, renorm, top_idx, top_w);
         return hipGetLastError();
     }
-    // T <= 8: a workgroup per token (latency).  More: token groups over the
-    // idle lanes and four tokens per thread.
-    auto go = [&](auto tt_c, auto pf_c, auto xs_c, int G) {
+    // T <= 8: a workgroup per token, and with a logits workspace and E a
+    // multiple of 16 (>= 32), one per 32- or 16-expert slice of it (each
+    // streams its slice of the router; k_route_finish then takes the softmax
+    // and top-K).  More
+    // tokens: token groups over the idle lanes and four tokens per thread.
+    auto go = [&](auto tt_c, auto pf_c, auto xs_c, int G, int ES, int lgES) {
         constexpr int TT = decltype(tt_c)::value, PF = decltype(pf_c)::value, XS = decltype(xs_c)::value;
         const int TW = G * TT;
         const int NP = (N + kRouteRowPad - 1) / kRouteRowPad * kRouteRowPad;
-        int KC = 4 * 256 * PF / E / 32 * 32;          // router slots fit
+        int KC = 4 * 256 * PF / ES / 32 * 32;         // router slots fit
         KC = KC < NP ? KC : NP;
         int lgq = 0;
         for (;;) {                                     // x slots fit
@@ -471,18 +499,28 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
             KC -= 32;
         }
         if (KC < 32 || (TW << lgq) > 256 * XS) return hipErrorInvalidValue;
-        const size_t fl = 2 * ((size_t)KC * E + (size_t)TW * (KC + 4)) + route_slack(E);
+        const size_t fl = 2 * ((size_t)KC * ES + (size_t)TW * (KC + 4)) + route_slack(ES);
         const size_t fin = (size_t)route_finish_floats(TW, E);
         const size_t lds = (fl > fin ? fl : fin) * sizeof(float);
-        hipLaunchKernelGGL((k_route<TT, PF, XS>), dim3((T + TW - 1) / TW), dim3(256), lds, st, router_p, x, T, N, E,
-                           K, renorm, KC, G, lgq, top_idx, top_w);
+        hipLaunchKernelGGL((k_route<TT, PF, XS>), dim3((T + TW - 1) / TW, E / ES), dim3(256), lds, st, router_p, x,
+                           T, N, E, K, renorm, KC, G, lgq, lgES, lgES >= 0 ? logits_ws : nullptr, top_idx, top_w);
         return hipGetLastError();
     };
     using I = std::integral_constant<int, 1>;
-    if (T <= 8) return go(I{}, std::integral_constant<int, 16>{}, I{}, 1);
+    if (T <= 8) {
+        if (logits_ws && E % 16 == 0 && E >= 32) {
+            const bool s32 = E % 32 == 0 && E >= 64;   // 32-expert slices, or 16 for E = 32, 48, ...
+            hipError_t r = go(I{}, std::integral_constant<int, 16>{}, I{}, 1, s32 ? 32 : 16, s32 ? 5 : 4);
+            if (r != hipSuccess) return r;
+            hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits_ws, T, E, K, renorm, top_idx, top_w);
+            return hipGetLastError();
+        }
+        return go(I{}, std::integral_constant<int, 16>{}, I{}, 1, E, -1);
+    }
     int G = 256 / E;
     G = G > 8 ? 8 : G;
-    return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}, G);
+    return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}, G,
+              E, -1);
 }
 
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st)

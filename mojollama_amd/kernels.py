@@ -110,7 +110,9 @@ def load_kernels(path=LIB_PATH):
     so.mllm_router_packed_size.restype = ctypes.c_long
     so.mllm_router_pack.argtypes = [cvp, ci, ci, cvp, cvp]
     so.mllm_router_pack.restype = ci
-    so.mllm_route.argtypes = [cvp, cvp, ci, ci, ci, ci, ci, cvp, cvp, cvp]
+    so.mllm_route_workspace_size.argtypes = [ci, ci]
+    so.mllm_route_workspace_size.restype = ctypes.c_long
+    so.mllm_route.argtypes = [cvp, cvp, ci, ci, ci, ci, ci, cvp, cvp, cvp, cvp]
     so.mllm_route.restype = ci
     so.mllm_dequant.argtypes = [ci, cvp, ci, ci, cvp, cvp]
     so.mllm_dequant.restype = ci
@@ -191,16 +193,20 @@ class DeviceOps:
                     "mllm_router_pack")
         return out
 
-    def route(self, router, x, K, renorm, packed=None):
-        """Top-K routing of x [T][N] by the fp32 router [E][N] (device)."""
+    def route(self, router, x, K, renorm, packed=None, slices=True):
+        """Top-K routing of x [T][N] by the fp32 router [E][N] (device); slices=False
+        keeps one workgroup per token at T <= 8 (no workspace)."""
         torch = self.torch
         E, N = router.shape
         rp = self.router_pack(router) if packed is None else packed
         T = x.numel() // N
         idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
         w = torch.empty((T, K), dtype=torch.float32, device=x.device)
+        ws = torch.empty(self.so.mllm_route_workspace_size(T, E) // 4, dtype=torch.float32, device=x.device) \
+            if slices else None
         self._check(self.so.mllm_route(rp.data_ptr(), x.data_ptr(), T, N, E, K, int(renorm), idx.data_ptr(),
-                                       w.data_ptr(), self._stream()), "mllm_route")
+                                       w.data_ptr(), ws.data_ptr() if ws is not None else None, self._stream()),
+                    "mllm_route")
         return idx, w
 
     def dequant(self, sem, packed, n_rows, n_cols):

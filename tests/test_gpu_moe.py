@@ -93,18 +93,19 @@ def test_golden_route_selection_bitexact(lib, golden, tag):
     assert O.norm_err(ffn, g["ffn"]) < MOE_TOL
 
 
-@pytest.mark.parametrize("T", [3, 300])
+@pytest.mark.parametrize("T,slices", [(3, True), (3, False), (300, True)])
 @pytest.mark.parametrize("E,N,Kk,renorm", [(32, 2880, 4, 0), (128, 2048, 8, 1), (8, 256, 2, 0), (256, 512, 16, 1),
-                                           (6, 250, 2, 1), (36, 2884, 4, 0), (30, 1000, 3, 0)])
-def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm, T):
-    """Both streamed variants (T <= 8, token groups), the any-shape fallback
-    (N not a multiple of 4) and a ragged last chunk (N % 8 == 4)."""
+                                           (6, 250, 2, 1), (36, 2884, 4, 0), (30, 1000, 3, 0), (64, 2880, 4, 1)])
+def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm, T, slices):
+    """The streamed variants (T <= 8 per token or over 32-expert slices, token
+    groups), the any-shape fallback (N not a multiple of 4) and a ragged last
+    chunk (N % 8 == 4)."""
     import torch
     rng = np.random.default_rng(E + N + T)
     rw = W.gen_router(rng, E, N)
     x = W.gen_x(rng, T, N)
     ri, rwt = orc.route(rw, x, Kk, renorm)
-    idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
+    idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm, slices=slices)
     assert np.array_equal(idx.cpu().numpy(), ri)
     assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
 

@@ -6,8 +6,11 @@
 // One decode GEMV launch.  A "job" is one matrix-vector product; blockIdx.y
 // walks the jobs.  Matrix of job j: `W` when `table` is null, otherwise
 // table[idx ? idx[j] : j] (device arrays).  x / out of job j start at
-// x + j*x_job_stride / out + j*out_job_stride (elements); token b of a job
-// reads x + b*ldx and writes out + b*ldo.
+// x + (j / job_div)*x_job_stride / out + j*out_job_stride (elements; job_div
+// 0 or 1 = one x per job); token b of a job reads x + b*ldx and writes
+// out + b*ldo.  With job_split > 0, jobs j >= job_split run as job
+// j - job_split of a second list (table2, out2), so two projections of the
+// same activations (MoE gate and up) share one launch.
 struct mllm_gemv_args {
     mllm_packed W;
     const mllm_packed *table;
@@ -21,7 +24,23 @@ struct mllm_gemv_args {
     int n_rows, n_cols, B;
     int k_tile;   // activation elements staged in LDS per pass (set by the launcher)
     mllm_xq xq;   // Q8_0 activation pack (Q8 semantics only); job/token strides follow x's
+    int job_div;
+    int job_split;
+    const mllm_packed *table2;
+    float *out2;
+    // fp32-activation semantics at B == 1: the activation is silu(x) * x_up
+    // (mllm_silu_mul, same offsets as x) instead of x.
+    const float *x_up;
 };
+
+// moe_forward_omp's SiLU product (QK:2157-2164): the gate clamped to +-80,
+// then silu(g) * u.  Every kernel that forms it uses this one expression.
+__device__ __forceinline__ float mllm_silu_mul(float g, float u)
+{
+    g = g < -80.0f ? -80.0f : g;
+    g = g > 80.0f ? 80.0f : g;
+    return (g / (1.0f + expf(-g))) * u;
+}
 
 hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStream_t st);
 
@@ -31,9 +50,11 @@ mllm_packed mllm_packed_view(int ly, const uint8_t *packed, int n_rows, int n_co
 
 // quantize_row_q8_0 over T rows of n_cols floats (QK:1406-1455), bit-exact.
 // Writes the raw 34-byte blocks to q8_raw (if non-null) and the activation
-// pack (q / d / s4 / sq) to the xq arrays (if non-null).
+// pack (q / d / s4 / sq) to the xq arrays (if non-null).  With x_up, the
+// rows quantised are mllm_silu_mul(x, x_up).
 hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t *q8_raw,
-                                     int8_t *xq_q, float *xq_d, float *xq_s4, int *xq_sq, hipStream_t st);
+                                     int8_t *xq_q, float *xq_d, float *xq_s4, int *xq_sq, hipStream_t st,
+                                     const float *x_up = nullptr);
 
 // Router: logits by a sequential fp32 FMA chain (CE:614-618), softmax with
 // expf, insertion top-k with strict '>' (CE:628-638), optional renormalise
@@ -49,7 +70,7 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st);
 
 // out[t][i] = sum_k (in k order) w[t][k] * d[t][k][i]; fused selects fmaf (moe_ffn CE:662) or
-// add-of-product (moe_forward_omp QK:2243-2244).
+// add-of-product (moe_forward_omp QK:2243-2244).  d == nullptr: every d term is 0.
 hipError_t mllm_launch_combine(const float *d, const float *w, int T, int K, int N, float *out, int fused,
                                hipStream_t st);
 

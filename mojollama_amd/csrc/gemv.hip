@@ -43,6 +43,8 @@ hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStr
 {
     if (a.B <= 0 || a.n_rows <= 0 || n_jobs <= 0) return hipSuccess;
     if (a.B > 8) return hipErrorInvalidValue;
+    if (a.x_up && (a.B != 1 || sem == SEM_F32 || mllm_sem_uses_q8(sem))) return hipErrorInvalidValue;
+    if (a.job_split > 0 && (a.job_split >= n_jobs || !a.out2 || (a.table && !a.table2))) return hipErrorInvalidValue;
     switch (sem) {
     case SEM_F32: launch_f32(a, n_jobs, st); break;
     case SEM_Q4_0: gemv_sem<SEM_Q4_0>(a, n_jobs, st); break;

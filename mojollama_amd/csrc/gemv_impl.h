@@ -36,14 +36,30 @@ MLLM_DEV float group_sum(float v)
     return v;
 }
 
-MLLM_DEV void resolve_job(const mllm_gemv_args &a, int job, mllm_packed &W)
+// Matrix, output and activation offsets of job `job` (blockIdx.y).
+struct job_view {
+    mllm_packed W;
+    float *out;
+    long xj;   // activation row index: x starts at xj * x_job_stride
+};
+
+MLLM_DEV job_view view_job(const mllm_gemv_args &a, int job)
 {
+    job_view v;
+    const bool second = a.job_split > 0 && job >= a.job_split;
+    if (second) job -= a.job_split;
+    v.out = (second ? a.out2 : a.out) + job * a.out_job_stride;
+    v.xj = a.job_div > 1 ? job / a.job_div : job;
+    // W is taken from the argument block only on the table-less path, so no
+    // address choice mixes the argument block with a table (which would put
+    // the kernel arguments in scratch memory)
     if (a.table) {
-        int e = a.idx ? a.idx[job] : job;
-        W = a.table[e < 0 ? 0 : e];
+        const int e = a.idx ? a.idx[job] : job;
+        v.W = (second ? a.table2 : a.table)[e < 0 ? 0 : e];
     } else {
-        W = a.W;
+        v.W = a.W;
     }
+    return v;
 }
 
 // ---------------------------------------------------------------- activation digits
@@ -85,11 +101,18 @@ __host__ __device__ inline digit_geom digit_geom_for(int KT)
 // their max and sum over DPP.
 constexpr int kStageSlots = 4;
 
-struct x_stage {
+template <bool SILU> struct x_stage {
     float4 v[kStageSlots][2];
 };
+// SiLU-product staging: the gate half in v, the up half in u.
+template <> struct x_stage<true> {
+    float4 v[kStageSlots][2];
+    float4 u[kStageSlots][2];
+};
 
-MLLM_DEV void stage_load(x_stage &st, const float *__restrict__ x, int ldx, int B, int k0, int kn, int pass)
+template <bool SILU>
+MLLM_DEV void stage_load(x_stage<SILU> &st, const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B,
+                         int k0, int kn, int pass)
 {
     const int nh = kn >> 3;
 #pragma unroll
@@ -104,6 +127,16 @@ MLLM_DEV void stage_load(x_stage &st, const float *__restrict__ x, int ldx, int 
             } else {
                 st.v[q][0] = make_float4(gld<float>(src), gld<float>(src + 1), gld<float>(src + 2), gld<float>(src + 3));
                 st.v[q][1] = make_float4(gld<float>(src + 4), gld<float>(src + 5), gld<float>(src + 6), gld<float>(src + 7));
+            }
+            if constexpr (SILU) {
+                const float *su = xu + (long)b * ldx + k0 + 8 * h;
+                if ((ldx & 3) == 0) {
+                    st.u[q][0] = gld<float4>(su);
+                    st.u[q][1] = gld<float4>(su + 4);
+                } else {
+                    st.u[q][0] = make_float4(gld<float>(su), gld<float>(su + 1), gld<float>(su + 2), gld<float>(su + 3));
+                    st.u[q][1] = make_float4(gld<float>(su + 4), gld<float>(su + 5), gld<float>(su + 6), gld<float>(su + 7));
+                }
             }
         }
     }
@@ -120,8 +153,8 @@ MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
     return lo | hi;
 }
 
-template <int SEM>
-MLLM_DEV void stage_store(const x_stage &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass)
+template <int SEM, bool SILU>
+MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass)
 {
     const int nh = kn >> 3;
     constexpr float M = 12582912.0f;   // 1.5 * 2^23: t = y + M holds rne(y) in its low mantissa bits
@@ -130,8 +163,14 @@ MLLM_DEV void stage_store(const x_stage &st, uint8_t *lds, const digit_geom &dg,
         const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
         if (idx >= B * nh) continue;       // B * nh is even: both halves of a group take the same path
         const int b = idx / nh, h = idx - b * nh, g = h >> 1, half = h & 1;
-        const float v[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
-                            st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
+        float v[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
+                      st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
+        if constexpr (SILU) {
+            const float u[8] = {st.u[q][0].x, st.u[q][0].y, st.u[q][0].z, st.u[q][0].w,
+                                st.u[q][1].x, st.u[q][1].y, st.u[q][1].z, st.u[q][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = mllm_silu_mul(v[e], u[e]);
+        }
         float m = 0.0f, sum = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) { m = fmaxf(m, fabsf(v[e])); sum += v[e]; }
@@ -170,14 +209,14 @@ MLLM_DEV void stage_store(const x_stage &st, uint8_t *lds, const digit_geom &dg,
 
 // Stage tokens b < B, elements [k0, k0+kn), as digits; load_first = a pass-0
 // load already issued by the caller.
-template <int SEM>
-MLLM_DEV void stage_digits(x_stage &st, bool load_first, uint8_t *lds, const digit_geom &dg,
-                           const float *__restrict__ x, int ldx, int B, int k0, int kn)
+template <int SEM, bool SILU>
+MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, const digit_geom &dg,
+                           const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B, int k0, int kn)
 {
     const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
     for (int pass = 0; pass < passes; pass++) {
-        if (pass || !load_first) stage_load(st, x, ldx, B, k0, kn, pass);
-        stage_store<SEM>(st, lds, dg, B, kn, pass);
+        if (pass || !load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
+        stage_store<SEM, SILU>(st, lds, dg, B, kn, pass);
     }
 }
 
@@ -289,17 +328,17 @@ MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const uint8_t *xl, co
 }
 
 // fp32-activation semantics, K tiled through LDS (used when B*K does not fit)
-template <int SEM, int BM, int R, int LPR>
+template <int SEM, int BM, int R, int LPR, bool SILU>
 __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
 {
     extern __shared__ uint4 xl4[];
     uint8_t *xl = reinterpret_cast<uint8_t *>(xl4);
     constexpr int BE = sem_traits<SEM>::kBlockElems, CPB = sem_traits<SEM>::kChunksPerBlock;
-    const int job = blockIdx.y;
-    mllm_packed W;
-    resolve_job(a, job, W);
-    const float *__restrict__ x = a.x + job * a.x_job_stride;
-    float *__restrict__ out = a.out + job * a.out_job_stride;
+    const job_view jv = view_job(a, blockIdx.y);
+    const mllm_packed W = jv.W;
+    const float *__restrict__ x = a.x + jv.xj * a.x_job_stride;
+    const float *__restrict__ xu = SILU ? a.x_up + jv.xj * a.x_job_stride : nullptr;
+    float *__restrict__ out = jv.out;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane / LPR, sl = lane % LPR;
@@ -319,8 +358,8 @@ __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
     for (int k0 = 0; k0 < kused; k0 += KT) {
         const int kn = min(KT, kused - k0);
         if (k0) __syncthreads();
-        x_stage xst;
-        stage_digits<SEM>(xst, false, xl, dg, x, a.ldx, B, k0, kn);
+        x_stage<SILU> xst;
+        stage_digits<SEM, SILU>(xst, false, xl, dg, x, xu, a.ldx, B, k0, kn);
         __syncthreads();
         const int c_end = (k0 + kn) / BE * CPB;
         for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
@@ -399,12 +438,11 @@ __global__ __launch_bounds__(256) void k_gemv_q8(mllm_gemv_args a)
 {
     extern __shared__ float xl[];
     constexpr int BE = q8_traits<SEM>::kBlockElems, CPB = q8_traits<SEM>::kChunksPerBlock;
-    const int job = blockIdx.y;
-    mllm_packed W;
-    resolve_job(a, job, W);
-    float *__restrict__ out = a.out + job * a.out_job_stride;
-    const long q_job = job * a.x_job_stride;          // elements
-    const long b_job = job * (a.x_job_stride / 32);   // 32-blocks
+    const job_view jv = view_job(a, blockIdx.y);
+    const mllm_packed W = jv.W;
+    float *__restrict__ out = jv.out;
+    const long q_job = jv.xj * a.x_job_stride;          // elements
+    const long b_job = jv.xj * (a.x_job_stride / 32);   // 32-blocks
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane / LPR, sl = lane % LPR;
@@ -458,16 +496,16 @@ template <int SEM, bool Q8> struct gemv_geom {
     static constexpr int CPB = Q8 ? q8_traits<SEM>::kChunksPerBlock : sem_traits<SEM>::kChunksPerBlock;
 };
 
-template <int SEM, bool Q8, int BM, int R, int LPR>
+template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU>
 __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 {
+    static_assert(!(Q8 && SILU), "the SiLU product of Q8_0 activations is formed by the quantiser");
     extern __shared__ float xl[];
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
     constexpr int RPW = (64 / LPR) * R;                 // rows per wave and step
-    const int job = blockIdx.y;
-    mllm_packed W;
-    resolve_job(a, job, W);
-    float *__restrict__ out = a.out + job * a.out_job_stride;
+    const job_view jv = view_job(a, blockIdx.y);
+    const mllm_packed W = jv.W;
+    float *__restrict__ out = jv.out;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane / LPR, sl = lane % LPR;
@@ -536,15 +574,16 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     int rg = rg0, it = 0;
     if constexpr (Q8) {
         fetch_step(min(rg, nrg - 1), it, bufA);
-        stage_q8(xl, a.xq, job * a.x_job_stride, job * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride, 0,
+        stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride, 0,
                  kused);
     } else {
         // activation loads first, then the weights; the digits are computed while the weights are in flight
-        x_stage xst;
-        const float *xj = a.x + job * a.x_job_stride;
-        stage_load(xst, xj, a.ldx, B, 0, kused, 0);
+        x_stage<SILU> xst;
+        const float *xj = a.x + jv.xj * a.x_job_stride;
+        const float *xuj = SILU ? a.x_up + jv.xj * a.x_job_stride : nullptr;
+        stage_load<SILU>(xst, xj, xuj, a.ldx, B, 0, kused, 0);
         fetch_step(min(rg, nrg - 1), it, bufA);
-        stage_digits<SEM>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, a.ldx, B, 0, kused);
+        stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused);
     }
     __syncthreads();
     if (rg >= nrg) return;
@@ -567,10 +606,10 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 template <int BM>
 __global__ __launch_bounds__(256) void k_gemv_f32(mllm_gemv_args a)
 {
-    const int job = blockIdx.y;
-    const float *Wf = reinterpret_cast<const float *>(a.table ? a.table[a.idx ? a.idx[job] : job].p[0] : a.W.p[0]);
-    const float *x = a.x + job * a.x_job_stride;
-    float *out = a.out + job * a.out_job_stride;
+    const job_view jv = view_job(a, blockIdx.y);
+    const float *Wf = reinterpret_cast<const float *>(jv.W.p[0]);
+    const float *x = a.x + jv.xj * a.x_job_stride;
+    float *out = jv.out;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row = blockIdx.x * 4 + wave;
     if (row >= a.n_rows) return;
@@ -641,6 +680,32 @@ inline int device_cus()
 
 constexpr size_t kPersistentLds = 72 * 1024;
 
+template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU>
+void launch_lpr(bool persistent, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
+{
+    if (persistent) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, LPR, SILU>), grid, dim3(256), lds, st, a);
+    else if constexpr (Q8) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, LPR>), grid, dim3(256), lds, st, a);
+    else hipLaunchKernelGGL((k_gemv<SEM, BM, R, LPR, SILU>), grid, dim3(256), lds, st, a);
+}
+
+// The SiLU-product form exists for fp32-activation semantics at B == 1 only
+// (the caller checks).
+template <int SEM, bool Q8, int BM, int R>
+void launch_shape(bool persistent, int lpr, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
+{
+    if constexpr (!Q8 && BM == 1) {
+        if (a.x_up) {
+            if (lpr == 64) launch_lpr<SEM, Q8, BM, R, 64, true>(persistent, grid, lds, a, st);
+            else if (lpr == 32) launch_lpr<SEM, Q8, BM, R, 32, true>(persistent, grid, lds, a, st);
+            else launch_lpr<SEM, Q8, BM, R, 16, true>(persistent, grid, lds, a, st);
+            return;
+        }
+    }
+    if (lpr == 64) launch_lpr<SEM, Q8, BM, R, 64, false>(persistent, grid, lds, a, st);
+    else if (lpr == 32) launch_lpr<SEM, Q8, BM, R, 32, false>(persistent, grid, lds, a, st);
+    else launch_lpr<SEM, Q8, BM, R, 16, false>(persistent, grid, lds, a, st);
+}
+
 template <int SEM, int BM>
 void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
 {
@@ -672,10 +737,7 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     if (lds_p <= kPersistentLds) {
         const int per_cu = lds_p <= 40 * 1024 ? 3 : 2;
         const int wgs = std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs)));
-        dim3 grid(wgs, n_jobs);
-        if (lpr == 64) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64>), grid, dim3(256), lds_p, st, a);
-        else if (lpr == 32) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 32>), grid, dim3(256), lds_p, st, a);
-        else hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 16>), grid, dim3(256), lds_p, st, a);
+        launch_shape<SEM, Q8, BM, R>(true, lpr, dim3(wgs, n_jobs), lds_p, a, st);
         return;
     }
     // K tiled through 48 KB of LDS
@@ -685,16 +747,7 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     if (kt < 256) kt = 256;
     a.k_tile = kt;
     const size_t lds = Q8 ? (size_t)BM * (kt + kt / 16 + 8 * (kt / 32)) : (size_t)BM * digit_geom_for(kt).tstride;
-    dim3 grid(wg_needed, n_jobs);
-    if constexpr (Q8) {
-        if (lpr == 64) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 64>), grid, dim3(256), lds, st, a);
-        else if (lpr == 32) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 32>), grid, dim3(256), lds, st, a);
-        else hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, 16>), grid, dim3(256), lds, st, a);
-    } else {
-        if (lpr == 64) hipLaunchKernelGGL((k_gemv<SEM, BM, R, 64>), grid, dim3(256), lds, st, a);
-        else if (lpr == 32) hipLaunchKernelGGL((k_gemv<SEM, BM, R, 32>), grid, dim3(256), lds, st, a);
-        else hipLaunchKernelGGL((k_gemv<SEM, BM, R, 16>), grid, dim3(256), lds, st, a);
-    }
+    launch_shape<SEM, Q8, BM, R>(false, lpr, dim3(wg_needed, n_jobs), lds, a, st);
 }
 
 // Launch the GEMV of one semantic for B = a.B (1..8).

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(1024) void k_bucket(const int *__restrict__ idx, in
 }
 
 // out[t][n] = sum over k (in order) of w[t][k] * dn[pos_of[t*K+k]][n], as
-// moe_forward_omp's combined[row] += top_weight * dot (QK:2243-2244).
+// moe_forward_omp's combined[row] += top_weight * dot (QK:2243-2244); every dn
+// term is 0 when dn is null (a down type the reference leaves at zero).
 __global__ void k_combine_pos(const float *__restrict__ dn, const float *__restrict__ w,
                               const int *__restrict__ pos_of, int K, int N, float *__restrict__ out)
 {
@@ -130,7 +131,7 @@ __global__ void k_combine_pos(const float *__restrict__ dn, const float *__restr
     float acc = 0.0f;
     for (int k = 0; k < K; k++) {
         const int pos = pos_of[t * K + k];
-        if (pos >= 0) acc += w[t * K + k] * dn[(long)pos * N + n];
+        if (pos >= 0) acc += w[t * K + k] * (dn ? dn[(long)pos * N + n] : 0.0f);
     }
     out[(long)t * N + n] = acc;
 }
@@ -339,43 +340,47 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             b.n_rows = N; b.n_cols = M;
             b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;
             CK(mllm_launch_qgemm(L->sem_d, xmode_of(L->sem_d), false, b, max_tiles, st));
-        } else {
-            CK(hipMemsetAsync(s.dn, 0, (size_t)TK * N * 4, st));
         }
-        hipLaunchKernelGGL(k_combine_pos, dim3((N + 255) / 256, T), dim3(256), 0, st, s.dn, s.w, s.pos_of, K, N, out);
+        hipLaunchKernelGGL(k_combine_pos, dim3((N + 255) / 256, T), dim3(256), 0, st, L->sem_d >= 0 ? s.dn : nullptr,
+                           s.w, s.pos_of, K, N, out);
         CK(hipGetLastError());
     } else {
-        // decode: per token, one GEMV job per routing slot (expert picked on the device)
-        for (int t = 0; t < T; t++) {
-            for (int wch = 0; wch < 2; wch++) {
-                mllm_gemv_args a{};
-                a.table = L->tab + (size_t)wch * E; a.idx = s.idx + (size_t)t * K;
-                a.x = x + (size_t)t * N; a.x_job_stride = 0; a.ldx = N;
-                a.out = (wch == 0 ? s.g : s.u) + (size_t)t * K * M; a.out_job_stride = M; a.ldo = M;
-                a.n_rows = M; a.n_cols = N; a.B = 1;
-                const long nb = N / 32;
-                a.xq = {q + (size_t)t * nb * 32, d + t * nb, s4 + t * nb, sq + t * nb};
-                CK(mllm_launch_gemv(wch == 0 ? L->sem_g : L->sem_u, a, K, st));
-            }
-        }
-        CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
-        if (L->sem_d >= 0) {
-            if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
-            for (int t = 0; t < T; t++) {
-                mllm_gemv_args a{};
-                a.table = L->tab + 2 * (size_t)E; a.idx = s.idx + (size_t)t * K;
-                a.x = s.h + (size_t)t * K * M; a.x_job_stride = M; a.ldx = M;
-                a.out = s.dn + (size_t)t * K * N; a.out_job_stride = N; a.ldo = N;
-                a.n_rows = N; a.n_cols = M; a.B = 1;
-                const long nb = M / 32;
-                a.xq = {hq + (size_t)t * K * nb * 32, hd + (size_t)t * K * nb, hs4 + (size_t)t * K * nb,
-                        hsq + (size_t)t * K * nb};
-                CK(mllm_launch_gemv(L->sem_d, a, K, st));
-            }
+        // decode: one GEMV launch per projection over all T*K (token, slot)
+        // jobs, the expert picked on the device; gate and up share a launch
+        // when their semantics agree, and the SiLU product is formed while
+        // the down projection stages its activations (or quantises them)
+        mllm_gemv_args a{};
+        a.table = L->tab; a.idx = s.idx; a.job_div = K;
+        a.x = x; a.x_job_stride = N; a.ldx = N;
+        a.out = s.g; a.out_job_stride = M; a.ldo = M;
+        a.n_rows = M; a.n_cols = N; a.B = 1;
+        a.xq = xqx;
+        if (L->sem_g == L->sem_u) {
+            a.job_split = TK; a.table2 = L->tab + E; a.out2 = s.u;
+            CK(mllm_launch_gemv(L->sem_g, a, 2 * TK, st));
         } else {
-            CK(hipMemsetAsync(s.dn, 0, (size_t)TK * N * 4, st));
+            CK(mllm_launch_gemv(L->sem_g, a, TK, st));
+            a.table = L->tab + E; a.out = s.u;
+            CK(mllm_launch_gemv(L->sem_u, a, TK, st));
         }
-        CK(mllm_launch_combine(s.dn, s.w, T, K, N, out, 0, st));
+        if (L->sem_d >= 0) {
+            mllm_gemv_args b{};
+            b.table = L->tab + 2 * (size_t)E; b.idx = s.idx;
+            b.x = s.g; b.x_job_stride = M; b.ldx = M;
+            b.out = s.dn; b.out_job_stride = N; b.ldo = N;
+            b.n_rows = N; b.n_cols = M; b.B = 1;
+            if (mllm_sem_uses_q8(L->sem_d)) {
+                CK(mllm_launch_quantize_q8_0(s.g, TK, M, nullptr, hq, hd, hs4, hsq, st, s.u));
+                b.xq = xqh;
+            } else if (L->sem_d == SEM_F32) {
+                CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
+                b.x = s.h;
+            } else {
+                b.x_up = s.u;
+            }
+            CK(mllm_launch_gemv(L->sem_d, b, TK, st));
+        }
+        CK(mllm_launch_combine(L->sem_d >= 0 ? s.dn : nullptr, s.w, T, K, N, out, 0, st));
     }
     if (idx_out) CK(hipMemcpyAsync(idx_out, s.idx, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
     if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));

@@ -78,7 +78,7 @@ __global__ void k_pack(int ly, const uint8_t *__restrict__ raw, uint8_t *__restr
 // stored as fp16 RNE.
 __global__ void k_quantize_q8_0(const float *__restrict__ x, int T, int n_cols, uint8_t *__restrict__ q8_raw,
                                 int8_t *__restrict__ xq_q, float *__restrict__ xq_d, float *__restrict__ xq_s4,
-                                int *__restrict__ xq_sq)
+                                int *__restrict__ xq_sq, const float *__restrict__ x_up)
 {
     const int nb = n_cols / 32;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -86,8 +86,14 @@ __global__ void k_quantize_q8_0(const float *__restrict__ x, int T, int n_cols, 
     const long t = i / nb, j = i % nb;
     const float *s = x + t * (long)n_cols + 32 * j;
     float v[32];
+    if (x_up) {
+        const float *su = x_up + t * (long)n_cols + 32 * j;
 #pragma unroll
-    for (int k = 0; k < 32; k++) v[k] = s[k];
+        for (int k = 0; k < 32; k++) v[k] = mllm_silu_mul(s[k], su[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; k++) v[k] = s[k];
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 32; k++) { float a = fabsf(v[k]); amax = (a > amax) ? a : amax; }
@@ -400,9 +406,8 @@ __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict_
 {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float gv = g[i];
-    if (clamp) { gv = gv < -80.0f ? -80.0f : gv; gv = gv > 80.0f ? 80.0f : gv; }
-    h[i] = (gv / (1.0f + expf(-gv))) * u[i];
+    const float gv = g[i];
+    h[i] = clamp ? mllm_silu_mul(gv, u[i]) : (gv / (1.0f + expf(-gv))) * u[i];
 }
 
 __global__ void k_combine(const float *__restrict__ d, const float *__restrict__ w, int K, int N,
@@ -413,7 +418,7 @@ __global__ void k_combine(const float *__restrict__ d, const float *__restrict__
     if (i >= N) return;
     float acc = 0.0f;
     for (int k = 0; k < K; k++) {
-        const float wk = w[(long)t * K + k], dv = d[((long)t * K + k) * N + i];
+        const float wk = w[(long)t * K + k], dv = d ? d[((long)t * K + k) * N + i] : 0.0f;
         acc = fused ? fmaf(wk, dv, acc) : acc + wk * dv;
     }
     out[(long)t * N + i] = acc;
@@ -447,12 +452,12 @@ hipError_t mllm_launch_pack(int ly, const uint8_t *raw, uint8_t *packed, int n_r
 }
 
 hipError_t mllm_launch_quantize_q8_0(const float *x, int T, int n_cols, uint8_t *q8_raw, int8_t *xq_q, float *xq_d,
-                                     float *xq_s4, int *xq_sq, hipStream_t st)
+                                     float *xq_s4, int *xq_sq, hipStream_t st, const float *x_up)
 {
     const long n = (long)T * (n_cols / 32);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, x, T, n_cols, q8_raw,
-                       xq_q, xq_d, xq_s4, xq_sq);
+                       xq_q, xq_d, xq_s4, xq_sq, x_up);
     return hipGetLastError();
 }
 

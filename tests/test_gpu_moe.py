@@ -226,6 +226,26 @@ def test_moe_layer_small_vs_oracle(dev, orc, qts, T):
     assert O.norm_err(got, ref) < moe_tol(qts)
 
 
+@pytest.mark.parametrize("qts", [(12, 14, 6), (2, 3, 12), (6, 6, 2), (39, 39, 39), (14, 14, 14)])
+@pytest.mark.parametrize("T", [2, 8])
+def test_moe_layer_decode_vs_oracle(dev, orc, qts, T):
+    """Decode path (T <= 8): one launch over all T*K (token, slot) jobs, gate and up fused when their
+    semantics agree ((2, 3) and (12, 14) run two launches), the SiLU product formed by the down
+    projection's staging (fp32 activations) or its Q8_0 quantiser (MXFP4), Q4_K down left at zero."""
+    got, ref = _moe_case(dev, orc, qts, N=512, M=256, E=16, Kk=4, T=T, renorm=T % 2, seed=11 * T + sum(qts))
+    if qts[2] == 12:
+        assert not np.any(got) and not np.any(ref)
+        return
+    assert O.norm_err(got, ref) < moe_tol(qts)
+
+
+@pytest.mark.parametrize("qts,N,M,Kk,T", [((39, 39, 39), 2880, 2880, 4, 1), ((12, 12, 14), 2048, 768, 8, 8)])
+def test_moe_layer_decode_real_shapes(dev, orc, qts, N, M, Kk, T):
+    """GPT-OSS-20B (batch 1) and Qwen3-30B-A3B (batch 8) expert shapes on the decode path."""
+    got, ref = _moe_case(dev, orc, qts, N=N, M=M, E=16, Kk=Kk, T=T, renorm=int(qts[0] == 12), seed=T + N)
+    assert O.norm_err(got, ref) < moe_tol(qts)
+
+
 def test_moe_layer_gptoss_shape(dev, orc):
     """GPT-OSS-20B expert shapes (N = M = 2880, MXFP4, top-4), batched path."""
     got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=24, renorm=1, seed=4)

@@ -292,12 +292,14 @@ size_t planes_bytes(int sem, long rows, int n_cols)
     return align256((size_t)act_nplanes(sem) * act_planes_elems(rows, n_cols) * 2) + align256(rows * 4);
 }
 
-// Scratch of run_gemv: Q8_0 activation pack, split planes, split-K partials.
+// Scratch of run_gemv's GEMM path (B > 8): Q8_0 activation pack, split
+// planes, split-K partials.  The GEMV path needs none (Q8_0 activations are
+// quantised by the GEMV workgroups).
 size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
 {
-    const bool gemm = B > 8 && mllm_qgemm_supported(sem);
+    if (!(B > 8 && mllm_qgemm_supported(sem))) return 0;
     return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0) +
-           (gemm ? align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4) : 0);
+           align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4);
 }
 
 // Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data.
@@ -305,13 +307,13 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
              void *scratch, hipStream_t st)
 {
     const bool q8 = mllm_sem_uses_q8(sem);
-    xq_bufs xb{};
-    if (q8) {
-        xb = xq_carve(scratch, B, n_cols);
-        HIP_OK(mllm_launch_quantize_q8_0(x, B, n_cols, nullptr, xb.q, xb.d, xb.s4, xb.sq, st));
-    }
     if (B > 8 && mllm_qgemm_supported(sem)) {
         // prefill / batched: quantised-weight MFMA GEMM over the B tokens
+        xq_bufs xb{};
+        if (q8) {
+            xb = xq_carve(scratch, B, n_cols);
+            HIP_OK(mllm_launch_quantize_q8_0(x, B, n_cols, nullptr, xb.q, xb.d, xb.s4, xb.sq, st));
+        }
         qgemm_args g{};
         g.W = W;
         if (q8) g.xq = {xb.q, xb.d, xb.s4, xb.sq};
@@ -339,10 +341,6 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
         a.out = out + (long)b0 * n_rows;
         a.ldo = n_rows;
         a.n_rows = n_rows; a.n_cols = n_cols; a.B = B - b0 < 8 ? B - b0 : 8;
-        if (q8) {
-            const long nb = n_cols / 32;
-            a.xq = {xb.q + (long)b0 * n_cols, xb.d + b0 * nb, xb.s4 + b0 * nb, xb.sq + b0 * nb};
-        }
         HIP_OK(mllm_launch_gemv(sem, a, 1, st));
     }
     return 0;
@@ -539,11 +537,10 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         if (su >= 0 && get_weight(up_raw[e], mllm_sem_layout(su), F, N, tab[K + k])) return;
         if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k])) return;
     }
-    // device scratch: x | g[K][F] | u[K][F] | h[K][F] | dn[K][N] | w[K] | xq(x) | xq(h)
+    // device scratch: x | g[K][F] | u[K][F] | h[K][F] | dn[K][N] | w[K]
     size_t o_x = 0, o_g = align256(o_x + N * 4), o_u = align256(o_g + (size_t)K * F * 4),
            o_h = align256(o_u + (size_t)K * F * 4), o_dn = align256(o_h + (size_t)K * F * 4),
-           o_w = align256(o_dn + (size_t)K * N * 4), o_xq = align256(o_w + K * 4),
-           o_hq = align256(o_xq + xq_bytes(1, N)), total = align256(o_hq + xq_bytes(K, F));
+           o_w = align256(o_dn + (size_t)K * N * 4), total = align256(o_w + K * 4);
     if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
         c.h_in.ensure(N * 4 + K * 4 + tab.size() * sizeof(mllm_packed)) || c.h_out.ensure(N * 4)) {
         set_error("moe_forward_omp: scratch allocation failed");
@@ -562,33 +559,37 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
     CK(hipMemcpyAsync(dx, hin, N * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(dw, hin + N * 4, K * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(dtab, hin + N * 4 + K * 4, tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
-    xq_bufs xqx = xq_carve(S + o_xq, 1, N), xqh = xq_carve(S + o_hq, K, F);
-    if (mllm_sem_uses_q8(sg) || mllm_sem_uses_q8(su))
-        CK(mllm_launch_quantize_q8_0(dx, 1, N, nullptr, xqx.q, xqx.d, xqx.s4, xqx.sq, st));
-    auto gu = [&](int sem, const mllm_packed *t, float *out) -> hipError_t {
-        if (sem < 0) return hipMemsetAsync(out, 0, (size_t)K * F * 4, st);
-        mllm_gemv_args a{};
-        a.table = t; a.x = dx; a.x_job_stride = 0; a.ldx = N;
-        a.out = out; a.out_job_stride = F; a.ldo = F;
-        a.n_rows = F; a.n_cols = N; a.B = 1;
-        a.xq = {xqx.q, xqx.d, xqx.s4, xqx.sq};
-        return mllm_launch_gemv(sem, a, K, st);
-    };
-    CK(gu(sg, dtab, dg));
-    CK(gu(su, dtab + K, du));
-    CK(mllm_launch_silu_mul(dg, du, dh, (long)K * F, 1, st));
-    if (sd < 0) {
-        CK(hipMemsetAsync(ddn, 0, (size_t)K * N * 4, st));
+    // gate and up in one launch when their semantics agree; Q8_0 activations
+    // quantised by the GEMV workgroups; silu(g) * u formed by the down
+    // projection's staging (fp32 activations) or its quantisation (Q8_0)
+    mllm_gemv_args a{};
+    a.table = dtab; a.x = dx; a.x_job_stride = 0; a.ldx = N;
+    a.out = dg; a.out_job_stride = F; a.ldo = F;
+    a.n_rows = F; a.n_cols = N; a.B = 1;
+    if (sg >= 0 && sg == su) {
+        a.job_split = K; a.table2 = dtab + K; a.out2 = du;
+        CK(mllm_launch_gemv(sg, a, 2 * K, st));
     } else {
-        if (mllm_sem_uses_q8(sd)) CK(mllm_launch_quantize_q8_0(dh, K, F, nullptr, xqh.q, xqh.d, xqh.s4, xqh.sq, st));
-        mllm_gemv_args a{};
-        a.table = dtab + 2 * K; a.x = dh; a.x_job_stride = F; a.ldx = F;
-        a.out = ddn; a.out_job_stride = N; a.ldo = N;
-        a.n_rows = N; a.n_cols = F; a.B = 1;
-        a.xq = {xqh.q, xqh.d, xqh.s4, xqh.sq};
-        CK(mllm_launch_gemv(sd, a, K, st));
+        if (sg >= 0) CK(mllm_launch_gemv(sg, a, K, st));
+        else CK(hipMemsetAsync(dg, 0, (size_t)K * F * 4, st));
+        a.table = dtab + K; a.out = du;
+        if (su >= 0) CK(mllm_launch_gemv(su, a, K, st));
+        else CK(hipMemsetAsync(du, 0, (size_t)K * F * 4, st));
     }
-    CK(mllm_launch_combine(ddn, dw, 1, K, N, dx, 0, st));
+    if (sd >= 0) {
+        mllm_gemv_args b{};
+        b.table = dtab + 2 * K; b.x = dg; b.x_job_stride = F; b.ldx = F;
+        b.out = ddn; b.out_job_stride = N; b.ldo = N;
+        b.n_rows = N; b.n_cols = F; b.B = 1;
+        if (sd == SEM_F32) {
+            CK(mllm_launch_silu_mul(dg, du, dh, (long)K * F, 1, st));
+            b.x = dh;
+        } else {
+            b.x_up = du;
+        }
+        CK(mllm_launch_gemv(sd, b, K, st));
+    }
+    CK(mllm_launch_combine(sd >= 0 ? ddn : nullptr, dw, 1, K, N, dx, 0, st));
     CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
 #undef CK
@@ -736,12 +737,12 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     }
     const float *rt = nullptr;
     if (get_router(router, E, N, &rt)) return -1;
-    // scratch: x[T][N] | idx[T][K] | w[T][K] | g,u,h [T*K][M] | dn [T*K][N] | out[T][N] | xq(x) | xq(h)
+    // scratch: x[T][N] | idx[T][K] | w[T][K] | g,u,h [T*K][M] | dn [T*K][N] | out[T][N] | routing logits
     const size_t TK = (size_t)T * K;
     size_t o_x = 0, o_i = align256(o_x + (size_t)T * N * 4), o_w = align256(o_i + TK * 4), o_g = align256(o_w + TK * 4),
            o_u = align256(o_g + TK * M * 4), o_h = align256(o_u + TK * M * 4), o_dn = align256(o_h + TK * M * 4),
-           o_o = align256(o_dn + TK * N * 4), o_xq = align256(o_o + (size_t)T * N * 4),
-           o_hq = align256(o_xq + xq_bytes(T, N)), total = align256(o_hq + xq_bytes(TK, M));
+           o_o = align256(o_dn + TK * N * 4), o_l = align256(o_o + (size_t)T * N * 4),
+           total = align256(o_l + (size_t)mllm_route_workspace_floats(T, E) * 4);
     if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
         c.h_in.ensure((size_t)T * N * 4) || c.h_out.ensure((size_t)T * N * 4)) {
         set_error("moe_ffn: scratch allocation failed");
@@ -756,34 +757,30 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
     HIP_OK(hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st));
     HIP_OK(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
-    HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, nullptr, st));
-    xq_bufs xqx = xq_carve(S + o_xq, T, N), xqh = xq_carve(S + o_hq, (long)TK, M);
-    if (mllm_sem_uses_q8(sems[0]) || mllm_sem_uses_q8(sems[1]))
-        HIP_OK(mllm_launch_quantize_q8_0(dx, T, N, nullptr, xqx.q, xqx.d, xqx.s4, xqx.sq, st));
-    for (int t = 0; t < T; t++) {
-        for (int w = 0; w < 2; w++) {
-            mllm_gemv_args a{};
-            a.table = dtab + (size_t)w * E; a.idx = didx + (size_t)t * K;
-            a.x = dx + (size_t)t * N; a.x_job_stride = 0; a.ldx = N;
-            a.out = (w == 0 ? dg : du) + (size_t)t * K * M; a.out_job_stride = M; a.ldo = M;
-            a.n_rows = M; a.n_cols = N; a.B = 1;
-            const long nb = N / 32;
-            a.xq = {xqx.q + (size_t)t * N, xqx.d + t * nb, xqx.s4 + t * nb, xqx.sq + t * nb};
-            HIP_OK(mllm_launch_gemv(sems[w], a, K, st));
-        }
+    HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, (float *)(S + o_l), st));
+    // one GEMV launch per projection over the T*K (token, slot) jobs, gate
+    // and up together when their semantics agree; Q8_0 activations quantised
+    // by the GEMV workgroups.  The SiLU here is unclamped (CE:649-652).
+    mllm_gemv_args a{};
+    a.table = dtab; a.idx = didx; a.job_div = K;
+    a.x = dx; a.x_job_stride = N; a.ldx = N;
+    a.out = dg; a.out_job_stride = M; a.ldo = M;
+    a.n_rows = M; a.n_cols = N; a.B = 1;
+    if (sems[0] == sems[1]) {
+        a.job_split = (int)TK; a.table2 = dtab + E; a.out2 = du;
+        HIP_OK(mllm_launch_gemv(sems[0], a, 2 * (int)TK, st));
+    } else {
+        HIP_OK(mllm_launch_gemv(sems[0], a, (int)TK, st));
+        a.table = dtab + E; a.out = du;
+        HIP_OK(mllm_launch_gemv(sems[1], a, (int)TK, st));
     }
     HIP_OK(mllm_launch_silu_mul(dg, du, dh, (long)TK * M, 0, st));
-    if (mllm_sem_uses_q8(sems[2])) HIP_OK(mllm_launch_quantize_q8_0(dh, (int)TK, M, nullptr, xqh.q, xqh.d, xqh.s4, xqh.sq, st));
-    for (int t = 0; t < T; t++) {
-        mllm_gemv_args a{};
-        a.table = dtab + 2 * (size_t)E; a.idx = didx + (size_t)t * K;
-        a.x = dh + (size_t)t * K * M; a.x_job_stride = M; a.ldx = M;
-        a.out = ddn + (size_t)t * K * N; a.out_job_stride = N; a.ldo = N;
-        a.n_rows = N; a.n_cols = M; a.B = 1;
-        const long nb = M / 32;
-        a.xq = {xqh.q + (size_t)t * K * M, xqh.d + t * K * nb, xqh.s4 + t * K * nb, xqh.sq + t * K * nb};
-        HIP_OK(mllm_launch_gemv(sems[2], a, K, st));
-    }
+    mllm_gemv_args b{};
+    b.table = dtab + 2 * (size_t)E; b.idx = didx;
+    b.x = dh; b.x_job_stride = M; b.ldx = M;
+    b.out = ddn; b.out_job_stride = N; b.ldo = N;
+    b.n_rows = N; b.n_cols = M; b.B = 1;
+    HIP_OK(mllm_launch_gemv(sems[2], b, (int)TK, st));
     HIP_OK(mllm_launch_combine(ddn, dwt, T, K, N, dout, 1, st));
     HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
     HIP_OK(hipStreamSynchronize(st));

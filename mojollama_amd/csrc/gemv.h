@@ -23,13 +23,15 @@ struct mllm_gemv_args {
     int ldo;
     int n_rows, n_cols, B;
     int k_tile;   // activation elements staged in LDS per pass (set by the launcher)
-    mllm_xq xq;   // Q8_0 activation pack (Q8 semantics only); job/token strides follow x's
+    mllm_xq xq;   // Q8_0 activation pack (Q8 semantics); job/token strides follow x's.
+                  // xq.q == nullptr: each workgroup quantises x (fp32) itself.
     int job_div;
     int job_split;
     const mllm_packed *table2;
     float *out2;
-    // fp32-activation semantics at B == 1: the activation is silu(x) * x_up
-    // (mllm_silu_mul, same offsets as x) instead of x.
+    // The activation is silu(x) * x_up (mllm_silu_mul, same offsets as x)
+    // instead of x: fp32-activation semantics at B == 1, and Q8 semantics
+    // quantising in the kernel.
     const float *x_up;
 };
 

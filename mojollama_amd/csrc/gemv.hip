@@ -43,7 +43,11 @@ hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStr
 {
     if (a.B <= 0 || a.n_rows <= 0 || n_jobs <= 0) return hipSuccess;
     if (a.B > 8) return hipErrorInvalidValue;
-    if (a.x_up && (a.B != 1 || sem == SEM_F32 || mllm_sem_uses_q8(sem))) return hipErrorInvalidValue;
+    // x_up: the SiLU product, formed in the digit staging (fp32-activation
+    // semantics, B == 1) or in the in-kernel Q8_0 quantisation (Q8 semantics
+    // with no precomputed pack).
+    if (a.x_up && (sem == SEM_F32 || (mllm_sem_uses_q8(sem) ? a.xq.q != nullptr : a.B != 1)))
+        return hipErrorInvalidValue;
     if (a.job_split > 0 && (a.job_split >= n_jobs || !a.out2 || (a.table && !a.table2))) return hipErrorInvalidValue;
     switch (sem) {
     case SEM_F32: launch_f32(a, n_jobs, st); break;

@@ -431,6 +431,86 @@ MLLM_DEV void stage_q8(float *xl, const mllm_xq &xq, long q_job, long b_job, int
     }
 }
 
+// Quantise the activation of tokens b < B, elements [k0, k0+kn), straight
+// into the LDS form stage_q8 copies, with the arithmetic of
+// quantize_row_q8_0 (QK:1406-1455, k_quantize_q8_0): per 32-block amax,
+// d = amax/127 (1 when 0), q = rint(clamp(x * (1/d), +-127)), the scale kept
+// as its fp16 rounding, and the Q4_K min-term sum over elements 0-7 and
+// 16-23.  The activation is mllm_silu_mul(x, xu) when xu is given.  Four
+// lanes share a block (8 elements each) and combine amax and the sum over
+// DPP; a pass covers 256 quarter-blocks and its loads are issued first
+// (q8f_load), the caller placing the weight prefetch between the two halves.
+struct q8f_stage {
+    float4 v[2], u[2];
+};
+
+MLLM_DEV void q8f_load(q8f_stage &st, const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B,
+                       int k0, int kn, int pass)
+{
+    const int nq = kn >> 3, i = threadIdx.x + 256 * pass;
+    if (i >= B * nq) return;
+    const int b = i / nq, e = (i - b * nq) << 3;
+    const float *src = x + (long)b * ldx + k0 + e;
+    const float *su = xu ? xu + (long)b * ldx + k0 + e : nullptr;
+    if ((ldx & 3) == 0) {
+        st.v[0] = gld<float4>(src);
+        st.v[1] = gld<float4>(src + 4);
+        if (su) { st.u[0] = gld<float4>(su); st.u[1] = gld<float4>(su + 4); }
+    } else {
+        st.v[0] = make_float4(gld<float>(src), gld<float>(src + 1), gld<float>(src + 2), gld<float>(src + 3));
+        st.v[1] = make_float4(gld<float>(src + 4), gld<float>(src + 5), gld<float>(src + 6), gld<float>(src + 7));
+        if (su) {
+            st.u[0] = make_float4(gld<float>(su), gld<float>(su + 1), gld<float>(su + 2), gld<float>(su + 3));
+            st.u[1] = make_float4(gld<float>(su + 4), gld<float>(su + 5), gld<float>(su + 6), gld<float>(su + 7));
+        }
+    }
+}
+
+MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT, int tstride, int qstride, int kn,
+                        int pass)
+{
+    const int nq = kn >> 3, i = threadIdx.x + 256 * pass;
+    if (i >= B * nq) return;           // B * nq is a multiple of 4: a block's four lanes take the same path
+    const int b = i / nq, qi = i - b * nq, e = qi << 3;
+    float v[8] = {st.v[0].x, st.v[0].y, st.v[0].z, st.v[0].w, st.v[1].x, st.v[1].y, st.v[1].z, st.v[1].w};
+    if (silu) {
+        const float u[8] = {st.u[0].x, st.u[0].y, st.u[0].z, st.u[0].w, st.u[1].x, st.u[1].y, st.u[1].z, st.u[1].w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = mllm_silu_mul(v[k], u[k]);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) { const float a = fabsf(v[k]); amax = (a > amax) ? a : amax; }
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, false)));
+    float d = amax / 127.0f;
+    if (d == 0.0f) d = 1.0f;
+    const float id = 1.0f / d;
+    uint32_t w[2] = {0, 0};
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        float p = v[k] * id;
+        p = (p > -127.0f) ? p : -127.0f;
+        p = (p < 127.0f) ? p : 127.0f;
+        const int q = (int)rintf(p);
+        sum += q;
+        w[k >> 2] |= (uint32_t)(q & 0xFF) << (8 * (k & 3));
+    }
+    // min-term sum: quarters 0 and 2 of the block (elements 0-7, 16-23)
+    int s4 = (qi & 1) ? 0 : sum;
+    s4 += __builtin_amdgcn_mov_dpp(s4, 0xB1, 0xF, 0xF, false);
+    s4 += __builtin_amdgcn_mov_dpp(s4, 0x4E, 0xF, 0xF, false);
+    uint8_t *lq = reinterpret_cast<uint8_t *>(xl) + b * tstride * 4;
+    *reinterpret_cast<uint2 *>(lq + e + ((e >> 8) << 4)) = make_uint2(w[0], w[1]);
+    if ((qi & 3) == 0) {
+        const float dd = h2f(__builtin_bit_cast(uint16_t, (_Float16)d));
+        float *tf = xl + b * tstride + qstride / 4;
+        tf[e >> 5] = dd;
+        tf[KT / 32 + (e >> 5)] = dd * (float)s4;
+    }
+}
+
 // Q8_0-activation semantics: the quantised activation (int8 quants, decoded
 // scales, Q4_K min-term sums) is staged in LDS the same way.
 template <int SEM, int BM, int R, int LPR>
@@ -461,10 +541,20 @@ __global__ __launch_bounds__(256) void k_gemv_q8(mllm_gemv_args a)
 #pragma unroll
         for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
 
+    const float *xf = a.x + jv.xj * a.x_job_stride;
+    const float *xuf = a.x_up ? a.x_up + jv.xj * a.x_job_stride : nullptr;
     for (int k0 = 0; k0 < kused; k0 += KT) {
         const int kn = min(KT, kused - k0);
         if (k0) __syncthreads();
-        stage_q8(xl, a.xq, q_job, b_job, a.ldx, B, KT, tstride, qstride, k0, kn);
+        if (a.xq.q) {
+            stage_q8(xl, a.xq, q_job, b_job, a.ldx, B, KT, tstride, qstride, k0, kn);
+        } else {
+            for (int pass = 0; pass * 256 < B * (kn >> 3); pass++) {
+                q8f_stage qs;
+                q8f_load(qs, xf, xuf, a.ldx, B, k0, kn, pass);
+                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kn, pass);
+            }
+        }
         __syncthreads();
         const int c_end = (k0 + kn) / BE * CPB;
         for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
@@ -573,9 +663,23 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     raw_chunk bufA[R], bufB[R];
     int rg = rg0, it = 0;
     if constexpr (Q8) {
-        fetch_step(min(rg, nrg - 1), it, bufA);
-        stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride, 0,
-                 kused);
+        if (a.xq.q) {
+            fetch_step(min(rg, nrg - 1), it, bufA);
+            stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride,
+                     0, kused);
+        } else {
+            // quantise in the workgroup: activation loads first, then the weights
+            const float *xf = a.x + jv.xj * a.x_job_stride;
+            const float *xuf = a.x_up ? a.x_up + jv.xj * a.x_job_stride : nullptr;
+            q8f_stage qs;
+            q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, 0);
+            fetch_step(min(rg, nrg - 1), it, bufA);
+            for (int pass = 0;;) {
+                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass);
+                if (++pass * 256 >= B * (kused >> 3)) break;
+                q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, pass);
+            }
+        }
     } else {
         // activation loads first, then the weights; the digits are computed while the weights are in flight
         x_stage<SILU> xst;

@@ -288,14 +288,14 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     if (L->sem_g < 0 || L->sem_u < 0) return -1;   // reference-zero gate/up types are not served here
     int8_t *q; float *d, *s4; int *sq;
     const mllm_xq xqx = xq_at(s.xq_x, T, N, &q, &d, &s4, &sq);
-    if (mllm_sem_uses_q8(L->sem_g) || mllm_sem_uses_q8(L->sem_u))
-        CK(mllm_launch_quantize_q8_0(x, T, N, nullptr, q, d, s4, sq, st));
     int8_t *hq; float *hd, *hs4; int *hsq;
     const mllm_xq xqh = xq_at(s.xq_h, TK, M, &hq, &hd, &hs4, &hsq);
 
     const bool batched = T > 8 && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
                          (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d));
     if (batched) {
+        if (mllm_sem_uses_q8(L->sem_g) || mllm_sem_uses_q8(L->sem_u))
+            CK(mllm_launch_quantize_q8_0(x, T, N, nullptr, q, d, s4, sq, st));
         hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), 0, st, s.idx, TK, E, K, s.off, s.perm, s.pos_of,
                            s.tok, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles);
         CK(hipGetLastError());
@@ -347,14 +347,14 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     } else {
         // decode: one GEMV launch per projection over all T*K (token, slot)
         // jobs, the expert picked on the device; gate and up share a launch
-        // when their semantics agree, and the SiLU product is formed while
-        // the down projection stages its activations (or quantises them)
+        // when their semantics agree; Q8_0 activations are quantised by the
+        // GEMV workgroups themselves, and the SiLU product is formed while
+        // the down projection stages (or quantises) its activations
         mllm_gemv_args a{};
         a.table = L->tab; a.idx = s.idx; a.job_div = K;
         a.x = x; a.x_job_stride = N; a.ldx = N;
         a.out = s.g; a.out_job_stride = M; a.ldo = M;
         a.n_rows = M; a.n_cols = N; a.B = 1;
-        a.xq = xqx;
         if (L->sem_g == L->sem_u) {
             a.job_split = TK; a.table2 = L->tab + E; a.out2 = s.u;
             CK(mllm_launch_gemv(L->sem_g, a, 2 * TK, st));
@@ -369,10 +369,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             b.x = s.g; b.x_job_stride = M; b.ldx = M;
             b.out = s.dn; b.out_job_stride = N; b.ldo = N;
             b.n_rows = N; b.n_cols = M; b.B = 1;
-            if (mllm_sem_uses_q8(L->sem_d)) {
-                CK(mllm_launch_quantize_q8_0(s.g, TK, M, nullptr, hq, hd, hs4, hsq, st, s.u));
-                b.xq = xqh;
-            } else if (L->sem_d == SEM_F32) {
+            if (L->sem_d == SEM_F32) {
                 CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
                 b.x = s.h;
             } else {

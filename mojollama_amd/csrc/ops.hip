@@ -145,14 +145,36 @@ __device__ __forceinline__ float expf_cr(float v) { return (float)exp((double)v)
 // LDS as p[tw * PS + e], PS = route_pitch(E): max by strict '>' from p[0],
 // exp element-wise, sequential sum, x 1/(sum+1e-10), then the top-K of the
 // strict-'>' insertion in index order, optionally renormalised by the
-// sequential sum of the K weights.  That insertion keeps a stable descending
-// order (an element goes after every earlier one that is >= it) and never
-// takes a NaN, so element j lands at slot rank(j) = #{j' : p[j'] > p[j]} +
-// #{j' < j : p[j'] == p[j]} when that is < K -- computed here one thread per
-// element.  Slots no element reaches keep (-1, -1e30), as the reference's
-// initial list does.  Needs route_finish_floats(TW, E) floats at p.
+// sequential sum of the K weights.
+//   * The strict-'>' scan from p[0] ends at p[0] when p[0] is NaN and at the
+//     largest non-NaN value otherwise (a NaN never compares greater); of equal
+//     +0/-0 it keeps the first, and x - (+0) and x - (-0) are equal for every
+//     x but -0, where exp gives 1 either way.  So the maximum is taken as a
+//     wave reduction with fmaxf (which drops NaNs) and p[0] checked for NaN.
+//   * The sums stay sequential, one lane reading 16-byte groups.
+//   * The insertion keeps a stable descending order (an element goes after
+//     every earlier one that is >= it) and never takes a NaN, so element j
+//     lands at slot rank(j) = #{j' : p[j'] > p[j]} + #{j' < j : p[j'] == p[j]}
+//     when that is < K -- computed one thread per element.
+// Slots no element reaches keep (-1, -1e30), as the reference's initial list
+// does.  Needs route_finish_floats(TW, E) floats at p (16-byte aligned).
 __host__ __device__ constexpr int route_pitch(int E) { return (E + 3) / 4 * 4 + 4; }
 __host__ __device__ constexpr int route_finish_floats(int TW, int E) { return TW * route_pitch(E) + 2 * TW + 32 * TW; }
+
+// Sequential sum of n floats at v (16-byte aligned).
+__device__ __forceinline__ float seq_sum(const float *v, int n)
+{
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    float s = 0.0f;
+    int j = 0;
+#pragma unroll 4
+    for (; j + 4 <= n; j += 4) {
+        const float4 q = v4[j >> 2];
+        s += q.x; s += q.y; s += q.z; s += q.w;
+    }
+    for (; j < n; j++) s += v[j];
+    return s;
+}
 
 __device__ __forceinline__ void route_finish(float *p, int TW, int t0, int T, int E, int K, int renorm,
                                              int *__restrict__ top_idx, float *__restrict__ top_w)
@@ -160,13 +182,15 @@ __device__ __forceinline__ void route_finish(float *p, int TW, int t0, int T, in
     const int PS = route_pitch(E);
     float *s_mx = p + TW * PS, *s_inv = s_mx + TW, *s_v = s_inv + TW;
     int *s_i = reinterpret_cast<int *>(s_v + 16 * TW);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     for (int q = tid; q < 16 * TW; q += blockDim.x) { s_v[q] = -1e30f; s_i[q] = -1; }
-    if (tid < TW) {
-        const float *pt = p + tid * PS;
-        float mx = pt[0];
-        for (int j = 1; j < E; j++) if (pt[j] > mx) mx = pt[j];
-        s_mx[tid] = mx;
+    for (int tw = wave; tw < TW; tw += nw) {
+        const float *pt = p + tw * PS;
+        float m = -INFINITY;
+        for (int j = lane; j < E; j += 64) m = fmaxf(m, pt[j]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) s_mx[tw] = pt[0] != pt[0] ? pt[0] : m;
     }
     __syncthreads();
     for (int q = tid; q < TW * E; q += blockDim.x) {
@@ -174,12 +198,7 @@ __device__ __forceinline__ void route_finish(float *p, int TW, int t0, int T, in
         p[tw * PS + j] = expf_cr(p[tw * PS + j] - s_mx[tw]);
     }
     __syncthreads();
-    if (tid < TW) {
-        const float *pt = p + tid * PS;
-        float sum = 0.0f;                        // sequential, as CE:624
-        for (int j = 0; j < E; j++) sum += pt[j];
-        s_inv[tid] = 1.0f / (sum + 1e-10f);
-    }
+    if (tid < TW) s_inv[tid] = 1.0f / (seq_sum(p + tid * PS, E) + 1e-10f);   // sequential, as CE:624
     __syncthreads();
     for (int q = tid; q < TW * E; q += blockDim.x) {
         const int tw = q / E, j = q - tw * E;
@@ -189,13 +208,18 @@ __device__ __forceinline__ void route_finish(float *p, int TW, int t0, int T, in
     for (int q = tid; q < TW * E; q += blockDim.x) {
         const int tw = q / E, j = q - tw * E;
         const float *pt = p + tw * PS;
+        const float4 *pt4 = reinterpret_cast<const float4 *>(pt);
         const float v = pt[j];
         if (v != v) continue;                    // NaN: never inserted
-        int r = 0;
-        for (int jj = 0; jj < E; jj++) {
-            const float u = pt[jj];
-            r += (u > v) || (u == v && jj < j);
+        int r = 0, jj = 0;
+        for (; jj + 4 <= E; jj += 4) {
+            const float4 u = pt4[jj >> 2];
+            r += (u.x > v) || (u.x == v && jj < j);
+            r += (u.y > v) || (u.y == v && jj + 1 < j);
+            r += (u.z > v) || (u.z == v && jj + 2 < j);
+            r += (u.w > v) || (u.w == v && jj + 3 < j);
         }
+        for (; jj < E; jj++) r += (pt[jj] > v) || (pt[jj] == v && jj < j);
         if (r < K) { s_v[tw * 16 + r] = v; s_i[tw * 16 + r] = j; }
     }
     __syncthreads();
@@ -371,11 +395,249 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ router_
     route_finish(p, TW, t0, T, E, K, renorm, top_idx, top_w);
 }
 
+// Routing logits for a few tokens (decode), spread over many CUs: a
+// workgroup takes an ES-expert slice of the router (ES small, so the slice of
+// all N rows fits in registers and LDS at once) and one token, lane e of
+// wave 0 running the chain of expert e0 + e (the other waves help load; a
+// second chain wave per workgroup would share the LDS issue slots the chain
+// is bound by); raw logits go to `logits` for k_route_finish.  Every load of
+// the slice and of the token's x is issued at the start, in NCH chunks of KC
+// steps; chunk c is stored to LDS and its chains advanced while the later
+// chunks are still in flight.  LDS holds each expert's router values as one
+// contiguous row of float4 (stride RS, RS % 16 == 1 so the lanes' 16-byte
+// reads fall on distinct banks) and x after them; steps from N up to NCH*KC
+// are zero in both, and fma(0, 0, d) == d (up to the sign of a zero, which
+// neither the softmax nor the comparisons of the selection can see).
+//
+// The chain itself (chain72) is scheduled by hand: its operands come from
+// LDS in groups of 24 steps (12 ds_read_b128: 6 of router, 6 of x) with two
+// groups in flight, and lgkmcnt can only count 15 outstanding reads, so a
+// compiler-scheduled loop waits for every read (lgkmcnt(0)) each group and
+// runs about twice as slow as the FMA latency allows.  The loop reads up to
+// 48 steps past its last group (rows carry that much slack).
+__device__ __forceinline__ float chain72(float dot, unsigned r_lds, unsigned x_lds, int iters)
+{
+    // dot = fma(x[i], r[i], dot) for i = 0 .. 72*iters-1 in order; r and x
+    // are float4 runs at LDS byte addresses r_lds and x_lds.
+    asm volatile(
+        "s_waitcnt lgkmcnt(0)\n"
+        "ds_read_b128 v[64:67], %1 offset:0\n"
+        "ds_read_b128 v[68:71], %1 offset:16\n"
+        "ds_read_b128 v[72:75], %1 offset:32\n"
+        "ds_read_b128 v[76:79], %1 offset:48\n"
+        "ds_read_b128 v[80:83], %1 offset:64\n"
+        "ds_read_b128 v[84:87], %1 offset:80\n"
+        "ds_read_b128 v[88:91], %2 offset:0\n"
+        "ds_read_b128 v[92:95], %2 offset:16\n"
+        "ds_read_b128 v[96:99], %2 offset:32\n"
+        "ds_read_b128 v[100:103], %2 offset:48\n"
+        "ds_read_b128 v[104:107], %2 offset:64\n"
+        "ds_read_b128 v[108:111], %2 offset:80\n"
+        "ds_read_b128 v[112:115], %1 offset:96\n"
+        "ds_read_b128 v[116:119], %1 offset:112\n"
+        "ds_read_b128 v[120:123], %1 offset:128\n"
+        "ds_read_b128 v[124:127], %1 offset:144\n"
+        "ds_read_b128 v[128:131], %1 offset:160\n"
+        "ds_read_b128 v[132:135], %1 offset:176\n"
+        "ds_read_b128 v[136:139], %2 offset:96\n"
+        "ds_read_b128 v[140:143], %2 offset:112\n"
+        "ds_read_b128 v[144:147], %2 offset:128\n"
+        "ds_read_b128 v[148:151], %2 offset:144\n"
+        "ds_read_b128 v[152:155], %2 offset:160\n"
+        "ds_read_b128 v[156:159], %2 offset:176\n"
+        "1:\n"
+        "ds_read_b128 v[160:163], %1 offset:192\n"
+        "ds_read_b128 v[164:167], %1 offset:208\n"
+        "ds_read_b128 v[168:171], %1 offset:224\n"
+        "ds_read_b128 v[172:175], %1 offset:240\n"
+        "ds_read_b128 v[176:179], %1 offset:256\n"
+        "ds_read_b128 v[180:183], %1 offset:272\n"
+        "ds_read_b128 v[184:187], %2 offset:192\n"
+        "ds_read_b128 v[188:191], %2 offset:208\n"
+        "ds_read_b128 v[192:195], %2 offset:224\n"
+        "ds_read_b128 v[196:199], %2 offset:240\n"
+        "ds_read_b128 v[200:203], %2 offset:256\n"
+        "ds_read_b128 v[204:207], %2 offset:272\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fmac_f32 %0, v88, v64\n"
+        "v_fmac_f32 %0, v89, v65\n"
+        "v_fmac_f32 %0, v90, v66\n"
+        "v_fmac_f32 %0, v91, v67\n"
+        "v_fmac_f32 %0, v92, v68\n"
+        "v_fmac_f32 %0, v93, v69\n"
+        "v_fmac_f32 %0, v94, v70\n"
+        "v_fmac_f32 %0, v95, v71\n"
+        "v_fmac_f32 %0, v96, v72\n"
+        "v_fmac_f32 %0, v97, v73\n"
+        "v_fmac_f32 %0, v98, v74\n"
+        "v_fmac_f32 %0, v99, v75\n"
+        "v_fmac_f32 %0, v100, v76\n"
+        "v_fmac_f32 %0, v101, v77\n"
+        "v_fmac_f32 %0, v102, v78\n"
+        "v_fmac_f32 %0, v103, v79\n"
+        "v_fmac_f32 %0, v104, v80\n"
+        "v_fmac_f32 %0, v105, v81\n"
+        "v_fmac_f32 %0, v106, v82\n"
+        "v_fmac_f32 %0, v107, v83\n"
+        "v_fmac_f32 %0, v108, v84\n"
+        "v_fmac_f32 %0, v109, v85\n"
+        "v_fmac_f32 %0, v110, v86\n"
+        "v_fmac_f32 %0, v111, v87\n"
+        "ds_read_b128 v[64:67], %1 offset:288\n"
+        "ds_read_b128 v[68:71], %1 offset:304\n"
+        "ds_read_b128 v[72:75], %1 offset:320\n"
+        "ds_read_b128 v[76:79], %1 offset:336\n"
+        "ds_read_b128 v[80:83], %1 offset:352\n"
+        "ds_read_b128 v[84:87], %1 offset:368\n"
+        "ds_read_b128 v[88:91], %2 offset:288\n"
+        "ds_read_b128 v[92:95], %2 offset:304\n"
+        "ds_read_b128 v[96:99], %2 offset:320\n"
+        "ds_read_b128 v[100:103], %2 offset:336\n"
+        "ds_read_b128 v[104:107], %2 offset:352\n"
+        "ds_read_b128 v[108:111], %2 offset:368\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fmac_f32 %0, v136, v112\n"
+        "v_fmac_f32 %0, v137, v113\n"
+        "v_fmac_f32 %0, v138, v114\n"
+        "v_fmac_f32 %0, v139, v115\n"
+        "v_fmac_f32 %0, v140, v116\n"
+        "v_fmac_f32 %0, v141, v117\n"
+        "v_fmac_f32 %0, v142, v118\n"
+        "v_fmac_f32 %0, v143, v119\n"
+        "v_fmac_f32 %0, v144, v120\n"
+        "v_fmac_f32 %0, v145, v121\n"
+        "v_fmac_f32 %0, v146, v122\n"
+        "v_fmac_f32 %0, v147, v123\n"
+        "v_fmac_f32 %0, v148, v124\n"
+        "v_fmac_f32 %0, v149, v125\n"
+        "v_fmac_f32 %0, v150, v126\n"
+        "v_fmac_f32 %0, v151, v127\n"
+        "v_fmac_f32 %0, v152, v128\n"
+        "v_fmac_f32 %0, v153, v129\n"
+        "v_fmac_f32 %0, v154, v130\n"
+        "v_fmac_f32 %0, v155, v131\n"
+        "v_fmac_f32 %0, v156, v132\n"
+        "v_fmac_f32 %0, v157, v133\n"
+        "v_fmac_f32 %0, v158, v134\n"
+        "v_fmac_f32 %0, v159, v135\n"
+        "ds_read_b128 v[112:115], %1 offset:384\n"
+        "ds_read_b128 v[116:119], %1 offset:400\n"
+        "ds_read_b128 v[120:123], %1 offset:416\n"
+        "ds_read_b128 v[124:127], %1 offset:432\n"
+        "ds_read_b128 v[128:131], %1 offset:448\n"
+        "ds_read_b128 v[132:135], %1 offset:464\n"
+        "ds_read_b128 v[136:139], %2 offset:384\n"
+        "ds_read_b128 v[140:143], %2 offset:400\n"
+        "ds_read_b128 v[144:147], %2 offset:416\n"
+        "ds_read_b128 v[148:151], %2 offset:432\n"
+        "ds_read_b128 v[152:155], %2 offset:448\n"
+        "ds_read_b128 v[156:159], %2 offset:464\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fmac_f32 %0, v184, v160\n"
+        "v_fmac_f32 %0, v185, v161\n"
+        "v_fmac_f32 %0, v186, v162\n"
+        "v_fmac_f32 %0, v187, v163\n"
+        "v_fmac_f32 %0, v188, v164\n"
+        "v_fmac_f32 %0, v189, v165\n"
+        "v_fmac_f32 %0, v190, v166\n"
+        "v_fmac_f32 %0, v191, v167\n"
+        "v_fmac_f32 %0, v192, v168\n"
+        "v_fmac_f32 %0, v193, v169\n"
+        "v_fmac_f32 %0, v194, v170\n"
+        "v_fmac_f32 %0, v195, v171\n"
+        "v_fmac_f32 %0, v196, v172\n"
+        "v_fmac_f32 %0, v197, v173\n"
+        "v_fmac_f32 %0, v198, v174\n"
+        "v_fmac_f32 %0, v199, v175\n"
+        "v_fmac_f32 %0, v200, v176\n"
+        "v_fmac_f32 %0, v201, v177\n"
+        "v_fmac_f32 %0, v202, v178\n"
+        "v_fmac_f32 %0, v203, v179\n"
+        "v_fmac_f32 %0, v204, v180\n"
+        "v_fmac_f32 %0, v205, v181\n"
+        "v_fmac_f32 %0, v206, v182\n"
+        "v_fmac_f32 %0, v207, v183\n"
+        "v_add_u32 %1, 288, %1\n"
+        "v_add_u32 %2, 288, %2\n"
+        "s_sub_i32 %3, %3, 1\n"
+        "s_cmp_lg_u32 %3, 0\n"
+        "s_cbranch_scc1 1b\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        : "+v"(dot), "+v"(r_lds), "+v"(x_lds), "+s"(iters)
+        :
+        : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75",
+          "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87",
+          "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99",
+          "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111",
+          "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123",
+          "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135",
+          "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147",
+          "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159",
+          "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171",
+          "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183",
+          "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195",
+          "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207",
+          "scc", "memory");
+    return dot;
+}
+
+constexpr int kChainIter = 72, kChainSlack = 48;
+
+template <int NCH, int SPC, int XPC>
+__global__ __launch_bounds__(256) void k_route_slice(const float *__restrict__ router_p, const float *__restrict__ x,
+                                                     int T, int N, int E, int KC, int ES, int RS, int XS,
+                                                     float *__restrict__ logits)
+{
+    extern __shared__ float4 lds4[];
+    const int e0 = blockIdx.x * ES, t = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KC4 = KC >> 2, N4 = N >> 2;
+    float4 *rl = lds4;                                        // [ES][RS]
+    float4 *xl = lds4 + (long)ES * RS;                        // [XS]
+    const float4 *r4 = reinterpret_cast<const float4 *>(router_p) + e0;
+    float4 pr[NCH][SPC], px[NCH][XPC];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int q0 = c * KC4;
+#pragma unroll
+        for (int s = 0; s < SPC; s++) {
+            const int j = tid + s * 256, r = j / ES;
+            pr[c][s] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < KC4 && q0 + r < N4) pr[c][s] = gld<float4>(r4 + (long)(q0 + r) * E + (j - r * ES));
+        }
+#pragma unroll
+        for (int s = 0; s < XPC; s++) {
+            const int q = tid + s * 256;
+            px[c][s] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (q < KC4 && q0 + q < N4) px[c][s] = gld<float4>(x + (long)t * N + 4 * (q0 + q));
+        }
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int q0 = c * KC4;
+#pragma unroll
+        for (int s = 0; s < SPC; s++) {
+            const int j = tid + s * 256, r = j / ES;
+            if (r < KC4) rl[(j - r * ES) * RS + q0 + r] = pr[c][s];
+        }
+#pragma unroll
+        for (int s = 0; s < XPC; s++) {
+            const int q = tid + s * 256;
+            if (q < KC4) xl[q0 + q] = px[c][s];
+        }
+        __syncthreads();
+        if (wave == 0 && lane < ES)
+            dot = chain72(dot, (unsigned)(uintptr_t)(rl + lane * RS + q0), (unsigned)(uintptr_t)(xl + q0), KC / kChainIter);
+    }
+    if (wave == 0 && lane < ES) logits[(long)t * E + e0 + lane] = dot;
+}
+
 // Softmax and top-K of logits[t][0..E) written by the expert slices of k_route.
 __global__ __launch_bounds__(256) void k_route_finish(const float *__restrict__ logits, int T, int E, int K, int renorm,
                                                       int *__restrict__ top_idx, float *__restrict__ top_w)
 {
-    __shared__ float p[route_finish_floats(1, 256)];
+    __shared__ __align__(16) float p[route_finish_floats(1, 256)];
     const int t = blockIdx.x;
     if (threadIdx.x < E) p[threadIdx.x] = logits[(long)t * E + threadIdx.x];
     __syncthreads();
@@ -388,7 +650,7 @@ __global__ __launch_bounds__(256) void k_route_any(const float *__restrict__ rou
                                                    int T, int N, int E, int K, int renorm,
                                                    int *__restrict__ top_idx, float *__restrict__ top_w)
 {
-    __shared__ float p[route_finish_floats(1, 256)];
+    __shared__ __align__(16) float p[route_finish_floats(1, 256)];
     const int t = blockIdx.x, e = threadIdx.x;
     if (e < E) {
         const float *xt = x + (long)t * N;
@@ -476,6 +738,9 @@ hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out
 
 long mllm_route_workspace_floats(int T, int E) { return (long)T * E; }
 
+// Decode routing shape: row chunks, and router / x float4 loads per thread and chunk.
+constexpr int kRouteSliceChunks = 2, kRouteSliceSlots = 8, kRouteSliceXSlots = 2;
+
 hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, float *logits_ws, hipStream_t st)
 {
@@ -485,11 +750,30 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
         hipLaunchKernelGGL(k_route_any, dim3(T), dim3(256), 0, st, router_p, x, T, N, E, K, renorm, top_idx, top_w);
         return hipGetLastError();
     }
-    // T <= 8: a workgroup per token, and with a logits workspace and E a
-    // multiple of 16 (>= 32), one per 32- or 16-expert slice of it (each
+    // T <= 8, N % 4 == 0 and a logits workspace: k_route_slice over the
+    // widest power-of-two expert slices whose rows fit its registers, then
+    // k_route_finish.
+    if (T <= 8 && logits_ws) {
+        constexpr int NCH = kRouteSliceChunks, SPC = kRouteSliceSlots, XPC = kRouteSliceXSlots;
+        const int KC = (N + NCH * kChainIter - 1) / (NCH * kChainIter) * kChainIter;   // steps per chunk
+        int ES = 16;
+        while (ES > 1 && ((KC / 4) * ES > 256 * SPC || E % ES != 0)) ES >>= 1;
+        if ((KC / 4) * ES <= 256 * SPC && KC / 4 <= 256 * XPC && E % ES == 0) {
+            // row strides in float4: NCH*KC/4 steps + slack, rounded to 1 mod 16
+            const int rows = NCH * KC / 4 + kChainSlack / 4;
+            const int RS = (rows + 15) / 16 * 16 + 1, XS = RS;
+            const size_t lds = ((size_t)ES * RS + (size_t)XS) * sizeof(float4);
+            hipLaunchKernelGGL((k_route_slice<NCH, SPC, XPC>), dim3(E / ES, T), dim3(256), lds, st, router_p,
+                               x, T, N, E, KC, ES, RS, XS, logits_ws);
+            hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits_ws, T, E, K, renorm, top_idx, top_w);
+            return hipGetLastError();
+        }
+    }
+    // Other T <= 8: a workgroup per token, and with a logits workspace and E
+    // a multiple of 16 (>= 32), one per 32- or 16-expert slice of it (each
     // streams its slice of the router; k_route_finish then takes the softmax
-    // and top-K).  More
-    // tokens: token groups over the idle lanes and four tokens per thread.
+    // and top-K).  More tokens: token groups over the idle lanes and four
+    // tokens per thread.
     auto go = [&](auto tt_c, auto pf_c, auto xs_c, int G, int ES, int lgES) {
         constexpr int TT = decltype(tt_c)::value, PF = decltype(pf_c)::value, XS = decltype(xs_c)::value;
         const int TW = G * TT;

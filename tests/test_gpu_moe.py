@@ -246,6 +246,30 @@ def test_moe_layer_decode_real_shapes(dev, orc, qts, N, M, Kk, T):
     assert O.norm_err(got, ref) < moe_tol(qts)
 
 
+def test_moe_layer_repeated_decode_calls(dev, orc):
+    """Decode routing's arrival counters are left at zero by every call: alternating T = 1, 5, 8, 1
+    calls on one layer keep matching the oracle's routing."""
+    import torch
+    rng = np.random.default_rng(21)
+    qts, N, M, E, Kk = (12, 12, 14), 512, 256, 32, 4
+    gates = [W.gen_weights(rng, qts[0], M, N) for _ in range(E)]
+    ups = [W.gen_weights(rng, qts[1], M, N) for _ in range(E)]
+    downs = [W.gen_weights(rng, qts[2], N, M) for _ in range(E)]
+    router = W.gen_router(rng, E, N)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    layer = dev.moe_prepare(qts, N, M, E, Kk, [cu(g) for g in gates], [cu(u) for u in ups], [cu(d) for d in downs],
+                            cu(router), 1)
+    for T in (1, 5, 8, 1, 8):
+        x = W.gen_x(rng, T, N)
+        idx = torch.empty((T, Kk), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, Kk), dtype=torch.float32, device="cuda")
+        got = layer.forward(cu(x), idx=idx, w=w).cpu().numpy()
+        ri, rw = orc.route(router, x, Kk, 1)
+        assert np.array_equal(idx.cpu().numpy(), ri), f"routing differs at T={T}"
+        ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in range(T)])
+        assert O.norm_err(got, ref) < MOE_TOL
+
+
 def test_moe_layer_gptoss_shape(dev, orc):
     """GPT-OSS-20B expert shapes (N = M = 2880, MXFP4, top-4), batched path."""
     got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=24, renorm=1, seed=4)

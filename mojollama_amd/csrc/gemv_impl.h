@@ -827,6 +827,10 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     if (BM == 1) {
         const long row_bytes = (long)kused / 32 * sem_traits<SEM>::kBytesPer32;
         lpr = row_bytes <= 1800 ? 16 : row_bytes <= 5000 ? 32 : 64;
+        // short matrices: wider lane groups (fewer rows per workgroup) until
+        // the launch has about two workgroups per CU
+        auto wgs_at = [&](int l) { const int rpw = 4 * (64 / l) * R; return (long)(a.n_rows + rpw - 1) / rpw * n_jobs; };
+        while (lpr < 64 && wgs_at(lpr) < 2L * device_cus()) lpr *= 2;
     } else {
         // lanes per row: enough chunks per lane to keep every lane busy on short rows
         if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;

@@ -738,6 +738,9 @@ hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out
 
 long mllm_route_workspace_floats(int T, int E) { return (long)T * E; }
 
+// Workgroups the T > 8 routing launch aims for.
+constexpr int kRouteMinGroups = 128;
+
 // Decode routing shape: row chunks, and router / x float4 loads per thread and chunk.
 constexpr int kRouteSliceChunks = 2, kRouteSliceSlots = 8, kRouteSliceXSlots = 2;
 
@@ -806,8 +809,12 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
         }
         return go(I{}, std::integral_constant<int, 16>{}, I{}, 1, E, -1);
     }
+    // token groups per workgroup: as many as the 256 threads hold, but few
+    // enough that the launch has about one workgroup per CU (each
+    // workgroup's time is its chains' latency, whatever its token count)
     int G = 256 / E;
     G = G > 8 ? 8 : G;
+    while (G > 1 && (T + 4 * G - 1) / (4 * G) < kRouteMinGroups) G >>= 1;
     return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}, G,
               E, -1);
 }

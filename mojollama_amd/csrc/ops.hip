@@ -633,6 +633,70 @@ __global__ __launch_bounds__(256) void k_route_slice(const float *__restrict__ r
     if (wave == 0 && lane < ES) logits[(long)t * E + e0 + lane] = dot;
 }
 
+// Routing logits for many tokens: a workgroup takes RT_T tokens x RT_E
+// experts and every lane runs one (token, expert) chain, so all 256 lanes of
+// every workgroup are busy.  Router rows and x rows are staged in LDS in
+// chunks of KC steps (each row contiguous, stride RS float4 with RS % 16 == 1
+// so the 16 token rows a wave reads fall on distinct banks), two buffers:
+// chunk c+1 is loaded into registers while chunk c's chains run, and stored
+// to the other buffer afterwards.  The chains use chain72 (the hand-scheduled
+// loop of k_route_slice).  Steps from N up to the padded length are zero in
+// both operands.  Raw logits go to `logits` for k_route_finish.
+constexpr int RT_T = 16, RT_E = 16;     // tokens and experts per workgroup
+constexpr int RT_KC = 432;              // steps per chunk (6 chain72 iterations)
+constexpr int RT_RS = 129;              // row stride in float4: >= 108 + 12 of slack, 1 mod 16
+constexpr int RT_ROWS = RT_T + RT_E;
+constexpr int RT_SLOTS = (RT_ROWS * (RT_KC / 4) + 255) / 256;   // float4 loads per thread and chunk
+
+__global__ __launch_bounds__(256) void k_route_tile(const float *__restrict__ router_p, const float *__restrict__ x,
+                                                    int T, int N, int E, int nch, float *__restrict__ logits)
+{
+    extern __shared__ float4 lds4[];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
+    // lane (token tt, expert te): a wave holds 16 tokens x 4 experts
+    const int tt = tid & 15, te = tid >> 4;
+    const int N4 = N >> 2, KQ = RT_KC / 4;
+    const float4 *r4 = reinterpret_cast<const float4 *>(router_p);
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float4 st[RT_SLOTS];
+    // slot j of a chunk: row j / KQ (experts first, then tokens), quad j % KQ
+    auto load = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < RT_SLOTS; s++) {
+            const int j = tid + 256 * s, row = j / KQ, q = c * KQ + (j - row * KQ);
+            st[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < RT_E) {
+                if (e0 + row < E && q < N4) st[s] = gld<float4>(r4 + (long)q * E + e0 + row);
+            } else if (row < RT_ROWS) {
+                const int t = t0 + row - RT_E;
+                if (t < T && q < N4) st[s] = gld<float4>(x4 + (long)t * N4 + q);
+            }
+        }
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+        float4 *b = lds4 + buf * RT_ROWS * RT_RS;
+#pragma unroll
+        for (int s = 0; s < RT_SLOTS; s++) {
+            const int j = tid + 256 * s, row = j / KQ;
+            if (row < RT_ROWS) b[row * RT_RS + (j - row * KQ)] = st[s];
+        }
+    };
+    float dot = 0.0f;
+    load(0);
+    store(0);
+    for (int c = 0; c < nch; c++) {
+        if (c + 1 < nch) load(c + 1);
+        __syncthreads();                              // chunk c stored by every thread
+        const float4 *b = lds4 + (c & 1) * RT_ROWS * RT_RS;
+        dot = chain72(dot, (unsigned)(uintptr_t)(b + te * RT_RS), (unsigned)(uintptr_t)(b + (RT_E + tt) * RT_RS),
+                      RT_KC / kChainIter);
+        // buffer (c+1)&1 was last read by chunk c-1's chains, before this iteration's barrier
+        if (c + 1 < nch) store((c + 1) & 1);
+    }
+    if (t0 + tt < T && e0 + te < E) logits[(long)(t0 + tt) * E + e0 + te] = dot;
+}
+
 // Softmax and top-K of logits[t][0..E) written by the expert slices of k_route.
 __global__ __launch_bounds__(256) void k_route_finish(const float *__restrict__ logits, int T, int E, int K, int renorm,
                                                       int *__restrict__ top_idx, float *__restrict__ top_w)
@@ -771,6 +835,15 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
             hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits_ws, T, E, K, renorm, top_idx, top_w);
             return hipGetLastError();
         }
+    }
+    // More tokens with a logits workspace: k_route_tile, then k_route_finish.
+    if (T > 8 && logits_ws && N % 4 == 0) {
+        const int nch = (N + RT_KC - 1) / RT_KC;
+        const size_t lds = 2 * (size_t)RT_ROWS * RT_RS * sizeof(float4);
+        hipLaunchKernelGGL(k_route_tile, dim3((T + RT_T - 1) / RT_T, (E + RT_E - 1) / RT_E), dim3(256), lds, st,
+                           router_p, x, T, N, E, nch, logits_ws);
+        hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits_ws, T, E, K, renorm, top_idx, top_w);
+        return hipGetLastError();
     }
     // Other T <= 8: a workgroup per token, and with a logits workspace and E
     // a multiple of 16 (>= 32), one per 32- or 16-expert slice of it (each

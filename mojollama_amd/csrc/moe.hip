@@ -25,42 +25,76 @@ namespace {
 
 constexpr int kTileEntries = 64;   // entries per grouped-GEMM work tile (gemm.hip TM)
 
-// Stable bucketing of entries i = t*K + k by expert idx[i], in one workgroup of
-// 1024 threads: an LDS histogram, an exclusive scan over experts (bucket
-// offsets off[0..E] and the work-tile list: <= kTileEntries consecutive
-// positions of one expert), then passes of 1024 entries in index order.  An
-// entry's position is its expert's running base + the entries of that expert
-// in earlier waves of the pass + its rank among its wave's equal lanes below
-// it (a 64-step scan of the wave), so the order is the entries' index order
-// without atomics.  perm[pos] = i, pos_of[i] = pos (-1 for an expert id
-// outside [0, E)), tok[pos] = i / K when tok is given.
+// Stable bucketing of entries i = t*K + k by expert idx[i]: entry i lands at
+// pos = off[e] + #{j < i : idx[j] == e}, so each bucket keeps index order
+// (no atomics decide an order).  Two launches over blocks of 1024 entries:
+//   k_bucket_rank: per block, an entry's rank among the block's entries of
+//     its expert (its rank among its wave's equal lanes below it -- a 64-step
+//     scan of the wave -- plus that expert's count in the block's earlier
+//     waves) and the block's histogram hist[b][e];
+//   k_bucket_place: per block, the bucket offsets off[0..E] (an exclusive
+//     scan over experts of the histogram totals) plus the earlier blocks'
+//     counts give each entry its position: perm[pos] = i, pos_of[i] = pos
+//     (-1 for an expert id outside [0, E)), tok[pos] = i / K when tok is
+//     given; block 0 also writes off[] and the work-tile list (<=
+//     kTileEntries consecutive positions of one expert).
 constexpr int kBucketThreads = 1024, kBucketWaves = kBucketThreads / 64;
 
-__global__ __launch_bounds__(1024) void k_bucket(const int *__restrict__ idx, int TK, int E, int K,
-                                                 int *__restrict__ off, int *__restrict__ perm,
-                                                 int *__restrict__ pos_of, int *__restrict__ tok,
-                                                 int *__restrict__ tile_expert, int *__restrict__ tile_begin,
-                                                 int *__restrict__ tile_end, int *__restrict__ n_tiles)
+__global__ __launch_bounds__(1024) void k_bucket_rank(const int *__restrict__ idx, int TK, int E,
+                                                      int *__restrict__ hist, int *__restrict__ rank)
 {
-    __shared__ int cnt[256], base[256], tbase[257], scan[256];
     __shared__ int wcnt[kBucketWaves][256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < 256; e += kBucketThreads) cnt[e] = 0;
-    __syncthreads();
-    for (int i = tid; i < TK; i += kBucketThreads) {
-        const int e = idx[i];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);    // a count: order-free
+    for (int q = tid; q < kBucketWaves * 256; q += kBucketThreads) (&wcnt[0][0])[q] = 0;
+    const int i = blockIdx.x * kBucketThreads + tid;
+    int e = i < TK ? idx[i] : -1;
+    const bool valid = e >= 0 && e < E;
+    if (!valid) e = -1;
+    int r = 0, tot = 0;
+    for (int j = 0; j < 64; j++) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        const int m = ej == e;
+        tot += m;
+        r += m & (j < lane);
     }
     __syncthreads();
-    // exclusive scans over experts of counts and of tile counts (Hillis-Steele, 256 wide)
-    int c = 0, nt = 0;
+    if (valid && r == 0) wcnt[wave][e] = tot;
+    __syncthreads();
+    if (valid) {
+        for (int w = 0; w < wave; w++) r += wcnt[w][e];
+        rank[i] = r;
+    }
+    if (tid < E) {
+        int h = 0;
+        for (int w = 0; w < kBucketWaves; w++) h += wcnt[w][tid];
+        hist[(long)blockIdx.x * E + tid] = h;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_bucket_place(const int *__restrict__ idx, int TK, int E, int K, int nblk,
+                                                       const int *__restrict__ hist, const int *__restrict__ rank,
+                                                       int *__restrict__ off, int *__restrict__ perm,
+                                                       int *__restrict__ pos_of, int *__restrict__ tok,
+                                                       int *__restrict__ tile_expert, int *__restrict__ tile_begin,
+                                                       int *__restrict__ tile_end, int *__restrict__ n_tiles)
+{
+    __shared__ int base[256], scan[256], tbase[256];
+    const int tid = threadIdx.x;
+    // per expert: its total, and the entries of it in earlier blocks
+    int c = 0, before = 0, nt = 0;
     if (tid < 256) {
-        c = tid < E ? cnt[tid] : 0;
+        if (tid < E)
+            for (int b = 0; b < nblk; b++) {
+                const int h = hist[(long)b * E + tid];
+                c += h;
+                before += b < (int)blockIdx.x ? h : 0;
+            }
         nt = (c + kTileEntries - 1) / kTileEntries;
         scan[tid] = c;
         tbase[tid] = nt;
     }
     __syncthreads();
+    // inclusive scans over experts (Hillis-Steele, 256 wide)
     for (int d = 1; d < 256; d <<= 1) {
         int v = 0, w = 0;
         if (tid < 256 && tid >= d) { v = scan[tid - d]; w = tbase[tid - d]; }
@@ -69,55 +103,49 @@ __global__ __launch_bounds__(1024) void k_bucket(const int *__restrict__ idx, in
         __syncthreads();
     }
     if (tid < E) {
-        const int b = scan[tid] - c, tb = tbase[tid] - nt;   // exclusive
-        base[tid] = b;
-        off[tid] = b;
-        for (int t = 0; t < nt; t++) {
-            tile_expert[tb + t] = tid;
-            tile_begin[tb + t] = b + t * kTileEntries;
-            tile_end[tb + t] = b + min(c, (t + 1) * kTileEntries);
+        const int b = scan[tid] - c;   // exclusive
+        base[tid] = b + before;
+        if (blockIdx.x == 0) {
+            off[tid] = b;
+            const int tb = tbase[tid] - nt;
+            for (int t = 0; t < nt; t++) {
+                tile_expert[tb + t] = tid;
+                tile_begin[tb + t] = b + t * kTileEntries;
+                tile_end[tb + t] = b + min(c, (t + 1) * kTileEntries);
+            }
         }
     }
-    if (tid == E - 1) {
+    if (blockIdx.x == 0 && tid == E - 1) {
         off[E] = scan[tid];
         *n_tiles = tbase[tid];
     }
     __syncthreads();
-    for (int p0 = 0; p0 < TK; p0 += kBucketThreads) {
-        const int i = p0 + tid;
-        int e = i < TK ? idx[i] : -1;
-        const bool valid = e >= 0 && e < E;
-        if (!valid) e = -1;
-        // rank among the wave's lanes below with the same expert, and the wave's count of it
-        int rank = 0, tot = 0;
-        for (int j = 0; j < 64; j++) {
-            const int ej = __builtin_amdgcn_readlane(e, j);
-            const int m = ej == e;
-            tot += m;
-            rank += m & (j < lane);
-        }
-        for (int q = tid; q < kBucketWaves * 256; q += kBucketThreads) (&wcnt[0][0])[q] = 0;
-        __syncthreads();
-        if (valid && rank == 0) wcnt[wave][e] = tot;
-        __syncthreads();
-        if (valid) {
-            int pos = base[e] + rank;
-            for (int w = 0; w < wave; w++) pos += wcnt[w][e];
-            perm[pos] = i;
-            pos_of[i] = pos;
-            if (tok) tok[pos] = i / K;
-        } else if (i < TK) {
-            pos_of[i] = -1;
-        }
-        __syncthreads();
-        if (tid < E) {
-            int add = 0;
-            for (int w = 0; w < kBucketWaves; w++) add += wcnt[w][tid];
-            base[tid] += add;
-        }
-        __syncthreads();
+    const int i = blockIdx.x * kBucketThreads + tid;
+    if (i >= TK) return;
+    const int e = idx[i];
+    if (e >= 0 && e < E) {
+        const int pos = base[e] + rank[i];
+        perm[pos] = i;
+        pos_of[i] = pos;
+        if (tok) tok[pos] = i / K;
+    } else {
+        pos_of[i] = -1;
     }
 }
+
+// Both bucketing launches; hist needs (TK/1024 + 1) * E ints and rank TK ints of scratch.
+hipError_t launch_bucket(const int *idx, int TK, int E, int K, int *hist, int *rank, int *off, int *perm,
+                         int *pos_of, int *tok, int *tile_expert, int *tile_begin, int *tile_end, int *n_tiles,
+                         hipStream_t st)
+{
+    const int nblk = (TK + kBucketThreads - 1) / kBucketThreads;
+    hipLaunchKernelGGL(k_bucket_rank, dim3(nblk), dim3(kBucketThreads), 0, st, idx, TK, E, hist, rank);
+    hipLaunchKernelGGL(k_bucket_place, dim3(nblk), dim3(kBucketThreads), 0, st, idx, TK, E, K, nblk, hist, rank,
+                       off, perm, pos_of, tok, tile_expert, tile_begin, tile_end, n_tiles);
+    return hipGetLastError();
+}
+
+size_t bucket_scratch_ints(int TK, int E) { return (size_t)(TK / kBucketThreads + 1) * E + TK; }
 
 // out[t][n] = sum over k (in order) of w[t][k] * dn[pos_of[t*K+k]][n], as
 // moe_forward_omp's combined[row] += top_weight * dot (QK:2243-2244); every dn
@@ -188,7 +216,7 @@ struct mllm_moe_layer {
 };
 
 struct moe_ws {
-    int *idx, *off, *perm, *pos_of, *tok, *tile_expert, *tile_begin, *tile_end, *n_tiles;
+    int *idx, *off, *perm, *pos_of, *tok, *tile_expert, *tile_begin, *tile_end, *n_tiles, *bscr;
     float *w, *g, *u, *h, *dn;
     uint8_t *xq_x, *xq_h;
     __bf16 *xp_x, *xp_h;      // split planes of x [T][N] and h [T*K][M] (batched path)
@@ -209,6 +237,7 @@ static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *
     s.perm = (int *)take(TK * 4);
     s.pos_of = (int *)take(TK * 4);
     s.tok = (int *)take(TK * 4);
+    s.bscr = (int *)take(bucket_scratch_ints((int)TK, L.E) * 4);
     s.tile_expert = (int *)take(max_tiles * 4);
     s.tile_begin = (int *)take(max_tiles * 4);
     s.tile_end = (int *)take(max_tiles * 4);
@@ -296,9 +325,8 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     if (batched) {
         if (mllm_sem_uses_q8(L->sem_g) || mllm_sem_uses_q8(L->sem_u))
             CK(mllm_launch_quantize_q8_0(x, T, N, nullptr, q, d, s4, sq, st));
-        hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), 0, st, s.idx, TK, E, K, s.off, s.perm, s.pos_of,
-                           s.tok, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles);
-        CK(hipGetLastError());
+        CK(launch_bucket(s.idx, TK, E, K, s.bscr, s.bscr + (TK / kBucketThreads + 1) * E, s.off, s.perm, s.pos_of,
+                         s.tok, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles, st));
         const int max_tiles = TK / kTileEntries + E + 1;
         // gate + up (+ SiLU) in bucket order
         qgemm_args a{};
@@ -390,9 +418,15 @@ MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm,
 {
     if (E <= 0 || E > 256 || TK <= 0) return -1;
     const int max_tiles = TK / kTileEntries + E + 1;
-    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), 0, (hipStream_t)stream, idx, TK, E, 1, off, perm,
-                       pos_of, nullptr, tiles, tiles + max_tiles, tiles + 2 * max_tiles, tiles + 3 * max_tiles);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    // scratch for this test entry point, allocated here (it is not a hot path)
+    int *scr = nullptr;
+    if (hipMalloc(&scr, bucket_scratch_ints(TK, E) * sizeof(int)) != hipSuccess) return -1;
+    const hipError_t r = launch_bucket(idx, TK, E, 1, scr, scr + (TK / kBucketThreads + 1) * E, off, perm, pos_of,
+                                       nullptr, tiles, tiles + max_tiles, tiles + 2 * max_tiles, tiles + 3 * max_tiles,
+                                       (hipStream_t)stream);
+    const hipError_t r2 = hipStreamSynchronize((hipStream_t)stream);
+    (void)hipFree(scr);
+    return r == hipSuccess && r2 == hipSuccess ? 0 : -1;
 }
 
 } // extern "C"

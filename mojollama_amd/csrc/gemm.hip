@@ -634,10 +634,11 @@ bool mllm_qgemm_supported(int sem)
     return sem != SEM_F32 && sem != SEM_Q5_0_Q8;
 }
 
-// A dense launch with fewer output tiles than CUs is split along K towards
-// ~512 workgroups, each split keeping at least 16 K steps of 64 columns (the
-// partial sums cost an extra pass over ksplit x entries x rows floats, which
-// does not pay on a launch that already fills the GPU).
+// A dense launch with fewer output tiles than CUs is split along K into at
+// most 512 workgroups (two per CU: a launch past that runs a second, partial
+// round of workgroups), each split keeping at least 4 K steps of 64 columns
+// (the partial sums cost an extra pass over ksplit x entries x rows floats,
+// which does not pay on a launch that already fills the GPU).
 int mllm_qgemm_ksplit(int sem, int n_rows, int n_cols, int n_entries)
 {
     if (!mllm_qgemm_supported(sem) || n_entries <= 0) return 1;
@@ -645,8 +646,8 @@ int mllm_qgemm_ksplit(int sem, int n_rows, int n_cols, int n_entries)
     const long tiles = (long)((n_rows + 127) / 128) * ((n_entries + tm - 1) / tm);
     if (tiles >= 256) return 1;
     const int steps = (n_cols + 63) / 64;
-    int ks = (int)((512 + tiles - 1) / tiles);
-    ks = std::min(ks, std::max(1, steps / 16));
+    int ks = (int)(512 / tiles);
+    ks = std::min(ks, std::max(1, steps / 4));
     return std::max(1, std::min(ks, 16));
 }
 

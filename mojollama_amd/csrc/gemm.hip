@@ -243,7 +243,9 @@ MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, in
 }
 
 // Activation task of thread tid.  XM_PLANES: TM_/32 16-byte pieces per plane
-// (entry q/8, columns 8*(q%8) .. +8 of the step, q = tid + 256*i); Q4_K_Q8:
+// (entry q/8, columns 8*(q%8) .. +8 of the step, q = tid + 256*i), planes
+// p < npl only (the lower plane of a tile whose activations are all exact in
+// bf16 is zero and neither loaded, stored nor read); Q4_K_Q8:
 // entry tid/2, part tid&1 (16 quants of one sub-block, k < 16); other Q8
 // forms: entry tid/4, 16 columns at (tid&3)*16.
 template <int TM_, int NB> struct araw {
@@ -255,7 +257,7 @@ template <int TM_, int NB> struct araw {
 
 template <int SEM, int XM, int TM_>
 MLLM_DEV void fetch_a(const qgemm_args &a, const int *ent_row, int n_ent, int k0, int kused,
-                      araw<TM_, gemm_cfg<SEM, XM>::NB> &ar)
+                      araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int npl)
 {
     using C = gemm_cfg<SEM, XM>;
     const int tid = threadIdx.x;
@@ -267,7 +269,8 @@ MLLM_DEV void fetch_a(const qgemm_args &a, const int *ent_row, int n_ent, int k0
             const int q = tid + 256 * i, er = q >> 3, c8 = q & 7;
             const __bf16 *src = a.xp.base + (long)ent_row[er] * a.xp.ldp + k0 + 8 * c8;
 #pragma unroll
-            for (int p = 0; p < C::NB; p++) ar.p[p][i] = gld<uint4>(reinterpret_cast<const uint4 *>(src + p * a.xp.plane));
+            for (int p = 0; p < C::NB; p++)
+                if (p < npl) ar.p[p][i] = gld<uint4>(reinterpret_cast<const uint4 *>(src + p * a.xp.plane));
         }
     } else if constexpr (C::A4) {
         const int er = min(tid >> 1, TM_ - 1), part = tid & 1;
@@ -287,7 +290,7 @@ MLLM_DEV void fetch_a(const qgemm_args &a, const int *ent_row, int n_ent, int k0
 // kused and entries past n_ent are zero.
 template <int SEM, int XM, int TM_>
 MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k0, int kused, __bf16 *Bp,
-                    float *tsum_l)
+                    float *tsum_l, int npl)
 {
     using C = gemm_cfg<SEM, XM>;
     constexpr int LDA = C::LDA, NB = C::NB, PS = TM_ * C::LDA;
@@ -298,7 +301,8 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
         for (int i = 0; i < araw<TM_, NB>::NP; i++) {
             const int q = tid + 256 * i, er = q >> 3, c8 = q & 7;
 #pragma unroll
-            for (int p = 0; p < NB; p++) *reinterpret_cast<uint4 *>(Bp + p * PS + er * LDA + 8 * c8) = ar.p[p][i];
+            for (int p = 0; p < NB; p++)
+                if (p < npl) *reinterpret_cast<uint4 *>(Bp + p * PS + er * LDA + 8 * c8) = ar.p[p][i];
         }
     } else if constexpr (C::A4) {
         if (tid < 2 * TM_) {
@@ -425,13 +429,13 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         const int k0 = min(s, s_end - 1) * KS;   // past the end: refetch the last step (unused)
         fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w, 0);
         if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u, 128);
-        fetch_a<SEM, XM, TM>(a, s_row, n_ent, k0, kused, b.x);
+        fetch_a<SEM, XM, TM>(a, s_row, n_ent, k0, kused, b.x, pb_end);
     };
     auto put_step = [&](int s, const stepbuf &b) __attribute__((always_inline)) {
         const int k0 = s * KS;
         put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr, 0);
         if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr, 128);
-        put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, (C::A4 || XM == XM_Q8D) ? s_tsum : nullptr);
+        put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, (C::A4 || XM == XM_Q8D) ? s_tsum : nullptr, pb_end);
     };
     auto mfma_step = [&]() __attribute__((always_inline)) {
         // MFMA 16x16x32: lane l supplies row/entry (l % 16), k = 8*(l/16) .. +8 of a 32-wide slice
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
             for (int p = 0; p < NB; p++)
 #pragma unroll
                 for (int j = 0; j < JT; j++)
-                    bv[p][j] = *reinterpret_cast<const bf16x8 *>(s_b + p * TM * LDA + (we0 + 16 * j + li) * LDA + ks + lk);
+                    if (p < pb_end) bv[p][j] = *reinterpret_cast<const bf16x8 *>(s_b + p * TM * LDA + (we0 + 16 * j + li) * LDA + ks + lk);
 #pragma unroll
             for (int i = 0; i < IT; i++) {
                 const int ar_ = (wr0 + 16 * i + li) * LDA + ks + lk;

@@ -80,6 +80,14 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
  * are not used as scratch. */
 MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up_buf, float *ffn_buf, int B);
 
+/* moe_ffn (CE:591-665) for each of B tokens, keeping every token's result:
+ * ffn_out[b*N + n] (moe_ffn itself keeps only the last token's, CE:610-643).
+ * No reference counterpart: the batched form of moe_ffn for prefill-sized B.
+ * B > 8 tokens run the grouped-GEMM MoE layer (GPU bucketing by expert) with
+ * moe_ffn's semantics: quant_matmul_omp per projection, unclamped SiLU, the
+ * un-renormalised top-K routing, k-order combine. */
+MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_out, int B);
+
 /* QK:1029-1030: accepted and ignored / number of compute units. */
 MLLM_API void set_num_threads(int n);
 MLLM_API int get_max_threads(void);

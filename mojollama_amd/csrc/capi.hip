@@ -26,6 +26,7 @@
 #include "gemm.h"
 #include "gemv.h"
 #include "mllm.h"
+#include "moe.h"
 
 namespace {
 
@@ -195,7 +196,8 @@ uint64_t fingerprint(const void *p, long n)
     memcpy(&w, b + (n >= 8 ? n - 8 : 0), (size_t)(n >= 8 ? 8 : n));
     return (h ^ w) * 1099511628211ull;
 }
-std::map<std::tuple<const void *, int, int>, float *> g_router_cache;  // (host, E, N) -> routing layout
+// (host, E, N) -> routing-layout copy and the fingerprint of the host router it was made from
+std::map<std::tuple<const void *, int, int>, std::pair<float *, uint64_t>> g_router_cache;
 
 // Upload + pack a raw host matrix (once).  Returns its packed view.
 int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
@@ -237,14 +239,16 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
 
 // Router [E][N] fp32 on the host -> device copy in the routing layout
 // (mllm_router_pack: element (i, e) at ((i/4)*E + e)*4 + i%4, zero pad
-// rows), cached.
+// rows), cached like the weights: a hit whose host contents changed (a new
+// router at a freed one's address) is packed again, the old copy retired.
 int get_router(const float *host, int E, int N, const float **dev_out)
 {
     auto key = std::make_tuple((const void *)host, E, N);
+    const uint64_t fp = fingerprint(host, (long)E * N * 4);
     {
         std::lock_guard<std::mutex> lk(g_cache_mu);
         auto it = g_router_cache.find(key);
-        if (it != g_router_cache.end()) { *dev_out = it->second; return 0; }
+        if (it != g_router_cache.end() && it->second.second == fp) { *dev_out = it->second.first; return 0; }
     }
     std::vector<float> t((size_t)mllm_router_packed_floats(N, E), 0.0f);
     for (int e = 0; e < E; e++)
@@ -253,9 +257,17 @@ int get_router(const float *host, int E, int N, const float **dev_out)
     HIP_OK(hipMalloc(&d, t.size() * 4));
     HIP_OK(hipMemcpy(d, t.data(), t.size() * 4, hipMemcpyHostToDevice));
     std::lock_guard<std::mutex> lk(g_cache_mu);
-    auto ins = g_router_cache.emplace(key, d);
-    if (!ins.second) (void)hipFree(d);
-    *dev_out = ins.first->second;
+    auto it = g_router_cache.find(key);
+    if (it == g_router_cache.end()) {
+        it = g_router_cache.emplace(key, std::make_pair(d, fp)).first;
+    } else if (it->second.second != fp) {
+        // another thread may still be reading the old copy: retire it
+        g_retired.push_back((uint8_t *)it->second.first);
+        it->second = std::make_pair(d, fp);
+    } else {
+        (void)hipFree(d);   // another thread packed the same contents meanwhile
+    }
+    *dev_out = it->second.first;
     return 0;
 }
 
@@ -596,6 +608,9 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
     memcpy(combined, c.h_out.p, N * 4);
 }
 
+int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3], const int qts[3], int N, int E, int K,
+                              int M, const float *x_host, float *out_host, int T);
+
 MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up_buf, float *ffn_buf, int B)
 {
     (void)gate_buf; (void)up_buf;
@@ -608,6 +623,20 @@ MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up
                                bc_field<const uint8_t **>(c, BC_DOWN)[l]};
     // With B > 1 the reference clears ffn_buf per token, so only the last token's result survives (CE:610-643).
     mllm_moe_ffn_dev_tokens(router, bases, qts, N, E, K, M, x + (long)(B - 1) * N, ffn_buf, 1);
+}
+
+// moe_ffn (CE:591-665) applied to each of B tokens, every token's result kept:
+// ffn_out[b*N + n].  No scratch of the caller's is used.
+MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_out, int B)
+{
+    if (B <= 0) return;
+    const int N = bc_field<int>(c, BC_N), E = bc_field<int>(c, BC_NE), K = bc_field<int>(c, BC_NK),
+              M = bc_field<int>(c, BC_M);
+    const int qts[3] = {bc_field<int>(c, BC_QG), bc_field<int>(c, BC_QU), bc_field<int>(c, BC_QD)};
+    const float *router = bc_field<const float **>(c, BC_ROUTER)[l];
+    const uint8_t *bases[3] = {bc_field<const uint8_t **>(c, BC_GATE)[l], bc_field<const uint8_t **>(c, BC_UP)[l],
+                               bc_field<const uint8_t **>(c, BC_DOWN)[l]};
+    mllm_moe_ffn_host_batched(router, bases, qts, N, E, K, M, x, ffn_out, B);
 }
 
 // Out-of-path symbols the reference caller binds unconditionally (TE:263-311,397-408).
@@ -625,7 +654,7 @@ MLLM_API void mllm_cache_clear(void)
     g_cache.clear();
     for (uint8_t *p : g_retired) (void)hipFree(p);
     g_retired.clear();
-    for (auto &kv : g_router_cache) (void)hipFree(kv.second);
+    for (auto &kv : g_router_cache) (void)hipFree(kv.second.first);
     g_router_cache.clear();
 }
 
@@ -784,6 +813,57 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     HIP_OK(mllm_launch_combine(ddn, dwt, T, K, N, dout, 1, st));
     HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
     HIP_OK(hipStreamSynchronize(st));
+    memcpy(out_host, c.h_out.p, (size_t)T * N * 4);
+    return 0;
+}
+
+// moe_ffn over T tokens of host data, every token's result kept: T > 8 tokens
+// whose expert types the grouped GEMM serves run the batched MoE layer (GPU
+// bucketing, grouped MFMA GEMMs) with moe_ffn's semantics (quant_matmul_omp
+// per projection, unclamped SiLU, no renormalisation); the rest the token path.
+int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3], const int qts[3], int N, int E, int K,
+                              int M, const float *x_host, float *out_host, int T)
+{
+    const int sems[3] = {sem_for(ENT_QMM, qts[0]), sem_for(ENT_QMM, qts[1]), sem_for(ENT_QMM, qts[2])};
+    if (T <= 8 || sems[0] < 0 || sems[1] < 0 || sems[2] < 0 || K > 16 || E > 256 || K > E ||
+        !mllm_moe_batched_supported(sems[0], sems[1], sems[2]))
+        return mllm_moe_ffn_dev_tokens(router, bases, qts, N, E, K, M, x_host, out_host, T);
+    thread_ctx &c = t_ctx;
+    if (c.init()) return -1;
+    std::vector<mllm_packed> tab(3 * (size_t)E);
+    for (int w = 0; w < 3; w++) {
+        const long stride = moe_ffn_stride(w, qts[w], N, M);
+        const int rows = w < 2 ? M : N, cols = w < 2 ? N : M;
+        for (int e = 0; e < E; e++)
+            if (get_weight(bases[w] + (long)e * stride, mllm_sem_layout(sems[w]), rows, cols, tab[(size_t)w * E + e])) return -1;
+    }
+    const float *rt = nullptr;
+    if (get_router(router, E, N, &rt)) return -1;
+    if (c.d_tab.ensure(tab.size() * sizeof(mllm_packed))) { set_error("moe_ffn_batched: allocation failed"); return -1; }
+    mllm_moe_layer *L = mllm_moe_layer_from_views(sems[0], sems[1], sems[2], N, M, E, K, (mllm_packed *)c.d_tab.p, rt,
+                                                  0, 0);
+    if (!L) { set_error("moe_ffn_batched: bad layer shape"); return -1; }
+    // scratch: x[T][N] | out[T][N] | layer workspace
+    const size_t ws = (size_t)mllm_moe_workspace_size(L, T);
+    const size_t o_o = align256((size_t)T * N * 4), o_ws = align256(o_o + (size_t)T * N * 4), total = o_ws + ws;
+    if (c.d_scr.ensure(total) || c.h_in.ensure((size_t)T * N * 4) || c.h_out.ensure((size_t)T * N * 4)) {
+        mllm_moe_release(L);
+        set_error("moe_ffn_batched: scratch allocation failed");
+        return -1;
+    }
+    uint8_t *S = (uint8_t *)c.d_scr.p;
+    float *dx = (float *)S, *dout = (float *)(S + o_o);
+    hipStream_t st = c.st;
+    memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
+    int rc = -1;
+    if (hipMemcpyAsync(c.d_tab.p, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st) == hipSuccess &&
+        hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st) == hipSuccess &&
+        mllm_moe_forward(L, dx, T, dout, S + o_ws, (long)ws, nullptr, nullptr, st) == 0 &&
+        hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess)
+        rc = 0;
+    mllm_moe_release(L);
+    if (rc) { set_error("moe_ffn_batched: launch failed"); return -1; }
     memcpy(out_host, c.h_out.p, (size_t)T * N * 4);
     return 0;
 }

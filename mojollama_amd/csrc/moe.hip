@@ -20,6 +20,7 @@
 #include "gemm.h"
 #include "gemv.h"
 #include "mllm.h"
+#include "moe.h"
 
 namespace {
 
@@ -211,8 +212,10 @@ int xmode_of(int sem)
 struct mllm_moe_layer {
     int N, M, E, K, renorm;
     int sem_g, sem_u, sem_d;
-    float *router_p;    // device, routing layout (mllm_router_pack), owned
-    mllm_packed *tab;   // device: [E] gate, [E] up, [E] down
+    int clamp;          // SiLU with the gate clamped to +-80 (moe_forward_omp) or not (moe_ffn)
+    int owns_router, owns_tab;
+    float *router_p;    // device, routing layout (mllm_router_pack); freed with the layer when owned
+    mllm_packed *tab;   // device: [E] gate, [E] up, [E] down; freed with the layer when owned
 };
 
 struct moe_ws {
@@ -266,6 +269,9 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
     if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0) return nullptr;
     mllm_moe_layer *L = new mllm_moe_layer;
     L->N = N; L->M = M; L->E = E; L->K = K; L->renorm = renorm;
+    L->clamp = 1;
+    L->owns_router = 1;
+    L->owns_tab = 1;
     L->sem_g = sem_gu_of(qt_gate, qt_up, 0);
     L->sem_u = sem_gu_of(qt_gate, qt_up, 1);
     L->sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);     // Q4_K down: the reference adds zeros
@@ -292,8 +298,8 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
 MLLM_API void mllm_moe_release(mllm_moe_layer *L)
 {
     if (!L) return;
-    if (L->tab) (void)hipFree(L->tab);
-    if (L->router_p) (void)hipFree(L->router_p);
+    if (L->tab && L->owns_tab) (void)hipFree(L->tab);
+    if (L->router_p && L->owns_router) (void)hipFree(L->router_p);
     delete L;
 }
 
@@ -342,7 +348,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
         a.row_of = s.tok;
         a.n_rows = M; a.n_cols = N;
         a.tile_expert = s.tile_expert; a.tile_begin = s.tile_begin; a.tile_end = s.tile_end; a.n_tiles = s.n_tiles;
-        a.clamp_silu = 1;
+        a.clamp_silu = L->clamp;
         if (L->sem_g == L->sem_u) {
             a.out = s.h; a.ldo = M;
             CK(mllm_launch_qgemm(L->sem_g, xmode_of(L->sem_g), true, a, max_tiles, st));
@@ -351,7 +357,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             CK(mllm_launch_qgemm(L->sem_g, xmode_of(L->sem_g), false, a, max_tiles, st));
             a.table = L->tab + E; a.out = s.u;
             CK(mllm_launch_qgemm(L->sem_u, xmode_of(L->sem_u), false, a, max_tiles, st));
-            CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
+            CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, L->clamp, st));
         }
         // down, rows of h already in bucket order
         if (L->sem_d >= 0) {
@@ -397,8 +403,10 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             b.x = s.g; b.x_job_stride = M; b.ldx = M;
             b.out = s.dn; b.out_job_stride = N; b.ldo = N;
             b.n_rows = N; b.n_cols = M; b.B = 1;
-            if (L->sem_d == SEM_F32) {
-                CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, 1, st));
+            if (L->sem_d == SEM_F32 || !L->clamp) {
+                // the down GEMV forms the clamped SiLU product itself; a separate
+                // product for fp32 rows and for the unclamped SiLU
+                CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, L->clamp, st));
                 b.x = s.h;
             } else {
                 b.x_up = s.u;
@@ -430,3 +438,24 @@ MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm,
 }
 
 } // extern "C"
+
+// moe_ffn's SiLU is unclamped (CE:649-652).
+mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N, int M, int E, int K,
+                                          const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp)
+{
+    if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0 || !tab_dev || !router_p) return nullptr;
+    mllm_moe_layer *L = new mllm_moe_layer;
+    L->N = N; L->M = M; L->E = E; L->K = K; L->renorm = renorm;
+    L->clamp = clamp;
+    L->owns_router = 0;
+    L->owns_tab = 0;
+    L->sem_g = sem_g; L->sem_u = sem_u; L->sem_d = sem_d;
+    L->router_p = const_cast<float *>(router_p);
+    L->tab = const_cast<mllm_packed *>(tab_dev);
+    return L;
+}
+
+bool mllm_moe_batched_supported(int sem_g, int sem_u, int sem_d)
+{
+    return mllm_qgemm_supported(sem_g) && mllm_qgemm_supported(sem_u) && (sem_d < 0 || mllm_qgemm_supported(sem_d));
+}

@@ -83,6 +83,8 @@ def load_kernels(path=LIB_PATH):
         getattr(so, name).restype = None
     so.moe_ffn.argtypes = [cvp, ci, cf, cf, cf, cf, ci]
     so.moe_ffn.restype = None
+    so.moe_ffn_batched.argtypes = [cvp, ci, cf, cf, ci]
+    so.moe_ffn_batched.restype = None
     so.quantize_row_q8_0.argtypes = [cf, cu, ci]
     so.quantize_row_q8_0.restype = ci
     so.get_max_threads.argtypes = []

@@ -317,3 +317,67 @@ def test_device_route_exact_ties(dev, orc, T, renorm):
     idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
     assert np.array_equal(idx.cpu().numpy(), ri)
     assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
+
+
+def _moe_ffn_case(qts, N, M, E, Kk, T, seed):
+    rng = np.random.default_rng(seed)
+    gate = np.concatenate([W.gen_weights(rng, qts[0], M, N) for _ in range(E)])
+    upw = np.concatenate([W.gen_weights(rng, qts[1], M, N) for _ in range(E)])
+    down = np.concatenate([W.gen_weights(rng, qts[2], N, M) for _ in range(E)])
+    router = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, T, N)
+    return gate, upw, down, router, x
+
+
+@pytest.mark.parametrize("tag", ["q4k", "mxfp4"])
+def test_golden_moe_ffn_batched(lib, golden, tag):
+    """moe_ffn_batched keeps every token's moe_ffn result (B <= 8: the token path)."""
+    g = golden(f"moe_ffn_{tag}.npz")
+    N, E, Kk, M = (int(g[k]) for k in ("N", "E", "K", "M"))
+    bc = BCView(N, E, Kk, M, g["router"], g["gate"], g["up"], g["down"], tuple(int(v) for v in g["qts"]))
+    T = g["x"].shape[0]
+    out = np.full((T, N), np.nan, np.float32)
+    lib.moe_ffn_batched(bc.ptr(), 0, fp(np.ascontiguousarray(g["x"], np.float32)), fp(out), T)
+    assert O.norm_err(out, g["out"]) < MOE_TOL, K.last_error(lib)
+
+
+@pytest.mark.parametrize("qts", [(12, 12, 14), (39, 39, 39), (14, 14, 14)])
+@pytest.mark.parametrize("T", [37, 160])
+def test_moe_ffn_batched_vs_oracle(lib, orc, qts, T):
+    """B > 8: the grouped-GEMM layer with moe_ffn's semantics (quant_matmul_omp per
+    projection, unclamped SiLU, no renormalisation) against the oracle's moe_ffn
+    token by token, and against this library's own moe_ffn at B = 1."""
+    N, M, E, Kk = 256, 256, 8, 2
+    gate, upw, down, router, x = _moe_ffn_case(qts, N, M, E, Kk, T, seed=T + sum(qts))
+    bc = BCView(N, E, Kk, M, router, gate, upw, down, qts)
+    out = np.full((T, N), np.nan, np.float32)
+    lib.moe_ffn_batched(bc.ptr(), 0, fp(np.ascontiguousarray(x)), fp(out), T)
+    ref = np.stack([orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t]) for t in range(T)])
+    assert O.norm_err(out, ref) < MOE_TOL, K.last_error(lib)
+    one = np.stack([moe_ffn(lib, bc, x[t], N) for t in range(0, T, 7)])
+    assert O.norm_err(out[::7], one) < MOE_TOL
+
+
+def test_moe_ffn_batched_large_gate(lib, orc):
+    """Gate values past +-80 take moe_ffn's unclamped SiLU on the batched path."""
+    qts, N, M, E, Kk, T = (39, 39, 39), 256, 256, 8, 2, 24
+    gate, upw, down, router, x = _moe_ffn_case(qts, N, M, E, Kk, T, seed=5)
+    x = x * 60.0   # gate outputs well beyond 80 in magnitude
+    bc = BCView(N, E, Kk, M, router, gate, upw, down, qts)
+    out = np.full((T, N), np.nan, np.float32)
+    lib.moe_ffn_batched(bc.ptr(), 0, fp(np.ascontiguousarray(x, np.float32)), fp(out), T)
+    ref = np.stack([orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t]) for t in range(T)])
+    assert O.norm_err(out, ref) < MOE_TOL, K.last_error(lib)
+
+
+def test_moe_ffn_router_rewritten_in_place(lib, orc):
+    """A router whose host contents change at the same address is packed again
+    (the device cache keys on the address and checks the contents)."""
+    qts, N, M, E, Kk, T = (14, 14, 14), 256, 256, 8, 2, 3
+    gate, upw, down, router, x = _moe_ffn_case(qts, N, M, E, Kk, T, seed=11)
+    bc = BCView(N, E, Kk, M, router, gate, upw, down, qts)
+    for step in range(2):
+        got = np.stack([moe_ffn(lib, bc, x[t], N) for t in range(T)])
+        ref = np.stack([orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t]) for t in range(T)])
+        assert O.norm_err(got, ref) < MOE_TOL, step
+        router[:] = router[::-1].copy()   # other experts win, same buffer

@@ -12,6 +12,10 @@
 // weights (int4 times a power of two) and Q8_0 quants; their partners then
 // get three, which makes those products exact to fp32.  Everything else uses
 // two planes each and the three leading products (normalised error ~5e-6).
+// Q4_K against Q8_0 quants runs on v_mfma_f32_16x16x32_f16 instead: the
+// sub-block scale times the nibble and the quants are small integers, exact
+// in fp16, so each MFMA returns the step's integer dot exactly and the
+// super-block scale d is applied to it per row.
 //
 // Tiling.  Workgroup = 4 wave64s, tile TN (128, or 64 when gate and up share
 // it) rows x 64 entries, K staged KE columns at a time; a wave owns 32 rows
@@ -25,12 +29,16 @@
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int SEM, int XM> struct gemm_cfg {
+    // Q4_K against Q8_0 quants (dot_q4_k_q8_0): the integer part sc * nibble
+    // (<= 945) and the quants are exact in fp16, so one fp16 MFMA per tile
+    // gives the sub-blocks' integer dot exactly; d is applied per step.
     static constexpr bool A4 = (SEM == SEM_Q4_K_Q8);
     static constexpr bool WEXACT = (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP || SEM == SEM_MXFP4_Q8);
-    static constexpr int NA = WEXACT ? 1 : (A4 ? 3 : 2);
+    static constexpr int NA = (WEXACT || A4) ? 1 : 2;
     // Q8_0 quants are exact in one bf16 plane; XM_Q8D applies their block scale
     // after each 32-column MFMA (one Q8_0 block per k-slice).
     static constexpr int NB = (XM == XM_Q8 || XM == XM_Q8D) ? 1 : (XM == XM_PLANES && !WEXACT) ? 2 : 3;
@@ -54,6 +62,16 @@ template <bool DUAL, int TM_> struct tile_cfg {
     static constexpr int IT = TN / WR / 16;
     static constexpr int JT = TM_ / WE / 16;
 };
+
+// 16 values exact in fp16 (integers below 2048) as fp16, in bf16-typed storage.
+MLLM_DEV void put16_f16(__bf16 *dst, const float (&v)[16])
+{
+    f16x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { a[i] = (_Float16)v[i]; b[i] = (_Float16)v[8 + i]; }
+    *reinterpret_cast<f16x8 *>(dst) = a;
+    *reinterpret_cast<f16x8 *>(dst + 8) = b;
+}
 
 MLLM_DEV void put16(__bf16 *dst, const float (&v)[16])
 {
@@ -194,17 +212,21 @@ MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, in
             // dot_q4_k_q8_0 (QK:1647-1735): the integer term reads k < 16 of each 32-element
             // sub-block; group g of a super-block holds sub-blocks 2g (low nibbles) and 2g+1
             // (high nibbles).  Step columns: 0..15 = sub-block 2g, 16..31 = 2g+1, w = d*sc_j*nib.
-            // this task: half sub = 0 (sub-block 2g, low nibbles) or 1 (2g+1, high nibbles)
+            // this task: half sub = 0 (sub-block 2g, low nibbles) or 1 (2g+1, high nibbles);
+            // stored: sc_j * nibble (fp16, exact); per row dmin at dmin_l[rr], d at dmin_l[TN_ + rr]
             const int g = c & 3;
             int s1, m1, s2, m2;
             kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
-            const float ds = h2f(r.m.x & 0xFFFF) * (float)(sub ? s2 : s1);
+            const float sc = (float)(sub ? s2 : s1);
             const uint32_t Aw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
             float v[16];
 #pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = ds * (float)((Aw[e >> 2] >> (8 * (e & 3) + 4 * sub)) & 15);
-            put16_planes<NA>(A, PS, rr * LDA + 16 * sub, v);
-            if (dmin_l && sub == 0) dmin_l[rr] = h2f(r.m.x >> 16);
+            for (int e = 0; e < 16; e++) v[e] = sc * (float)((Aw[e >> 2] >> (8 * (e & 3) + 4 * sub)) & 15);
+            put16_f16(A + rr * LDA + 16 * sub, v);
+            if (dmin_l && sub == 0) {
+                dmin_l[rr] = h2f(r.m.x >> 16);
+                dmin_l[TN_ + rr] = h2f(r.m.x & 0xFFFF);
+            }
         } else if constexpr (SEM == SEM_MXFP4_Q8) {
             // mxfp4_row_dot_q8 (QK:629-678) with the token's Q8 scale moved to the activation
             // side: w = sext4(n) * 2^(E-127), exact in bf16.
@@ -316,7 +338,7 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
                 zero16(v);
                 if (part == 0 && tsum_l) tsum_l[er] = 0.0f;
             }
-            put16_planes<NB>(Bp, PS, er * LDA + 16 * part, v);
+            put16_f16(Bp + er * LDA + 16 * part, v);
         }
     } else {
         if (tid < 4 * TM_) {
@@ -362,7 +384,7 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
     __shared__ __attribute__((aligned(16))) __bf16 s_b[NB * TM * LDA];
     __shared__ int s_row[TM];
     // s_tsum: Q4_K_Q8 min-term sums per entry, or Q8D block scales per entry and 32-column half
-    __shared__ float s_dmin[C::A4 ? TN : 1], s_dmin2[C::A4 && DUAL ? TN : 1],
+    __shared__ __attribute__((aligned(16))) float s_dmin[C::A4 ? 2 * TN : 1], s_dmin2[C::A4 && DUAL ? 2 * TN : 1],
         s_tsum[C::A4 ? TM : (XM == XM_Q8D ? 2 * TM : 1)];
     constexpr int BE = mllm_sem_uses_q8(SEM) ? q8_traits<SEM>::kBlockElems : sem_traits<SEM>::kBlockElems;
 
@@ -462,6 +484,17 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
 #pragma unroll
                         for (int v = 0; v < 4; v++) acc[i][j][v] = fmaf(sc, d[v], acc[i][j][v]);
                     }
+                } else if constexpr (C::A4) {
+                    // exact integer dot of the step's two 16-column sub-block halves, then d per row
+                    const f32x4 dr = *reinterpret_cast<const f32x4 *>(s_dmin + TN + wr0 + 16 * i + 4 * (lane >> 4));
+#pragma unroll
+                    for (int j = 0; j < JT; j++) {
+                        const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[0]),
+                                                                             __builtin_bit_cast(f16x8, bv[0][j]),
+                                                                             f32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[i][j][v] = fmaf(dr[v], t[v], acc[i][j][v]);
+                    }
                 } else {
 #pragma unroll
                     for (int j = 0; j < JT; j++)
@@ -482,6 +515,16 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
                             const float sc = s_tsum[2 * (we0 + 16 * j + li) + (ks >> 5)];
 #pragma unroll
                             for (int v = 0; v < 4; v++) acc2[i][j][v] = fmaf(sc, d[v], acc2[i][j][v]);
+                        }
+                    } else if constexpr (C::A4) {
+                        const f32x4 dr = *reinterpret_cast<const f32x4 *>(s_dmin2 + TN + wr0 + 16 * i + 4 * (lane >> 4));
+#pragma unroll
+                        for (int j = 0; j < JT; j++) {
+                            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[0]),
+                                                                                 __builtin_bit_cast(f16x8, bv[0][j]),
+                                                                                 f32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; v++) acc2[i][j][v] = fmaf(dr[v], t[v], acc2[i][j][v]);
                         }
                     } else {
 #pragma unroll

@@ -177,15 +177,50 @@ def cpu_reference(layers_np, lm_np, B, passes=5):
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
-def bench_prefill(torch, dev, args):
+def cpu_batch_matmul_reference(name, raw_np, R, C, M, reps=3):
+    """The reference's *_batch_matmul (oracle/_ref, AVX2 + OpenMP) on one matrix at batch M:
+    median seconds per call after one warm-up, or None when the reference build is absent."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    if not O.ref_available():
+        return None, 0
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    ref = O.RefLib()
+    ref.so.set_num_threads(cores)
+    fn = getattr(ref.so, name)
+    x = W.gen_x(np.random.default_rng(6), M, C)
+    out = np.zeros(M * R, np.float32)
+    call = lambda: fn(raw_np.ctypes.data_as(K.cu), x.ctypes.data_as(K.cf), out.ctypes.data_as(K.cf), R, C, M)  # noqa: E731
+    call()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        call()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts)), cores
+
+
+def bench_prefill(torch, dev, args, with_cpu=False):
     """configs[2]: Q4_K gate/up 5632x2048 and Q6_K down 2048x5632 at M in {128, 512, 1280}
-    bf16-valued activations, *_batch_matmul semantics, through the MFMA GEMM."""
+    bf16-valued activations, *_batch_matmul semantics, through the MFMA GEMM; with_cpu adds
+    the reference's q4_k/q6_k_batch_matmul at M = 128 on the host cores."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(3)
     out = {}
     mats = {"gate_q4k": (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048), "down_q6k": (K.Q6_K_SEQ, W.QT_Q6_K, 2048, 5632)}
+    cpu_names = {"gate_q4k": "q4_k_batch_matmul", "down_q6k": "q6_k_batch_matmul"}
     for name, (sem, qt, R, C) in mats.items():
         raw = W.gen_weights_torch(gen, qt, R, C)
+        if with_cpu:
+            sec, cores = cpu_batch_matmul_reference(cpu_names[name], raw.cpu().numpy(), R, C, 128)
+            if sec:
+                tf = 2.0 * R * C * 128 / sec / 1e12
+                out.setdefault("cpu_baseline", {})[f"{name}_M128"] = {
+                    "value": round(tf, 4), "unit": "TFLOP/s", "cores": cores, "kind": "reference",
+                    "ms": round(sec * 1e3, 2),
+                    "sample": f"{cpu_names[name]} (oracle/_ref, AVX2+OpenMP, {cores} threads), B=128, median of 3"}
+                print(f"[bench] CPU reference {cpu_names[name]} M=128: {sec * 1e3:.1f} ms, {tf * 1e3:.1f} GFLOP/s",
+                      file=sys.stderr, flush=True)
         packed = dev.pack(sem, raw, R, C)
         for M in (128, 512, 1280):
             x = torch.randn(M, C, device="cuda", generator=gen).bfloat16().float()
@@ -352,6 +387,31 @@ def main():
     q8_gbs = algo_bytes(q8[0], 1) / (ms_q8 * 1e-3 / len(q8)) / 1e9
     print(f"[bench] Q8_0 5632x2048 GEMV: {ms_q8 * 1e3 / len(q8):.2f} us/launch, {q8_gbs:.1f} GB/s", file=sys.stderr,
           flush=True)
+    q8_cpu = None
+    if not args.no_cpu:
+        # the reference's q8_0_batch_matmul at B = 1 on the host cores, 24 rotating matrices (over 280 MB)
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        if O.ref_available():
+            w8 = [W.gen_weights(np.random.default_rng(100 + i), W.QT_Q8_0, 5632, 2048) for i in range(24)]
+            cores = min(len(os.sched_getaffinity(0)), 16)
+            ref = O.RefLib()
+            ref.so.set_num_threads(cores)
+            xh = W.gen_x(np.random.default_rng(0), 1, 2048)
+            oh = np.zeros(5632, np.float32)
+            ref.so.q8_0_batch_matmul(w8[0].ctypes.data_as(K.cu), xh.ctypes.data_as(K.cf), oh.ctypes.data_as(K.cf),
+                                     5632, 2048, 1)   # warm-up
+            t0 = time.perf_counter()
+            for w in w8 * 2:
+                ref.so.q8_0_batch_matmul(w.ctypes.data_as(K.cu), xh.ctypes.data_as(K.cf), oh.ctypes.data_as(K.cf),
+                                         5632, 2048, 1)
+            sec = (time.perf_counter() - t0) / (2 * len(w8))
+            q8_cpu = {"value": round(algo_bytes(q8[0], 1) / sec / 1e9, 2), "unit": "GB/s", "cores": cores,
+                      "kind": "reference", "us": round(sec * 1e6, 1),
+                      "sample": f"q8_0_batch_matmul (oracle/_ref, AVX2+OpenMP, {cores} threads), B=1, "
+                                f"48 calls over 24 rotating 12 MB matrices"}
+            print(f"[bench] CPU reference q8_0_batch_matmul: {sec * 1e6:.1f} us, {q8_cpu['value']} GB/s",
+                  file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
@@ -367,7 +427,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        extra["configs2_prefill_gemm"] = bench_prefill(torch, dev, args)
+        extra["configs2_prefill_gemm"] = bench_prefill(torch, dev, args, with_cpu=not args.no_cpu)
         extra["configs3_gptoss_moe"] = bench_moe(torch, dev, args, "gptoss", with_cpu=not args.no_cpu)
         extra["configs4_qwen3_moe"] = bench_moe(torch, dev, args, "qwen3", with_cpu=not args.no_cpu)
 
@@ -391,7 +451,7 @@ def main():
                    "B4": {"ms_per_pass": round(results[4][0], 4), "GB/s": round(results[4][1], 1)},
                    "B8": {"ms_per_pass": round(results[8][0], 4), "GB/s": round(results[8][1], 1)},
                    "configs0_q8_0_gemv": {"us": round(ms_q8 * 1e3 / len(q8), 3), "GB/s": round(q8_gbs, 1),
-                                          "hbm_frac": round(q8_gbs / HBM_PEAK_GBS, 4)}},
+                                          "hbm_frac": round(q8_gbs / HBM_PEAK_GBS, 4), "cpu_baseline": q8_cpu}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "kernel": f"k_gemv_p<Q4_K_GGML,B=1> fused gate+up 11264x2048 ({gu_bytes:,} algorithmic B/launch)"},

@@ -388,26 +388,40 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         s_tsum[C::A4 ? TM : (XM == XM_Q8D ? 2 * TM : 1)];
     constexpr int BE = mllm_sem_uses_q8(SEM) ? q8_traits<SEM>::kBlockElems : sem_traits<SEM>::kBlockElems;
 
-    // ---- work tile
+    // ---- work tile.  Workgroups reach the 8 XCDs round-robin by linear id and
+    // each XCD has its own L2.  The live (weight tile, entry tile) pairs -- an
+    // expert launch sizes its grid for the most tiles the bucketing can make,
+    // of which *n_tiles are real -- are remapped so that each XCD takes an
+    // equal contiguous range of them, entry tile fastest: the entry tiles that
+    // share a weight tile run on one XCD, close together in time.
+    int bx, by;
+    {
+        const int nx = gridDim.x, ny = a.tile_expert ? *a.n_tiles : (int)gridDim.y, total = nx * ny;
+        const int L = blockIdx.x + nx * blockIdx.y;
+        if (L >= total) return;
+        const int xcd = L & 7;
+        const int w = xcd * (total >> 3) + min(xcd, total & 7) + (L >> 3);
+        by = w % ny;
+        bx = w / ny;
+    }
     int p0, p1;
     mllm_packed W, W2;
     if (a.tile_expert) {
-        const int ti = blockIdx.y;
-        if (ti >= *a.n_tiles) return;
+        const int ti = by;
         const int e = a.tile_expert[ti];
         p0 = a.tile_begin[ti];
         p1 = a.tile_end[ti];
         W = a.table[e];
         if constexpr (DUAL) W2 = a.table2[e];
     } else {
-        p0 = blockIdx.y * TM;
+        p0 = by * TM;
         p1 = min(p0 + TM, a.n_entries);
         W = a.W;
         if constexpr (DUAL) W2 = a.W2;
     }
     const int n_ent = p1 - p0;
     if (n_ent <= 0) return;
-    const int n0 = blockIdx.x * TN;
+    const int n0 = bx * TN;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int lo_any = 0;   // some entry's activation is not bf16-exact: the lo plane takes part
     if (tid < TM) {

@@ -381,3 +381,13 @@ def test_moe_ffn_router_rewritten_in_place(lib, orc):
         ref = np.stack([orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t]) for t in range(T)])
         assert O.norm_err(got, ref) < MOE_TOL, step
         router[:] = router[::-1].copy()   # other experts win, same buffer
+
+
+@pytest.mark.parametrize("qts,N,M", [((39, 39, 39), 224, 96), ((2, 2, 2), 160, 96), ((39, 39, 2), 96, 160)])
+@pytest.mark.parametrize("E,Kk,T", [(12, 3, 9), (12, 3, 50), (5, 1, 23)])
+def test_moe_layer_batched_odd_shapes(dev, orc, qts, N, M, E, Kk, T):
+    """Batched path (T > 8) at shapes off every power of two: K not a multiple
+    of 64 (padded activation rows), rows not a multiple of the weight tile,
+    expert counts whose tiles spread unevenly over the XCDs, odd top-K."""
+    got, ref = _moe_case(dev, orc, qts, N=N, M=M, E=E, Kk=Kk, T=T, renorm=int(Kk > 1), seed=T * 7 + E + N)
+    assert O.norm_err(got, ref) < moe_tol(qts), K.last_error(dev.so)

@@ -289,18 +289,17 @@ MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
         k.x1 = k.x0 + 64;
     } else if constexpr (SEM == SEM_Q6_K_SEQ) {
         // CE:315-378: element e = nibble (e&1) of ql[e/2] | ((qh[e/4] >> 2(e&3)) & 3) << 4, minus 32; scale sc[e/16].
+        // Word m covers elements 8m' .. 8m'+7 of its qh word (m' = m & 1): their 16 qh bits h hold, in
+        // nibble t, element 2t's two bits below element 2t+1's.  Nibble t goes to byte t (one byte
+        // permute, one masked shift), then each half lands at bits 4-5 of its code byte.
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const uint32_t qw = (m < 2) ? r.b.x : r.b.y;
-            const int base = 8 * (m & 1);               // element offset within the 16 covered by qw
-            uint32_t ue = 0, uo = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                ue |= ((qw >> (2 * (base + 2 * t))) & 3u) << (8 * t + 4);
-                uo |= ((qw >> (2 * (base + 2 * t + 1))) & 3u) << (8 * t + 4);
-            }
-            k.U[2 * m] = (A[m] & L4) | ue;
-            k.U[2 * m + 1] = ((A[m] >> 4) & L4) | uo;
+            const uint32_t h = qw >> (16 * (m & 1));
+            uint32_t nb = __builtin_amdgcn_perm(h, h, 0x01010000u);     // bytes h0, h0, h1, h1
+            nb = (nb & 0x000F000Fu) | ((nb >> 4) & 0x0F000F00u);         // byte t = nibble t of h
+            k.U[2 * m] = (A[m] & L4) | ((nb & 0x03030303u) << 4);
+            k.U[2 * m + 1] = ((A[m] >> 4) & L4) | ((nb & 0x0C0C0C0Cu) << 2);
         }
         const float d = h2f(r.d);
         k.s0 = d * (float)(int8_t)(r.m.x & 0xFF);

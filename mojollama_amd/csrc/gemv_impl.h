@@ -74,9 +74,9 @@ MLLM_DEV job_view view_job(const mllm_gemv_args &a, int job)
 //
 // fp32-activation semantics run their dot products on integers.  Each
 // 16-element group of x is written as P * (d0 + d1/2^7 + d2/2^14) with P a
-// power of two (P >= max|x|/126, so |d0| <= 127) and d1, d2 in [-64, 64]:
-// all of it exact in fp32 except the discarded remainder, below 2^-15 of P,
-// i.e. within ~5e-7 of the group's largest element.  A run of 16 weight codes
+// power of two (max|x| / P in [32, 64), so |d0| <= 64) and d1, d2 in [-64, 64]:
+// all of it exact in fp32 except the discarded remainder, at most 2^-15 of P,
+// i.e. below 2^-20 of the group's largest element.  A run of 16 weight codes
 // u then dots each digit plane with v_dot4_i32_i8 (exact in int32), and
 //   sum_i (s*(u_i - bias) + o) * x_i = s*P*(I0 + I1/2^7 + I2/2^14) + (o - s*bias) * sum_i x_i.
 // LDS per token: three digit planes of PL = KT + KT/16 bytes (16 bytes of
@@ -261,18 +261,35 @@ MLLM_DEV float code_f(uint32_t U, int t)
     else return ubyte_f(U, t);
 }
 
-// sum over one run of u_i * x_i in units of P: I0 + I1/2^7 + I2/2^14.
+// sum over one run of u_i * x_i in units of P: I0 + I1/2^7 + I2/2^14.  Codes
+// |u| <= 64 (every format but Q8_0): the one integer (I0*2^7 + I1)*2^7 + I2,
+// formed by a single v_dot4 chain that shifts its accumulator between planes
+// and converted once; |d0|, |d1|, |d2| <= 64 over 16 elements bound it by
+// 16*64*64*(2^14 + 2^7 + 1) < 2^31.  Q8_0's codes reach -128, which could
+// carry the chain to 2^31: three accumulators there.
+template <int SEM>
 MLLM_DEV float run_idot(const uint32_t *U, const run_digits &x)
 {
-    int I[3];
+    if constexpr (SEM == SEM_Q8_0) {
+        int I[3];
 #pragma unroll
-    for (int p = 0; p < 3; p++) {
+        for (int p = 0; p < 3; p++) {
+            int acc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot4((int)U[j], (int)x.w[p][j], acc, false);
+            I[p] = acc;
+        }
+        return fmaf((float)I[2], 0x1p-14f, fmaf((float)I[1], 0x1p-7f, (float)I[0]));
+    } else {
         int acc = 0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot4((int)U[j], (int)x.w[p][j], acc, false);
-        I[p] = acc;
+        for (int p = 0; p < 3; p++) {
+            if (p) acc <<= 7;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_sdot4((int)U[j], (int)x.w[p][j], acc, false);
+        }
+        return (float)acc * 0x1p-14f;
     }
-    return fmaf((float)I[2], 0x1p-14f, fmaf((float)I[1], 0x1p-7f, (float)I[0]));
 }
 
 // Contribution of one decoded chunk to one token.
@@ -282,7 +299,7 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
     constexpr int ibias = digit_bias<SEM>();
     constexpr float bias = (float)ibias;
     constexpr bool need_sum = ibias != 0 || sem_traits<SEM>::kOffset;
-    float t = fmaf(k.s0 * x0.P, run_idot(k.U, x0), (k.s1 * x1.P) * run_idot(k.U + 4, x1));
+    float t = fmaf(k.s0 * x0.P, run_idot<SEM>(k.U, x0), (k.s1 * x1.P) * run_idot<SEM>(k.U + 4, x1));
     if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), x0.sum, fmaf(fmaf(-k.s1, bias, k.o1), x1.sum, t));
     if (!isfinite(t)) {
         // inf/NaN somewhere (scale, activation or an overflowing partial): weigh each

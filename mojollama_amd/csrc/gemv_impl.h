@@ -858,16 +858,19 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
     auto waste = [&](int lpr) { int it = (nch + lpr - 1) / lpr; return (double)(it * lpr - nch) / (it * lpr); };
     int lpr = 64;
+    auto wgs_at = [&](int l) { const int rpw = 4 * (64 / l) * R; return (long)(a.n_rows + rpw - 1) / rpw * n_jobs; };
     if (BM == 1) {
         const long row_bytes = (long)kused / 32 * sem_traits<SEM>::kBytesPer32;
         lpr = row_bytes <= 1800 ? 16 : row_bytes <= 5000 ? 32 : 64;
         // short matrices: wider lane groups (fewer rows per workgroup) until
         // the launch has about two workgroups per CU
-        auto wgs_at = [&](int l) { const int rpw = 4 * (64 / l) * R; return (long)(a.n_rows + rpw - 1) / rpw * n_jobs; };
         while (lpr < 64 && wgs_at(lpr) < 2L * device_cus()) lpr *= 2;
     } else {
-        // lanes per row: enough chunks per lane to keep every lane busy on short rows
-        if (nch < 64 || waste(64) > waste(32) + 0.05) lpr = 32;
+        // lanes per row: enough chunks per lane to keep every lane busy on short
+        // rows; 32 where that still leaves two workgroups per CU (fewer lane-group
+        // reductions per row: measured faster on the 11264-row gate+up, slower
+        // on 2048-2560 rows)
+        if (nch < 64 || waste(64) > waste(32) + 0.05 || wgs_at(32) >= 2L * device_cus()) lpr = 32;
         if (nch < 32 || (lpr == 32 && waste(32) > waste(16) + 0.05)) lpr = 16;
     }
     const int rows_per_wg = 4 * (64 / lpr) * R;

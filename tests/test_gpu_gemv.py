@@ -136,6 +136,34 @@ def test_device_gemv_vs_oracle(dev, orc, sem, B):
     assert O.norm_err(got, ref) < GEMV_TOL, (K.SEM_NAMES[sem], B)
 
 
+@pytest.mark.parametrize("sem", [K.Q4_0, K.Q8_0, K.Q4_K_GGML, K.Q5_K_GGML, K.Q6_K_SEQ])
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_device_gemv_nonfinite_scales(dev, orc, sem, B):
+    """Blocks whose fp16 scale is inf or NaN take the per-element path (w = s*q, then w*x, as
+    the reference weighs them): the NaN/inf pattern matches the oracle exactly, and rows
+    decoded beside them in the same lane group stay within tolerance."""
+    import torch
+    rng = np.random.default_rng(77 + 16 * B + sem)
+    qt = SEM_QT[sem]
+    be, bb = W.BLOCK[qt]
+    R, C = 24, 768 if be == 256 else 800
+    w = W.gen_weights(rng, qt, R, C).reshape(R, C // be, bb)
+    d_off = 208 if qt == W.QT_Q6_K else 0   # the block's fp16 d
+    for row, blk, bits in ((3, 1, 0x7C00), (6, 0, 0x7E00), (9, 2, 0xFC00)):
+        w[row, blk, d_off:d_off + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    w = w.ravel()
+    x = W.gen_x(rng, B, C)
+    ref = orc.gemv(sem, w, x, R, C, B).reshape(B, R)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy().reshape(B, R)
+    assert not np.all(np.isfinite(ref)), "the planted scales must reach the output"
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (K.SEM_NAMES[sem], B)
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf])
+    fin = np.isfinite(ref)
+    assert O.norm_err(got[fin], ref[fin]) < GEMV_TOL, (K.SEM_NAMES[sem], B)
+
+
 @pytest.mark.parametrize("sem", [K.Q4_0, K.Q4_1, K.Q5_0_F32, K.Q8_0, K.Q4_K_GGML, K.Q5_K_GGML, K.Q5_K_CE,
                                  K.Q6_K_GGML, K.Q6_K_LOWNIB, K.Q6_K_SEQ, K.MXFP4, K.MXFP4_CLAMP])
 def test_device_dequant_vs_oracle(dev, orc, sem):

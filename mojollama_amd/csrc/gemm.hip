@@ -45,7 +45,11 @@ template <int SEM, int XM> struct gemm_cfg {
     // K columns per step: A4 keeps only the 32 columns its dot reads of each 64
     static constexpr int KS = 64;
     static constexpr int KE = A4 ? 32 : 64;
-    static constexpr int LDA = KE + 8;
+    // LDS rows: 64-column bf16 tiles unpadded and swizzled (tile_off), except the
+    // exact-weight planes (their tiles already fit three workgroups per CU and the
+    // swizzle's addressing would spill there); others padded
+    static constexpr bool SWZ = (KE == 64) && !WEXACT;
+    static constexpr int LDA = SWZ ? 64 : KE + 8;
     // products w_i * b_j taken: i + j <= MAXT.  Two planes each: the three leading
     // terms (the dropped w1*b1 is ~2^-16 of the product, below the two-plane
     // truncation itself).  One exact plane against three, or three against
@@ -63,6 +67,20 @@ template <bool DUAL, int TM_> struct tile_cfg {
     static constexpr int JT = TM_ / WE / 16;
 };
 
+// Element offset of (row, col) in an LDS tile; col is a multiple of 8 (every
+// access moves 16-byte pieces).  The LDS serves a 16-byte access 16 lanes at a
+// time over 64 banks (256 bytes), so SWZ tiles keep 128-byte rows and store
+// piece p of row r at piece p ^ ((r >> 1) & 7): the MFMA operand reads (16 rows,
+// one piece each), the weight stores (8 rows x two 32-column halves) and the
+// activation stores (2 rows x 8 pieces) each touch 16 distinct 16-byte bank
+// groups, and the unpadded tile is small enough for a third workgroup per CU.
+template <bool SWZ, int LDA>
+MLLM_DEV int tile_off(int row, int col)
+{
+    if constexpr (SWZ) return row * 64 + ((((col >> 3) ^ (row >> 1)) & 7) << 3);
+    else return row * LDA + col;
+}
+
 // 16 values exact in fp16 (integers below 2048) as fp16, in bf16-typed storage.
 MLLM_DEV void put16_f16(__bf16 *dst, const float (&v)[16])
 {
@@ -73,18 +91,20 @@ MLLM_DEV void put16_f16(__bf16 *dst, const float (&v)[16])
     *reinterpret_cast<f16x8 *>(dst + 8) = b;
 }
 
-MLLM_DEV void put16(__bf16 *dst, const float (&v)[16])
+// 16 values as bf16 at columns col .. col+15 of row `row`.
+template <bool SWZ, int LDA>
+MLLM_DEV void put16(__bf16 *base, int row, int col, const float (&v)[16])
 {
     bf16x8 a, b;
 #pragma unroll
     for (int i = 0; i < 8; i++) { a[i] = (__bf16)v[i]; b[i] = (__bf16)v[8 + i]; }
-    *reinterpret_cast<bf16x8 *>(dst) = a;
-    *reinterpret_cast<bf16x8 *>(dst + 8) = b;
+    *reinterpret_cast<bf16x8 *>(base + tile_off<SWZ, LDA>(row, col)) = a;
+    *reinterpret_cast<bf16x8 *>(base + tile_off<SWZ, LDA>(row, col + 8)) = b;
 }
 
-// Store 16 values as NP bf16 planes (plane p at base + p*pstride, element offset off).
-template <int NP>
-MLLM_DEV void put16_planes(__bf16 *base, int pstride, int off, const float (&v)[16])
+// Store 16 values as NP bf16 planes (plane p at base + p*pstride), row `row`, columns col ..
+template <int NP, bool SWZ, int LDA>
+MLLM_DEV void put16_planes(__bf16 *base, int pstride, int row, int col, const float (&v)[16])
 {
     float r[16];
 #pragma unroll
@@ -97,7 +117,7 @@ MLLM_DEV void put16_planes(__bf16 *base, int pstride, int off, const float (&v)[
             t[i] = (float)(__bf16)r[i];
             r[i] -= t[i];
         }
-        put16(base + p * pstride + off, t);
+        put16<SWZ, LDA>(base + p * pstride, row, col, t);
     }
 }
 
@@ -243,23 +263,23 @@ MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, in
             } else {
                 zero16(v0); zero16(v1);
             }
-            put16_planes<NA>(A, PS, rr * LDA + 32 * sub, v0);
-            put16_planes<NA>(A, PS, rr * LDA + 32 * sub + 16, v1);
+            put16_planes<NA, C::SWZ, LDA>(A, PS, rr, 32 * sub, v0);
+            put16_planes<NA, C::SWZ, LDA>(A, PS, rr, 32 * sub + 16, v1);
         } else {
             constexpr bool SPLIT = wtask<SEM, XM>::SPLIT;
             if (!valid) {   // past the last block of an odd block count: zero columns
                 float z[16];
                 zero16(z);
-                put16_planes<NA>(A, PS, rr * LDA + 32 * sub, z);
-                put16_planes<NA>(A, PS, rr * LDA + 32 * sub + 16, z);
+                put16_planes<NA, C::SWZ, LDA>(A, PS, rr, 32 * sub, z);
+                put16_planes<NA, C::SWZ, LDA>(A, PS, rr, 32 * sub + 16, z);
                 continue;
             }
             const int q = (k0 % 256) / 64;
             float w0[16], w1[16];
             int x0, x1;
             chunk_weights<SEM>(r, c, w0, w1, x0, x1);
-            if (!SPLIT || (q & 1) == 0) put16_planes<NA>(A, PS, rr * LDA + (x0 - k0), w0);
-            if (!SPLIT || (q & 1) == 1) put16_planes<NA>(A, PS, rr * LDA + (x1 - k0), w1);
+            if (!SPLIT || (q & 1) == 0) put16_planes<NA, C::SWZ, LDA>(A, PS, rr, x0 - k0, w0);
+            if (!SPLIT || (q & 1) == 1) put16_planes<NA, C::SWZ, LDA>(A, PS, rr, x1 - k0, w1);
         }
     }
 }
@@ -324,7 +344,7 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
             const int q = tid + 256 * i, er = q >> 3, c8 = q & 7;
 #pragma unroll
             for (int p = 0; p < NB; p++)
-                if (p < npl) *reinterpret_cast<uint4 *>(Bp + p * PS + er * LDA + 8 * c8) = ar.p[p][i];
+                if (p < npl) *reinterpret_cast<uint4 *>(Bp + p * PS + tile_off<C::SWZ, LDA>(er, 8 * c8)) = ar.p[p][i];
         }
     } else if constexpr (C::A4) {
         if (tid < 2 * TM_) {
@@ -351,7 +371,7 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
             } else {
                 zero16(v);
             }
-            put16_planes<NB>(Bp, PS, er * LDA + seg, v);
+            put16_planes<NB, C::SWZ, LDA>(Bp, PS, er, seg, v);
             // Q8D: block scale of the entry's 32 columns at seg (one writer per block)
             if (XM == XM_Q8D && tsum_l && (seg & 16) == 0) tsum_l[2 * er + (seg >> 5)] = live ? ar.s0 : 0.0f;
         }
@@ -365,7 +385,10 @@ template <int SEM, int XM, bool DUAL, int TM> constexpr int qgemm_wgs_per_cu()
 {
     using C = gemm_cfg<SEM, XM>;
     constexpr int TN = tile_cfg<DUAL, TM>::TN;
-    constexpr int lds = 2 * (C::NA * TN * C::LDA * (DUAL ? 2 : 1) + C::NB * TM * C::LDA) + 4 * TM + 4 * 3 * TN + 8 * TM + 64;
+    // fused gate+up tiles are sized with padded rows (KE + 8 columns): their
+    // unpadded tiles would admit a third workgroup whose register budget spills
+    constexpr int RW = DUAL ? C::KE + 8 : C::LDA;
+    constexpr int lds = 2 * (C::NA * TN * RW * (DUAL ? 2 : 1) + C::NB * TM * RW) + 4 * TM + 4 * 3 * TN + 8 * TM + 64;
     constexpr int cap = XM == XM_Q8D ? 2 : 3;
     constexpr int n = 163840 / lds;
     return n < 1 ? 1 : n > cap ? cap : n;
@@ -456,6 +479,13 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
     // activation planes past the first all zero: their products are skipped (uniform per workgroup)
     const int pb_end = (XM == XM_PLANES && !lo_any) ? 1 : NB;
     const int li = lane & 15, lk = (lane >> 4) * 8;
+    // MFMA operand offset of row base + li (base a multiple of 16), columns ks + lk:
+    // on swizzled tiles (row >> 1) & 7 = li >> 1, and ks (0 or 32) flips piece bit 2
+    const int rsw = ((lane >> 4) ^ (li >> 1)) << 3;
+    auto roff = [&](int base, int ks) __attribute__((always_inline)) {
+        if constexpr (C::SWZ) return (base + li) * 64 + (rsw ^ ks);
+        else return (base + li) * LDA + ks + lk;
+    };
 
     struct stepbuf {
         wraw<SEM, XM, TN> w, u;
@@ -482,10 +512,10 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
             for (int p = 0; p < NB; p++)
 #pragma unroll
                 for (int j = 0; j < JT; j++)
-                    if (p < pb_end) bv[p][j] = *reinterpret_cast<const bf16x8 *>(s_b + p * TM * LDA + (we0 + 16 * j + li) * LDA + ks + lk);
+                    if (p < pb_end) bv[p][j] = *reinterpret_cast<const bf16x8 *>(s_b + p * TM * LDA + roff(we0 + 16 * j, ks));
 #pragma unroll
             for (int i = 0; i < IT; i++) {
-                const int ar_ = (wr0 + 16 * i + li) * LDA + ks + lk;
+                const int ar_ = roff(wr0 + 16 * i, ks);
                 bf16x8 av[NA];
 #pragma unroll
                 for (int p = 0; p < NA; p++) av[p] = *reinterpret_cast<const bf16x8 *>(s_a + p * TN * LDA + ar_);

@@ -727,9 +727,11 @@ bool mllm_qgemm_supported(int sem)
 
 // A dense launch with fewer output tiles than CUs is split along K into at
 // most 512 workgroups (two per CU: a launch past that runs a second, partial
-// round of workgroups), each split keeping at least 4 K steps of 64 columns
-// (the partial sums cost an extra pass over ksplit x entries x rows floats,
-// which does not pay on a launch that already fills the GPU).
+// round of workgroups), each split keeping at least 4 K steps of 64 columns,
+// and into at most 8 splits (the partial sums cost an extra pass over ksplit x
+// entries x rows floats, which does not pay on a launch that already fills the
+// GPU; 16 splits of the 2048-row down projection at M = 128 measured slower
+// than 8).
 int mllm_qgemm_ksplit(int sem, int n_rows, int n_cols, int n_entries)
 {
     if (!mllm_qgemm_supported(sem) || n_entries <= 0) return 1;
@@ -739,7 +741,7 @@ int mllm_qgemm_ksplit(int sem, int n_rows, int n_cols, int n_entries)
     const int steps = (n_cols + 63) / 64;
     int ks = (int)(512 / tiles);
     ks = std::min(ks, std::max(1, steps / 4));
-    return std::max(1, std::min(ks, 16));
+    return std::max(1, std::min(ks, 8));
 }
 
 // fp32 rows -> NP bf16 planes (one workgroup per row, 8 columns per thread and

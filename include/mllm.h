@@ -83,7 +83,7 @@ MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up
 /* moe_ffn (CE:591-665) for each of B tokens, keeping every token's result:
  * ffn_out[b*N + n] (moe_ffn itself keeps only the last token's, CE:610-643).
  * No reference counterpart: the batched form of moe_ffn for prefill-sized B.
- * B > 8 tokens run the grouped-GEMM MoE layer (GPU bucketing by expert) with
+ * B > 8 tokens run the MoE layer (grouped GEMMs above 24 tokens) with
  * moe_ffn's semantics: quant_matmul_omp per projection, unclamped SiLU, the
  * un-renormalised top-K routing, k-order combine. */
 MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_out, int B);
@@ -151,8 +151,8 @@ MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_col
  * moe_forward_omp (QK:2066-2250) computes when fed the C routing of moe_ffn
  * (CE:606-638), renormalised when `renorm` (GO:88-92): gate/up per type,
  * SiLU with the gate clamped to +-80, down per type, k-order combine.
- * T > 8 tokens run the batched path (GPU bucketing by expert, grouped MFMA
- * GEMMs); T <= 8 the decode GEMVs. */
+ * T > 24 tokens run the batched path (GPU bucketing by expert, grouped MFMA
+ * GEMMs); T <= 24 the decode GEMVs, one job per (token, slot). */
 typedef struct mllm_moe_layer mllm_moe_layer;
 MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
                                           const void *const *gate_packed, const void *const *up_packed,

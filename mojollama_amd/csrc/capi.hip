@@ -818,8 +818,8 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
 }
 
 // moe_ffn over T tokens of host data, every token's result kept: T > 8 tokens
-// whose expert types the grouped GEMM serves run the batched MoE layer (GPU
-// bucketing, grouped MFMA GEMMs) with moe_ffn's semantics (quant_matmul_omp
+// whose expert types the grouped GEMM serves run the MoE layer (decode GEMVs up
+// to 24 tokens, then GPU bucketing and grouped MFMA GEMMs) with moe_ffn's semantics (quant_matmul_omp
 // per projection, unclamped SiLU, no renormalisation); the rest the token path.
 int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3], const int qts[3], int N, int E, int K,
                               int M, const float *x_host, float *out_host, int T)

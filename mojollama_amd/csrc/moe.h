@@ -11,5 +11,5 @@
 mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N, int M, int E, int K,
                                           const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp);
 
-// Whether the grouped-GEMM (T > 8) path serves these semantics.
+// Whether the grouped-GEMM (T > 24) path serves these semantics.
 bool mllm_moe_batched_supported(int sem_g, int sem_u, int sem_d);

@@ -227,9 +227,9 @@ def test_moe_layer_small_vs_oracle(dev, orc, qts, T):
 
 
 @pytest.mark.parametrize("qts", [(12, 14, 6), (2, 3, 12), (6, 6, 2), (39, 39, 39), (14, 14, 14)])
-@pytest.mark.parametrize("T", [2, 8])
+@pytest.mark.parametrize("T", [2, 8, 24])
 def test_moe_layer_decode_vs_oracle(dev, orc, qts, T):
-    """Decode path (T <= 8): one launch over all T*K (token, slot) jobs, gate and up fused when their
+    """Decode path (T <= 24): one launch over all T*K (token, slot) jobs, gate and up fused when their
     semantics agree ((2, 3) and (12, 14) run two launches), the SiLU product formed by the down
     projection's staging (fp32 activations) or its Q8_0 quantiser (MXFP4), Q4_K down left at zero."""
     got, ref = _moe_case(dev, orc, qts, N=512, M=256, E=16, Kk=4, T=T, renorm=T % 2, seed=11 * T + sum(qts))
@@ -272,7 +272,7 @@ def test_moe_layer_repeated_decode_calls(dev, orc):
 
 def test_moe_layer_gptoss_shape(dev, orc):
     """GPT-OSS-20B expert shapes (N = M = 2880, MXFP4, top-4), batched path."""
-    got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=24, renorm=1, seed=4)
+    got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=32, renorm=1, seed=4)
     assert O.norm_err(got, ref) < moe_tol((39, 39, 39))
 
 
@@ -384,9 +384,9 @@ def test_moe_ffn_router_rewritten_in_place(lib, orc):
 
 
 @pytest.mark.parametrize("qts,N,M", [((39, 39, 39), 224, 96), ((2, 2, 2), 160, 96), ((39, 39, 2), 96, 160)])
-@pytest.mark.parametrize("E,Kk,T", [(12, 3, 9), (12, 3, 50), (5, 1, 23)])
+@pytest.mark.parametrize("E,Kk,T", [(12, 3, 29), (12, 3, 50), (5, 1, 27)])
 def test_moe_layer_batched_odd_shapes(dev, orc, qts, N, M, E, Kk, T):
-    """Batched path (T > 8) at shapes off every power of two: K not a multiple
+    """Batched path (T > 24) at shapes off every power of two: K not a multiple
     of 64 (padded activation rows), rows not a multiple of the weight tile,
     expert counts whose tiles spread unevenly over the XCDs, odd top-K."""
     got, ref = _moe_case(dev, orc, qts, N=N, M=M, E=E, Kk=Kk, T=T, renorm=int(Kk > 1), seed=T * 7 + E + N)

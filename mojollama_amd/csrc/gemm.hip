@@ -68,8 +68,9 @@ template <bool DUAL, int TM_> struct tile_cfg {
 };
 
 // Element offset of (row, col) in an LDS tile; col is a multiple of 8 (every
-// access moves 16-byte pieces).  The LDS serves a 16-byte access 16 lanes at a
-// time over 64 banks (256 bytes), so SWZ tiles keep 128-byte rows and store
+// access moves 16-byte pieces).  Taking the LDS to serve a 16-byte access 16
+// lanes at a time over 64 banks (256 bytes) -- the model that fits the bank
+// conflict counters of padded rows -- SWZ tiles keep 128-byte rows and store
 // piece p of row r at piece p ^ ((r >> 1) & 7): the MFMA operand reads (16 rows,
 // one piece each), the weight stores (8 rows x two 32-column halves) and the
 // activation stores (2 rows x 8 pieces) each touch 16 distinct 16-byte bank

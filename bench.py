@@ -235,36 +235,16 @@ def bench_prefill(torch, dev, args, with_cpu=False):
     return out
 
 
-def moe_cfg(tag):
-    return dict(W.GPTOSS) if tag == "gptoss" else dict(W.QWEN3)
-
-
 def bench_moe(torch, dev, args, tag, with_cpu, sizes=(1, 1280)):
     """one MoE FFN layer (all experts resident) at decode
     batch 1 and at 10 x 128 = 1280 tokens; tokens/s = tokens / layer time."""
-    c = moe_cfg(tag)
+    wl = W.moe_workload(tag, max(sizes))
+    c = wl["cfg"]
     N, E, Kk, M = c["N"], c["E"], c["K"], c["M"]
-    qts = (c["qt_gate"], c["qt_up"], c["qt_down"])
+    qts = wl["qts"]
     renorm = 1
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(4 if tag == "gptoss" else 5)
-    if tag == "gptoss":
-        # fused gate/up tensor per expert (5760 x 2880): gate = rows [0, M), up = rows [M, 2M)
-        rb = W.row_bytes(qts[0], N)
-        fused = [W.gen_weights_torch(gen, qts[0], 2 * M, N) for _ in range(E)]
-        gates = [f[:M * rb] for f in fused]
-        ups = [f[M * rb:] for f in fused]
-    else:
-        gates = [W.gen_weights_torch(gen, qts[0], M, N) for _ in range(E)]
-        ups = [W.gen_weights_torch(gen, qts[1], M, N) for _ in range(E)]
-    downs = [W.gen_weights_torch(gen, qts[2], N, M) for _ in range(E)]
-    rng = np.random.default_rng(7)
-    router_np = W.gen_router(rng, E, N)
-    T = max(sizes)
-    if tag == "qwen3":
-        x_np, router_np, hot, _ = W.skewed_tokens(rng, router_np, T)
-    else:
-        x_np = W.gen_x(rng, T, N)
+    gates, ups, downs = wl["gates"], wl["ups"], wl["downs"]
+    router_np, x_np = wl["router"], wl["x"]
     router = torch.from_numpy(router_np).cuda()
     layer = dev.moe_prepare(qts, N, M, E, Kk, gates, ups, downs, router, renorm)
     x = torch.from_numpy(x_np).cuda()

@@ -20,6 +20,7 @@
 #include <string.h>
 #include <map>
 #include <mutex>
+#include <shared_mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -199,6 +200,12 @@ uint64_t fingerprint(const void *p, long n)
 // (host, E, N) -> routing-layout copy and the fingerprint of the host router it was made from
 std::map<std::tuple<const void *, int, int>, std::pair<float *, uint64_t>> g_router_cache;
 
+// Drop-in calls hold this shared for their whole duration; mllm_cache_clear
+// takes it exclusively, so it never frees a device copy that a call in flight
+// has looked up and not yet finished using.
+std::shared_mutex g_api_mu;
+#define API_GUARD std::shared_lock<std::shared_mutex> api_guard_(g_api_mu)
+
 // Upload + pack a raw host matrix (once).  Returns its packed view.
 int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
 {
@@ -273,6 +280,64 @@ int get_router(const float *host, int E, int N, const float **dev_out)
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+long moe_ffn_stride(int which, int qt, int N, int M);
+
+// moe_ffn's per-layer expert table: the three expert tensors of a layer
+// (gate, up, down, E experts each at the strides of CE:593-605) -> a device
+// array of 3*E packed views, built once per (tensors, shape, types) and
+// checked on each call by one fingerprint per tensor (a tensor freed and
+// another allocated at its address has other contents), instead of looking
+// up and fingerprinting each of the 3*E expert matrices per call.
+struct layer_key {
+    const void *b[3];
+    int qt[3], sem[3], N, E, M;
+    bool operator<(const layer_key &o) const
+    {
+        return std::tie(b[0], b[1], b[2], qt[0], qt[1], qt[2], sem[0], sem[1], sem[2], N, E, M) <
+               std::tie(o.b[0], o.b[1], o.b[2], o.qt[0], o.qt[1], o.qt[2], o.sem[0], o.sem[1], o.sem[2], o.N, o.E, o.M);
+    }
+};
+struct layer_entry {
+    mllm_packed *dtab = nullptr;
+    uint64_t fp[3] = {0, 0, 0};
+};
+std::map<layer_key, layer_entry> g_layer_cache;
+
+int get_layer_table(const uint8_t *const bases[3], const int qts[3], const int sems[3], int N, int E, int M,
+                    const mllm_packed **dtab_out)
+{
+    layer_key k{};
+    uint64_t fp[3];
+    for (int w = 0; w < 3; w++) {
+        k.b[w] = bases[w]; k.qt[w] = qts[w]; k.sem[w] = sems[w];
+        fp[w] = fingerprint(bases[w], moe_ffn_stride(w, qts[w], N, M) * E);
+    }
+    k.N = N; k.E = E; k.M = M;
+    {
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        auto it = g_layer_cache.find(k);
+        if (it != g_layer_cache.end() && !memcmp(it->second.fp, fp, sizeof fp)) { *dtab_out = it->second.dtab; return 0; }
+    }
+    std::vector<mllm_packed> tab(3 * (size_t)E);
+    for (int w = 0; w < 3; w++) {
+        const long stride = moe_ffn_stride(w, qts[w], N, M);
+        const int rows = w < 2 ? M : N, cols = w < 2 ? N : M;
+        for (int e = 0; e < E; e++)
+            if (get_weight(bases[w] + (long)e * stride, mllm_sem_layout(sems[w]), rows, cols, tab[(size_t)w * E + e])) return -1;
+    }
+    mllm_packed *d = nullptr;
+    HIP_OK(hipMalloc(&d, tab.size() * sizeof(mllm_packed)));
+    HIP_OK(hipMemcpy(d, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice));
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto it = g_layer_cache.find(k);
+    if (it != g_layer_cache.end()) g_retired.push_back((uint8_t *)it->second.dtab);   // a call in flight may read it
+    layer_entry &en = g_layer_cache[k];
+    en.dtab = d;
+    memcpy(en.fp, fp, sizeof fp);
+    *dtab_out = d;
+    return 0;
+}
+
 // Scratch layout for the Q8_0 activation pack of T rows x n_cols.
 struct xq_bufs {
     int8_t *q; float *d; float *s4; int *sq;
@@ -309,7 +374,7 @@ size_t planes_bytes(int sem, long rows, int n_cols)
 // quantised by the GEMV workgroups).
 size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
 {
-    if (!(B > 8 && mllm_qgemm_supported(sem))) return 0;
+    if (!(B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem))) return 0;
     return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0) +
            align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4);
 }
@@ -319,7 +384,7 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
              void *scratch, hipStream_t st)
 {
     const bool q8 = mllm_sem_uses_q8(sem);
-    if (B > 8 && mllm_qgemm_supported(sem)) {
+    if (B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem)) {
         // prefill / batched: quantised-weight MFMA GEMM over the B tokens
         xq_bufs xb{};
         if (q8) {
@@ -401,7 +466,7 @@ template <class T> static T bc_field(const void *c, int off)
 
 // moe_ffn's expert strides (CE:593-605): gate/up default to the Q4_K size and
 // down to the Q6_K size; only codes 12/13/14/39 change them.
-static long moe_ffn_stride(int which, int qt, int N, int M)
+long moe_ffn_stride(int which, int qt, int N, int M)
 {
     if (which < 2) {
         long s = (long)M * (N / 256) * 144;
@@ -424,6 +489,7 @@ extern "C" {
 
 MLLM_API void quant_matmul_omp(const uint8_t *W, const float *x, float *out, int n_rows, int n_cols, int quant_type)
 {
+    API_GUARD;
     const int sem = sem_for(ENT_QMM, quant_type);
     if (sem < 0) { set_error("quant_matmul_omp: unknown quant type %d (output untouched)", quant_type); return; }
     host_gemv(sem, W, x, out, n_rows, n_cols, 1);
@@ -431,12 +497,14 @@ MLLM_API void quant_matmul_omp(const uint8_t *W, const float *x, float *out, int
 
 MLLM_API void f32_matmul_omp(const float *W, const float *x, float *out, int n_rows, int n_cols)
 {
+    API_GUARD;
     host_gemv(SEM_F32, (const uint8_t *)W, x, out, n_rows, n_cols, 1);
 }
 
 #define MLLM_BMM(name, qt)                                                                           \
     MLLM_API void name(const uint8_t *W, const float *x, float *out, int n_rows, int nc, int B)     \
     {                                                                                                \
+        API_GUARD;                                                                                   \
         host_gemv(sem_for(ENT_BMM, qt), W, x, out, n_rows, nc, B);                                 \
     }
 MLLM_BMM(q4_0_batch_matmul, 2)
@@ -451,6 +519,7 @@ MLLM_API void batch_qkv_omp(const uint8_t *Wq, const uint8_t *Wk, const uint8_t 
                             float *out_k, float *out_v, int nq, int nk, int nv, int n_cols, int qtype_q, int qtype_k,
                             int qtype_v)
 {
+    API_GUARD;
     const uint8_t *Ws[3] = {Wq, Wk, Wv};
     float *outs[3] = {out_q, out_k, out_v};
     const int ns[3] = {nq, nk, nv}, qts[3] = {qtype_q, qtype_k, qtype_v};
@@ -464,6 +533,7 @@ MLLM_API void batch_qkv_omp(const uint8_t *Wq, const uint8_t *Wk, const uint8_t 
 MLLM_API void batch_gate_up_omp(const uint8_t *Wg, const uint8_t *Wu, const float *x, float *out_gate, float *out_up,
                                 int ng, int nu, int n_cols, int qtype_g, int qtype_u)
 {
+    API_GUARD;
     const int sg = sem_for(ENT_ROWS, qtype_g), su = sem_for(ENT_ROWS, qtype_u);
     if (sg >= 0) host_gemv(sg, Wg, x, out_gate, ng, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_g);
     if (su >= 0) host_gemv(su, Wu, x, out_up, nu, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_u);
@@ -493,6 +563,7 @@ MLLM_API int quantize_row_q8_0(const float *x, uint8_t *q8, int n_cols)
 // *_dequantize_row (QK:762-878): the ggml definitions, rounded as the reference rounds them.
 static void dequant_row(int sem, const uint8_t *W, float *out, int n_values)
 {
+    API_GUARD;
     if (n_values <= 0) return;
     thread_ctx &c = t_ctx;
     if (c.init()) return;
@@ -527,8 +598,10 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
                               const int *top_indices, const float *top_weights, int top_k, float *combined,
                               float *prealloc_buf, uint8_t *prealloc_q8)
 {
+    API_GUARD;
     (void)prealloc_buf;
-    if (top_k <= 0 || n_embd <= 0) return;
+    if (n_embd <= 0) return;
+    if (top_k <= 0) { memset(combined, 0, (size_t)n_embd * 4); return; }   // the reference clears combined (QK:2179)
     if (top_k > 64) { set_error("moe_forward_omp: top_k %d > 64", top_k); return; }
     thread_ctx &c = t_ctx;
     if (c.init()) return;
@@ -540,11 +613,18 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         set_error("moe_forward_omp: MXFP4 down projection needs prealloc_q8 (the reference dereferences NULL); down treated as zero");
         sd = -1;
     }
-    const int K = top_k, F = n_ff_expert, N = n_embd;
+    // slots with a negative expert id (left empty by a routing) add nothing and are dropped;
+    // the remaining slots keep their order, so the k-order combine is unchanged
+    std::vector<int> sel;
+    std::vector<float> selw;
+    for (int k = 0; k < top_k; k++)
+        if (top_indices[k] >= 0) { sel.push_back(top_indices[k]); selw.push_back(top_weights[k]); }
+    if (sel.empty()) { memset(combined, 0, (size_t)n_embd * 4); return; }
+    const int K = (int)sel.size(), F = n_ff_expert, N = n_embd;
     // tables of the selected experts' packed views: [0,K) gate, [K,2K) up, [2K,3K) down
     std::vector<mllm_packed> tab(3 * K);
     for (int k = 0; k < K; k++) {
-        const int e = top_indices[k];
+        const int e = sel[k];
         if (sg >= 0 && get_weight(gate_raw[e], mllm_sem_layout(sg), F, N, tab[k])) return;
         if (su >= 0 && get_weight(up_raw[e], mllm_sem_layout(su), F, N, tab[K + k])) return;
         if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k])) return;
@@ -563,7 +643,7 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
           *ddn = (float *)(S + o_dn), *dw = (float *)(S + o_w);
     uint8_t *hin = (uint8_t *)c.h_in.p;
     memcpy(hin, x_norm, N * 4);
-    memcpy(hin + N * 4, top_weights, K * 4);
+    memcpy(hin + N * 4, selw.data(), K * 4);
     memcpy(hin + N * 4 + K * 4, tab.data(), tab.size() * sizeof(mllm_packed));
     mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
     hipStream_t st = c.st;
@@ -601,7 +681,7 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         }
         CK(mllm_launch_gemv(sd, b, K, st));
     }
-    CK(mllm_launch_combine(sd >= 0 ? ddn : nullptr, dw, 1, K, N, dx, 0, st));
+    CK(mllm_launch_combine(sd >= 0 ? ddn : nullptr, dw, nullptr, 1, K, N, dx, 0, st));
     CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
 #undef CK
@@ -613,6 +693,7 @@ int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3]
 
 MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up_buf, float *ffn_buf, int B)
 {
+    API_GUARD;
     (void)gate_buf; (void)up_buf;
     if (B <= 0) return;
     const int N = bc_field<int>(c, BC_N), E = bc_field<int>(c, BC_NE), K = bc_field<int>(c, BC_NK),
@@ -629,6 +710,7 @@ MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up
 // ffn_out[b*N + n].  No scratch of the caller's is used.
 MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_out, int B)
 {
+    API_GUARD;
     if (B <= 0) return;
     const int N = bc_field<int>(c, BC_N), E = bc_field<int>(c, BC_NE), K = bc_field<int>(c, BC_NK),
               M = bc_field<int>(c, BC_M);
@@ -648,8 +730,11 @@ MLLM_API const char *mllm_last_error(void) { return g_last_error.c_str(); }
 
 MLLM_API void mllm_cache_clear(void)
 {
+    std::unique_lock<std::shared_mutex> api(g_api_mu);   // waits for drop-in calls in flight
     std::lock_guard<std::mutex> lk(g_cache_mu);
     (void)hipDeviceSynchronize();
+    for (auto &kv : g_layer_cache) (void)hipFree(kv.second.dtab);
+    g_layer_cache.clear();
     for (auto &kv : g_cache) (void)hipFree(kv.second.dev);
     g_cache.clear();
     for (uint8_t *p : g_retired) (void)hipFree(p);
@@ -756,14 +841,9 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
         return -1;
     }
     if (K > 16 || E > 256) { set_error("moe_ffn: E<=256 and K<=16 required"); return -1; }
-    // per-expert packed views, cached per (layer tensor, expert)
-    std::vector<mllm_packed> tab(3 * (size_t)E);
-    for (int w = 0; w < 3; w++) {
-        const long stride = moe_ffn_stride(w, qts[w], N, M);
-        const int rows = w < 2 ? M : N, cols = w < 2 ? N : M;
-        for (int e = 0; e < E; e++)
-            if (get_weight(bases[w] + (long)e * stride, mllm_sem_layout(sems[w]), rows, cols, tab[(size_t)w * E + e])) return -1;
-    }
+    // per-expert packed views: the layer's device table (cached per layer)
+    const mllm_packed *dtab = nullptr;
+    if (get_layer_table(bases, qts, sems, N, E, M, &dtab)) return -1;
     const float *rt = nullptr;
     if (get_router(router, E, N, &rt)) return -1;
     // scratch: x[T][N] | idx[T][K] | w[T][K] | g,u,h [T*K][M] | dn [T*K][N] | out[T][N] | routing logits
@@ -772,8 +852,7 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
            o_u = align256(o_g + TK * M * 4), o_h = align256(o_u + TK * M * 4), o_dn = align256(o_h + TK * M * 4),
            o_o = align256(o_dn + TK * N * 4), o_l = align256(o_o + (size_t)T * N * 4),
            total = align256(o_l + (size_t)mllm_route_workspace_floats(T, E) * 4);
-    if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
-        c.h_in.ensure((size_t)T * N * 4) || c.h_out.ensure((size_t)T * N * 4)) {
+    if (c.d_scr.ensure(total) || c.h_in.ensure((size_t)T * N * 4) || c.h_out.ensure((size_t)T * N * 4)) {
         set_error("moe_ffn: scratch allocation failed");
         return -1;
     }
@@ -781,11 +860,9 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     float *dx = (float *)(S + o_x), *dwt = (float *)(S + o_w), *dg = (float *)(S + o_g), *du = (float *)(S + o_u),
           *dh = (float *)(S + o_h), *ddn = (float *)(S + o_dn), *dout = (float *)(S + o_o);
     int *didx = (int *)(S + o_i);
-    mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
     hipStream_t st = c.st;
     memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
     HIP_OK(hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st));
-    HIP_OK(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
     HIP_OK(mllm_launch_route(rt, dx, T, N, E, K, 0, didx, dwt, (float *)(S + o_l), st));
     // one GEMV launch per projection over the T*K (token, slot) jobs, gate
     // and up together when their semantics agree; Q8_0 activations quantised
@@ -810,7 +887,7 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     b.out = ddn; b.out_job_stride = N; b.ldo = N;
     b.n_rows = N; b.n_cols = M; b.B = 1;
     HIP_OK(mllm_launch_gemv(sems[2], b, (int)TK, st));
-    HIP_OK(mllm_launch_combine(ddn, dwt, T, K, N, dout, 1, st));
+    HIP_OK(mllm_launch_combine(ddn, dwt, didx, T, K, N, dout, 1, st));
     HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
     HIP_OK(hipStreamSynchronize(st));
     memcpy(out_host, c.h_out.p, (size_t)T * N * 4);
@@ -830,18 +907,11 @@ int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3]
         return mllm_moe_ffn_dev_tokens(router, bases, qts, N, E, K, M, x_host, out_host, T);
     thread_ctx &c = t_ctx;
     if (c.init()) return -1;
-    std::vector<mllm_packed> tab(3 * (size_t)E);
-    for (int w = 0; w < 3; w++) {
-        const long stride = moe_ffn_stride(w, qts[w], N, M);
-        const int rows = w < 2 ? M : N, cols = w < 2 ? N : M;
-        for (int e = 0; e < E; e++)
-            if (get_weight(bases[w] + (long)e * stride, mllm_sem_layout(sems[w]), rows, cols, tab[(size_t)w * E + e])) return -1;
-    }
+    const mllm_packed *dtab = nullptr;
+    if (get_layer_table(bases, qts, sems, N, E, M, &dtab)) return -1;
     const float *rt = nullptr;
     if (get_router(router, E, N, &rt)) return -1;
-    if (c.d_tab.ensure(tab.size() * sizeof(mllm_packed))) { set_error("moe_ffn_batched: allocation failed"); return -1; }
-    mllm_moe_layer *L = mllm_moe_layer_from_views(sems[0], sems[1], sems[2], N, M, E, K, (mllm_packed *)c.d_tab.p, rt,
-                                                  0, 0);
+    mllm_moe_layer *L = mllm_moe_layer_from_views(sems[0], sems[1], sems[2], N, M, E, K, dtab, rt, 0, 0);
     if (!L) { set_error("moe_ffn_batched: bad layer shape"); return -1; }
     // scratch: x[T][N] | out[T][N] | layer workspace
     const size_t ws = (size_t)mllm_moe_workspace_size(L, T);
@@ -856,8 +926,7 @@ int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3]
     hipStream_t st = c.st;
     memcpy(c.h_in.p, x_host, (size_t)T * N * 4);
     int rc = -1;
-    if (hipMemcpyAsync(c.d_tab.p, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st) == hipSuccess &&
-        hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st) == hipSuccess &&
+    if (hipMemcpyAsync(dx, c.h_in.p, (size_t)T * N * 4, hipMemcpyHostToDevice, st) == hipSuccess &&
         mllm_moe_forward(L, dx, T, dout, S + o_ws, (long)ws, nullptr, nullptr, st) == 0 &&
         hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
         hipStreamSynchronize(st) == hipSuccess)

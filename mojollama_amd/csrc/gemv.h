@@ -44,7 +44,11 @@ __device__ __forceinline__ float mllm_silu_mul(float g, float u)
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// n_cols below one quant block (no whole block per row): every output is 0, as
+// the reference's dot over n_cols / block = 0 blocks; no weight is read.
 hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStream_t st);
+// Elements per quant block of a semantic's weight layout (1 for fp32 rows).
+int mllm_sem_block_elems(int sem);
 
 // Repack raw GGUF blocks (device) into the plane layout `ly`.
 hipError_t mllm_launch_pack(int ly, const uint8_t *raw, uint8_t *packed, int n_rows, int n_cols, hipStream_t st);
@@ -72,9 +76,10 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st);
 
 // out[t][i] = sum_k (in k order) w[t][k] * d[t][k][i]; fused selects fmaf (moe_ffn CE:662) or
-// add-of-product (moe_forward_omp QK:2243-2244).  d == nullptr: every d term is 0.
-hipError_t mllm_launch_combine(const float *d, const float *w, int T, int K, int N, float *out, int fused,
-                               hipStream_t st);
+// add-of-product (moe_forward_omp QK:2243-2244).  d == nullptr: every d term is 0.  Slots whose
+// expert idx[t][k] is negative (left empty by the routing) are skipped; idx == nullptr: none are.
+hipError_t mllm_launch_combine(const float *d, const float *w, const int *idx, int T, int K, int N, float *out,
+                               int fused, hipStream_t st);
 
 // fp32 rows of a packed matrix under a fp32-weight semantic; returns 0 or -1
 // (semantic without an fp32 weight form, or launch failure).

@@ -15,7 +15,26 @@ void launch_f32(const mllm_gemv_args &a, int n_jobs, hipStream_t st)
     else hipLaunchKernelGGL(k_gemv_f32<8>, grid, dim3(256), 0, st, a);
 }
 
+// Rows of a matrix with fewer columns than one quant block: the reference's
+// dot products run over n_cols / block = 0 blocks and give 0, so every output
+// row of every job and token is written 0 (no weight or activation is read).
+__global__ void k_gemv_zero(mllm_gemv_args a)
+{
+    const int job = blockIdx.y;
+    const bool second = a.job_split > 0 && job >= a.job_split;
+    float *out = (second ? a.out2 : a.out) + (long)(second ? job - a.job_split : job) * a.out_job_stride;
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= a.n_rows) return;
+    for (int b = 0; b < a.B; b++) out[(long)b * a.ldo + r] = 0.0f;
+}
+
 } // namespace
+
+int mllm_sem_block_elems(int sem)
+{
+    if (sem == SEM_F32) return 1;
+    return mllm_layout_info(mllm_sem_layout(sem)).block_elems;
+}
 
 int mllm_launch_dequant(int sem, const mllm_packed &W, int n_rows, int n_cols, float *out, hipStream_t st)
 {
@@ -49,6 +68,10 @@ hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStr
     if (a.x_up && (sem == SEM_F32 || (mllm_sem_uses_q8(sem) ? a.xq.q != nullptr : a.B != 1)))
         return hipErrorInvalidValue;
     if (a.job_split > 0 && (a.job_split >= n_jobs || !a.out2 || (a.table && !a.table2))) return hipErrorInvalidValue;
+    if (a.n_cols < mllm_sem_block_elems(sem)) {
+        hipLaunchKernelGGL(k_gemv_zero, dim3((a.n_rows + 255) / 256, n_jobs), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     switch (sem) {
     case SEM_F32: launch_f32(a, n_jobs, st); break;
     case SEM_Q4_0: gemv_sem<SEM_Q4_0>(a, n_jobs, st); break;

@@ -635,6 +635,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     const int grp = lane / LPR, sl = lane % LPR;
     const int nb = a.n_cols / BE, kused = nb * BE, nch = nb * CPB;
     const int iters = (nch + LPR - 1) / LPR;
+    if (iters == 0) return;   // no whole block per row: the launcher writes zeros instead of launching this
     const int nrg = (a.n_rows + RPW - 1) / RPW;
     const int wstride = gridDim.x * 4;
     const int rg0 = blockIdx.x * 4 + wave;

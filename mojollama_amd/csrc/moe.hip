@@ -333,8 +333,12 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     int8_t *hq; float *hd, *hs4; int *hsq;
     const mllm_xq xqh = xq_at(s.xq_h, TK, M, &hq, &hd, &hs4, &hsq);
 
+    // the grouped GEMMs need at least one quant block per row (else the decode
+    // GEMVs write the reference's zeros)
     const bool batched = T > kMoeDecodeMaxT && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
-                         (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d));
+                         (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d)) &&
+                         N >= mllm_sem_block_elems(L->sem_g) && N >= mllm_sem_block_elems(L->sem_u) &&
+                         (L->sem_d < 0 || M >= mllm_sem_block_elems(L->sem_d));
     if (batched) {
         if (mllm_sem_uses_q8(L->sem_g) || mllm_sem_uses_q8(L->sem_u))
             CK(mllm_launch_quantize_q8_0(x, T, N, nullptr, q, d, s4, sq, st));
@@ -420,7 +424,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             }
             CK(mllm_launch_gemv(L->sem_d, b, TK, st));
         }
-        CK(mllm_launch_combine(L->sem_d >= 0 ? s.dn : nullptr, s.w, T, K, N, out, 0, st));
+        CK(mllm_launch_combine(L->sem_d >= 0 ? s.dn : nullptr, s.w, s.idx, T, K, N, out, 0, st));
     }
     if (idx_out) CK(hipMemcpyAsync(idx_out, s.idx, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
     if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));

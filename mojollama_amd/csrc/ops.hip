@@ -736,14 +736,18 @@ __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict_
     h[i] = clamp ? mllm_silu_mul(gv, u[i]) : (gv / (1.0f + expf(-gv))) * u[i];
 }
 
-__global__ void k_combine(const float *__restrict__ d, const float *__restrict__ w, int K, int N,
-                          float *__restrict__ out, int fused)
+__global__ void k_combine(const float *__restrict__ d, const float *__restrict__ w, const int *__restrict__ idx,
+                          int K, int N, float *__restrict__ out, int fused)
 {
     const int t = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
     float acc = 0.0f;
     for (int k = 0; k < K; k++) {
+        // a slot the routing left empty (expert -1: a token whose logits hold
+        // an inf or NaN never inserts an expert) adds nothing, as the
+        // reference skips e < 0 (CE:640-641)
+        if (idx && idx[(long)t * K + k] < 0) continue;
         const float wk = w[(long)t * K + k], dv = d ? d[((long)t * K + k) * N + i] : 0.0f;
         acc = fused ? fmaf(wk, dv, acc) : acc + wk * dv;
     }
@@ -899,10 +903,10 @@ hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n
     return hipGetLastError();
 }
 
-hipError_t mllm_launch_combine(const float *d, const float *w, int T, int K, int N, float *out, int fused,
-                               hipStream_t st)
+hipError_t mllm_launch_combine(const float *d, const float *w, const int *idx, int T, int K, int N, float *out,
+                               int fused, hipStream_t st)
 {
     if (T <= 0 || N <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_combine, dim3((N + 255) / 256, T), dim3(256), 0, st, d, w, K, N, out, fused);
+    hipLaunchKernelGGL(k_combine, dim3((N + 255) / 256, T), dim3(256), 0, st, d, w, idx, K, N, out, fused);
     return hipGetLastError();
 }

@@ -124,3 +124,38 @@ def gen_weights_torch(gen, qt, n_rows, n_cols, device="cuda"):
     elif qt == QT_MXFP4:
         blk[:, 16] = (127 + torch.randint(-8, 1, (nb,), device=device, generator=gen)).to(torch.uint8)
     return blk.reshape(-1)
+
+
+def moe_workload(tag, T=1280, device="cuda"):
+    """The configs[3] ("gptoss") / configs[4] ("qwen3") MoE workload exactly as
+    bench.py times it: per-expert raw GGUF weights drawn on the GPU with a
+    seeded torch Generator (GPT-OSS: one fused 5760-row gate/up tensor per
+    expert, gate = rows [0, M), up = rows [M, 2M), as the reference's caller
+    addresses it, TE:868-905), the fp32 router [E][N] and T tokens of hidden
+    states from numpy (Qwen3: the skewed case of `skewed_tokens`).
+    Returns a dict: cfg, qts, gates/ups/downs (lists of uint8 device tensors),
+    router (numpy [E][N]), x (numpy [T][N]), hot_experts, hot_tokens."""
+    import torch
+    c = dict(GPTOSS) if tag == "gptoss" else dict(QWEN3)
+    N, E, M = c["N"], c["E"], c["M"]
+    qts = (c["qt_gate"], c["qt_up"], c["qt_down"])
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4 if tag == "gptoss" else 5)
+    if tag == "gptoss":
+        rb = row_bytes(qts[0], N)
+        fused = [gen_weights_torch(gen, qts[0], 2 * M, N, device) for _ in range(E)]
+        gates = [f[:M * rb] for f in fused]
+        ups = [f[M * rb:] for f in fused]
+    else:
+        gates = [gen_weights_torch(gen, qts[0], M, N, device) for _ in range(E)]
+        ups = [gen_weights_torch(gen, qts[1], M, N, device) for _ in range(E)]
+    downs = [gen_weights_torch(gen, qts[2], N, M, device) for _ in range(E)]
+    rng = np.random.default_rng(7)
+    router = gen_router(rng, E, N)
+    hot, hot_tok = np.zeros(0, np.int64), np.zeros(0, np.int64)
+    if tag == "qwen3":
+        x, router, hot, hot_tok = skewed_tokens(rng, router, T)
+    else:
+        x = gen_x(rng, T, N)
+    return dict(cfg=c, qts=qts, gates=gates, ups=ups, downs=downs, router=router, x=x, hot_experts=hot,
+                hot_tokens=hot_tok)

@@ -231,3 +231,17 @@ def norm_err(got, ref):
     if den == 0.0:
         return float(num)
     return float(num / den)
+
+
+def elem_rel_err(got, ref, floor=1e-3):
+    """Per-element relative error max |got-ref| / |ref| over the elements with
+    |ref| >= floor * max|ref| (nearer zero a relative error only measures fp32
+    summation noise against a vanishing reference)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if not ref.size:
+        return 0.0
+    big = np.abs(ref) >= floor * np.max(np.abs(ref))
+    if not np.any(big):
+        return 0.0
+    return float(np.max(np.abs(got[big] - ref[big]) / np.abs(ref[big])))

@@ -227,3 +227,16 @@ def test_gemv_linearity_full_shape(dev):
     yc = dev.gemv(K.Q6_K_SEQ, packed, comb, R, C)[0]
     ref = y[0] * 0.5 + y[1] * 2.0
     assert O.norm_err(yc.cpu().numpy(), ref.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("qt,nc", [(8, 16), (12, 128), (14, 128), (39, 16), (2, 16), (13, 200)])
+def test_short_rows_give_zeros(lib, qt, nc):
+    """Rows shorter than one quant block: zeros, as the reference writes
+    (no kernel reads a block that is not there)."""
+    rng = np.random.default_rng(qt + nc)
+    w = rng.integers(0, 256, 64, dtype=np.uint8)
+    x = W.gen_x(rng, 12, nc)
+    assert np.all(qmm(lib, w, x[0], 4, nc, qt) == 0.0), K.last_error(lib)
+    name = {8: "q8_0", 12: "q4_k", 14: "q6_k", 39: "mxfp4", 2: "q4_0", 13: "q5_k"}[qt]
+    for B in (1, 5, 12):          # B = 12 would take the MFMA GEMM with whole blocks
+        assert np.all(bmm(lib, name, w, x[:B], 4, nc, B) == 0.0)

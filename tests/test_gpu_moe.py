@@ -391,3 +391,75 @@ def test_moe_layer_batched_odd_shapes(dev, orc, qts, N, M, E, Kk, T):
     expert counts whose tiles spread unevenly over the XCDs, odd top-K."""
     got, ref = _moe_case(dev, orc, qts, N=N, M=M, E=E, Kk=Kk, T=T, renorm=int(Kk > 1), seed=T * 7 + E + N)
     assert O.norm_err(got, ref) < moe_tol(qts), K.last_error(dev.so)
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+def test_moe_ffn_nonfinite_token_gives_zeros(lib, orc, bad):
+    """moe_ffn on a token whose logits hold an inf or NaN: no expert is
+    selected and the output is zero, as the reference's moe_ffn gives
+    (CE:640-641); the other tokens are unchanged."""
+    qts, N, M, E, Kk, T = (12, 12, 14), 256, 256, 8, 2, 3
+    gate, upw, down, router, x = _moe_ffn_case(qts, N, M, E, Kk, T, seed=41)
+    x[1, 37] = bad
+    bc = BCView(N, E, Kk, M, router, gate, upw, down, qts)
+    for t in range(T):
+        got = moe_ffn(lib, bc, x[t], N)
+        ref = orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t])
+        if t == 1:
+            assert np.all(got == 0.0) and np.all(ref == 0.0)
+        else:
+            assert O.norm_err(got, ref) < MOE_TOL
+    out = np.full((T, N), np.nan, np.float32)
+    lib.moe_ffn_batched(bc.ptr(), 0, fp(np.ascontiguousarray(x)), fp(out), T)
+    assert np.all(out[1] == 0.0) and np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("T", [4, 30])
+def test_moe_layer_nonfinite_token_gives_zeros(dev, orc, T):
+    """mllm_moe_forward at T = 4 (decode GEMVs) and T = 30 (grouped GEMMs): a
+    token with a NaN element is routed to no expert (idx -1) and its output
+    row is zero on both paths; every other token matches the oracle."""
+    import torch
+    rng = np.random.default_rng(50 + T)
+    qts, N, M, E, Kk = (12, 12, 14), 512, 256, 16, 4
+    gates = [W.gen_weights(rng, qts[0], M, N) for _ in range(E)]
+    ups = [W.gen_weights(rng, qts[1], M, N) for _ in range(E)]
+    downs = [W.gen_weights(rng, qts[2], N, M) for _ in range(E)]
+    router = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, T, N)
+    x[1, 5] = np.nan
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    layer = dev.moe_prepare(qts, N, M, E, Kk, [cu(g) for g in gates], [cu(u) for u in ups], [cu(d) for d in downs],
+                            cu(router), 1)
+    idx = torch.empty((T, Kk), dtype=torch.int32, device="cuda")
+    got = layer.forward(cu(x), idx=idx).cpu().numpy()
+    ri, rw = orc.route(router, x, Kk, 1)
+    assert np.array_equal(idx.cpu().numpy(), ri) and np.all(ri[1] == -1)
+    assert np.all(got[1] == 0.0)
+    keep = [t for t in range(T) if t != 1]
+    ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in keep])
+    assert O.norm_err(got[keep], ref) < MOE_TOL
+
+
+def test_moe_forward_omp_empty_slots(lib, orc):
+    """moe_forward_omp with a slot whose expert id is -1 (a routing that left it
+    empty) adds nothing for it; top_k = 0 clears combined (QK:2179)."""
+    rng = np.random.default_rng(61)
+    qts, n_embd, n_ff, E = (12, 12, 14), 512, 256, 4
+    gates = [W.gen_weights(rng, qts[0], n_ff, n_embd) for _ in range(E)]
+    ups = [W.gen_weights(rng, qts[1], n_ff, n_embd) for _ in range(E)]
+    downs = [W.gen_weights(rng, qts[2], n_embd, n_ff) for _ in range(E)]
+    x = W.gen_x(rng, 1, n_embd)[0]
+    got = moe_forward(lib, gates, ups, downs, x, n_ff, n_embd, qts, np.array([2, -1, 0], np.int32),
+                      np.array([0.5, 0.3, 0.2], np.float32))
+    ref = orc.moe_forward_token(gates, ups, downs, x, n_ff, n_embd, qts, np.array([2, 0], np.int32),
+                                np.array([0.5, 0.2], np.float32))
+    assert O.norm_err(got, ref) < MOE_TOL
+    arr = ctypes.POINTER(ctypes.c_uint8) * E
+    out = np.full(n_embd, 3.0, np.float32)
+    ti = np.zeros(1, np.int32)
+    tw = np.zeros(1, np.float32)
+    lib.moe_forward_omp(arr(*[up(a) for a in gates]), arr(*[up(a) for a in ups]), arr(*[up(a) for a in downs]),
+                        fp(x), n_ff, n_embd, 12, 12, 14, ti.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), fp(tw), 0,
+                        fp(out), fp(np.zeros(16, np.float32)), up(np.zeros(64, np.uint8)))
+    assert np.all(out == 0.0)

@@ -171,6 +171,51 @@ def test_live_moe_forward_null_q8_scratch_differs_only_for_mxfp4_down(orc, ref):
     assert O.norm_err(b, a) < 1e-4
 
 
+@pytest.mark.parametrize("qt,nc", [(8, 16), (12, 128), (14, 128), (39, 16), (2, 16), (13, 200)])
+def test_live_short_rows_give_zeros(orc, ref, qt, nc):
+    """Rows shorter than one quant block: the reference's dot runs over
+    n_cols / block = 0 blocks and writes 0; so does the oracle."""
+    rng = np.random.default_rng(qt + nc)
+    w = rng.integers(0, 256, 64, dtype=np.uint8)
+    x = W.gen_x(rng, 1, nc)
+    out = np.full(4, 7.0, np.float32)
+    ref.quant_matmul(w, x, 4, nc, qt, out=out)
+    assert np.all(out == 0.0)
+    assert np.all(orc.gemv(orc.sem_for(0, qt), w, x, 4, nc, 1) == 0.0)
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+def test_live_moe_ffn_nonfinite_token_gives_zeros(orc, ref, bad):
+    """A token whose router logits hold an inf or NaN: the reference's moe_ffn
+    inserts no expert (strict '>' against NaN probabilities), skips the empty
+    slots (CE:640-641) and returns zeros; the oracle routes it to no expert."""
+    import ctypes
+    from helpers import BCView, fp
+    rng = np.random.default_rng(17)
+    N, E, Kk, M, qts = 256, 8, 2, 256, (12, 12, 14)
+    gate = np.concatenate([W.gen_weights(rng, 12, M, N) for _ in range(E)])
+    upw = np.concatenate([W.gen_weights(rng, 12, M, N) for _ in range(E)])
+    down = np.concatenate([W.gen_weights(rng, 14, N, M) for _ in range(E)])
+    router = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, 2, N)
+    x[1, 37] = bad
+    bc = BCView(N, E, Kk, M, router, gate, upw, down, qts)
+    ref.so.moe_ffn.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.POINTER(ctypes.c_float)] * 4 + [ctypes.c_int]
+    ref.so.moe_ffn.restype = None
+    for t in range(2):
+        out = np.full(N, 5.0, np.float32)
+        gb, ub = np.zeros(4096, np.float32), np.zeros(4096, np.float32)
+        xx = x[t].copy()
+        ref.so.moe_ffn(bc.ptr(), 0, fp(xx), fp(gb), fp(ub), fp(out), 1)
+        mine = orc.moe_ffn_token(router, gate, upw, down, qts, N, E, Kk, M, x[t])
+        if t == 1:
+            assert np.all(out == 0.0) and np.all(mine == 0.0)
+            idx, _ = orc.route(router, x[1:2], Kk, 0)
+            assert np.all(idx == -1)
+        else:
+            assert O.norm_err(mine, out) < 1e-4
+
+
 # ------------------------------------------------ 3. mathematical pins
 
 def _np_decode_q8_0(w, R, C):

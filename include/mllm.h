@@ -162,6 +162,18 @@ MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *layer, int T);
 /* out[T][N]; idx_out/w_out (optional, device [T][K]) receive the routing. */
 MLLM_API int mllm_moe_forward(const mllm_moe_layer *layer, const float *x, int T, float *out, void *workspace,
                               long ws_bytes, int *idx_out, float *w_out, void *stream);
+/* mllm_moe_forward without a workspace argument and without allocating.  No
+ * counterpart in the reference: for callers that cannot call hipMalloc (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * The workspace is a static device array of MLLM_MOE_NOALLOC_SCRATCH_BYTES
+ * that each GPU the library runs on holds until the process ends; T whose
+ * workspace (mllm_moe_workspace_size) exceeds it is rejected with -1 and an
+ * error (64 tokens fit at both benchmark MoE shapes).  All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race.  Same results as mllm_moe_forward. */
+#define MLLM_MOE_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+MLLM_API int mllm_moe_forward_noalloc(const mllm_moe_layer *layer, const float *x, int T, float *out, int *idx_out,
+                                      float *w_out, void *stream);
 /* The stable expert bucketing on its own: entries idx[TK] over E experts ->
  * off[E+1], perm[pos] = entry, pos_of[entry] = pos (-1 for idx < 0), and
  * tiles = 3 arrays of (TK/64 + E + 1) ints (expert, begin, end) + count. */

@@ -484,6 +484,9 @@ long moe_ffn_stride(int which, int qt, int N, int M)
 
 } // namespace
 
+// Error reporting for the other translation units of the library.
+void mllm_set_error(const char *msg) { set_error("%s", msg); }
+
 // =============================================================== drop-in ABI
 extern "C" {
 

@@ -13,3 +13,6 @@ mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N
 
 // Whether the grouped-GEMM (T > 24) path serves these semantics.
 bool mllm_moe_batched_supported(int sem_g, int sem_u, int sem_d);
+
+// Record an error for mllm_last_error() (logged once to stderr).
+void mllm_set_error(const char *msg);

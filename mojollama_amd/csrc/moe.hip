@@ -14,8 +14,10 @@
 //   in k order through the inverse permutation.
 // Decode flow (T <= 24): the same stages with the decode GEMV kernels, one job
 // per (token, slot), no bucketing.
+#include <stdio.h>
 #include <string.h>
 #include <algorithm>
+#include <mutex>
 #include <vector>
 #include "gemm.h"
 #include "gemv.h"
@@ -430,6 +432,67 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
 #undef CK
     return 0;
+}
+
+} // extern "C"
+
+// ------------------------------------------------ no-allocation forward
+// mllm_moe_forward_noalloc's workspace: a file-scope device array that every
+// GPU the library runs on holds until the process ends.  In host code its
+// name is a host-side stand-in, not a device address: the device address is
+// taken once per device with hipGetSymbolAddress (with that device current)
+// and only that address is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[MLLM_MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up on the first call on that device.
+int scratch_for_current_device(void **out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        mllm_set_error("mllm_moe_forward_noalloc: no current HIP device");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess || !p) {
+            char msg[160];
+            snprintf(msg, sizeof msg, "mllm_moe_forward_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                     hipGetErrorString(r));
+            mllm_set_error(msg);
+            return -1;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+} // namespace
+
+extern "C" {
+
+MLLM_API int mllm_moe_forward_noalloc(const mllm_moe_layer *L, const float *x, int T, float *out, int *idx_out,
+                                      float *w_out, void *stream)
+{
+    if (!L || T <= 0) { mllm_set_error("mllm_moe_forward_noalloc: no layer or T <= 0"); return -1; }
+    const size_t need = moe_ws_layout(*L, T, nullptr, nullptr);
+    if (need > (size_t)MLLM_MOE_NOALLOC_SCRATCH_BYTES) {
+        char msg[200];
+        snprintf(msg, sizeof msg,
+                 "mllm_moe_forward_noalloc: T=%d needs %zu bytes of workspace, above the %d-byte static maximum",
+                 T, need, (int)MLLM_MOE_NOALLOC_SCRATCH_BYTES);
+        mllm_set_error(msg);
+        return -1;
+    }
+    void *ws = nullptr;
+    if (scratch_for_current_device(&ws)) return -1;
+    return mllm_moe_forward(L, x, T, out, ws, (long)need, idx_out, w_out, stream);
 }
 
 // Bucketing alone (for tests): perm/pos_of/off of the entries idx [TK] over E experts.

@@ -127,6 +127,8 @@ def load_kernels(path=LIB_PATH):
     so.mllm_moe_workspace_size.restype = ctypes.c_long
     so.mllm_moe_forward.argtypes = [cvp, cvp, ci, cvp, cvp, ctypes.c_long, cvp, cvp, cvp]
     so.mllm_moe_forward.restype = ci
+    so.mllm_moe_forward_noalloc.argtypes = [cvp, cvp, ci, cvp, cvp, cvp, cvp]
+    so.mllm_moe_forward_noalloc.restype = ci
     so.mllm_moe_bucket.argtypes = [cvp, ci, ci, cvp, cvp, cvp, cvp, cvp]
     so.mllm_moe_bucket.restype = ci
     if path == LIB_PATH:

@@ -122,6 +122,46 @@ MLLM_API long mllm_gemv_workspace_size(int sem, int n_rows, int n_cols, int B);
 MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
                        int B, void *workspace, void *stream);
 
+/* The decode GEMV with the work around it fused in (the RMSNorm before the
+ * QKV and gate/up projections, TE:1516,1641 / GO:29-34, the residual adds
+ * after the output and down projections, TE:1628-1651, the SiLU product
+ * before the down projection).  Every field may be NULL / 0:
+ *   x_up:     activation = silu(x) * x_up (silu_clamp: gate clamped to +-80,
+ *             moe_forward_omp QK:2157-2164; else plain silu);
+ *   x_res:    activation v = x + x_res;
+ *   res_out:  v is written here (the new residual stream; must not overlap x
+ *             or x_res);
+ *   rms_w:    activation = RMSNorm(v) * rms_w over n_cols, rms_div 0:
+ *             v * (1/sqrtf(mean(v^2) + eps)) (simd_ops rms_norm), 1:
+ *             v / sqrtf(mean(v^2) + eps) (gptoss_batch_forward.c rms_norm);
+ *   out_add:  out = out_add + W * activation (may equal out).
+ * x_up excludes x_res/res_out/rms_w and silu_pair.  Shapes the decode kernel
+ * can stage at once (B <= 8; paired rows at B == 1) run as one launch; others
+ * form the activation in the workspace first and the SiLU product after the
+ * GEMV (mllm_gemv_fused_workspace_size bytes). */
+typedef struct {
+    const float *x_up;
+    int silu_clamp;
+    const float *x_res;
+    float *res_out;
+    const float *rms_w;
+    float rms_eps;
+    int rms_div;
+    const float *out_add;
+    int x_ld;             /* token stride of x, x_up, x_res and res_out (0: n_cols) */
+    int silu_pair;        /* the matrix holds 2*n_rows rows, gate rows then up rows (a stacked
+                             gate/up pair): out[r] = silu(gate_r . v) * (up_r . v), silu_clamp as above */
+} mllm_gemv_fusion;
+MLLM_API long mllm_gemv_fused_workspace_size(int sem, int n_rows, int n_cols, int B, const mllm_gemv_fusion *f);
+MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows,
+                             int n_cols, int B, const mllm_gemv_fusion *f, void *workspace, void *stream);
+
+/* A plain streaming read of `bytes` (a multiple of 16) at a 16-byte aligned
+ * device address, every word read once: the bandwidth ceiling a kernel that
+ * reads the same bytes in one launch is measured against.  sink: 16 bytes of
+ * device memory (written only if the data xor to a fixed pattern). */
+MLLM_API int mllm_read_probe(const void *dev, long bytes, void *sink, void *stream);
+
 /* quantize_row_q8_0 over T rows. */
 MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *q8_dev, void *stream);
 

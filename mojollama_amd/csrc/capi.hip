@@ -244,6 +244,64 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
     return 0;
 }
 
+// Several host matrices of one layout and width stacked row-wise into one
+// packed device matrix (the q/k/v or gate/up matrices of batch_qkv_omp /
+// batch_gate_up_omp, so one GEMV launch covers them), cached by the tuple of
+// host pointers and row counts and checked by each matrix's fingerprint.
+std::map<std::vector<long>, wentry> g_concat_cache;
+
+int get_weight_concat(const uint8_t *const *hosts, const int *rows, int n, int ly, int cols, mllm_packed &view)
+{
+    std::vector<long> key;
+    uint64_t fp = 1469598103934665603ull;
+    long total_rows = 0, total_raw = 0;
+    for (int i = 0; i < n; i++) {
+        key.push_back((long)(uintptr_t)hosts[i]);
+        key.push_back(rows[i]);
+        const long raw = raw_row_bytes(ly, cols) * rows[i];
+        fp = (fp ^ fingerprint(hosts[i], raw)) * 1099511628211ull;
+        total_rows += rows[i];
+        total_raw += raw;
+    }
+    key.push_back(ly);
+    key.push_back(cols);
+    {
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        auto it = g_concat_cache.find(key);
+        if (it != g_concat_cache.end()) {
+            if (it->second.fp == fp) { view = it->second.view; return 0; }
+            g_retired.push_back(it->second.dev);
+            g_concat_cache.erase(it);
+        }
+    }
+    thread_ctx &c = t_ctx;
+    wentry e;
+    e.bytes = mllm_packed_bytes(ly, (int)total_rows, cols, nullptr);
+    HIP_OK(hipMalloc(&e.dev, e.bytes));
+    uint8_t *tmp = nullptr;
+    if (total_raw > 0) {
+        if (hipMalloc(&tmp, total_raw) != hipSuccess) { (void)hipFree(e.dev); set_error("hipMalloc(raw %ld) failed", total_raw); return -1; }
+        hipError_t r = hipSuccess;
+        long off = 0;
+        for (int i = 0; i < n && r == hipSuccess; i++) {
+            const long raw = raw_row_bytes(ly, cols) * rows[i];
+            if (raw > 0) r = hipMemcpyAsync(tmp + off, hosts[i], raw, hipMemcpyHostToDevice, c.st);
+            off += raw;
+        }
+        if (r == hipSuccess) r = mllm_launch_pack(ly, tmp, e.dev, (int)total_rows, cols, c.st);
+        if (r == hipSuccess) r = hipStreamSynchronize(c.st);
+        (void)hipFree(tmp);
+        if (r != hipSuccess) { (void)hipFree(e.dev); set_error("weight upload failed: %s", hipGetErrorString(r)); return -1; }
+    }
+    e.view = mllm_packed_view(ly, e.dev, (int)total_rows, cols);
+    e.fp = fp;
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto ins = g_concat_cache.emplace(key, e);
+    if (!ins.second) (void)hipFree(e.dev);
+    view = ins.first->second.view;
+    return 0;
+}
+
 // Router [E][N] fp32 on the host -> device copy in the routing layout
 // (mllm_router_pack: element (i, e) at ((i/4)*E + e)*4 + i%4, zero pad
 // rows), cached like the weights: a hit whose host contents changed (a new
@@ -379,9 +437,11 @@ size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
            align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4);
 }
 
-// Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data.
+// Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data;
+// out_add (optional, same layout as out, not overlapping it on the MFMA path)
+// is added to the result.
 int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_rows, int n_cols, int B,
-             void *scratch, hipStream_t st)
+             void *scratch, hipStream_t st, const float *out_add = nullptr)
 {
     const bool q8 = mllm_sem_uses_q8(sem);
     if (B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem)) {
@@ -408,6 +468,7 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
             g.part = (float *)((uint8_t *)scratch + (q8 ? xq_bytes(B, n_cols) : 0) +
                                (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0));
         HIP_OK(mllm_launch_qgemm(sem, gemm_xmode(sem), false, g, 0, st));
+        if (out_add) HIP_OK(mllm_launch_add(out, out_add, (long)B * n_rows, st));
         return 0;
     }
     for (int b0 = 0; b0 < B; b0 += 8) {
@@ -418,6 +479,7 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
         a.out = out + (long)b0 * n_rows;
         a.ldo = n_rows;
         a.n_rows = n_rows; a.n_cols = n_cols; a.B = B - b0 < 8 ? B - b0 : 8;
+        a.out_add = out_add ? out_add + (long)b0 * n_rows : nullptr;
         HIP_OK(mllm_launch_gemv(sem, a, 1, st));
     }
     return 0;
@@ -444,6 +506,54 @@ int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows,
     HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
     HIP_OK(hipStreamSynchronize(c.st));
     memcpy(out, c.h_out.p, obytes);
+    return 0;
+}
+
+// n matrices applied to one host activation (batch_qkv_omp / batch_gate_up_omp,
+// QK:1139-1222): x uploaded once; consecutive matrices of one semantic
+// stacked into one packed matrix and run as one GEMV launch; results
+// copied back with one transfer and one synchronisation.  A matrix whose
+// type the reference's row path does not know (sems[i] < 0) leaves its
+// output untouched.
+int host_multi_gemv(const int *sems, const uint8_t *const *Ws, float *const *outs, const int *rows, int n,
+                    const float *x, int n_cols)
+{
+    thread_ctx &c = t_ctx;
+    if (c.init()) return -1;
+    long total = 0;
+    for (int i = 0; i < n; i++) total += rows[i] > 0 && sems[i] >= 0 ? rows[i] : 0;
+    if (total == 0) return 0;
+    const size_t xbytes = (size_t)n_cols * 4, obytes = (size_t)total * 4;
+    if (c.d_in.ensure(xbytes) || c.d_out.ensure(obytes) || c.h_in.ensure(xbytes) || c.h_out.ensure(obytes)) {
+        set_error("staging allocation failed");
+        return -1;
+    }
+    memcpy(c.h_in.p, x, xbytes);
+    HIP_OK(hipMemcpyAsync(c.d_in.p, c.h_in.p, xbytes, hipMemcpyHostToDevice, c.st));
+    long at = 0;
+    for (int i = 0; i < n;) {
+        if (sems[i] < 0 || rows[i] <= 0) { i++; continue; }
+        int j = i + 1;
+        while (j < n && sems[j] == sems[i] && rows[j] > 0) j++;
+        int grp_rows = 0;
+        for (int k = i; k < j; k++) grp_rows += rows[k];
+        mllm_packed view;
+        if (j - i == 1 ? get_weight(Ws[i], mllm_sem_layout(sems[i]), rows[i], n_cols, view)
+                       : get_weight_concat(Ws + i, rows + i, j - i, mllm_sem_layout(sems[i]), n_cols, view))
+            return -1;
+        if (run_gemv(sems[i], view, (const float *)c.d_in.p, (float *)c.d_out.p + at, grp_rows, n_cols, 1, nullptr, c.st))
+            return -1;
+        at += grp_rows;
+        i = j;
+    }
+    HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
+    HIP_OK(hipStreamSynchronize(c.st));
+    at = 0;
+    for (int i = 0; i < n; i++) {
+        if (sems[i] < 0 || rows[i] <= 0) continue;
+        memcpy(outs[i], (const float *)c.h_out.p + at, (size_t)rows[i] * 4);
+        at += rows[i];
+    }
     return 0;
 }
 
@@ -526,20 +636,27 @@ MLLM_API void batch_qkv_omp(const uint8_t *Wq, const uint8_t *Wk, const uint8_t 
     const uint8_t *Ws[3] = {Wq, Wk, Wv};
     float *outs[3] = {out_q, out_k, out_v};
     const int ns[3] = {nq, nk, nv}, qts[3] = {qtype_q, qtype_k, qtype_v};
+    int sems[3];
     for (int i = 0; i < 3; i++) {
-        const int sem = sem_for(ENT_ROWS, qts[i]);
-        if (sem < 0) { set_error("batch_qkv_omp: unknown quant type %d", qts[i]); continue; }
-        host_gemv(sem, Ws[i], x, outs[i], ns[i], n_cols, 1);
+        sems[i] = sem_for(ENT_ROWS, qts[i]);
+        if (sems[i] < 0) set_error("batch_qkv_omp: unknown quant type %d (output untouched)", qts[i]);
     }
+    host_multi_gemv(sems, Ws, outs, ns, 3, x, n_cols);
 }
 
 MLLM_API void batch_gate_up_omp(const uint8_t *Wg, const uint8_t *Wu, const float *x, float *out_gate, float *out_up,
                                 int ng, int nu, int n_cols, int qtype_g, int qtype_u)
 {
     API_GUARD;
-    const int sg = sem_for(ENT_ROWS, qtype_g), su = sem_for(ENT_ROWS, qtype_u);
-    if (sg >= 0) host_gemv(sg, Wg, x, out_gate, ng, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_g);
-    if (su >= 0) host_gemv(su, Wu, x, out_up, nu, n_cols, 1); else set_error("batch_gate_up_omp: unknown quant type %d", qtype_u);
+    const uint8_t *Ws[2] = {Wg, Wu};
+    float *outs[2] = {out_gate, out_up};
+    const int ns[2] = {ng, nu}, qts[2] = {qtype_g, qtype_u};
+    int sems[2];
+    for (int i = 0; i < 2; i++) {
+        sems[i] = sem_for(ENT_ROWS, qts[i]);
+        if (sems[i] < 0) set_error("batch_gate_up_omp: unknown quant type %d (output untouched)", qts[i]);
+    }
+    host_multi_gemv(sems, Ws, outs, ns, 2, x, n_cols);
 }
 
 MLLM_API int quantize_row_q8_0(const float *x, uint8_t *q8, int n_cols)
@@ -738,6 +855,8 @@ MLLM_API void mllm_cache_clear(void)
     (void)hipDeviceSynchronize();
     for (auto &kv : g_layer_cache) (void)hipFree(kv.second.dtab);
     g_layer_cache.clear();
+    for (auto &kv : g_concat_cache) (void)hipFree(kv.second.dev);
+    g_concat_cache.clear();
     for (auto &kv : g_cache) (void)hipFree(kv.second.dev);
     g_cache.clear();
     for (uint8_t *p : g_retired) (void)hipFree(p);
@@ -784,6 +903,133 @@ MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, floa
     if (gemv_scratch_bytes(sem, n_rows, n_cols, B) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
     mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
     return run_gemv(sem, view, x_dev, out_dev, n_rows, n_cols, B, workspace, (hipStream_t)stream);
+}
+
+// --------------------------------------------------- fused decode GEMV (f1)
+static bool fusion_has_pro(const mllm_gemv_fusion *f) { return f && (f->x_res || f->res_out || f->rms_w); }
+static int fusion_ld(const mllm_gemv_fusion *f, int n_cols) { return f && f->x_ld ? f->x_ld : n_cols; }
+static bool fusion_pair(const mllm_gemv_fusion *f) { return f && f->silu_pair; }
+
+// Whether one decode-GEMV launch takes the whole fusion.  Otherwise the
+// activation is formed by its own kernel into the workspace, paired rows run
+// as one GEMV over both halves followed by the SiLU product, and on the MFMA
+// path the residual is added after the GEMM.
+static bool fusion_direct(int sem, int n_cols, int B, const mllm_gemv_fusion *f)
+{
+    if (B > 8 || sem == SEM_F32 || n_cols < mllm_sem_block_elems(sem)) return false;
+    const bool pro = fusion_has_pro(f), pair = fusion_pair(f);
+    if (pair && B != 1) return false;
+    if (pro && (n_cols % 4 || fusion_ld(f, n_cols) % 4)) return false;
+    if (pro || pair) return mllm_gemv_fused_fits(sem, n_cols, B, pro);
+    if (f && f->x_up) return mllm_sem_uses_q8(sem) || B == 1;
+    return true;
+}
+
+// workspace: [activation B x n_cols] [residual copy B x n_rows] [pair output B x 2 n_rows] [GEMV scratch]
+struct fused_ws { size_t keep, pair, gemv, total; };
+static fused_ws fused_layout(int sem, int n_rows, int n_cols, int B, const mllm_gemv_fusion *f)
+{
+    fused_ws w{0, 0, 0, 0};
+    if (fusion_direct(sem, n_cols, B, f)) return w;
+    const bool pair = fusion_pair(f);
+    size_t o = 0;
+    if (f && (fusion_has_pro(f) || f->x_up)) o += align256((size_t)B * n_cols * 4);
+    w.keep = o;
+    if (f && f->out_add && B > 8 && !pair) o += align256((size_t)B * n_rows * 4);
+    w.pair = o;
+    if (pair) o += align256((size_t)B * 2 * n_rows * 4);
+    w.gemv = o;
+    w.total = o + gemv_scratch_bytes(sem, pair ? 2 * n_rows : n_rows, n_cols, B);
+    return w;
+}
+
+MLLM_API long mllm_gemv_fused_workspace_size(int sem, int n_rows, int n_cols, int B, const mllm_gemv_fusion *f)
+{
+    if (sem < 0 || sem >= SEM_COUNT || B <= 0) return -1;
+    return (long)fused_layout(sem, n_rows, n_cols, B, f).total;
+}
+
+MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows,
+                             int n_cols, int B, const mllm_gemv_fusion *f, void *workspace, void *stream)
+{
+    if (sem < 0 || sem >= SEM_COUNT) { set_error("mllm_gemv_fused: bad semantic %d", sem); return -1; }
+    if (n_rows <= 0 || B <= 0) return 0;
+    if (((uintptr_t)x_dev & 15) || ((uintptr_t)packed_dev & 255)) { set_error("mllm_gemv_fused: misaligned pointer"); return -1; }
+    const bool pro = fusion_has_pro(f), pair = fusion_pair(f);
+    if ((pro || pair) && f->x_up) {
+        set_error("mllm_gemv_fused: x_up excludes the residual/norm prologue and paired rows");
+        return -1;
+    }
+    if (f && (((uintptr_t)f->x_up | (uintptr_t)f->x_res | (uintptr_t)f->res_out | (uintptr_t)f->rms_w |
+               (uintptr_t)f->out_add) & 15)) {
+        set_error("mllm_gemv_fused: fusion vectors must be 16-byte aligned");
+        return -1;
+    }
+    const int ldx = fusion_ld(f, n_cols);
+    if (ldx < n_cols) { set_error("mllm_gemv_fused: x_ld %d < n_cols %d", ldx, n_cols); return -1; }
+    if (f && f->res_out) {
+        // res_out is written while other workgroups still read x and x_res
+        const size_t span = ((size_t)(B - 1) * ldx + n_cols) * 4;
+        const uintptr_t ro = (uintptr_t)f->res_out, re = ro + span;
+        auto overlaps = [&](const void *p) {
+            const uintptr_t a = (uintptr_t)p, b = a + span;
+            return p && a < re && ro < b;
+        };
+        if (overlaps(x_dev) || overlaps(f->x_res)) { set_error("mllm_gemv_fused: res_out overlaps x or x_res"); return -1; }
+    }
+    const fused_ws L = fused_layout(sem, n_rows, n_cols, B, f);
+    if (L.total && !workspace) { set_error("mllm_gemv_fused: needs a workspace of %zu bytes", L.total); return -1; }
+    hipStream_t st = (hipStream_t)stream;
+    const int mrows = pair ? 2 * n_rows : n_rows;   // rows of the matrix (the stacked gate/up pair)
+    mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, mrows, n_cols);
+    const float *out_add = f ? f->out_add : nullptr;
+    if (fusion_direct(sem, n_cols, B, f)) {
+        mllm_gemv_args a{};
+        a.W = view;
+        a.x = x_dev; a.ldx = ldx;
+        a.out = out_dev; a.ldo = n_rows;
+        a.n_rows = n_rows; a.n_cols = n_cols; a.B = B;
+        if (f) {
+            a.x_up = f->x_up; a.silu_noclamp = !f->silu_clamp;
+            a.x_res = f->x_res; a.res_out = f->res_out; a.rms_w = f->rms_w; a.rms_eps = f->rms_eps;
+            a.rms_div = f->rms_div;
+            a.out_add = out_add;
+            a.silu_pair = f->silu_pair ? 1 : 0;
+        }
+        HIP_OK(mllm_launch_gemv(sem, a, 1, st));
+        return 0;
+    }
+    uint8_t *ws = (uint8_t *)workspace;
+    const float *xa = x_dev;
+    if (f && (pro || f->x_up)) {
+        float *xe = (float *)ws;
+        HIP_OK(mllm_launch_act_prologue(x_dev, f->x_res, f->res_out, f->rms_w, f->rms_eps, f->rms_div, f->x_up,
+                                        f->silu_clamp, B, n_cols, ldx, xe, st));
+        xa = xe;
+    } else if (ldx != n_cols) {
+        set_error("mllm_gemv_fused: a strided x (x_ld) needs a fused activation step on this path");
+        return -1;
+    }
+    if (pair) {
+        float *y = (float *)(ws + L.pair);
+        if (run_gemv(sem, view, xa, y, mrows, n_cols, B, ws + L.gemv, st)) return -1;
+        HIP_OK(mllm_launch_silu_pair(y, B, n_rows, f->silu_clamp, out_dev, out_add, st));
+        return 0;
+    }
+    if (out_add && B > 8) {
+        // the MFMA path writes out before the residual is added: add from a copy
+        float *keep = (float *)(ws + L.keep);
+        HIP_OK(hipMemcpyAsync(keep, out_add, (size_t)B * n_rows * 4, hipMemcpyDeviceToDevice, st));
+        out_add = keep;
+    }
+    return run_gemv(sem, view, xa, out_dev, n_rows, n_cols, B, ws + L.gemv, st, out_add);
+}
+
+MLLM_API int mllm_read_probe(const void *dev, long bytes, void *sink, void *stream)
+{
+    if (((uintptr_t)dev & 15) || (bytes & 15) || !sink) { set_error("mllm_read_probe: 16-byte aligned, multiple of 16"); return -1; }
+    HIP_OK(mllm_launch_read_probe(dev, bytes, sink, (hipStream_t)stream));
+    return 0;
 }
 
 MLLM_API int mllm_quantize_q8_0(const float *x_dev, int T, int n_cols, uint8_t *q8_dev, void *stream)

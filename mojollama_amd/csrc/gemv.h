@@ -31,24 +31,58 @@ struct mllm_gemv_args {
     float *out2;
     // The activation is silu(x) * x_up (mllm_silu_mul, same offsets as x)
     // instead of x: fp32-activation semantics at B == 1, and Q8 semantics
-    // quantising in the kernel.
+    // quantising in the kernel.  silu_noclamp: the gate is not clamped
+    // (moe_ffn CE:649-652, the dense FFN's silu).
     const float *x_up;
+    int silu_noclamp;
+    // Fused prologue (single-matrix launches, no job table): token b's
+    // activation is v = x[b] + x_res[b] (x_res optional, same strides as x),
+    // res_out[b] = v when res_out is given (the new residual stream), then
+    // with rms_w the RMS norm of v over its n_cols elements times rms_w:
+    //   rms_div == 0: v * (1 / sqrtf(mean(v^2) + eps)) * rms_w   (simd_ops rms_norm, TE:1516,1641)
+    //   rms_div == 1: (v / sqrtf(mean(v^2) + eps)) * rms_w       (gptoss_batch_forward.c GO:29-34)
+    const float *x_res;
+    float *res_out;
+    const float *rms_w;
+    float rms_eps;
+    int rms_div;
+    // Fused epilogue: out[b][r] = out_add[b][r] + (W x)[b][r] (same strides as
+    // out; may alias out): the residual add after a projection.
+    const float *out_add;
+    int pro_lds;   // byte offset of the prologue's LDS scratch (set by the launcher)
+    // Paired rows (batch 1): output row r is silu(g_r . x) * (u_r . x) (the
+    // gate clamped to +-80 unless silu_noclamp), g_r = row r and u_r = row
+    // r + n_rows of the matrix, or with table2 row r of table2's matrix for the
+    // job's expert: gate, up and the SiLU product in one launch.
+    int silu_pair;
 };
 
 // moe_forward_omp's SiLU product (QK:2157-2164): the gate clamped to +-80,
-// then silu(g) * u.  Every kernel that forms it uses this one expression.
-__device__ __forceinline__ float mllm_silu_mul(float g, float u)
+// then silu(g) * u.  Every kernel that forms it uses this one expression;
+// clamp = false gives the unclamped form of moe_ffn and the dense FFN.
+__device__ __forceinline__ float mllm_silu_mul(float g, float u, bool clamp = true)
 {
-    g = g < -80.0f ? -80.0f : g;
-    g = g > 80.0f ? 80.0f : g;
+    if (clamp) {
+        g = g < -80.0f ? -80.0f : g;
+        g = g > 80.0f ? 80.0f : g;
+    }
     return (g / (1.0f + expf(-g))) * u;
 }
+
+// Whether a launch asks for the fused activation prologue.
+inline __host__ __device__ bool mllm_has_prologue(const mllm_gemv_args &a) { return a.x_res || a.rms_w || a.res_out; }
+// Whether the persistent kernel's fused forms (prologue, paired rows) stage
+// this launch's activation at once; paired rows need B == 1.
+bool mllm_gemv_fused_fits(int sem, int n_cols, int B, bool prologue);
 
 // n_cols below one quant block (no whole block per row): every output is 0, as
 // the reference's dot over n_cols / block = 0 blocks; no weight is read.
 hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStream_t st);
 // Elements per quant block of a semantic's weight layout (1 for fp32 rows).
 int mllm_sem_block_elems(int sem);
+// Whether mllm_launch_gemv takes the fused prologue for this shape (the
+// persistent kernel stages all of K; else the caller runs the prologue first).
+bool mllm_gemv_prologue_fits(int sem, int n_cols, int B);
 
 // Repack raw GGUF blocks (device) into the plane layout `ly`.
 hipError_t mllm_launch_pack(int ly, const uint8_t *raw, uint8_t *packed, int n_rows, int n_cols, hipStream_t st);
@@ -71,6 +105,20 @@ hipError_t mllm_launch_router_pack(const float *router, int N, int E, float *out
 long mllm_route_workspace_floats(int T, int E);
 hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, float *logits_ws, hipStream_t st);
+
+// The fused GEMV activation on its own, T rows of n (one workgroup each):
+// v = (x_up ? silu(x) * x_up : x) + x_res; res_out = v; with rms_w the RMS
+// norm of v (div: (v / rms) * w, else v * (1 / rms) * w).  Any pointer but x
+// and out may be null.
+hipError_t mllm_launch_act_prologue(const float *x, const float *x_res, float *res_out, const float *rms_w, float eps,
+                                    int div, const float *x_up, int clamp, int T, int n, int ldx, float *out,
+                                    hipStream_t st);
+// Plain streaming read of bytes / 16 words (mllm_read_probe).
+hipError_t mllm_launch_read_probe(const void *p, long bytes, void *sink, hipStream_t st);
+// out[i] += add[i], i < n.
+hipError_t mllm_launch_add(float *out, const float *add, long n, hipStream_t st);
+// out[b][r] = silu(y[b][r]) * y[b][n + r] (+ add[b][r]); y is [B][2n].
+hipError_t mllm_launch_silu_pair(const float *y, int B, int n, int clamp, float *out, const float *add, hipStream_t st);
 
 // h[i] = silu(g[i]) * u[i] (clamp g to +-80 when clamp != 0), i < n.
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st);

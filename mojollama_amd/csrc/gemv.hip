@@ -25,10 +25,21 @@ __global__ void k_gemv_zero(mllm_gemv_args a)
     float *out = (second ? a.out2 : a.out) + (long)(second ? job - a.job_split : job) * a.out_job_stride;
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= a.n_rows) return;
-    for (int b = 0; b < a.B; b++) out[(long)b * a.ldo + r] = 0.0f;
+    for (int b = 0; b < a.B; b++) out[(long)b * a.ldo + r] = a.out_add ? a.out_add[(long)b * a.ldo + r] : 0.0f;
 }
 
 } // namespace
+
+bool mllm_gemv_fused_fits(int sem, int n_cols, int B, bool prologue)
+{
+    if (sem == SEM_F32 || B < 1 || B > 8 || n_cols < mllm_sem_block_elems(sem)) return false;
+    const bool q8 = mllm_sem_uses_q8(sem);
+    const int be = mllm_layout_info(mllm_sem_layout(sem)).block_elems;
+    const int BM = B == 1 ? 1 : B == 2 ? 2 : B <= 4 ? 4 : 8;
+    return persistent_lds(q8, be, n_cols, BM, prologue) <= kPersistentLds;
+}
+
+bool mllm_gemv_prologue_fits(int sem, int n_cols, int B) { return mllm_gemv_fused_fits(sem, n_cols, B, true); }
 
 int mllm_sem_block_elems(int sem)
 {
@@ -68,9 +79,37 @@ hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStr
     if (a.x_up && (sem == SEM_F32 || (mllm_sem_uses_q8(sem) ? a.xq.q != nullptr : a.B != 1)))
         return hipErrorInvalidValue;
     if (a.job_split > 0 && (a.job_split >= n_jobs || !a.out2 || (a.table && !a.table2))) return hipErrorInvalidValue;
+    // the fused forms run in the persistent kernel only: the prologue on one
+    // matrix with a fp32 activation (or one the kernel quantises itself),
+    // paired rows at batch 1
+    const bool pro = mllm_has_prologue(a), pair = a.silu_pair != 0;
+    if (pro && (a.table || n_jobs != 1 || a.x_up || a.xq.q)) return hipErrorInvalidValue;
+    if (pair && (a.B != 1 || a.x_up || a.xq.q || (a.table && !a.table2) || a.job_split > 0)) return hipErrorInvalidValue;
+    if ((pro || pair) && !mllm_gemv_fused_fits(sem, a.n_cols, a.B, pro)) return hipErrorInvalidValue;
+    if (a.out_add && (a.table || n_jobs != 1)) return hipErrorInvalidValue;
     if (a.n_cols < mllm_sem_block_elems(sem)) {
         hipLaunchKernelGGL(k_gemv_zero, dim3((a.n_rows + 255) / 256, n_jobs), dim3(256), 0, st, a);
         return hipGetLastError();
+    }
+    if (pro || pair) {
+        switch (sem) {
+        case SEM_Q4_0: return gemv_fused_sem<SEM_Q4_0>(a, n_jobs, st);
+        case SEM_Q4_1: return gemv_fused_sem<SEM_Q4_1>(a, n_jobs, st);
+        case SEM_Q5_0_F32: return gemv_fused_sem<SEM_Q5_0_F32>(a, n_jobs, st);
+        case SEM_Q5_0_Q8: return gemv_fused_sem<SEM_Q5_0_Q8>(a, n_jobs, st);
+        case SEM_Q8_0: return gemv_fused_sem<SEM_Q8_0>(a, n_jobs, st);
+        case SEM_Q4_K_GGML: return gemv_fused_sem<SEM_Q4_K_GGML>(a, n_jobs, st);
+        case SEM_Q4_K_Q8: return gemv_fused_sem<SEM_Q4_K_Q8>(a, n_jobs, st);
+        case SEM_Q5_K_GGML: return gemv_fused_sem<SEM_Q5_K_GGML>(a, n_jobs, st);
+        case SEM_Q5_K_CE: return gemv_fused_sem<SEM_Q5_K_CE>(a, n_jobs, st);
+        case SEM_Q6_K_GGML: return gemv_fused_sem<SEM_Q6_K_GGML>(a, n_jobs, st);
+        case SEM_Q6_K_LOWNIB: return gemv_fused_sem<SEM_Q6_K_LOWNIB>(a, n_jobs, st);
+        case SEM_Q6_K_SEQ: return gemv_fused_sem<SEM_Q6_K_SEQ>(a, n_jobs, st);
+        case SEM_MXFP4: return gemv_fused_sem<SEM_MXFP4>(a, n_jobs, st);
+        case SEM_MXFP4_CLAMP: return gemv_fused_sem<SEM_MXFP4_CLAMP>(a, n_jobs, st);
+        case SEM_MXFP4_Q8: return gemv_fused_sem<SEM_MXFP4_Q8>(a, n_jobs, st);
+        default: return hipErrorInvalidValue;
+        }
     }
     switch (sem) {
     case SEM_F32: launch_f32(a, n_jobs, st); break;

@@ -158,6 +158,81 @@ MLLM_DEV void stage_load(x_stage<SILU> &st, const float *__restrict__ x, const f
 // Value of the partner lane (lane ^ 1).
 MLLM_DEV float lane_pair(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); }
 
+// ---------------------------------------------------------------- fused prologue
+//
+// Residual add and RMS norm applied to the activation while it is staged
+// (mllm_gemv_args: x_res, res_out, rms_w).  Every workgroup reduces each
+// token's sum(v^2) itself (the vector is a few KB), so no other launch or
+// cross-workgroup step is needed.  The scale is 1/rms (rms_div == 0) or rms
+// (rms_div == 1).
+
+// v (8 elements k .. k+7 of token b): + x_res, then the RMS scale and weight.
+// res / w are loaded here (L2 hits: the reduction read them already).
+MLLM_DEV void prologue_apply8(float (&v)[8], const mllm_gemv_args &a, float sc, int b, int k)
+{
+    if (a.x_res) {
+        const float *r = a.x_res + (long)b * a.ldx + k;
+        const float4 r0 = gld<float4>(r), r1 = gld<float4>(r + 4);
+        v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
+        v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+    }
+    if (a.rms_w) {
+        const float4 w0 = gld<float4>(a.rms_w + k), w1 = gld<float4>(a.rms_w + k + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (a.rms_div ? v[e] / sc : v[e] * sc) * w[e];
+    }
+}
+
+MLLM_DEV void f4x2_to8(const float4 (&p)[2], float (&v)[8])
+{
+    v[0] = p[0].x; v[1] = p[0].y; v[2] = p[0].z; v[3] = p[0].w;
+    v[4] = p[1].x; v[5] = p[1].y; v[6] = p[1].z; v[7] = p[1].w;
+}
+MLLM_DEV void f8_to4x2(const float (&v)[8], float4 (&p)[2])
+{
+    p[0] = make_float4(v[0], v[1], v[2], v[3]);
+    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// Per-token RMS scale of v = x + res over n elements into sc[b] (LDS; red:
+// 4*8 floats of LDS scratch), and res_out = v written by workgroup (0, 0).
+// Whole workgroup; ends with a barrier.
+MLLM_DEV void prologue_reduce(const mllm_gemv_args &a, int B, float *red, float *sc)
+{
+    const int n = a.n_cols, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool vec = (n & 3) == 0 && (a.ldx & 3) == 0;
+    const bool writer = a.res_out && blockIdx.x == 0 && blockIdx.y == 0;
+    for (int b = 0; b < B; b++) {
+        const float *xb = a.x + (long)b * a.ldx, *rb = a.x_res ? a.x_res + (long)b * a.ldx : nullptr;
+        float *ob = writer ? a.res_out + (long)b * a.ldx : nullptr;
+        float ss = 0.0f;
+        if (vec) {
+            for (int i = 4 * tid; i < n; i += 1024) {
+                float4 v = gld<float4>(xb + i);
+                if (rb) { const float4 r = gld<float4>(rb + i); v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w; }
+                if (ob) *reinterpret_cast<float4 *>(ob + i) = v;
+                ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+            }
+        } else {
+            for (int i = tid; i < n; i += 256) {
+                float v = xb[i] + (rb ? rb[i] : 0.0f);
+                if (ob) ob[i] = v;
+                ss = fmaf(v, v, ss);
+            }
+        }
+        ss = group_sum<64>(ss);
+        if (lane == 0) red[wave * 8 + b] = ss;
+    }
+    __syncthreads();
+    if (tid < B) {
+        const float t = red[tid] + red[8 + tid] + red[16 + tid] + red[24 + tid];
+        const float r = sqrtf(t / (float)n + a.rms_eps);
+        sc[tid] = a.rms_div ? r : 1.0f / r;
+    }
+    __syncthreads();
+}
+
 // Byte 0 of a, b, c, d packed into one word (a lowest).
 MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 {
@@ -167,7 +242,8 @@ MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 }
 
 template <int SEM, bool SILU>
-MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass)
+MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass,
+                          bool clamp)
 {
     const int nh = kn >> 3;
     constexpr float M = 12582912.0f;   // 1.5 * 2^23: t = y + M holds rne(y) in its low mantissa bits
@@ -182,7 +258,7 @@ MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
             const float u[8] = {st.u[q][0].x, st.u[q][0].y, st.u[q][0].z, st.u[q][0].w,
                                 st.u[q][1].x, st.u[q][1].y, st.u[q][1].z, st.u[q][1].w};
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = mllm_silu_mul(v[e], u[e]);
+            for (int e = 0; e < 8; e++) v[e] = mllm_silu_mul(v[e], u[e], clamp);
         }
         float m = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -224,12 +300,13 @@ MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
 // load already issued by the caller.
 template <int SEM, bool SILU>
 MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, const digit_geom &dg,
-                           const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B, int k0, int kn)
+                           const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B, int k0, int kn,
+                           bool clamp = true)
 {
     const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
     for (int pass = 0; pass < passes; pass++) {
         if (pass || !load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
-        stage_store<SEM, SILU>(st, lds, dg, B, kn, pass);
+        stage_store<SEM, SILU>(st, lds, dg, B, kn, pass, clamp);
     }
 }
 
@@ -393,7 +470,7 @@ __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
         const int kn = min(KT, kused - k0);
         if (k0) __syncthreads();
         x_stage<SILU> xst;
-        stage_digits<SEM, SILU>(xst, false, xl, dg, x, xu, a.ldx, B, k0, kn);
+        stage_digits<SEM, SILU>(xst, false, xl, dg, x, xu, a.ldx, B, k0, kn, !a.silu_noclamp);
         __syncthreads();
         const int c_end = (k0 + kn) / BE * CPB;
         for (int c = k0 / BE * CPB + sl; c < c_end; c += LPR) {
@@ -409,7 +486,8 @@ __global__ __launch_bounds__(256) void k_gemv(mllm_gemv_args a)
         for (int b = 0; b < BM; b++) {
             const float v = group_sum<LPR>(acc[r][b]);
             const int row = row0 + r;
-            if (sl == 0 && row < a.n_rows && b < B) out[(long)b * a.ldo + row] = v;
+            if (sl == 0 && row < a.n_rows && b < B)
+                out[(long)b * a.ldo + row] = a.out_add ? a.out_add[(long)b * a.ldo + row] + v : v;
         }
     }
 }
@@ -501,7 +579,7 @@ MLLM_DEV void q8f_load(q8f_stage &st, const float *__restrict__ x, const float *
 }
 
 MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT, int tstride, int qstride, int kn,
-                        int pass)
+                        int pass, bool clamp = true)
 {
     const int nq = kn >> 3, i = threadIdx.x + 256 * pass;
     if (i >= B * nq) return;           // B * nq is a multiple of 4: a block's four lanes take the same path
@@ -510,7 +588,7 @@ MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT
     if (silu) {
         const float u[8] = {st.u[0].x, st.u[0].y, st.u[0].z, st.u[0].w, st.u[1].x, st.u[1].y, st.u[1].z, st.u[1].w};
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = mllm_silu_mul(v[k], u[k]);
+        for (int k = 0; k < 8; k++) v[k] = mllm_silu_mul(v[k], u[k], clamp);
     }
     float amax = 0.0f;
 #pragma unroll
@@ -586,7 +664,7 @@ __global__ __launch_bounds__(256) void k_gemv_q8(mllm_gemv_args a)
             for (int pass = 0; pass * 256 < B * (kn >> 3); pass++) {
                 q8f_stage qs;
                 q8f_load(qs, xf, xuf, a.ldx, B, k0, kn, pass);
-                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kn, pass);
+                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kn, pass, !a.silu_noclamp);
             }
         }
         __syncthreads();
@@ -604,7 +682,8 @@ __global__ __launch_bounds__(256) void k_gemv_q8(mllm_gemv_args a)
         for (int b = 0; b < BM; b++) {
             const float v = group_sum<LPR>(acc[r][b]);
             const int row = row0 + r;
-            if (sl == 0 && row < a.n_rows && b < B) out[(long)b * a.ldo + row] = v;
+            if (sl == 0 && row < a.n_rows && b < B)
+                out[(long)b * a.ldo + row] = a.out_add ? a.out_add[(long)b * a.ldo + row] + v : v;
         }
     }
 }
@@ -620,15 +699,40 @@ template <int SEM, bool Q8> struct gemv_geom {
     static constexpr int CPB = Q8 ? q8_traits<SEM>::kChunksPerBlock : sem_traits<SEM>::kChunksPerBlock;
 };
 
-template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU>
+// FUSE bits of the persistent kernel (mllm_gemv_args): kFusePro = the
+// residual / RMS-norm prologue; kFusePair = paired rows with the SiLU product
+// in the epilogue: output row o is silu(row o . x) * (row o' . x), row o' the
+// "up" row o + n_rows of the same matrix, or row o of table2's matrix in a
+// job launch (the gate/up pair of an MoE expert).
+constexpr int kFusePro = 1, kFusePair = 2;
+
+template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU, int FUSE>
 __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 {
     static_assert(!(Q8 && SILU), "the SiLU product of Q8_0 activations is formed by the quantiser");
+    static_assert(!(SILU && FUSE), "the SiLU staging and the fusions are exclusive");
+    constexpr bool PRO = (FUSE & kFusePro) != 0, PAIR = (FUSE & kFusePair) != 0;
+    static_assert(!PAIR || R % 2 == 0, "paired rows need an even row count per lane group");
     extern __shared__ float xl[];
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
-    constexpr int RPW = (64 / LPR) * R;                 // rows per wave and step
+    constexpr int HR = PAIR ? R / 2 : R;               // output rows per lane group and step
+    constexpr int OPW = (64 / LPR) * HR;               // output rows per wave and step
     const job_view jv = view_job(a, blockIdx.y);
     const mllm_packed W = jv.W;
+    // the "up" rows of a pair: table2's matrix of the job's expert, else the same matrix n_rows further
+    mllm_packed W2 = W;
+    int up_off = a.n_rows;
+    if constexpr (PAIR) {
+        if (a.table2) {
+            typedef const __attribute__((address_space(4))) int cint;
+            typedef const __attribute__((address_space(4))) uint64_t cu64;
+            const int e = a.idx ? *(cint *)(a.idx + blockIdx.y) : (int)blockIdx.y;
+            cu64 *tp = (cu64 *)(a.table2 + (e < 0 ? 0 : e));
+#pragma unroll
+            for (int i = 0; i < MLLM_MAX_PLANES; i++) W2.p[i] = (const uint8_t *)tp[i];
+            up_off = 0;
+        }
+    }
     float *__restrict__ out = jv.out;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -636,7 +740,8 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     const int nb = a.n_cols / BE, kused = nb * BE, nch = nb * CPB;
     const int iters = (nch + LPR - 1) / LPR;
     if (iters == 0) return;   // no whole block per row: the launcher writes zeros instead of launching this
-    const int nrg = (a.n_rows + RPW - 1) / RPW;
+    const int n_out = a.n_rows;
+    const int nrg = (n_out + OPW - 1) / OPW;
     const int wstride = gridDim.x * 4;
     const int rg0 = blockIdx.x * 4 + wave;
     const int B = a.B;
@@ -646,13 +751,18 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     const int qstride = KT + (KT >> 4), tstride = qstride / 4 + 2 * (KT / 32);
 
     // A step is (row group rg, chunk pass it); the next step advances it, then rg.
+    // Lane group rows: outputs o0 .. o0+HR-1; with PAIR, slots HR.. hold their up rows.
     auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) __attribute__((always_inline)) {
         const int c = min(it * LPR + sl, nch - 1);
-        const int r0 = rg * RPW + grp * R;
+        const int o0 = rg * OPW + grp * HR;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            if constexpr (Q8) q8_fetch<SEM>(W, nb, min(r0 + r, a.n_rows - 1), c, buf[r]);
-            else fetch<SEM>(W, nb, min(r0 + r, a.n_rows - 1), c, buf[r]);
+            const int o = min(o0 + (r % HR), n_out - 1);
+            const bool up = PAIR && r >= HR;
+            const mllm_packed &M = up ? W2 : W;
+            const int row = up ? o + up_off : o;
+            if constexpr (Q8) q8_fetch<SEM>(M, nb, row, c, buf[r]);
+            else fetch<SEM>(M, nb, row, c, buf[r]);
         }
     };
     float acc[R][BM];
@@ -676,14 +786,22 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 #pragma unroll
             for (int b = 0; b < BM; b++) acc[r][b] += live ? part[r][b] : 0.0f;
         if (it == iters - 1) {
-            const int r0 = rg * RPW + grp * R;
+            const int o0 = rg * OPW + grp * HR;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
+            for (int r = 0; r < HR; r++) {
 #pragma unroll
                 for (int b = 0; b < BM; b++) {
-                    const float v = group_sum<LPR>(acc[r][b]);
+                    float v = group_sum<LPR>(acc[r][b]);
                     acc[r][b] = 0.0f;
-                    if (sl == 0 && r0 + r < a.n_rows && b < B) out[(long)b * a.ldo + r0 + r] = v;
+                    if constexpr (PAIR) {
+                        const float u = group_sum<LPR>(acc[r + HR][b]);
+                        acc[r + HR][b] = 0.0f;
+                        v = mllm_silu_mul(v, u, !a.silu_noclamp);
+                    }
+                    if (sl == 0 && o0 + r < n_out && b < B) {
+                        const long o = (long)b * a.ldo + o0 + r;
+                        out[o] = a.out_add ? a.out_add[o] + v : v;
+                    }
                 }
             }
         }
@@ -697,7 +815,110 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     // for the older buffer instead of draining all loads.
     raw_chunk bufA[R], bufB[R];
     int rg = rg0, it = 0;
-    if constexpr (Q8) {
+    if constexpr (PRO) {
+        // residual / RMS-norm prologue (single-matrix launches).  LDS past the
+        // staged activation holds the reduction.
+        float *red = xl + a.pro_lds / 4;
+        const float *x0 = a.x;
+        const bool writer = a.res_out && blockIdx.x == 0;
+        if constexpr (!Q8) {
+            x_stage<false> xst;
+            const int nh = kused >> 3;
+            if (B == 1 && a.n_cols == kused && nh <= 512) {
+                // one token, whole row in two slots: x, residual and weight
+                // loaded once; the sum of squares reduced from registers
+                stage_load<false>(xst, x0, nullptr, a.ldx, 1, 0, kused, 0);
+                float4 rr[2][2], ww[2][2];
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    if (256 * q >= nh) break;
+                    const int k = 8 * min(256 * q + (int)threadIdx.x, nh - 1);
+                    if (a.x_res) { rr[q][0] = gld<float4>(a.x_res + k); rr[q][1] = gld<float4>(a.x_res + k + 4); }
+                    if (a.rms_w) { ww[q][0] = gld<float4>(a.rms_w + k); ww[q][1] = gld<float4>(a.rms_w + k + 4); }
+                }
+                fetch_step(min(rg, nrg - 1), it, bufA);
+                float ss = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int idx = 256 * q + threadIdx.x;
+                    if (256 * q >= nh || idx >= nh) continue;
+                    float v[8];
+                    f4x2_to8(xst.v[q], v);
+                    if (a.x_res) {
+                        float r[8];
+                        f4x2_to8(rr[q], r);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] += r[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ss = fmaf(v[e], v[e], ss);
+                    f8_to4x2(v, xst.v[q]);
+                    if (writer) {
+                        *reinterpret_cast<float4 *>(a.res_out + 8 * idx) = xst.v[q][0];
+                        *reinterpret_cast<float4 *>(a.res_out + 8 * idx + 4) = xst.v[q][1];
+                    }
+                }
+                if (a.rms_w) {
+                    ss = group_sum<64>(ss);
+                    if (lane == 0) red[wave] = ss;
+                    __syncthreads();
+                    const float t = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.n_cols + a.rms_eps);
+                    const float sc = a.rms_div ? t : 1.0f / t;
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        if (256 * q >= nh) break;
+                        float v[8], w[8];
+                        f4x2_to8(xst.v[q], v);
+                        f4x2_to8(ww[q], w);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] = (a.rms_div ? v[e] / sc : v[e] * sc) * w[e];
+                        f8_to4x2(v, xst.v[q]);
+                    }
+                }
+                stage_store<SEM, false>(xst, reinterpret_cast<uint8_t *>(xl), dg, 1, kused, 0, true);
+            } else {
+                // any B: a first pass reduces the sum of squares, the staging
+                // pass then applies the residual and the norm
+                float *sc = red + 32;
+                fetch_step(min(rg, nrg - 1), it, bufA);
+                prologue_reduce(a, B, red, sc);
+                const int passes = (B * nh + 256 * kStageSlots - 1) / (256 * kStageSlots);
+                for (int pass = 0; pass < passes; pass++) {
+                    stage_load<false>(xst, x0, nullptr, a.ldx, B, 0, kused, pass);
+#pragma unroll
+                    for (int q = 0; q < kStageSlots; q++) {
+                        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
+                        if (idx >= B * nh) continue;
+                        const int b = idx / nh, h = idx - b * nh;
+                        float v[8];
+                        f4x2_to8(xst.v[q], v);
+                        prologue_apply8(v, a, sc[b], b, 8 * h);
+                        f8_to4x2(v, xst.v[q]);
+                    }
+                    stage_store<SEM, false>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true);
+                }
+            }
+        } else {
+            // Q8_0 activations quantised here, from the prologue's activation
+            float *sc = red + 32;
+            fetch_step(min(rg, nrg - 1), it, bufA);
+            prologue_reduce(a, B, red, sc);
+            const int nq = kused >> 3;
+            for (int pass = 0; pass * 256 < B * nq; pass++) {
+                q8f_stage qs;
+                q8f_load(qs, x0, nullptr, a.ldx, B, 0, kused, pass);
+                const int i = threadIdx.x + 256 * pass;
+                if (i < B * nq) {
+                    const int b = i / nq, e = (i - b * nq) << 3;
+                    float v[8];
+                    f4x2_to8(qs.v, v);
+                    prologue_apply8(v, a, sc[b], b, e);
+                    f8_to4x2(v, qs.v);
+                }
+                q8f_store(qs, false, xl, B, KT, tstride, qstride, kused, pass);
+            }
+        }
+    } else if constexpr (Q8) {
         if (a.xq.q) {
             fetch_step(min(rg, nrg - 1), it, bufA);
             stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride,
@@ -710,7 +931,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, 0);
             fetch_step(min(rg, nrg - 1), it, bufA);
             for (int pass = 0;;) {
-                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass);
+                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass, !a.silu_noclamp);
                 if (++pass * 256 >= B * (kused >> 3)) break;
                 q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, pass);
             }
@@ -722,7 +943,8 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
         const float *xuj = SILU ? a.x_up + jv.xj * a.x_job_stride : nullptr;
         stage_load<SILU>(xst, xj, xuj, a.ldx, B, 0, kused, 0);
         fetch_step(min(rg, nrg - 1), it, bufA);
-        stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused);
+        stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
+                                !a.silu_noclamp);
     }
     __syncthreads();
     if (rg >= nrg) return;
@@ -765,7 +987,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(mllm_gemv_args a)
 #pragma unroll
     for (int b = 0; b < BM; b++) {
         float v = group_sum<64>(acc[b]);
-        if (lane == 0 && b < a.B) out[(long)b * a.ldo + row] = v;
+        if (lane == 0 && b < a.B) out[(long)b * a.ldo + row] = a.out_add ? a.out_add[(long)b * a.ldo + row] + v : v;
     }
 }
 
@@ -822,7 +1044,7 @@ constexpr size_t kPersistentLds = 72 * 1024;
 template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU>
 void launch_lpr(bool persistent, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
 {
-    if (persistent) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, LPR, SILU>), grid, dim3(256), lds, st, a);
+    if (persistent) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, LPR, SILU, 0>), grid, dim3(256), lds, st, a);
     else if constexpr (Q8) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, LPR>), grid, dim3(256), lds, st, a);
     else hipLaunchKernelGGL((k_gemv<SEM, BM, R, LPR, SILU>), grid, dim3(256), lds, st, a);
 }
@@ -845,21 +1067,20 @@ void launch_shape(bool persistent, int lpr, dim3 grid, size_t lds, const mllm_ge
     else launch_lpr<SEM, Q8, BM, R, 16, false>(persistent, grid, lds, a, st);
 }
 
-template <int SEM, int BM>
-void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
+// Lanes per row of a launch: at batch 1, 16 lanes per row up to ~1.8 KB of
+// row bytes and 32 up to ~5 KB, measured fastest on MI355X across the
+// TinyLlama/GPT-OSS shapes, widened on short matrices until the launch has
+// about two workgroups per CU; larger batches reuse each chunk's decode over
+// R rows x B tokens.  HR = output rows per lane group.
+template <int SEM, bool Q8, int BM>
+int pick_lpr(const mllm_gemv_args &a, int n_jobs, int HR)
 {
-    constexpr bool Q8 = mllm_sem_uses_q8(SEM);
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
     const int kused = a.n_cols / BE * BE;
     const int nch = kused / BE * CPB;
-    // Batch 1: one row per lane group, 16 lanes per row up to ~1.8 KB of row
-    // bytes and 32 up to ~5 KB, measured fastest on MI355X across the
-    // TinyLlama/GPT-OSS shapes; larger batches reuse each chunk's decode over
-    // R rows x B tokens.
-    constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
     auto waste = [&](int lpr) { int it = (nch + lpr - 1) / lpr; return (double)(it * lpr - nch) / (it * lpr); };
     int lpr = 64;
-    auto wgs_at = [&](int l) { const int rpw = 4 * (64 / l) * R; return (long)(a.n_rows + rpw - 1) / rpw * n_jobs; };
+    auto wgs_at = [&](int l) { const int rpw = 4 * (64 / l) * HR; return (long)(a.n_rows + rpw - 1) / rpw * n_jobs; };
     if (BM == 1) {
         const long row_bytes = (long)kused / 32 * sem_traits<SEM>::kBytesPer32;
         lpr = row_bytes <= 1800 ? 16 : row_bytes <= 5000 ? 32 : 64;
@@ -874,10 +1095,22 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
         if (nch < 64 || waste(64) > waste(32) + 0.05 || wgs_at(32) >= 2L * device_cus()) lpr = 32;
         if (nch < 32 || (lpr == 32 && waste(32) > waste(16) + 0.05)) lpr = 16;
     }
+    return lpr;
+}
+
+template <int SEM, int BM>
+void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
+{
+    constexpr bool Q8 = mllm_sem_uses_q8(SEM);
+    constexpr int BE = gemv_geom<SEM, Q8>::BE;
+    const int kused = a.n_cols / BE * BE;
+    constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
+    const int lpr = pick_lpr<SEM, Q8, BM>(a, n_jobs, R);
     const int rows_per_wg = 4 * (64 / lpr) * R;
     const int wg_needed = (a.n_rows + rows_per_wg - 1) / rows_per_wg;
 
-    // whole-K staging for the persistent kernel
+    // whole-K staging for the persistent kernel (+ the prologue's reduction
+    // scratch and scales past it)
     const int ktp = (kused + 255) / 256 * 256;
     const size_t lds_p = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
     if (lds_p <= kPersistentLds) {
@@ -896,6 +1129,71 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     launch_shape<SEM, Q8, BM, R>(false, lpr, dim3(wg_needed, n_jobs), lds, a, st);
 }
 
+// LDS bytes the persistent kernel stages for whole K at batch BM (the
+// launcher takes it when they fit kPersistentLds), with the prologue scratch.
+inline size_t persistent_lds(bool q8, int block_elems, int n_cols, int BM, bool prologue)
+{
+    const int kused = n_cols / block_elems * block_elems;
+    const int ktp = (kused + 255) / 256 * 256;
+    size_t l = q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
+    if (prologue) l = (l + 15) / 16 * 16 + 256;
+    return l;
+}
+
+// The fused persistent kernel (prologue and / or paired rows; the caller has
+// checked that the whole activation fits the kernel's LDS).  Paired rows run
+// at batch 1 only; the fused launches take 32 or 64 lanes per row at B > 1.
+template <int SEM, bool Q8, int BM, int R, int FUSE>
+void launch_fused_lpr(int lpr, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
+{
+    if (lpr == 64) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64, false, FUSE>), grid, dim3(256), lds, st, a);
+    else if (lpr == 32 || BM > 1) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 32, false, FUSE>), grid, dim3(256), lds, st, a);
+    else if constexpr (BM == 1) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 16, false, FUSE>), grid, dim3(256), lds, st, a);
+}
+
+template <int SEM, int BM>
+hipError_t launch_fused(mllm_gemv_args a, int n_jobs, hipStream_t st)
+{
+    constexpr bool Q8 = mllm_sem_uses_q8(SEM);
+    const bool pro = mllm_has_prologue(a), pair = a.silu_pair != 0;
+    if (pair && BM != 1) return hipErrorInvalidValue;
+    constexpr int BE = gemv_geom<SEM, Q8>::BE;
+    const int kused = a.n_cols / BE * BE;
+    const int ktp = (kused + 255) / 256 * 256;
+    size_t lds = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
+    if (pro) {
+        lds = (lds + 15) / 16 * 16;
+        a.pro_lds = (int)lds;
+        lds += 256;
+    }
+    if (lds > kPersistentLds) return hipErrorInvalidValue;
+    constexpr int R = (BM == 1) ? 2 : (BM == 2) ? 4 : 2;   // paired rows: one gate and one up row at B=1
+    const int HR = pair ? 1 : (BM == 1 ? 1 : R);
+    int lpr = pick_lpr<SEM, Q8, BM>(a, n_jobs, HR);
+    if (BM > 1 && lpr < 32) lpr = 32;
+    const int outs_per_wg = 4 * (64 / lpr) * HR;
+    const int wg_needed = (a.n_rows + outs_per_wg - 1) / outs_per_wg;
+    const int per_cu = lds <= 40 * 1024 ? 3 : 2;
+    const dim3 grid(std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs))), n_jobs);
+    if constexpr (BM == 1) {
+        if (pair && pro) launch_fused_lpr<SEM, Q8, 1, 2, kFusePro | kFusePair>(lpr, grid, lds, a, st);
+        else if (pair) launch_fused_lpr<SEM, Q8, 1, 2, kFusePair>(lpr, grid, lds, a, st);
+        else launch_fused_lpr<SEM, Q8, 1, 1, kFusePro>(lpr, grid, lds, a, st);
+    } else {
+        launch_fused_lpr<SEM, Q8, BM, R, kFusePro>(lpr, grid, lds, a, st);
+    }
+    return hipGetLastError();
+}
+
+template <int SEM>
+hipError_t launch_fused_any_b(const mllm_gemv_args &a, int n_jobs, hipStream_t st)
+{
+    if (a.B == 1) return launch_fused<SEM, 1>(a, n_jobs, st);
+    if (a.B == 2) return launch_fused<SEM, 2>(a, n_jobs, st);
+    if (a.B <= 4) return launch_fused<SEM, 4>(a, n_jobs, st);
+    return launch_fused<SEM, 8>(a, n_jobs, st);
+}
+
 // Launch the GEMV of one semantic for B = a.B (1..8).
 template <int SEM>
 void launch_sem_any_b(const mllm_gemv_args &a, int n_jobs, hipStream_t st)
@@ -906,14 +1204,20 @@ void launch_sem_any_b(const mllm_gemv_args &a, int n_jobs, hipStream_t st)
     else launch_sem<SEM, 8>(a, n_jobs, st);
 }
 
-// Per-semantic entry points, defined in gemv_*.hip.
+// Per-semantic entry points, defined in gemv_*.hip (fused forms in gemv_f*.hip).
 template <int SEM> void gemv_sem(const mllm_gemv_args &a, int n_jobs, hipStream_t st);
+template <int SEM> hipError_t gemv_fused_sem(const mllm_gemv_args &a, int n_jobs, hipStream_t st);
 template <int SEM> hipError_t dequant_sem(const mllm_packed &W, int n_rows, int n_cols, float *out, hipStream_t st);
 
 #define MLLM_GEMV_INSTANTIATE(SEM)                                                                   \
     template <> void gemv_sem<SEM>(const mllm_gemv_args &a, int n_jobs, hipStream_t st)              \
     {                                                                                                \
         launch_sem_any_b<SEM>(a, n_jobs, st);                                                        \
+    }
+#define MLLM_GEMV_FUSED_INSTANTIATE(SEM)                                                             \
+    template <> hipError_t gemv_fused_sem<SEM>(const mllm_gemv_args &a, int n_jobs, hipStream_t st)  \
+    {                                                                                                \
+        return launch_fused_any_b<SEM>(a, n_jobs, st);                                               \
     }
 #define MLLM_DEQUANT_INSTANTIATE(SEM)                                                                \
     template <> hipError_t dequant_sem<SEM>(const mllm_packed &W, int n_rows, int n_cols, float *out, \

@@ -736,6 +736,59 @@ __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict_
     h[i] = clamp ? mllm_silu_mul(gv, u[i]) : (gv / (1.0f + expf(-gv))) * u[i];
 }
 
+// The activation of a fused GEMV formed on its own, for launches the fused
+// prologue does not take (see mllm_gemv_args): one workgroup per token b,
+// v = x + x_res, res_out = v, RMS norm with rms_w, or silu(x) * x_up.
+__global__ __launch_bounds__(256) void k_act_prologue(const float *__restrict__ x, const float *__restrict__ x_res,
+                                                      float *__restrict__ res_out, const float *__restrict__ rms_w,
+                                                      float eps, int div, const float *__restrict__ x_up, int clamp,
+                                                      int n, int ldx, float *__restrict__ out)
+{
+    __shared__ float red[4];
+    const long xo = (long)blockIdx.x * ldx, o = (long)blockIdx.x * n;
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+    for (int i = tid; i < n; i += 256) {
+        float v = x[xo + i];
+        if (x_up) v = mllm_silu_mul(v, x_up[xo + i], clamp != 0);
+        if (x_res) v += x_res[xo + i];
+        if (res_out) res_out[xo + i] = v;
+        ss = fmaf(v, v, ss);
+        out[o + i] = v;
+    }
+    if (!rms_w) return;
+    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float r = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
+    const float sc = div ? r : 1.0f / r;
+    for (int i = tid; i < n; i += 256) {
+        const float v = out[o + i];       // written by this same thread above
+        out[o + i] = (div ? v / sc : v * sc) * rms_w[i];
+    }
+}
+
+// out[b][r] = silu(y[b][r]) * y[b][n + r] (+ add[b][r]) for the stacked
+// gate/up rows of a paired GEMV that ran unfused (y: [B][2n]).
+__global__ void k_silu_pair(const float *__restrict__ y, int B, int n, int clamp, float *__restrict__ out,
+                            const float *__restrict__ add)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
+    if (r >= n || b >= B) return;
+    const float *yb = y + (long)b * 2 * n;
+    const float v = mllm_silu_mul(yb[r], yb[n + r], clamp != 0);
+    const long o = (long)b * n + r;
+    out[o] = add ? add[o] + v : v;
+}
+
+
+// out[i] += add[i], i < n (the residual epilogue of launches that cannot fuse it).
+__global__ void k_add(float *__restrict__ out, const float *__restrict__ add, long n)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] += add[i];
+}
+
 __global__ void k_combine(const float *__restrict__ d, const float *__restrict__ w, const int *__restrict__ idx,
                           int K, int N, float *__restrict__ out, int fused)
 {
@@ -894,6 +947,56 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
     while (G > 1 && (T + 4 * G - 1) / (4 * G) < kRouteMinGroups) G >>= 1;
     return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}, G,
               E, -1);
+}
+
+hipError_t mllm_launch_act_prologue(const float *x, const float *x_res, float *res_out, const float *rms_w, float eps,
+                                    int div, const float *x_up, int clamp, int T, int n, int ldx, float *out,
+                                    hipStream_t st)
+{
+    if (T <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_act_prologue, dim3(T), dim3(256), 0, st, x, x_res, res_out, rms_w, eps, div, x_up, clamp, n,
+                       ldx, out);
+    return hipGetLastError();
+}
+
+// Plain streaming read: two 16-byte loads in flight per lane, each word once.
+__global__ __launch_bounds__(256) void k_read_probe(const uint4 *__restrict__ p, long n16, uint4 *__restrict__ sink)
+{
+    const long G = (long)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += 2 * G) {
+        const uint4 a = p[i];
+        const uint4 b = i + G < n16 ? p[i + G] : make_uint4(0, 0, 0, 0);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = make_uint4(acc, acc, acc, acc);
+}
+
+hipError_t mllm_launch_read_probe(const void *p, long bytes, void *sink, hipStream_t st)
+{
+    const long n16 = bytes / 16;
+    if (n16 <= 0) return hipSuccess;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    long g = std::min<long>(4L * cus, (n16 + 511) / 512);
+    hipLaunchKernelGGL(k_read_probe, dim3((unsigned)std::max<long>(1, g)), dim3(256), 0, st, (const uint4 *)p, n16,
+                       (uint4 *)sink);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_silu_pair(const float *y, int B, int n, int clamp, float *out, const float *add, hipStream_t st)
+{
+    if (B <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu_pair, dim3((n + 255) / 256, B), dim3(256), 0, st, y, B, n, clamp, out, add);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_add(float *out, const float *add, long n, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, add, n);
+    return hipGetLastError();
 }
 
 hipError_t mllm_launch_silu_mul(const float *g, const float *u, float *h, long n, int clamp, hipStream_t st)

@@ -40,6 +40,12 @@ def build(verbose=False):
         raise RuntimeError("libmllm_gpu build failed:\n" + (r.stdout or "") + (r.stderr or ""))
 
 
+class GemvFusion(ctypes.Structure):
+    """mllm_gemv_fusion (include/mllm.h): the prologue/epilogue fused into a decode GEMV."""
+    _fields_ = [("x_up", cvp), ("silu_clamp", ci), ("x_res", cvp), ("res_out", cvp), ("rms_w", cvp),
+                ("rms_eps", ctypes.c_float), ("rms_div", ci), ("out_add", cvp), ("x_ld", ci), ("silu_pair", ci)]
+
+
 _LIB = None
 
 
@@ -106,6 +112,12 @@ def load_kernels(path=LIB_PATH):
     so.mllm_gemv_workspace_size.restype = ctypes.c_long
     so.mllm_gemv.argtypes = [ci, cvp, cvp, cvp, ci, ci, ci, cvp, cvp]
     so.mllm_gemv.restype = ci
+    so.mllm_gemv_fused_workspace_size.argtypes = [ci, ci, ci, ci, ctypes.POINTER(GemvFusion)]
+    so.mllm_gemv_fused_workspace_size.restype = ctypes.c_long
+    so.mllm_gemv_fused.argtypes = [ci, cvp, cvp, cvp, ci, ci, ci, ctypes.POINTER(GemvFusion), cvp, cvp]
+    so.mllm_gemv_fused.restype = ci
+    so.mllm_read_probe.argtypes = [cvp, ctypes.c_long, cvp, cvp]
+    so.mllm_read_probe.restype = ci
     so.mllm_quantize_q8_0.argtypes = [cvp, ci, ci, cvp, cvp]
     so.mllm_quantize_q8_0.restype = ci
     so.mllm_router_packed_size.argtypes = [ci, ci]
@@ -178,6 +190,31 @@ class DeviceOps:
             ws = self.workspace(sem, n_cols, B, x.device, n_rows)
         self._check(self.so.mllm_gemv(sem, packed.data_ptr(), x.data_ptr(), out.data_ptr(), n_rows, n_cols, B,
                                       ws.data_ptr() if ws is not None else None, self._stream()), "mllm_gemv")
+        return out
+
+    def fusion(self, x_up=None, silu_clamp=True, x_res=None, res_out=None, rms_w=None, rms_eps=1e-6, rms_div=False,
+               out_add=None, x_ld=0, silu_pair=False):
+        """An mllm_gemv_fusion over torch tensors or device addresses (None = field unused)."""
+        p = lambda t: (t if isinstance(t, int) else t.data_ptr()) if t is not None else None  # noqa: E731
+        return GemvFusion(p(x_up), int(silu_clamp), p(x_res), p(res_out), p(rms_w), float(rms_eps), int(rms_div),
+                          p(out_add), int(x_ld), int(silu_pair))
+
+    def gemv_fused(self, sem, packed, x, n_rows, n_cols, fusion, out=None, ws=None, B=None):
+        """mllm_gemv_fused: y = W * prologue(x) (+ out_add), one launch where it fits.
+        x: a tensor, or a device address with B given (a strided view inside a wider row)."""
+        torch = self.torch
+        if B is None:
+            B = x.numel() // n_cols
+        xp = x if isinstance(x, int) else x.data_ptr()
+        dev = torch.device("cuda")
+        if out is None:
+            out = torch.empty((B, n_rows), dtype=torch.float32, device=dev)
+        if ws is None:
+            n = self.so.mllm_gemv_fused_workspace_size(sem, n_rows, n_cols, B, ctypes.byref(fusion))
+            ws = torch.empty(max(n, 256), dtype=torch.uint8, device=dev) if n > 0 else None
+        self._check(self.so.mllm_gemv_fused(sem, packed.data_ptr(), xp, out.data_ptr(), n_rows, n_cols, B,
+                                            ctypes.byref(fusion), ws.data_ptr() if ws is not None else None,
+                                            self._stream()), "mllm_gemv_fused")
         return out
 
     def quantize_q8_0(self, x, n_cols):

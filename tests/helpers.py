@@ -1,32 +1,9 @@
 """Shared test helpers: the BC struct view moe_ffn reads, and tolerances."""
 import ctypes
 
-import numpy as np
+import numpy as np  # noqa: F401
 
-# moe_ffn reads these BC fields (x86-64 offsets of the engine's struct, CE:536-589).
-BC_SIZE, BC_N, BC_NE, BC_NK, BC_M = 736, 4, 224, 228, 232
-BC_ROUTER, BC_GATE, BC_UP, BC_DOWN, BC_QG, BC_QU, BC_QD = 240, 248, 256, 264, 272, 276, 280
-
-
-class BCView:
-    """A zeroed BC-sized buffer with the moe_ffn fields of layer 0 filled in."""
-
-    def __init__(self, N, E, K, M, router, gate, upw, down, qts):
-        self.buf = (ctypes.c_uint64 * (BC_SIZE // 8))()
-        base = ctypes.addressof(self.buf)
-        self.keep = [router, gate, upw, down]
-        self.pr = (ctypes.c_void_p * 1)(router.ctypes.data)
-        self.pg = (ctypes.c_void_p * 1)(gate.ctypes.data)
-        self.pu = (ctypes.c_void_p * 1)(upw.ctypes.data)
-        self.pd = (ctypes.c_void_p * 1)(down.ctypes.data)
-        for off, v in ((BC_N, N), (BC_NE, E), (BC_NK, K), (BC_M, M),
-                       (BC_QG, qts[0]), (BC_QU, qts[1]), (BC_QD, qts[2])):
-            ctypes.c_int.from_address(base + off).value = v
-        for off, p in ((BC_ROUTER, self.pr), (BC_GATE, self.pg), (BC_UP, self.pu), (BC_DOWN, self.pd)):
-            ctypes.c_void_p.from_address(base + off).value = ctypes.addressof(p)
-
-    def ptr(self):
-        return ctypes.addressof(self.buf)
+from mojollama_amd.workloads import BCView  # noqa: E402,F401  (the BC struct moe_ffn reads)
 
 
 # Normalised max error bound (max|got - ref| / max|ref|) per semantic for the

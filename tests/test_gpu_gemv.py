@@ -240,3 +240,38 @@ def test_short_rows_give_zeros(lib, qt, nc):
     name = {8: "q8_0", 12: "q4_k", 14: "q6_k", 39: "mxfp4", 2: "q4_0", 13: "q5_k"}[qt]
     for B in (1, 5, 12):          # B = 12 would take the MFMA GEMM with whole blocks
         assert np.all(bmm(lib, name, w, x[:B], 4, nc, B) == 0.0)
+
+
+@pytest.mark.parametrize("qt", [12, 14, 8, 39])
+def test_batch_qkv_gate_up_one_launch(lib, orc, qt):
+    """batch_qkv_omp / batch_gate_up_omp with matrices of one type (stacked into
+    one packed matrix, one GEMV launch) at the TinyLlama shapes, against the
+    oracle's row-path semantics (QK:1095-1222); rewriting a matrix in place
+    re-packs the stack."""
+    rng = np.random.default_rng(400 + qt)
+    C = 2048
+    Wq, Wk, Wv = (W.gen_weights(rng, qt, r, C) for r in (2048, 256, 256))
+    x = W.gen_x(rng, 1, C)[0]
+    sem = orc.sem_for(2, qt)
+    for step in range(2):
+        oq, ok, ov = (np.full(r, np.nan, np.float32) for r in (2048, 256, 256))
+        lib.batch_qkv_omp(up(Wq), up(Wk), up(Wv), fp(x), fp(oq), fp(ok), fp(ov), 2048, 256, 256, C, qt, qt, qt)
+        for got, w, r in ((oq, Wq, 2048), (ok, Wk, 256), (ov, Wv, 256)):
+            assert O.norm_err(got, orc.gemv(sem, w, x, r, C, 1)[0]) < GEMV_TOL, (step, r)
+        Wk[:] = W.gen_weights(rng, qt, 256, C)   # same buffer, new contents
+    Wg, Wu = (W.gen_weights(rng, qt, 5632, C) for _ in range(2))
+    og, ou = np.full(5632, np.nan, np.float32), np.full(5632, np.nan, np.float32)
+    lib.batch_gate_up_omp(up(Wg), up(Wu), fp(x), fp(og), fp(ou), 5632, 5632, C, qt, qt)
+    assert O.norm_err(og, orc.gemv(sem, Wg, x, 5632, C, 1)[0]) < GEMV_TOL
+    assert O.norm_err(ou, orc.gemv(sem, Wu, x, 5632, C, 1)[0]) < GEMV_TOL
+
+
+def test_batch_qkv_unknown_type_leaves_output(lib, orc):
+    rng = np.random.default_rng(5)
+    C = 512
+    Wq, Wv = W.gen_weights(rng, 12, 32, C), W.gen_weights(rng, 12, 16, C)
+    x = W.gen_x(rng, 1, C)[0]
+    oq, ok, ov = np.full(32, np.nan, np.float32), np.full(16, 7.0, np.float32), np.full(16, np.nan, np.float32)
+    lib.batch_qkv_omp(up(Wq), up(Wq), up(Wv), fp(x), fp(oq), fp(ok), fp(ov), 32, 16, 16, C, 12, 7, 12)
+    assert np.all(ok == 7.0)
+    assert O.norm_err(ov, orc.gemv(orc.sem_for(2, 12), Wv, x, 16, C, 1)[0]) < GEMV_TOL

@@ -436,13 +436,14 @@ def bench_moe(torch, dev, args, tag, sizes=(1, 1280)):
     need = sorted(set(int(e) for e in idx_h.ravel()))
     host = {e: (gates[e].cpu().numpy(), ups[e].cpu().numpy(), downs[e].cpu().numpy()) for e in need}
     dummy = host[need[0]]
-    ptrs = [[host.get(e, dummy)[i] for e in range(E)] for i in range(3)]
+    call = MoECall([[host.get(e, dummy)[i] for e in range(E)] for i in range(3)], M, N, qts, Kk)
+    call.prepare(x_np[:n_tok], idx_h, w_h)
     for t in range(n_tok):
-        moe_forward_call(dev.so, ptrs, x_np[t], M, N, qts, idx_h[t], w_h[t])     # first calls upload the experts
+        call(dev.so, t)     # first calls upload the experts
     ts = []
     for t in range(n_tok):
         s0 = time.perf_counter()
-        moe_forward_call(dev.so, ptrs, x_np[t], M, N, qts, idx_h[t], w_h[t])
+        call(dev.so, t)
         ts.append(time.perf_counter() - s0)
     res["host_abi_moe_forward_omp_us"] = round(float(np.median(ts)) * 1e6, 1)
     log(f"host-ABI moe_forward_omp ({tag}): {res['host_abi_moe_forward_omp_us']} us per call")
@@ -451,21 +452,34 @@ def bench_moe(torch, dev, args, tag, sizes=(1, 1280)):
     return res
 
 
-def moe_forward_call(lib, ptrs, x, M, N, qts, ti, tw):
-    """moe_forward_omp (QK:2066) through a library's host ABI, with the scratch
-    sizes of the reference's caller (TE:954-960)."""
-    E, Kk = len(ptrs[0]), len(ti)
-    arr = ctypes.POINTER(ctypes.c_uint8) * E
-    pg, pu, pd = (arr(*[a.ctypes.data_as(K.cu) for a in lst]) for lst in ptrs)
-    comb = np.zeros(N, np.float32)
-    buf = np.zeros(3 * Kk * M, np.float32)
-    q8 = np.zeros(Kk * M * 34 // 32 + 64, np.uint8)
-    ti = np.ascontiguousarray(ti, np.int32)
-    tw = np.ascontiguousarray(tw, np.float32)
-    lib.moe_forward_omp(pg, pu, pd, np.ascontiguousarray(x, np.float32).ctypes.data_as(K.cf), M, N, qts[0], qts[1],
-                        qts[2], ti.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), tw.ctypes.data_as(K.cf), Kk,
-                        comb.ctypes.data_as(K.cf), buf.ctypes.data_as(K.cf), q8.ctypes.data_as(K.cu))
-    return comb
+class MoECall:
+    """moe_forward_omp (QK:2066) through a library's host ABI as the reference's
+    caller makes it (TE:2031-2085): per-expert pointer arrays built once
+    (TE:868-905), scratch sized as TE:954-960, caller-supplied routing."""
+
+    def __init__(self, ptrs, M, N, qts, Kk):
+        E = len(ptrs[0])
+        arr = ctypes.POINTER(ctypes.c_uint8) * E
+        self.keep = ptrs
+        self.pg, self.pu, self.pd = (arr(*[a.ctypes.data_as(K.cu) for a in lst]) for lst in ptrs)
+        self.M, self.N, self.qts, self.K = M, N, qts, Kk
+        self.comb = np.zeros(N, np.float32)
+        self.buf = np.zeros(3 * Kk * M, np.float32)
+        self.q8 = np.zeros(Kk * M * 34 // 32 + 64, np.uint8)
+        self.p = (self.comb.ctypes.data_as(K.cf), self.buf.ctypes.data_as(K.cf), self.q8.ctypes.data_as(K.cu))
+
+    def prepare(self, xs, idx, w):
+        """Per-token argument pointers, made before any timed call."""
+        self.args = [(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(i, np.int32),
+                      np.ascontiguousarray(v, np.float32)) for x, i, v in zip(xs, idx, w)]
+        self.cargs = [(x.ctypes.data_as(K.cf), i.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), v.ctypes.data_as(K.cf))
+                      for x, i, v in self.args]
+
+    def __call__(self, lib, t):
+        x, ti, tw = self.cargs[t]
+        lib.moe_forward_omp(self.pg, self.pu, self.pd, x, self.M, self.N, self.qts[0], self.qts[1], self.qts[2], ti,
+                            tw, self.K, self.p[0], self.p[1], self.p[2])
+        return self.comb
 
 
 # ------------------------------------------------------------------ host CPU reference (child process)
@@ -547,12 +561,10 @@ def cpu_leg(name, cores, model):
     downs = [W.gen_weights(rw, qts[2], N, M) for _ in range(E)]
     orc = O.Oracle()
     idx, w = orc.route(router, x[:n_tok], Kk, renorm=True)
+    call = MoECall((gates, ups, downs), M, N, qts, Kk)
+    call.prepare(x[:n_tok], idx, w)
     it = iter(range(10 ** 9))
-
-    def fwd():
-        t = next(it) % n_tok
-        moe_forward_call(ref.so, (gates, ups, downs), x[t], M, N, qts, idx[t], w[t])
-    sec = median_time(fwd, n_tok)
+    sec = median_time(lambda: call(ref.so, next(it) % n_tok), n_tok)
     res = {"moe_forward_omp": {
         "value": round(1 / sec, 2), "unit": "tokens/s", **tag, "ms": round(sec * 1e3, 2),
         "sample": f"moe_forward_omp (oracle/_ref) per token on {n_tok} tokens of the {tag_moe} workload (router and "

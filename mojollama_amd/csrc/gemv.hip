@@ -33,6 +33,8 @@ __global__ void k_gemv_zero(mllm_gemv_args a)
 bool mllm_gemv_fused_fits(int sem, int n_cols, int B, bool prologue)
 {
     if (sem == SEM_F32 || B < 1 || B > 8 || n_cols < mllm_sem_block_elems(sem)) return false;
+    // the prologue's norm covers the staged elements: whole blocks only
+    if (prologue && n_cols % mllm_sem_block_elems(sem)) return false;
     const bool q8 = mllm_sem_uses_q8(sem);
     const int be = mllm_layout_info(mllm_sem_layout(sem)).block_elems;
     const int BM = B == 1 ? 1 : B == 2 ? 2 : B <= 4 ? 4 : 8;

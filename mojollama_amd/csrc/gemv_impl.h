@@ -160,77 +160,74 @@ MLLM_DEV float lane_pair(float v) { return __int_as_float(__builtin_amdgcn_mov_d
 
 // ---------------------------------------------------------------- fused prologue
 //
-// Residual add and RMS norm applied to the activation while it is staged
-// (mllm_gemv_args: x_res, res_out, rms_w).  Every workgroup reduces each
-// token's sum(v^2) itself (the vector is a few KB), so no other launch or
-// cross-workgroup step is needed.  The scale is 1/rms (rms_div == 0) or rms
-// (rms_div == 1).
-
-// v (8 elements k .. k+7 of token b): + x_res, then the RMS scale and weight.
-// res / w are loaded here (L2 hits: the reduction read them already).
-MLLM_DEV void prologue_apply8(float (&v)[8], const mllm_gemv_args &a, float sc, int b, int k)
-{
-    if (a.x_res) {
-        const float *r = a.x_res + (long)b * a.ldx + k;
-        const float4 r0 = gld<float4>(r), r1 = gld<float4>(r + 4);
-        v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
-        v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
-    }
-    if (a.rms_w) {
-        const float4 w0 = gld<float4>(a.rms_w + k), w1 = gld<float4>(a.rms_w + k + 4);
-        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (a.rms_div ? v[e] / sc : v[e] * sc) * w[e];
-    }
-}
+// Residual add and RMS norm fused into the staging (mllm_gemv_args: x_res,
+// res_out, rms_w).  RMSNorm scales a token's whole activation by one scalar
+// s (1/rms, or rms with rms_div), so W . (v * s * w) = s * (W . (v * w)):
+// the kernel stages v * w at once, records sum(v^2) of each 8-element piece
+// in LDS, and each wave folds s into its outputs in the epilogue, after the
+// barrier that follows the staging anyway -- no extra pass over x and no
+// extra barrier.  (The product is reassociated relative to the reference's
+// (v * s) * w: one fp32 rounding apart.)
+struct pro_regs {
+    float4 r[kStageSlots][2];   // residual
+    float4 w[kStageSlots][2];   // RMS weight
+};
 
 MLLM_DEV void f4x2_to8(const float4 (&p)[2], float (&v)[8])
 {
     v[0] = p[0].x; v[1] = p[0].y; v[2] = p[0].z; v[3] = p[0].w;
     v[4] = p[1].x; v[5] = p[1].y; v[6] = p[1].z; v[7] = p[1].w;
 }
-MLLM_DEV void f8_to4x2(const float (&v)[8], float4 (&p)[2])
+
+// v (8 elements of token b at column k): + residual; res_out = v (writer
+// workgroup); part = sum v^2; v * rms weight.
+MLLM_DEV void prologue8(float (&v)[8], const float4 (&r)[2], const float4 (&w)[2], const mllm_gemv_args &a, int b,
+                        int k, bool writer, float *part)
 {
-    p[0] = make_float4(v[0], v[1], v[2], v[3]);
-    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    if (a.x_res) {
+        float rr[8];
+        f4x2_to8(r, rr);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] += rr[e];
+    }
+    if (writer) {
+        float *o = a.res_out + (long)b * a.ldx + k;
+        *reinterpret_cast<float4 *>(o) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (a.rms_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss = fmaf(v[e], v[e], ss);
+        *part = ss;
+        float ww[8];
+        f4x2_to8(w, ww);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] *= ww[e];
+    }
 }
 
-// Per-token RMS scale of v = x + res over n elements into sc[b] (LDS; red:
-// 4*8 floats of LDS scratch), and res_out = v written by workgroup (0, 0).
-// Whole workgroup; ends with a barrier.
-MLLM_DEV void prologue_reduce(const mllm_gemv_args &a, int B, float *red, float *sc)
+// Residual and RMS-weight loads of the half-groups stage_load loads (same
+// indices, clamped the same way).
+MLLM_DEV void pro_load(pro_regs &pr, const mllm_gemv_args &a, int B, int kn, int pass)
 {
-    const int n = a.n_cols, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool vec = (n & 3) == 0 && (a.ldx & 3) == 0;
-    const bool writer = a.res_out && blockIdx.x == 0 && blockIdx.y == 0;
-    for (int b = 0; b < B; b++) {
-        const float *xb = a.x + (long)b * a.ldx, *rb = a.x_res ? a.x_res + (long)b * a.ldx : nullptr;
-        float *ob = writer ? a.res_out + (long)b * a.ldx : nullptr;
-        float ss = 0.0f;
-        if (vec) {
-            for (int i = 4 * tid; i < n; i += 1024) {
-                float4 v = gld<float4>(xb + i);
-                if (rb) { const float4 r = gld<float4>(rb + i); v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w; }
-                if (ob) *reinterpret_cast<float4 *>(ob + i) = v;
-                ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
-            }
-        } else {
-            for (int i = tid; i < n; i += 256) {
-                float v = xb[i] + (rb ? rb[i] : 0.0f);
-                if (ob) ob[i] = v;
-                ss = fmaf(v, v, ss);
-            }
+    const int nh = kn >> 3, n = B * nh;
+#pragma unroll
+    for (int q = 0; q < kStageSlots; q++) {
+        const int base = 256 * (q + pass * kStageSlots);
+        if (base >= n) break;
+        const int idx = min(base + (int)threadIdx.x, n - 1);
+        const int b = idx / nh, h = idx - b * nh;
+        if (a.x_res) {
+            const float *src = a.x_res + (long)b * a.ldx + 8 * h;
+            pr.r[q][0] = gld<float4>(src);
+            pr.r[q][1] = gld<float4>(src + 4);
         }
-        ss = group_sum<64>(ss);
-        if (lane == 0) red[wave * 8 + b] = ss;
+        if (a.rms_w) {
+            pr.w[q][0] = gld<float4>(a.rms_w + 8 * h);
+            pr.w[q][1] = gld<float4>(a.rms_w + 8 * h + 4);
+        }
     }
-    __syncthreads();
-    if (tid < B) {
-        const float t = red[tid] + red[8 + tid] + red[16 + tid] + red[24 + tid];
-        const float r = sqrtf(t / (float)n + a.rms_eps);
-        sc[tid] = a.rms_div ? r : 1.0f / r;
-    }
-    __syncthreads();
 }
 
 // Byte 0 of a, b, c, d packed into one word (a lowest).
@@ -241,9 +238,10 @@ MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
     return lo | hi;
 }
 
-template <int SEM, bool SILU>
+template <int SEM, bool SILU, bool PRO = false>
 MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass,
-                          bool clamp)
+                          bool clamp, const pro_regs *pr = nullptr, const mllm_gemv_args *pa = nullptr,
+                          float *part = nullptr)
 {
     const int nh = kn >> 3;
     constexpr float M = 12582912.0f;   // 1.5 * 2^23: t = y + M holds rne(y) in its low mantissa bits
@@ -260,6 +258,8 @@ MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = mllm_silu_mul(v[e], u[e], clamp);
         }
+        if constexpr (PRO)
+            prologue8(v, pr->r[q], pr->w[q], *pa, b, 8 * h, pa->res_out && blockIdx.x == 0, part + idx);
         float m = 0.0f, sum = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) { m = fmaxf(m, fabsf(v[e])); sum += v[e]; }
@@ -554,6 +554,7 @@ MLLM_DEV void stage_q8(float *xl, const mllm_xq &xq, long q_job, long b_job, int
 // (q8f_load), the caller placing the weight prefetch between the two halves.
 struct q8f_stage {
     float4 v[2], u[2];
+    float4 r[2], w[2];   // residual and RMS weight (fused prologue)
 };
 
 MLLM_DEV void q8f_load(q8f_stage &st, const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B,
@@ -578,8 +579,25 @@ MLLM_DEV void q8f_load(q8f_stage &st, const float *__restrict__ x, const float *
     }
 }
 
+// The fused prologue's residual / RMS-weight loads for q8f_load's elements.
+MLLM_DEV void q8f_pro_load(q8f_stage &st, const mllm_gemv_args &a, int B, int kn, int pass)
+{
+    const int nq = kn >> 3, i = threadIdx.x + 256 * pass;
+    if (i >= B * nq) return;
+    const int b = i / nq, e = (i - b * nq) << 3;
+    if (a.x_res) {
+        const float *src = a.x_res + (long)b * a.ldx + e;
+        st.r[0] = gld<float4>(src);
+        st.r[1] = gld<float4>(src + 4);
+    }
+    if (a.rms_w) {
+        st.w[0] = gld<float4>(a.rms_w + e);
+        st.w[1] = gld<float4>(a.rms_w + e + 4);
+    }
+}
+
 MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT, int tstride, int qstride, int kn,
-                        int pass, bool clamp = true)
+                        int pass, bool clamp = true, const mllm_gemv_args *pa = nullptr, float *part = nullptr)
 {
     const int nq = kn >> 3, i = threadIdx.x + 256 * pass;
     if (i >= B * nq) return;           // B * nq is a multiple of 4: a block's four lanes take the same path
@@ -589,7 +607,12 @@ MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT
         const float u[8] = {st.u[0].x, st.u[0].y, st.u[0].z, st.u[0].w, st.u[1].x, st.u[1].y, st.u[1].z, st.u[1].w};
 #pragma unroll
         for (int k = 0; k < 8; k++) v[k] = mllm_silu_mul(v[k], u[k], clamp);
+    } else if (pa) {
+        prologue8(v, st.r, st.w, *pa, b, e, pa->res_out && blockIdx.x == 0, part + i);
     }
+    // prescale (the fused RMS norm): the block's unrounded scale d and its min-term
+    // quant count go to LDS; the caller turns them into fp16(s * d) once s is known
+    const bool prescale = pa && pa->rms_w;
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) { const float a = fabsf(v[k]); amax = (a > amax) ? a : amax; }
@@ -618,8 +641,8 @@ MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT
     if ((qi & 3) == 0) {
         const float dd = h2f(__builtin_bit_cast(uint16_t, (_Float16)d));
         float *tf = xl + b * tstride + qstride / 4;
-        tf[e >> 5] = dd;
-        tf[KT / 32 + (e >> 5)] = dd * (float)s4;
+        tf[e >> 5] = prescale ? d : dd;
+        tf[KT / 32 + (e >> 5)] = prescale ? (float)s4 : dd * (float)s4;
     }
 }
 
@@ -701,9 +724,10 @@ template <int SEM, bool Q8> struct gemv_geom {
 
 // FUSE bits of the persistent kernel (mllm_gemv_args): kFusePro = the
 // residual / RMS-norm prologue; kFusePair = paired rows with the SiLU product
-// in the epilogue: output row o is silu(row o . x) * (row o' . x), row o' the
-// "up" row o + n_rows of the same matrix, or row o of table2's matrix in a
-// job launch (the gate/up pair of an MoE expert).
+// in the epilogue: adjacent lane groups compute a gate row (even group) and
+// its up row (odd group: row o + n_rows of the same matrix, or row o of
+// table2's matrix in a job launch -- the gate/up pair of an MoE expert), and
+// the even group writes silu(gate) * up after one cross-lane exchange.
 constexpr int kFusePro = 1, kFusePair = 2;
 
 template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU, int FUSE>
@@ -712,11 +736,11 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     static_assert(!(Q8 && SILU), "the SiLU product of Q8_0 activations is formed by the quantiser");
     static_assert(!(SILU && FUSE), "the SiLU staging and the fusions are exclusive");
     constexpr bool PRO = (FUSE & kFusePro) != 0, PAIR = (FUSE & kFusePair) != 0;
-    static_assert(!PAIR || R % 2 == 0, "paired rows need an even row count per lane group");
+    static_assert(!PAIR || (R == 1 && LPR <= 32), "paired rows: one row per lane group, two groups per pair");
     extern __shared__ float xl[];
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
-    constexpr int HR = PAIR ? R / 2 : R;               // output rows per lane group and step
-    constexpr int OPW = (64 / LPR) * HR;               // output rows per wave and step
+    constexpr int GPW = 64 / LPR;                       // lane groups per wave
+    constexpr int OPW = PAIR ? GPW / 2 : GPW * R;       // output rows per wave and step
     const job_view jv = view_job(a, blockIdx.y);
     const mllm_packed W = jv.W;
     // the "up" rows of a pair: table2's matrix of the job's expert, else the same matrix n_rows further
@@ -751,18 +775,23 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     const int qstride = KT + (KT >> 4), tstride = qstride / 4 + 2 * (KT / 32);
 
     // A step is (row group rg, chunk pass it); the next step advances it, then rg.
-    // Lane group rows: outputs o0 .. o0+HR-1; with PAIR, slots HR.. hold their up rows.
+    // Output row of lane group grp, row r: o0 + r; with PAIR, o0 + grp / 2 of the gate (even) or up (odd) rows.
+    auto out_row = [&](int rg, int r) __attribute__((always_inline)) {
+        return PAIR ? rg * OPW + (grp >> 1) : rg * OPW + grp * R + r;
+    };
     auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) __attribute__((always_inline)) {
         const int c = min(it * LPR + sl, nch - 1);
-        const int o0 = rg * OPW + grp * HR;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int o = min(o0 + (r % HR), n_out - 1);
-            const bool up = PAIR && r >= HR;
-            const mllm_packed &M = up ? W2 : W;
-            const int row = up ? o + up_off : o;
-            if constexpr (Q8) q8_fetch<SEM>(M, nb, row, c, buf[r]);
-            else fetch<SEM>(M, nb, row, c, buf[r]);
+            const int o = min(out_row(rg, r), n_out - 1);
+            if constexpr (PAIR) {
+                const bool up = grp & 1;
+                if constexpr (Q8) q8_fetch<SEM>(up ? W2 : W, nb, up ? o + up_off : o, c, buf[r]);
+                else fetch<SEM>(up ? W2 : W, nb, up ? o + up_off : o, c, buf[r]);
+            } else {
+                if constexpr (Q8) q8_fetch<SEM>(W, nb, o, c, buf[r]);
+                else fetch<SEM>(W, nb, o, c, buf[r]);
+            }
         }
     };
     float acc[R][BM];
@@ -770,6 +799,9 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int b = 0; b < BM; b++) acc[r][b] = 0.0f;
+    float scale[BM];   // RMSNorm scale per token (prologue)
+#pragma unroll
+    for (int b = 0; b < BM; b++) scale[b] = 1.0f;
     auto run_step = [&](int rg, int it, const raw_chunk (&buf)[R]) __attribute__((always_inline)) {
         // a lane past the row's last chunk recomputes the last one and discards it
         const int c = min(it * LPR + sl, nch - 1);
@@ -786,21 +818,24 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 #pragma unroll
             for (int b = 0; b < BM; b++) acc[r][b] += live ? part[r][b] : 0.0f;
         if (it == iters - 1) {
-            const int o0 = rg * OPW + grp * HR;
 #pragma unroll
-            for (int r = 0; r < HR; r++) {
+            for (int r = 0; r < R; r++) {
+                const int o = out_row(rg, r);
 #pragma unroll
                 for (int b = 0; b < BM; b++) {
                     float v = group_sum<LPR>(acc[r][b]);
                     acc[r][b] = 0.0f;
+                    if constexpr (PRO && !Q8) v = a.rms_div ? v / scale[b] : v * scale[b];
+                    bool writes = sl == 0 && o < n_out && b < B;
                     if constexpr (PAIR) {
-                        const float u = group_sum<LPR>(acc[r + HR][b]);
-                        acc[r + HR][b] = 0.0f;
+                        // the odd group's up value to the even group's lanes
+                        const float u = __shfl_xor(v, LPR, 64);
                         v = mllm_silu_mul(v, u, !a.silu_noclamp);
+                        writes = writes && (grp & 1) == 0;
                     }
-                    if (sl == 0 && o0 + r < n_out && b < B) {
-                        const long o = (long)b * a.ldo + o0 + r;
-                        out[o] = a.out_add ? a.out_add[o] + v : v;
+                    if (writes) {
+                        const long oi = (long)b * a.ldo + o;
+                        out[oi] = a.out_add ? a.out_add[oi] + v : v;
                     }
                 }
             }
@@ -815,110 +850,9 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     // for the older buffer instead of draining all loads.
     raw_chunk bufA[R], bufB[R];
     int rg = rg0, it = 0;
-    if constexpr (PRO) {
-        // residual / RMS-norm prologue (single-matrix launches).  LDS past the
-        // staged activation holds the reduction.
-        float *red = xl + a.pro_lds / 4;
-        const float *x0 = a.x;
-        const bool writer = a.res_out && blockIdx.x == 0;
-        if constexpr (!Q8) {
-            x_stage<false> xst;
-            const int nh = kused >> 3;
-            if (B == 1 && a.n_cols == kused && nh <= 512) {
-                // one token, whole row in two slots: x, residual and weight
-                // loaded once; the sum of squares reduced from registers
-                stage_load<false>(xst, x0, nullptr, a.ldx, 1, 0, kused, 0);
-                float4 rr[2][2], ww[2][2];
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    if (256 * q >= nh) break;
-                    const int k = 8 * min(256 * q + (int)threadIdx.x, nh - 1);
-                    if (a.x_res) { rr[q][0] = gld<float4>(a.x_res + k); rr[q][1] = gld<float4>(a.x_res + k + 4); }
-                    if (a.rms_w) { ww[q][0] = gld<float4>(a.rms_w + k); ww[q][1] = gld<float4>(a.rms_w + k + 4); }
-                }
-                fetch_step(min(rg, nrg - 1), it, bufA);
-                float ss = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const int idx = 256 * q + threadIdx.x;
-                    if (256 * q >= nh || idx >= nh) continue;
-                    float v[8];
-                    f4x2_to8(xst.v[q], v);
-                    if (a.x_res) {
-                        float r[8];
-                        f4x2_to8(rr[q], r);
-#pragma unroll
-                        for (int e = 0; e < 8; e++) v[e] += r[e];
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; e++) ss = fmaf(v[e], v[e], ss);
-                    f8_to4x2(v, xst.v[q]);
-                    if (writer) {
-                        *reinterpret_cast<float4 *>(a.res_out + 8 * idx) = xst.v[q][0];
-                        *reinterpret_cast<float4 *>(a.res_out + 8 * idx + 4) = xst.v[q][1];
-                    }
-                }
-                if (a.rms_w) {
-                    ss = group_sum<64>(ss);
-                    if (lane == 0) red[wave] = ss;
-                    __syncthreads();
-                    const float t = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.n_cols + a.rms_eps);
-                    const float sc = a.rms_div ? t : 1.0f / t;
-#pragma unroll
-                    for (int q = 0; q < 2; q++) {
-                        if (256 * q >= nh) break;
-                        float v[8], w[8];
-                        f4x2_to8(xst.v[q], v);
-                        f4x2_to8(ww[q], w);
-#pragma unroll
-                        for (int e = 0; e < 8; e++) v[e] = (a.rms_div ? v[e] / sc : v[e] * sc) * w[e];
-                        f8_to4x2(v, xst.v[q]);
-                    }
-                }
-                stage_store<SEM, false>(xst, reinterpret_cast<uint8_t *>(xl), dg, 1, kused, 0, true);
-            } else {
-                // any B: a first pass reduces the sum of squares, the staging
-                // pass then applies the residual and the norm
-                float *sc = red + 32;
-                fetch_step(min(rg, nrg - 1), it, bufA);
-                prologue_reduce(a, B, red, sc);
-                const int passes = (B * nh + 256 * kStageSlots - 1) / (256 * kStageSlots);
-                for (int pass = 0; pass < passes; pass++) {
-                    stage_load<false>(xst, x0, nullptr, a.ldx, B, 0, kused, pass);
-#pragma unroll
-                    for (int q = 0; q < kStageSlots; q++) {
-                        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
-                        if (idx >= B * nh) continue;
-                        const int b = idx / nh, h = idx - b * nh;
-                        float v[8];
-                        f4x2_to8(xst.v[q], v);
-                        prologue_apply8(v, a, sc[b], b, 8 * h);
-                        f8_to4x2(v, xst.v[q]);
-                    }
-                    stage_store<SEM, false>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true);
-                }
-            }
-        } else {
-            // Q8_0 activations quantised here, from the prologue's activation
-            float *sc = red + 32;
-            fetch_step(min(rg, nrg - 1), it, bufA);
-            prologue_reduce(a, B, red, sc);
-            const int nq = kused >> 3;
-            for (int pass = 0; pass * 256 < B * nq; pass++) {
-                q8f_stage qs;
-                q8f_load(qs, x0, nullptr, a.ldx, B, 0, kused, pass);
-                const int i = threadIdx.x + 256 * pass;
-                if (i < B * nq) {
-                    const int b = i / nq, e = (i - b * nq) << 3;
-                    float v[8];
-                    f4x2_to8(qs.v, v);
-                    prologue_apply8(v, a, sc[b], b, e);
-                    f8_to4x2(v, qs.v);
-                }
-                q8f_store(qs, false, xl, B, KT, tstride, qstride, kused, pass);
-            }
-        }
-    } else if constexpr (Q8) {
+    // prologue: sum(v^2) of each staged 8-element piece, past the staged activation
+    float *part = xl + a.pro_lds / 4;
+    if constexpr (Q8) {
         if (a.xq.q) {
             fetch_step(min(rg, nrg - 1), it, bufA);
             stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride,
@@ -929,11 +863,14 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             const float *xuf = a.x_up ? a.x_up + jv.xj * a.x_job_stride : nullptr;
             q8f_stage qs;
             q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, 0);
+            if constexpr (PRO) q8f_pro_load(qs, a, B, kused, 0);
             fetch_step(min(rg, nrg - 1), it, bufA);
             for (int pass = 0;;) {
-                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass, !a.silu_noclamp);
+                q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass, !a.silu_noclamp,
+                          PRO ? &a : nullptr, part);
                 if (++pass * 256 >= B * (kused >> 3)) break;
                 q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, pass);
+                if constexpr (PRO) q8f_pro_load(qs, a, B, kused, pass);
             }
         }
     } else {
@@ -942,11 +879,61 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
         const float *xj = a.x + jv.xj * a.x_job_stride;
         const float *xuj = SILU ? a.x_up + jv.xj * a.x_job_stride : nullptr;
         stage_load<SILU>(xst, xj, xuj, a.ldx, B, 0, kused, 0);
-        fetch_step(min(rg, nrg - 1), it, bufA);
-        stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
-                                !a.silu_noclamp);
+        if constexpr (PRO) {
+            pro_regs pr;
+            pro_load(pr, a, B, kused, 0);
+            fetch_step(min(rg, nrg - 1), it, bufA);
+            const int passes = (B * (kused >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
+            for (int pass = 0; pass < passes; pass++) {
+                if (pass) {
+                    stage_load<false>(xst, xj, nullptr, a.ldx, B, 0, kused, pass);
+                    pro_load(pr, a, B, kused, pass);
+                }
+                stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true, &pr, &a,
+                                              part);
+            }
+        } else {
+            fetch_step(min(rg, nrg - 1), it, bufA);
+            stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
+                                    !a.silu_noclamp);
+        }
     }
     __syncthreads();
+    if constexpr (PRO) {
+        if (a.rms_w) {
+            // each wave sums every token's pieces (deterministic order) for its outputs' scale
+            const int nh = kused >> 3;
+#pragma unroll
+            for (int b = 0; b < BM; b++) {
+                if (b >= B) break;
+                float t = 0.0f;
+                for (int h = lane; h < nh; h += 64) t += part[b * nh + h];
+                t = group_sum<64>(t);
+                const float r = sqrtf(t / (float)a.n_cols + a.rms_eps);
+                scale[b] = a.rms_div ? r : 1.0f / r;
+            }
+            if constexpr (Q8) {
+                // Q8_0 activations: the quants of v * w equal those of the normalised
+                // activation (a common factor per token); its block scale is
+                // fp16(d * s), the scale quantize_row_q8_0 stores for the normalised
+                // values (QK:1406-1455) -- the dots (Q4_K x Q8_0 drops that scale from
+                // one of its terms, QK:1714-1723) then see the normalised activation
+                const int nbk = KT / 32;
+                for (int j = threadIdx.x; j < B * nbk; j += 256) {
+                    const int b = j / nbk, jj = j - b * nbk;
+                    float sb = scale[0];
+#pragma unroll
+                    for (int bb = 1; bb < BM; bb++) sb = b == bb ? scale[bb] : sb;
+                    float *tf = xl + b * tstride + qstride / 4;
+                    const float d = a.rms_div ? tf[jj] / sb : tf[jj] * sb;
+                    const float dd = h2f(__builtin_bit_cast(uint16_t, (_Float16)d));
+                    tf[jj] = dd;
+                    tf[nbk + jj] = dd * tf[nbk + jj];
+                }
+                __syncthreads();
+            }
+        }
+    }
     if (rg >= nrg) return;
     for (;;) {
         int rg1 = rg, it1 = it;
@@ -1136,7 +1123,7 @@ inline size_t persistent_lds(bool q8, int block_elems, int n_cols, int BM, bool 
     const int kused = n_cols / block_elems * block_elems;
     const int ktp = (kused + 255) / 256 * 256;
     size_t l = q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
-    if (prologue) l = (l + 15) / 16 * 16 + 256;
+    if (prologue) l = (l + 15) / 16 * 16 + (size_t)BM * (ktp / 8) * 4;
     return l;
 }
 
@@ -1146,8 +1133,11 @@ inline size_t persistent_lds(bool q8, int block_elems, int n_cols, int BM, bool 
 template <int SEM, bool Q8, int BM, int R, int FUSE>
 void launch_fused_lpr(int lpr, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
 {
-    if (lpr == 64) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64, false, FUSE>), grid, dim3(256), lds, st, a);
-    else if (lpr == 32 || BM > 1) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 32, false, FUSE>), grid, dim3(256), lds, st, a);
+    constexpr bool PAIR = (FUSE & kFusePair) != 0;
+    if constexpr (!PAIR) {
+        if (lpr == 64) { hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64, false, FUSE>), grid, dim3(256), lds, st, a); return; }
+    }
+    if (lpr >= 32 || BM > 1) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 32, false, FUSE>), grid, dim3(256), lds, st, a);
     else if constexpr (BM == 1) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 16, false, FUSE>), grid, dim3(256), lds, st, a);
 }
 
@@ -1164,20 +1154,27 @@ hipError_t launch_fused(mllm_gemv_args a, int n_jobs, hipStream_t st)
     if (pro) {
         lds = (lds + 15) / 16 * 16;
         a.pro_lds = (int)lds;
-        lds += 256;
+        lds += (size_t)BM * (ktp / 8) * 4;   // one sum of squares per staged 8-element piece
     }
     if (lds > kPersistentLds) return hipErrorInvalidValue;
-    constexpr int R = (BM == 1) ? 2 : (BM == 2) ? 4 : 2;   // paired rows: one gate and one up row at B=1
-    const int HR = pair ? 1 : (BM == 1 ? 1 : R);
-    int lpr = pick_lpr<SEM, Q8, BM>(a, n_jobs, HR);
+    constexpr int R = (BM == 1) ? 1 : (BM == 2) ? 4 : 2;
+    int lpr;
+    if (pair) {
+        // a pair takes two lane groups (its gate and its up row): size the launch over 2 n_rows rows
+        mllm_gemv_args rows2 = a;
+        rows2.n_rows = 2 * a.n_rows;
+        lpr = std::min(32, pick_lpr<SEM, Q8, BM>(rows2, n_jobs, 1));
+    } else {
+        lpr = pick_lpr<SEM, Q8, BM>(a, n_jobs, R);
+    }
     if (BM > 1 && lpr < 32) lpr = 32;
-    const int outs_per_wg = 4 * (64 / lpr) * HR;
+    const int outs_per_wg = pair ? 4 * (64 / lpr) / 2 : 4 * (64 / lpr) * R;
     const int wg_needed = (a.n_rows + outs_per_wg - 1) / outs_per_wg;
     const int per_cu = lds <= 40 * 1024 ? 3 : 2;
     const dim3 grid(std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs))), n_jobs);
     if constexpr (BM == 1) {
-        if (pair && pro) launch_fused_lpr<SEM, Q8, 1, 2, kFusePro | kFusePair>(lpr, grid, lds, a, st);
-        else if (pair) launch_fused_lpr<SEM, Q8, 1, 2, kFusePair>(lpr, grid, lds, a, st);
+        if (pair && pro) launch_fused_lpr<SEM, Q8, 1, 1, kFusePro | kFusePair>(lpr, grid, lds, a, st);
+        else if (pair) launch_fused_lpr<SEM, Q8, 1, 1, kFusePair>(lpr, grid, lds, a, st);
         else launch_fused_lpr<SEM, Q8, 1, 1, kFusePro>(lpr, grid, lds, a, st);
     } else {
         launch_fused_lpr<SEM, Q8, BM, R, kFusePro>(lpr, grid, lds, a, st);

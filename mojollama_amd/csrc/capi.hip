@@ -778,6 +778,21 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
     a.table = dtab; a.x = dx; a.x_job_stride = 0; a.ldx = N;
     a.out = dg; a.out_job_stride = F; a.ldo = F;
     a.n_rows = F; a.n_cols = N; a.B = 1;
+    if (sg >= 0 && sg == su && sd >= 0 && sd != SEM_F32 && mllm_gemv_fused_fits(sg, N, 1, false)) {
+        // gate, up and the clamped SiLU product in one launch (paired rows), then the down projection of h
+        a.table2 = dtab + K; a.silu_pair = 1; a.out = dh;
+        CK(mllm_launch_gemv(sg, a, K, st));
+        mllm_gemv_args b{};
+        b.table = dtab + 2 * K; b.x = dh; b.x_job_stride = F; b.ldx = F;
+        b.out = ddn; b.out_job_stride = N; b.ldo = N;
+        b.n_rows = N; b.n_cols = F; b.B = 1;
+        CK(mllm_launch_gemv(sd, b, K, st));
+        CK(mllm_launch_combine(ddn, dw, nullptr, 1, K, N, dx, 0, st));
+        CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
+        CK(hipStreamSynchronize(st));
+        memcpy(combined, c.h_out.p, N * 4);
+        return;
+    }
     if (sg >= 0 && sg == su) {
         a.job_split = K; a.table2 = dtab + K; a.out2 = du;
         CK(mllm_launch_gemv(sg, a, 2 * K, st));
@@ -1121,7 +1136,11 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     a.x = dx; a.x_job_stride = N; a.ldx = N;
     a.out = dg; a.out_job_stride = M; a.ldo = M;
     a.n_rows = M; a.n_cols = N; a.B = 1;
-    if (sems[0] == sems[1]) {
+    if (sems[0] == sems[1] && mllm_gemv_fused_fits(sems[0], N, 1, false)) {
+        // gate, up and the unclamped SiLU product (CE:649-652) in one launch (paired rows)
+        a.table2 = dtab + E; a.silu_pair = 1; a.silu_noclamp = 1; a.out = dh;
+        HIP_OK(mllm_launch_gemv(sems[0], a, (int)TK, st));
+    } else if (sems[0] == sems[1]) {
         a.job_split = (int)TK; a.table2 = dtab + E; a.out2 = du;
         HIP_OK(mllm_launch_gemv(sems[0], a, 2 * (int)TK, st));
     } else {
@@ -1129,7 +1148,7 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
         a.table = dtab + E; a.out = du;
         HIP_OK(mllm_launch_gemv(sems[1], a, (int)TK, st));
     }
-    HIP_OK(mllm_launch_silu_mul(dg, du, dh, (long)TK * M, 0, st));
+    if (!a.silu_pair) HIP_OK(mllm_launch_silu_mul(dg, du, dh, (long)TK * M, 0, st));
     mllm_gemv_args b{};
     b.table = dtab + 2 * (size_t)E; b.idx = didx;
     b.x = dh; b.x_job_stride = M; b.ldx = M;

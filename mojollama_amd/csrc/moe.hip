@@ -402,6 +402,23 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
         a.x = x; a.x_job_stride = N; a.ldx = N;
         a.out = s.g; a.out_job_stride = M; a.ldo = M;
         a.n_rows = M; a.n_cols = N; a.B = 1;
+        if (L->sem_g == L->sem_u && L->sem_d >= 0 && mllm_gemv_fused_fits(L->sem_g, N, 1, false)) {
+            // gate, up and the SiLU product in one launch (paired rows: the expert's
+            // gate row from table, its up row from table2), h written directly
+            a.table2 = L->tab + E; a.silu_pair = 1; a.silu_noclamp = !L->clamp;
+            a.out = s.h;
+            CK(mllm_launch_gemv(L->sem_g, a, TK, st));
+            mllm_gemv_args b{};
+            b.table = L->tab + 2 * (size_t)E; b.idx = s.idx;
+            b.x = s.h; b.x_job_stride = M; b.ldx = M;
+            b.out = s.dn; b.out_job_stride = N; b.ldo = N;
+            b.n_rows = N; b.n_cols = M; b.B = 1;
+            CK(mllm_launch_gemv(L->sem_d, b, TK, st));
+            CK(mllm_launch_combine(s.dn, s.w, s.idx, T, K, N, out, 0, st));
+            if (idx_out) CK(hipMemcpyAsync(idx_out, s.idx, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
+            if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
+            return 0;
+        }
         if (L->sem_g == L->sem_u) {
             a.job_split = TK; a.table2 = L->tab + E; a.out2 = s.u;
             CK(mllm_launch_gemv(L->sem_g, a, 2 * TK, st));

@@ -1040,6 +1040,64 @@ MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev
     return run_gemv(sem, view, xa, out_dev, n_rows, n_cols, B, ws + L.gemv, st, out_add);
 }
 
+// ------------------------------------------------ lm_head requantisation (f2)
+static int requant_sem(int qt) { return qt == 12 ? SEM_Q4_K_GGML : qt == 14 ? SEM_Q6_K_GGML : -1; }
+
+MLLM_API long mllm_requantize_workspace_size(int quant_type, int n_rows, int n_cols)
+{
+    const int sem = requant_sem(quant_type);
+    if (sem < 0 || n_rows <= 0 || n_cols <= 0) return -1;
+    return (long)(align256(mllm_packed_bytes(mllm_sem_layout(sem), n_rows, n_cols, nullptr)) +
+                  align256((size_t)n_rows * n_cols * 4));
+}
+
+MLLM_API int mllm_requantize_q8_0(int quant_type, const void *raw_dev, int n_rows, int n_cols, void *q8_dev,
+                                  void *workspace, void *stream)
+{
+    const int sem = requant_sem(quant_type);
+    if (sem < 0) { set_error("mllm_requantize_q8_0: type %d is not requantised (Q4_K and Q6_K only, TE:515-518)", quant_type); return -1; }
+    if (n_rows <= 0 || n_cols < 32) return 0;
+    if (!workspace) { set_error("mllm_requantize_q8_0: needs a workspace"); return -1; }
+    hipStream_t st = (hipStream_t)stream;
+    const int ly = mllm_sem_layout(sem);
+    uint8_t *packed = (uint8_t *)workspace;
+    float *f32 = (float *)(packed + align256(mllm_packed_bytes(ly, n_rows, n_cols, nullptr)));
+    HIP_OK(mllm_launch_pack(ly, (const uint8_t *)raw_dev, packed, n_rows, n_cols, st));
+    // columns past the last whole super-block stay 0 (TE's np.zeros buffer)
+    if (n_cols % 256) HIP_OK(mllm_launch_fill(f32, (long)n_rows * n_cols, 0.0f, st));
+    if (n_cols >= 256 &&
+        mllm_launch_dequant(sem, mllm_packed_view(ly, packed, n_rows, n_cols), n_rows, n_cols, f32, st) != 0) {
+        set_error("mllm_requantize_q8_0: dequantisation failed");
+        return -1;
+    }
+    HIP_OK(mllm_launch_requant_q8_0(f32, n_rows, n_cols, (uint8_t *)q8_dev, st));
+    return 0;
+}
+
+MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, int quant_type, uint8_t *out)
+{
+    API_GUARD;
+    const int sem = requant_sem(quant_type);
+    if (sem < 0) { set_error("requantize_output_q8_0: type %d is not requantised (Q4_K and Q6_K only)", quant_type); return -1; }
+    if (n_rows <= 0 || n_cols < 32) return 0;
+    thread_ctx &c = t_ctx;
+    if (c.init()) return -1;
+    const size_t raw = (size_t)raw_row_bytes(mllm_sem_layout(sem), n_cols) * n_rows;
+    const size_t q8 = (size_t)n_rows * (n_cols / 32) * 34;
+    const long ws = mllm_requantize_workspace_size(quant_type, n_rows, n_cols);
+    // a load-time conversion: its buffers are allocated for the call and freed after it
+    void *d_raw = nullptr, *d_q8 = nullptr, *d_ws = nullptr;
+    int rc = -1;
+    if (hipMalloc(&d_raw, raw ? raw : 256) == hipSuccess && hipMalloc(&d_q8, q8) == hipSuccess &&
+        hipMalloc(&d_ws, ws) == hipSuccess && hipMemcpyAsync(d_raw, W, raw, hipMemcpyHostToDevice, c.st) == hipSuccess &&
+        mllm_requantize_q8_0(quant_type, d_raw, n_rows, n_cols, d_q8, d_ws, c.st) == 0 &&
+        hipMemcpyAsync(out, d_q8, q8, hipMemcpyDeviceToHost, c.st) == hipSuccess && hipStreamSynchronize(c.st) == hipSuccess)
+        rc = 0;
+    (void)hipFree(d_raw); (void)hipFree(d_q8); (void)hipFree(d_ws);
+    if (rc) set_error("requantize_output_q8_0 failed");
+    return rc;
+}
+
 MLLM_API int mllm_read_probe(const void *dev, long bytes, void *sink, void *stream)
 {
     if (((uintptr_t)dev & 15) || (bytes & 15) || !sink) { set_error("mllm_read_probe: 16-byte aligned, multiple of 16"); return -1; }

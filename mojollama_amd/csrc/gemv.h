@@ -115,6 +115,10 @@ hipError_t mllm_launch_act_prologue(const float *x, const float *x_res, float *r
                                     hipStream_t st);
 // Plain streaming read of bytes / 16 words (mllm_read_probe).
 hipError_t mllm_launch_read_probe(const void *p, long bytes, void *sink, hipStream_t st);
+// TE:620-666 Q8_0 requantisation of fp32 rows [n_rows][n_cols] into raw 34-byte blocks.
+hipError_t mllm_launch_requant_q8_0(const float *w, int n_rows, int n_cols, uint8_t *out, hipStream_t st);
+// p[i] = v, i < n (a fill kernel: nothing here records a memset node).
+hipError_t mllm_launch_fill(float *p, long n, float v, hipStream_t st);
 // out[i] += add[i], i < n.
 hipError_t mllm_launch_add(float *out, const float *add, long n, hipStream_t st);
 // out[b][r] = silu(y[b][r]) * y[b][n + r] (+ add[b][r]); y is [B][2n].

@@ -782,6 +782,45 @@ __global__ void k_silu_pair(const float *__restrict__ y, int B, int n, int clamp
 }
 
 
+// The reference caller's lm_head requantisation (TE:620-666) of fp32 rows:
+// per 32 elements amax = max(max|x|, 1e-10f), d = amax / 127,
+// q = rint(x / d) clamped to +-127 (IEEE division, round half to even, as
+// numpy's float32 ops), written as raw Q8_0 blocks: fp16(d), then 32 quants.
+__global__ void k_requant_q8_0(const float *__restrict__ w, int n_rows, int n_cols, uint8_t *__restrict__ out)
+{
+    const int nb = n_cols / 32;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n_rows * nb) return;
+    const long r = i / nb, b = i - r * nb;
+    const float *x = w + r * n_cols + 32 * b;
+    float v[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+        v[k] = x[k];
+        const float a = fabsf(v[k]);
+        amax = a > amax ? a : amax;
+    }
+    amax = amax < 1e-10f ? 1e-10f : amax;
+    const float d = __fdiv_rn(amax, 127.0f);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
+    uint8_t *dst = out + i * 34;
+    dst[0] = (uint8_t)(h & 0xFF);
+    dst[1] = (uint8_t)(h >> 8);
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+        float q = rintf(__fdiv_rn(v[k], d));
+        q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
+        dst[2 + k] = (uint8_t)(int8_t)(int)q;
+    }
+}
+
+__global__ void k_fill_f32(float *__restrict__ p, long n, float v)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
 // out[i] += add[i], i < n (the residual epilogue of launches that cannot fuse it).
 __global__ void k_add(float *__restrict__ out, const float *__restrict__ add, long n)
 {
@@ -989,6 +1028,21 @@ hipError_t mllm_launch_silu_pair(const float *y, int B, int n, int clamp, float 
 {
     if (B <= 0 || n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_silu_pair, dim3((n + 255) / 256, B), dim3(256), 0, st, y, B, n, clamp, out, add);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_requant_q8_0(const float *w, int n_rows, int n_cols, uint8_t *out, hipStream_t st)
+{
+    const long n = (long)n_rows * (n_cols / 32);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_requant_q8_0, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, n_rows, n_cols, out);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_fill(float *p, long n, float v, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n, v);
     return hipGetLastError();
 }
 

@@ -116,6 +116,12 @@ def load_kernels(path=LIB_PATH):
     so.mllm_gemv_fused_workspace_size.restype = ctypes.c_long
     so.mllm_gemv_fused.argtypes = [ci, cvp, cvp, cvp, ci, ci, ci, ctypes.POINTER(GemvFusion), cvp, cvp]
     so.mllm_gemv_fused.restype = ci
+    so.requantize_output_q8_0.argtypes = [cu, ci, ci, ci, cu]
+    so.requantize_output_q8_0.restype = ci
+    so.mllm_requantize_workspace_size.argtypes = [ci, ci, ci]
+    so.mllm_requantize_workspace_size.restype = ctypes.c_long
+    so.mllm_requantize_q8_0.argtypes = [ci, cvp, ci, ci, cvp, cvp, cvp]
+    so.mllm_requantize_q8_0.restype = ci
     so.mllm_read_probe.argtypes = [cvp, ctypes.c_long, cvp, cvp]
     so.mllm_read_probe.restype = ci
     so.mllm_quantize_q8_0.argtypes = [cvp, ci, ci, cvp, cvp]

@@ -560,3 +560,45 @@ void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
     }
     free(g); free(u); free(dn);
 }
+
+/* ------------------------------------------------ lm_head requantisation */
+
+/* The reference caller's lm_head requantisation (TE:620-666,
+ * _requantize_output): each row of a Q4_K / Q6_K matrix dequantised as
+ * q4_k_dequantize_row / q6_k_dequantize_row do (QK:762-828; columns past the
+ * last whole super-block stay 0, as TE's np.zeros buffer leaves them), then
+ * per 32 elements in float32 as TE's numpy code computes it:
+ * amax = max(max|x|, 1e-10f), d = amax / 127, q = round-half-even(x / d)
+ * clamped to +-127, d stored as fp16 (RNE) before the 32 quants.
+ * Returns 0, or -1 for a type TE does not requantise this way. */
+int orc_requant_q8_0(int qt, const uint8_t *W, int n_rows, int n_cols, uint8_t *out)
+{
+    const int sem = qt == ORC_QT_Q4_K ? ORC_Q4_K_GGML : qt == ORC_QT_Q6_K ? ORC_Q6_K_GGML : -1;
+    if (sem < 0) return -1;
+    const long rb = orc_row_bytes(sem, n_cols);
+    const int nb = n_cols / 32;
+    float *w = (float *)malloc((size_t)(n_cols > 0 ? n_cols : 1) * sizeof(float));
+    if (!w) return -1;
+    for (int r = 0; r < n_rows; r++) {
+        memset(w, 0, (size_t)n_cols * sizeof(float));
+        orc_dequant_row(sem, W + (long)r * rb, w, n_cols / 256 * 256);
+        for (int b = 0; b < nb; b++) {
+            const float *x = w + 32 * b;
+            uint8_t *dst = out + ((long)r * nb + b) * 34;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) { const float a = fabsf(x[i]); if (a > amax) amax = a; }
+            if (amax < 1e-10f) amax = 1e-10f;
+            const float d = amax / 127.0f;
+            const uint16_t h = orc_f32_to_f16(d);
+            dst[0] = (uint8_t)(h & 0xff);
+            dst[1] = (uint8_t)(h >> 8);
+            for (int i = 0; i < 32; i++) {
+                float q = nearbyintf(x[i] / d);
+                q = q < -127.0f ? -127.0f : q > 127.0f ? 127.0f : q;
+                dst[2 + i] = (uint8_t)(int8_t)(int)q;
+            }
+        }
+    }
+    free(w);
+    return 0;
+}

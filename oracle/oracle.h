@@ -92,6 +92,12 @@ void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
                            int qt_gate, int qt_up, int qt_down, const int *top_idx,
                            const float *top_w, int top_k, int has_q8_scratch, float *out);
 
+/* TE:620-666 _requantize_output: Q4_K / Q6_K rows (ggml dequantisation) to
+ * Q8_0 blocks by TE's numpy rule (amax >= 1e-10, q = rint(x / (amax/127)),
+ * clamp +-127, fp16 scale).  out: n_rows * (n_cols/32) * 34 bytes.  -1 for
+ * other types. */
+int orc_requant_q8_0(int qt, const uint8_t *W, int n_rows, int n_cols, uint8_t *out);
+
 /* moe_ffn's expert strides (CE:593-605). */
 long orc_moe_ffn_stride(int which, int qt, int N, int M);
 

@@ -67,6 +67,8 @@ class Oracle:
         lib.orc_sem_for.restype = _ci
         lib.orc_route.argtypes = [_cf, _cf, _ci, _ci, _ci, _ci, _ci, ctypes.POINTER(ctypes.c_int), _cf]
         lib.orc_route.restype = None
+        lib.orc_requant_q8_0.argtypes = [_ci, _cu, _ci, _ci, _cu]
+        lib.orc_requant_q8_0.restype = _ci
         lib.orc_moe_ffn_stride.argtypes = [_ci, _ci, _ci, _ci]
         lib.orc_moe_ffn_stride.restype = ctypes.c_long
         lib.orc_moe_ffn_token.argtypes = [_cf, _cu, _cu, _cu, _ci, _ci, _ci, _ci, _ci, _ci, _ci, _cf, _cf]
@@ -124,6 +126,14 @@ class Oracle:
         w = np.zeros((T, K), dtype=np.float32)
         self.lib.orc_route(fp(router_w), fp(x), T, N, E, K, int(renorm), ip(idx), fp(w))
         return idx, w
+
+    def requant_q8_0(self, qt, W, n_rows, n_cols):
+        """TE:620-666: a Q4_K / Q6_K matrix requantised to raw Q8_0 blocks."""
+        out = np.zeros(n_rows * (n_cols // 32) * 34, dtype=np.uint8)
+        rc = self.lib.orc_requant_q8_0(qt, up(np.ascontiguousarray(W, dtype=np.uint8)), n_rows, n_cols, up(out))
+        if rc != 0:
+            raise ValueError(f"no requantisation for type {qt}")
+        return out
 
     def moe_ffn_stride(self, which, qt, N, M):
         return self.lib.orc_moe_ffn_stride(which, qt, N, M)

@@ -78,6 +78,42 @@ def expert_tensor(rng, qt, E, rows, cols):
     return np.concatenate([W.gen_weights(rng, qt, rows, cols) for _ in range(E)])
 
 
+def te_requantize(ref, W, qt, n_rows, n_cols):
+    """The reference caller's _requantize_output (TE:620-666) as it runs: each
+    row through the reference's own C dequantize_row, then TE's numpy Q8_0
+    quantisation, statement for statement."""
+    f32 = np.zeros((n_rows, n_cols), dtype=np.float32)
+    rb = n_cols // 256 * (144 if qt == 12 else 210)
+    fn = ref.so.q4_k_dequantize_row if qt == 12 else ref.so.q6_k_dequantize_row
+    for r in range(n_rows):
+        row = np.ascontiguousarray(W[r * rb:(r + 1) * rb])
+        fn(up(row), fp(f32[r]), n_cols)
+    n_blocks = n_cols // 32
+    blocks = f32.reshape(n_rows, n_blocks, 32)
+    amax = np.max(np.abs(blocks), axis=2, keepdims=True)
+    amax = np.clip(amax, 1e-10, None)
+    d = amax / 127.0
+    qs = np.clip(np.round(blocks / d), -127, 127).astype(np.int8)
+    d_u16 = d[:, :, 0].astype(np.float16).view(np.uint16)
+    q8 = np.zeros((n_rows, n_blocks, 34), dtype=np.uint8)
+    q8[:, :, 0] = d_u16 & 0xFF
+    q8[:, :, 1] = (d_u16 >> 8) & 0xFF
+    q8[:, :, 2:] = qs.view(np.uint8)
+    return q8.reshape(-1)
+
+
+def gen_requant(ref):
+    """lm_head requantisation fixtures: Q4_K and Q6_K matrices (one row's
+    super-blocks zeroed to exercise the amax floor) -> Q8_0."""
+    for qt, R, C, seed in ((12, 24, 768, 71), (14, 24, 768, 72)):
+        rng = np.random.default_rng(seed)
+        w = W.gen_weights(rng, qt, R, C)
+        rb = C // 256 * (144 if qt == 12 else 210)
+        w[3 * rb:4 * rb] = 0          # row 3: d = dmin = 0 -> all-zero blocks
+        out = te_requantize(ref, w, qt, R, C)
+        np.savez_compressed(os.path.join(OUT, f"requant_q8_{qt}.npz"), W=w, out=out, qt=qt, n_rows=R, n_cols=C)
+
+
 def main():
     ref = RefLib()
     ref.so.set_num_threads(1)
@@ -197,6 +233,7 @@ def main():
         assert np.all(sel.sum(1) == K)
         np.savez_compressed(os.path.join(OUT, f"route_sel_{tag}.npz"), seed=seed, N=N, E=E, K=K, T=T, M=M,
                             crc=crc(router, xs), sel=sel, ffn=ffn)
+    gen_requant(ref)
     print("golden vectors written to", OUT)
 
 

@@ -275,3 +275,30 @@ def test_batch_qkv_unknown_type_leaves_output(lib, orc):
     lib.batch_qkv_omp(up(Wq), up(Wq), up(Wv), fp(x), fp(oq), fp(ok), fp(ov), 32, 16, 16, C, 12, 7, 12)
     assert np.all(ok == 7.0)
     assert O.norm_err(ov, orc.gemv(orc.sem_for(2, 12), Wv, x, 16, C, 1)[0]) < GEMV_TOL
+
+
+@pytest.mark.parametrize("qt", [12, 14])
+def test_golden_requantize_output_q8_0(lib, golden, qt):
+    """TE's lm_head requantisation (TE:620-666) through the C ABI: bit-exact
+    with the fixture (the reference's dequantize_row + TE's numpy statements)."""
+    g = golden(f"requant_q8_{qt}.npz")
+    R, C = int(g["n_rows"]), int(g["n_cols"])
+    out = np.full(R * (C // 32) * 34, 0xAB, np.uint8)
+    assert lib.requantize_output_q8_0(up(g["W"]), R, C, qt, up(out)) == 0, K.last_error(lib)
+    assert np.array_equal(out, g["out"])
+
+
+def test_requantize_lm_head_full_shape(lib, orc):
+    """The TinyLlama lm_head (Q6_K 32000x2048): bit-exact with the oracle, and the
+    requantised Q8_0 head's logits within a Q8_0 step of the Q6_K head's."""
+    rng = np.random.default_rng(88)
+    R, C = 32000, 2048
+    w = W.gen_weights(rng, 14, R, C)
+    out = np.zeros(R * (C // 32) * 34, np.uint8)
+    assert lib.requantize_output_q8_0(up(w), R, C, 14, up(out)) == 0, K.last_error(lib)
+    assert np.array_equal(out, orc.requant_q8_0(14, w, R, C))
+    x = W.gen_x(rng, 1, C)[0]
+    q8_logits = qmm(lib, out, x, R, C, 8)
+    q6_logits = orc.gemv(K.Q6_K_GGML, w, x, R, C, 1)[0]   # the ggml order the requantisation decodes
+    assert O.norm_err(q8_logits, q6_logits) < 2e-2
+    assert lib.requantize_output_q8_0(up(w), R, C, 13, up(out)) == -1

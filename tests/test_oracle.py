@@ -120,6 +120,34 @@ def test_golden_route_selection_bitexact(orc, golden, tag):
     assert np.all(np.abs(ratio / ratio[:, :1] - 1.0) < 1e-5)
 
 
+@pytest.mark.parametrize("qt", [12, 14])
+def test_golden_requant_q8_0(orc, golden, qt):
+    """TE's lm_head requantisation (TE:620-666) as the fixture generator ran it:
+    the reference's own dequantize_row per row, then TE's numpy statements."""
+    g = golden(f"requant_q8_{qt}.npz")
+    got = orc.requant_q8_0(qt, g["W"], int(g["n_rows"]), int(g["n_cols"]))
+    assert np.array_equal(got, g["out"])
+
+
+def test_requant_q8_0_differs_from_quantize_row():
+    """TE's rule (x / d, amax floored at 1e-10) is not quantize_row_q8_0's
+    (x * (1/d), d = 1 for an all-zero block): the restatement keeps them apart
+    and stays within half a step of its input."""
+    orc = O.Oracle()
+    rng = np.random.default_rng(5)
+    R, C = 64, 512
+    w = W.gen_weights(rng, 14, R, C)
+    req = orc.requant_q8_0(14, w, R, C).reshape(R * C // 32, 34)
+    deq = orc.dequant(10, w, R, C).reshape(-1, 32)
+    d = req[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    q = req[:, 2:].view(np.int8).astype(np.float32)
+    # half a step, plus the stored scale's fp16 rounding (2^-11 relative) times |q| <= 127
+    step = np.abs(deq).max(1, keepdims=True) / 127
+    assert np.all(np.abs(q * d[:, None] - deq) <= step * (0.5 + 127 * 2.0 ** -11) * 1.001 + 1e-6)
+    row = orc.quantize_q8_0(deq.reshape(-1)).reshape(-1, 34)
+    assert not np.array_equal(row, req)
+
+
 # ----------------------------------------------------- 2. live reference
 
 @pytest.fixture(scope="module")

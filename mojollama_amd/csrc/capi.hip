@@ -160,6 +160,8 @@ struct thread_ctx {
 };
 thread_local thread_ctx t_ctx;
 
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
 // Weight cache: (host pointer, layout, rows, cols) -> packed device copy.
 struct wkey {
     const void *host;
@@ -174,6 +176,7 @@ struct wentry {
     long bytes = 0;
     uint64_t fp = 0;
     mllm_packed view;
+    int scale_flags = 0;   // mllm_launch_scale_scan of the packed copy
 };
 std::mutex g_cache_mu;
 std::map<wkey, wentry> g_cache;
@@ -206,8 +209,10 @@ std::map<std::tuple<const void *, int, int>, std::pair<float *, uint64_t>> g_rou
 std::shared_mutex g_api_mu;
 #define API_GUARD std::shared_lock<std::shared_mutex> api_guard_(g_api_mu)
 
-// Upload + pack a raw host matrix (once).  Returns its packed view.
-int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
+// Upload + pack a raw host matrix (once).  Returns its packed view and, with
+// scale_flags, the scale scan of the packed copy (mllm_launch_scale_scan, any
+// semantic of the layout: the flags depend on the bytes only).
+int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view, int *scale_flags = nullptr)
 {
     wkey k{host, ly, rows, cols};
     const long raw = raw_row_bytes(ly, cols) * rows;
@@ -216,7 +221,11 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
         std::lock_guard<std::mutex> lk(g_cache_mu);
         auto it = g_cache.find(k);
         if (it != g_cache.end()) {
-            if (it->second.fp == fpr) { view = it->second.view; return 0; }
+            if (it->second.fp == fpr) {
+                view = it->second.view;
+                if (scale_flags) *scale_flags = it->second.scale_flags;
+                return 0;
+            }
             g_retired.push_back(it->second.dev);
             g_cache.erase(it);
         }
@@ -226,21 +235,30 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view)
     wentry e;
     e.bytes = packed;
     HIP_OK(hipMalloc(&e.dev, packed));
-    void *tmp = nullptr;
+    e.view = mllm_packed_view(ly, e.dev, rows, cols);
+    uint8_t *tmp = nullptr;
     if (raw > 0) {
-        if (hipMalloc(&tmp, raw) != hipSuccess) { (void)hipFree(e.dev); set_error("hipMalloc(raw %ld) failed", raw); return -1; }
+        const long fo = align256(raw);   // the scan's flag word after the raw bytes
+        if (hipMalloc(&tmp, fo + 256) != hipSuccess) { (void)hipFree(e.dev); set_error("hipMalloc(raw %ld) failed", raw); return -1; }
+        int *fl = (int *)(tmp + fo);
+        const int sem_any = ly == LY_MXFP4 ? SEM_MXFP4 : ly == LY_Q6_K ? SEM_Q6_K_GGML : ly == LY_Q4_K ? SEM_Q4_K_GGML
+                          : ly == LY_Q5_K_GGML ? SEM_Q5_K_GGML : ly == LY_Q5_K_CE ? SEM_Q5_K_CE : ly == LY_Q8_0 ? SEM_Q8_0
+                          : ly == LY_Q4_0 ? SEM_Q4_0 : ly == LY_Q4_1 ? SEM_Q4_1 : ly == LY_Q5_0 ? SEM_Q5_0_F32 : SEM_F32;
         hipError_t r = hipMemcpyAsync(tmp, host, raw, hipMemcpyHostToDevice, c.st);
-        if (r == hipSuccess) r = mllm_launch_pack(ly, (const uint8_t *)tmp, e.dev, rows, cols, c.st);
+        if (r == hipSuccess) r = mllm_launch_pack(ly, tmp, e.dev, rows, cols, c.st);
+        if (r == hipSuccess) r = mllm_launch_fill((float *)fl, 1, 0.0f, c.st);
+        if (r == hipSuccess) r = mllm_launch_scale_scan(nullptr, &e.view, 1, sem_any, rows, cols, fl, c.st);
+        if (r == hipSuccess) r = hipMemcpyAsync(&e.scale_flags, fl, sizeof(int), hipMemcpyDeviceToHost, c.st);
         if (r == hipSuccess) r = hipStreamSynchronize(c.st);
         (void)hipFree(tmp);
         if (r != hipSuccess) { (void)hipFree(e.dev); set_error("weight upload failed: %s", hipGetErrorString(r)); return -1; }
     }
-    e.view = mllm_packed_view(ly, e.dev, rows, cols);
     e.fp = fpr;
     std::lock_guard<std::mutex> lk(g_cache_mu);
     auto ins = g_cache.emplace(k, e);
     if (!ins.second) (void)hipFree(e.dev);  // another thread uploaded it first
     view = ins.first->second.view;
+    if (scale_flags) *scale_flags = ins.first->second.scale_flags;
     return 0;
 }
 
@@ -336,7 +354,6 @@ int get_router(const float *host, int E, int N, const float **dev_out)
     return 0;
 }
 
-size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 long moe_ffn_stride(int which, int qt, int N, int M);
 
@@ -358,11 +375,12 @@ struct layer_key {
 struct layer_entry {
     mllm_packed *dtab = nullptr;
     uint64_t fp[3] = {0, 0, 0};
+    int gemv_only = 0;   // mllm_moe_needs_gemv of dtab
 };
 std::map<layer_key, layer_entry> g_layer_cache;
 
 int get_layer_table(const uint8_t *const bases[3], const int qts[3], const int sems[3], int N, int E, int M,
-                    const mllm_packed **dtab_out)
+                    const mllm_packed **dtab_out, int *gemv_only = nullptr)
 {
     layer_key k{};
     uint64_t fp[3];
@@ -374,7 +392,11 @@ int get_layer_table(const uint8_t *const bases[3], const int qts[3], const int s
     {
         std::lock_guard<std::mutex> lk(g_cache_mu);
         auto it = g_layer_cache.find(k);
-        if (it != g_layer_cache.end() && !memcmp(it->second.fp, fp, sizeof fp)) { *dtab_out = it->second.dtab; return 0; }
+        if (it != g_layer_cache.end() && !memcmp(it->second.fp, fp, sizeof fp)) {
+            *dtab_out = it->second.dtab;
+            if (gemv_only) *gemv_only = it->second.gemv_only;
+            return 0;
+        }
     }
     std::vector<mllm_packed> tab(3 * (size_t)E);
     for (int w = 0; w < 3; w++) {
@@ -386,13 +408,17 @@ int get_layer_table(const uint8_t *const bases[3], const int qts[3], const int s
     mllm_packed *d = nullptr;
     HIP_OK(hipMalloc(&d, tab.size() * sizeof(mllm_packed)));
     HIP_OK(hipMemcpy(d, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice));
+    const int go = mllm_moe_needs_gemv(d, sems[0], sems[1], sems[2], N, M, E);
+    if (go < 0) { (void)hipFree(d); set_error("MoE layer: scale scan failed"); return -1; }
     std::lock_guard<std::mutex> lk(g_cache_mu);
     auto it = g_layer_cache.find(k);
     if (it != g_layer_cache.end()) g_retired.push_back((uint8_t *)it->second.dtab);   // a call in flight may read it
     layer_entry &en = g_layer_cache[k];
     en.dtab = d;
+    en.gemv_only = go;
     memcpy(en.fp, fp, sizeof fp);
     *dtab_out = d;
+    if (gemv_only) *gemv_only = go;
     return 0;
 }
 
@@ -441,10 +467,10 @@ size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
 // out_add (optional, same layout as out, not overlapping it on the MFMA path)
 // is added to the result.
 int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_rows, int n_cols, int B,
-             void *scratch, hipStream_t st, const float *out_add = nullptr)
+             void *scratch, hipStream_t st, const float *out_add = nullptr, bool gemm_ok = true)
 {
     const bool q8 = mllm_sem_uses_q8(sem);
-    if (B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem)) {
+    if (gemm_ok && B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem)) {
         // prefill / batched: quantised-weight MFMA GEMM over the B tokens
         xq_bufs xb{};
         if (q8) {
@@ -493,7 +519,8 @@ int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows,
     if (c.init()) return -1;
     const int ly = mllm_sem_layout(sem);
     mllm_packed view;
-    if (get_weight(W, ly, n_rows, n_cols, view)) return -1;
+    int scale_flags = 0;
+    if (get_weight(W, ly, n_rows, n_cols, view, &scale_flags)) return -1;
     const size_t xbytes = (size_t)B * n_cols * 4, obytes = (size_t)B * n_rows * 4;
     if (c.d_in.ensure(xbytes) || c.d_out.ensure(obytes) || c.h_in.ensure(xbytes) || c.h_out.ensure(obytes) ||
         c.d_scr.ensure(gemv_scratch_bytes(sem, n_rows, n_cols, B))) {
@@ -502,7 +529,9 @@ int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows,
     }
     memcpy(c.h_in.p, x, xbytes);
     HIP_OK(hipMemcpyAsync(c.d_in.p, c.h_in.p, xbytes, hipMemcpyHostToDevice, c.st));
-    if (run_gemv(sem, view, (const float *)c.d_in.p, (float *)c.d_out.p, n_rows, n_cols, B, c.d_scr.p, c.st)) return -1;
+    if (run_gemv(sem, view, (const float *)c.d_in.p, (float *)c.d_out.p, n_rows, n_cols, B, c.d_scr.p, c.st, nullptr,
+                 !mllm_scales_need_gemv(sem, scale_flags)))
+        return -1;
     HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
     HIP_OK(hipStreamSynchronize(c.st));
     memcpy(out, c.h_out.p, obytes);
@@ -1234,10 +1263,11 @@ int mllm_moe_ffn_host_batched(const float *router, const uint8_t *const bases[3]
     thread_ctx &c = t_ctx;
     if (c.init()) return -1;
     const mllm_packed *dtab = nullptr;
-    if (get_layer_table(bases, qts, sems, N, E, M, &dtab)) return -1;
+    int gemv_only = 0;
+    if (get_layer_table(bases, qts, sems, N, E, M, &dtab, &gemv_only)) return -1;
     const float *rt = nullptr;
     if (get_router(router, E, N, &rt)) return -1;
-    mllm_moe_layer *L = mllm_moe_layer_from_views(sems[0], sems[1], sems[2], N, M, E, K, dtab, rt, 0, 0);
+    mllm_moe_layer *L = mllm_moe_layer_from_views(sems[0], sems[1], sems[2], N, M, E, K, dtab, rt, 0, 0, gemv_only);
     if (!L) { set_error("moe_ffn_batched: bad layer shape"); return -1; }
     // scratch: x[T][N] | out[T][N] | layer workspace
     const size_t ws = (size_t)mllm_moe_workspace_size(L, T);

@@ -376,7 +376,8 @@ MLLM_DEV float q8_dot(const raw_chunk &r, int c, const uint4 &qa, const uint4 &q
         return d * (float)(s1 * dlo + s2 * dhi) - dmin * s4sum;
     } else if constexpr (SEM == SEM_MXFP4_Q8) {
         float cs = e8m0f(r.d) * d8;
-        cs = fminf(fmaxf(cs, -1e20f), 1e20f);
+        cs = cs > 1e20f ? 1e20f : cs;      // comparisons, as QK:648-649: a NaN scale stays NaN
+        cs = cs < -1e20f ? -1e20f : cs;
         const uint32_t wv[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
         const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         int acc = 0;

@@ -69,6 +69,34 @@ __device__ __forceinline__ float mllm_silu_mul(float g, float u, bool clamp = tr
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// vmaxps(a, b): a if a > b, else b, so a NaN in either operand gives b.
+__device__ __forceinline__ float mllm_maxps(float a, float b) { return a > b ? a : b; }
+
+// quantize_row_q8_0's amax over one 32-block in the reference's vector order
+// (QK:1417-1425): eight lanes m_j fold |v[8i+j]|, i = 0..3, as
+// maxps(m_j, |v|); then maxps(m_j, m_j^4), (., j^2), (., j^1), lane 0 read.
+// Without a NaN this is max|v|; with one, amax is NaN exactly when the
+// reference's is.  fn(i) returns |v[i]|.
+__device__ __forceinline__ float mllm_q8_amax_tree(const float (&m)[8])
+{
+    const float t0 = mllm_maxps(m[0], m[4]), t1 = mllm_maxps(m[1], m[5]);
+    const float t2 = mllm_maxps(m[2], m[6]), t3 = mllm_maxps(m[3], m[7]);
+    return mllm_maxps(mllm_maxps(t0, t2), mllm_maxps(t1, t3));
+}
+
+template <class F>
+__device__ __forceinline__ float mllm_q8_amax_ref(F fn)
+{
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) m[j] = mllm_maxps(0.0f, fn(j));
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) m[j] = mllm_maxps(m[j], fn(8 * i + j));
+    return mllm_q8_amax_tree(m);
+}
+
 // Whether a launch asks for the fused activation prologue.
 inline __host__ __device__ bool mllm_has_prologue(const mllm_gemv_args &a) { return a.x_res || a.rms_w || a.res_out; }
 // Whether the persistent kernel's fused forms (prologue, paired rows) stage
@@ -119,6 +147,17 @@ hipError_t mllm_launch_read_probe(const void *p, long bytes, void *sink, hipStre
 hipError_t mllm_launch_requant_q8_0(const float *w, int n_rows, int n_cols, uint8_t *out, hipStream_t st);
 // p[i] = v, i < n (a fill kernel: nothing here records a memset node).
 hipError_t mllm_launch_fill(float *p, long n, float v, hipStream_t st);
+// ORs into *flags (device int): 1 = some block scale of the n_mats matrices in
+// tab_dev (device array; or the single host-side view `one` when tab_dev is
+// null) is inf/NaN, 2 = some E8M0 exponent is >= 178 (see k_scale_scan).
+hipError_t mllm_launch_scale_scan(const mllm_packed *tab_dev, const mllm_packed *one, int n_mats, int sem, int n_rows,
+                                  int n_cols, int *flags, hipStream_t st);
+// Whether a matrix of semantic sem whose scan gave `flags` must stay on the
+// GEMV path: the MFMA GEMMs fold block scales into bf16 weights, so a
+// non-finite scale meets zero activation planes (inf * 0 = NaN where the
+// reference's per-element product is +-inf), and the MXFP4 scale clamps
+// (QK:648-650, CE:454-456) are not applied there.
+bool mllm_scales_need_gemv(int sem, int flags);
 // out[i] += add[i], i < n.
 hipError_t mllm_launch_add(float *out, const float *add, long n, hipStream_t st);
 // out[b][r] = silu(y[b][r]) * y[b][n + r] (+ add[b][r]); y is [B][2n].

@@ -239,12 +239,13 @@ MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 }
 
 template <int SEM, bool SILU, bool PRO = false>
-MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass,
+MLLM_DEV bool stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass,
                           bool clamp, const pro_regs *pr = nullptr, const mllm_gemv_args *pa = nullptr,
                           float *part = nullptr)
 {
     const int nh = kn >> 3;
     constexpr float M = 12582912.0f;   // 1.5 * 2^23: t = y + M holds rne(y) in its low mantissa bits
+    bool any_bad = false;
 #pragma unroll
     for (int q = 0; q < kStageSlots; q++) {
         const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
@@ -266,6 +267,7 @@ MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
         m = fmaxf(m, lane_pair(m));
         sum += lane_pair(sum);
         const bool bad = !isfinite(sum);
+        any_bad |= bad;
         // P = 2^E with |x| / P < 64: E from m's exponent field
         const int E = (int)((__float_as_uint(m) >> 23) & 0xFF) - 132;
         uint32_t t[3][8];
@@ -294,6 +296,72 @@ MLLM_DEV void stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
             reinterpret_cast<float2 *>(tb + 3 * dg.PL)[g] = make_float2(P, bad ? P : sum);
         }
     }
+    return any_bad;
+}
+
+
+// The rare path of the digit staging: a group whose 16 values hold an inf or
+// NaN (or overflow their sum) was staged under P = NaN, which makes every
+// output NaN; the reference gives +-inf wherever no NaN arises.  A wave with
+// such a group stages its groups again from memory keeping each element's
+// class: a group holding +-inf gets digit +-64 for each infinite element and
+// 0 for the finite ones (their products are finite, the group's sum is not)
+// under P = +inf, which sends every chunk reading it to chunk_value's
+// per-element path; a NaN keeps P = NaN; an all-finite group whose sum
+// overflowed is staged as usual.  v = silu(x, xu) with xu, + x_res with x_res.
+template <int SEM>
+MLLM_DEV void stage_fix(uint8_t *lds, const digit_geom &dg, const float *__restrict__ x, const float *__restrict__ xu,
+                        const float *__restrict__ x_res, int ldx, int B, int k0, int kn, bool clamp)
+{
+    constexpr float M = 12582912.0f;
+    const int nh = kn >> 3, n = B * nh;
+    for (int base = 0; base < n; base += 256) {      // n even: both halves of a group stay in step
+        const int idx = base + (int)threadIdx.x;
+        if (idx >= n) break;
+        const int b = idx / nh, h = idx - b * nh, g = h >> 1, half = h & 1;
+        const long o = (long)b * ldx + k0 + 8 * h;
+        float v[8];
+        for (int e = 0; e < 8; e++) {
+            v[e] = x[o + e];
+            if (xu) v[e] = mllm_silu_mul(v[e], xu[o + e], clamp);
+            if (x_res) v[e] += x_res[o + e];
+        }
+        float m = 0.0f, sum = 0.0f, nf = 0.0f;     // nf: 1 per infinite element, 256 per NaN
+        for (int e = 0; e < 8; e++) {
+            m = fmaxf(m, fabsf(v[e]));
+            sum += v[e];
+            nf += v[e] != v[e] ? 256.0f : isinf(v[e]) ? 1.0f : 0.0f;
+        }
+        m = fmaxf(m, lane_pair(m));
+        sum += lane_pair(sum);
+        nf += lane_pair(nf);
+        const int E = (int)((__float_as_uint(m) >> 23) & 0xFF) - 132;
+        uint32_t t[3][8];
+        for (int e = 0; e < 8; e++) {
+            if (nf == 0.0f) {
+                const float y = ldexpf(v[e], -E);
+                const float t0 = y + M, r0 = y - (t0 - M);
+                const float t1 = fmaf(r0, 128.0f, M), r1 = fmaf(r0, 128.0f, M - t1);
+                t[0][e] = __float_as_uint(t0); t[1][e] = __float_as_uint(t1);
+                t[2][e] = __float_as_uint(fmaf(r1, 128.0f, M));
+            } else {
+                t[0][e] = __float_as_uint(M + (isinf(v[e]) ? copysignf(64.0f, v[e]) : 0.0f));
+                t[1][e] = t[2][e] = __float_as_uint(M);
+            }
+        }
+        uint8_t *tb = lds + b * dg.tstride;
+        for (int p = 0; p < 3; p++) {
+            uint32_t w[2];
+            for (int jj = 0; jj < 2; jj++)
+                w[jj] = pack_b0(t[p][code_pos<SEM>(jj, 0)], t[p][code_pos<SEM>(jj, 1)], t[p][code_pos<SEM>(jj, 2)],
+                                t[p][code_pos<SEM>(jj, 3)]);
+            *reinterpret_cast<uint2 *>(tb + p * dg.PL + dpad(16 * g) + 8 * half) = make_uint2(w[0], w[1]);
+        }
+        if (half == 0) {
+            const float P = nf == 0.0f ? ldexpf(1.0f, E) : nf < 256.0f ? __builtin_inff() : __int_as_float(0x7FC00000);
+            reinterpret_cast<float2 *>(tb + 3 * dg.PL)[g] = make_float2(P, nf == 0.0f ? sum : 0.0f);
+        }
+    }
 }
 
 // Stage tokens b < B, elements [k0, k0+kn), as digits; load_first = a pass-0
@@ -304,10 +372,12 @@ MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, con
                            bool clamp = true)
 {
     const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
+    bool bad = false;
     for (int pass = 0; pass < passes; pass++) {
         if (pass || !load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
-        stage_store<SEM, SILU>(st, lds, dg, B, kn, pass, clamp);
+        bad |= stage_store<SEM, SILU>(st, lds, dg, B, kn, pass, clamp);
     }
+    if (__any(bad)) stage_fix<SEM>(lds, dg, x, SILU ? xu : nullptr, nullptr, ldx, B, k0, kn, clamp);
 }
 
 // The digit words of the run starting at tile-relative element e.
@@ -386,6 +456,30 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
         // straight-line code that every lane runs.
         asm volatile("");
         t = 0.f;
+        // a group holding +-inf is staged under P = +inf with digits +-64 / 0:
+        // at P = 2^127 they rebuild +-inf / 0 (a NaN group keeps P = NaN)
+        const float P0 = x0.P > 0x1p127f ? 0x1p127f : x0.P, P1 = x1.P > 0x1p127f ? 0x1p127f : x1.P;
+        if constexpr (SEM == SEM_Q5_K_GGML) {
+            // q5_k_row_dot_avx2 factors the min out of each 32-element sub-block
+            // (QK:300, 338): d1 * sum(q x) - m1 * sum(x), here per 16-element run
+            // (o = -m1), which gives the same inf / NaN outcome
+            float qx0 = 0.f, sx0 = 0.f, qx1 = 0.f, sx1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float e0 = fmaf((float)(int8_t)(x0.w[2][j] >> (8 * q)), 0x1p-14f,
+                                          fmaf((float)(int8_t)(x0.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x0.w[0][j] >> (8 * q))));
+                    const float e1 = fmaf((float)(int8_t)(x1.w[2][j] >> (8 * q)), 0x1p-14f,
+                                          fmaf((float)(int8_t)(x1.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x1.w[0][j] >> (8 * q))));
+                    const float a0 = P0 * e0, a1 = P1 * e1;
+                    qx0 = fmaf(code_f<SEM>(k.U[j], q), a0, qx0);
+                    qx1 = fmaf(code_f<SEM>(k.U[4 + j], q), a1, qx1);
+                    sx0 += a0;
+                    sx1 += a1;
+                }
+            return fmaf(k.s0, qx0, k.o0 * sx0) + fmaf(k.s1, qx1, k.o1 * sx1);
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
@@ -396,8 +490,8 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
                                       fmaf((float)(int8_t)(x0.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x0.w[0][j] >> (8 * q))));
                 const float e1 = fmaf((float)(int8_t)(x1.w[2][j] >> (8 * q)), 0x1p-14f,
                                       fmaf((float)(int8_t)(x1.w[1][j] >> (8 * q)), 0x1p-7f, (float)(int8_t)(x1.w[0][j] >> (8 * q))));
-                t = fmaf(w0, x0.P * e0, t);
-                t = fmaf(w1, x1.P * e1, t);
+                t = fmaf(w0, P0 * e0, t);
+                t = fmaf(w1, P1 * e1, t);
             }
     }
     return t;
@@ -614,10 +708,31 @@ MLLM_DEV void q8f_store(const q8f_stage &st, bool silu, float *xl, int B, int KT
     // quant count go to LDS; the caller turns them into fp16(s * d) once s is known
     const bool prescale = pa && pa->rms_w;
     float amax = 0.0f;
+    bool nan = false;
 #pragma unroll
-    for (int k = 0; k < 8; k++) { const float a = fabsf(v[k]); amax = (a > amax) ? a : amax; }
-    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
-    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, false)));
+    for (int k = 0; k < 8; k++) {
+        const float a = fabsf(v[k]);
+        amax = (a > amax) ? a : amax;
+        nan |= a != a;
+    }
+    if (__any(nan)) {
+        // the reference's vmaxps order decides whether a NaN reaches amax: lane l
+        // of the quad holds elements 8l..8l+7, so its v[j] is the reference's
+        // lane j at step l; every lane folds the four steps from DPP broadcasts
+        float m[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int a = __float_as_int(fabsf(v[j]));
+            m[j] = mllm_maxps(0.0f, __int_as_float(__builtin_amdgcn_mov_dpp(a, 0x00, 0xF, 0xF, false)));
+            m[j] = mllm_maxps(m[j], __int_as_float(__builtin_amdgcn_mov_dpp(a, 0x55, 0xF, 0xF, false)));
+            m[j] = mllm_maxps(m[j], __int_as_float(__builtin_amdgcn_mov_dpp(a, 0xAA, 0xF, 0xF, false)));
+            m[j] = mllm_maxps(m[j], __int_as_float(__builtin_amdgcn_mov_dpp(a, 0xFF, 0xF, 0xF, false)));
+        }
+        amax = mllm_q8_amax_tree(m);
+    } else {
+        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, false)));
+    }
     float d = amax / 127.0f;
     if (d == 0.0f) d = 1.0f;
     const float id = 1.0f / d;
@@ -884,14 +999,20 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             pro_load(pr, a, B, kused, 0);
             fetch_step(min(rg, nrg - 1), it, bufA);
             const int passes = (B * (kused >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
+            bool bad = false;
             for (int pass = 0; pass < passes; pass++) {
                 if (pass) {
                     stage_load<false>(xst, xj, nullptr, a.ldx, B, 0, kused, pass);
                     pro_load(pr, a, B, kused, pass);
                 }
-                stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true, &pr, &a,
-                                              part);
+                bad |= stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true,
+                                                     &pr, &a, part);
             }
+            // with the RMS norm a non-finite value makes every output NaN, as the
+            // reference's normalised vector holds inf * 0 = NaN; without it the
+            // residual sum is staged again keeping its infinities
+            if (!a.rms_w && __any(bad))
+                stage_fix<SEM>(reinterpret_cast<uint8_t *>(xl), dg, xj, nullptr, a.x_res, a.ldx, B, 0, kused, true);
         } else {
             fetch_step(min(rg, nrg - 1), it, bufA);
             stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,

@@ -6,10 +6,23 @@
 // A MoE layer over the given semantics and per-expert packed views (device
 // array of 3*E: gate, up, down), routing from a router already in the routing
 // layout; both arrays stay the caller's and must outlive the layer's use.
-// clamp = 0 gives moe_ffn's unclamped SiLU.  Released with mllm_moe_release,
-// which frees neither array; creating one allocates nothing on the device.
+// clamp = 0 gives moe_ffn's unclamped SiLU; gemv_only (mllm_moe_needs_gemv
+// of the same table) keeps every T on the per-token GEMV path.  Released with
+// mllm_moe_release, which frees neither array; creating one allocates nothing
+// on the device.
 mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N, int M, int E, int K,
-                                          const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp);
+                                          const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp,
+                                          int gemv_only);
+
+// Whether the grouped GEMMs would depart from the reference on these weights
+// (1) or not (0); -1 on a HIP error.  They fold block scales into bf16
+// weights, so a non-finite scale meets zero activation planes (inf * 0 = NaN
+// where the reference's per-element product is +-inf); and an MXFP4 down
+// projection with Q8_0 activations whose exponent reaches 178 can meet the
+// reference's +-1e20 clamp of 2^(E-127) * d8 (QK:648-650), which the GEMMs do
+// not apply.  Such layers run on the per-token GEMV path.  Synchronous (a
+// setup-time scan of the block scales).
+int mllm_moe_needs_gemv(const mllm_packed *tab_dev, int sem_g, int sem_u, int sem_d, int N, int M, int E);
 
 // Whether the grouped-GEMM (T > 24) path serves these semantics.
 bool mllm_moe_batched_supported(int sem_g, int sem_u, int sem_d);

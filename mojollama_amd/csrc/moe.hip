@@ -215,6 +215,7 @@ struct mllm_moe_layer {
     int N, M, E, K, renorm;
     int sem_g, sem_u, sem_d;
     int clamp;          // SiLU with the gate clamped to +-80 (moe_forward_omp) or not (moe_ffn)
+    int gemv_only;      // weights the grouped GEMMs would not reproduce (mllm_moe_needs_gemv)
     int owns_router, owns_tab;
     float *router_p;    // device, routing layout (mllm_router_pack); freed with the layer when owned
     mllm_packed *tab;   // device: [E] gate, [E] up, [E] down; freed with the layer when owned
@@ -286,6 +287,7 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
     L->sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);     // Q4_K down: the reference adds zeros
     L->router_p = nullptr;
     L->tab = nullptr;
+    L->gemv_only = 0;
     std::vector<mllm_packed> tab(3 * (size_t)E);
     for (int e = 0; e < E; e++) {
         if (L->sem_g >= 0) tab[e] = mllm_packed_view(mllm_sem_layout(L->sem_g), (const uint8_t *)gate_packed[e], M, N);
@@ -297,7 +299,8 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
         hipMemcpy(L->tab, tab.data(), tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess ||
         hipMalloc(&L->router_p, rbytes) != hipSuccess ||
         mllm_launch_router_pack(router_dev, N, E, L->router_p, nullptr) != hipSuccess ||
-        hipStreamSynchronize(nullptr) != hipSuccess) {
+        hipStreamSynchronize(nullptr) != hipSuccess ||
+        (L->gemv_only = mllm_moe_needs_gemv(L->tab, L->sem_g, L->sem_u, L->sem_d, N, M, E)) < 0) {
         mllm_moe_release(L);
         return nullptr;
     }
@@ -337,7 +340,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
 
     // the grouped GEMMs need at least one quant block per row (else the decode
     // GEMVs write the reference's zeros)
-    const bool batched = T > kMoeDecodeMaxT && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
+    const bool batched = !L->gemv_only && T > kMoeDecodeMaxT && mllm_qgemm_supported(L->sem_g) && mllm_qgemm_supported(L->sem_u) &&
                          (L->sem_d < 0 || mllm_qgemm_supported(L->sem_d)) &&
                          N >= mllm_sem_block_elems(L->sem_g) && N >= mllm_sem_block_elems(L->sem_u) &&
                          (L->sem_d < 0 || M >= mllm_sem_block_elems(L->sem_d));
@@ -530,9 +533,26 @@ MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm,
 
 } // extern "C"
 
+int mllm_moe_needs_gemv(const mllm_packed *tab_dev, int sem_g, int sem_u, int sem_d, int N, int M, int E)
+{
+    int *f = nullptr, h[3] = {0, 0, 0};
+    if (hipMalloc(&f, sizeof h) != hipSuccess) return -1;
+    hipError_t r = hipMemset(f, 0, sizeof h);
+    if (r == hipSuccess && sem_g >= 0) r = mllm_launch_scale_scan(tab_dev, nullptr, E, sem_g, M, N, f, nullptr);
+    if (r == hipSuccess && sem_u >= 0) r = mllm_launch_scale_scan(tab_dev + E, nullptr, E, sem_u, M, N, f + 1, nullptr);
+    if (r == hipSuccess && sem_d >= 0)
+        r = mllm_launch_scale_scan(tab_dev + 2 * E, nullptr, E, sem_d, N, M, f + 2, nullptr);
+    if (r == hipSuccess) r = hipMemcpy(h, f, sizeof h, hipMemcpyDeviceToHost);
+    (void)hipFree(f);
+    if (r != hipSuccess) return -1;
+    return (sem_g >= 0 && mllm_scales_need_gemv(sem_g, h[0])) || (sem_u >= 0 && mllm_scales_need_gemv(sem_u, h[1])) ||
+           (sem_d >= 0 && mllm_scales_need_gemv(sem_d, h[2])) ? 1 : 0;
+}
+
 // moe_ffn's SiLU is unclamped (CE:649-652).
 mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N, int M, int E, int K,
-                                          const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp)
+                                          const mllm_packed *tab_dev, const float *router_p, int renorm, int clamp,
+                                          int gemv_only)
 {
     if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0 || !tab_dev || !router_p) return nullptr;
     mllm_moe_layer *L = new mllm_moe_layer;
@@ -543,6 +563,7 @@ mllm_moe_layer *mllm_moe_layer_from_views(int sem_g, int sem_u, int sem_d, int N
     L->sem_g = sem_g; L->sem_u = sem_u; L->sem_d = sem_d;
     L->router_p = const_cast<float *>(router_p);
     L->tab = const_cast<mllm_packed *>(tab_dev);
+    L->gemv_only = gemv_only;
     return L;
 }
 

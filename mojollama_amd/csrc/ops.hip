@@ -73,7 +73,8 @@ __global__ void k_pack(int ly, const uint8_t *__restrict__ raw, uint8_t *__restr
 
 // ---------------------------------------------------------------- quantise
 // One thread per 32-element block.  Mirrors quantize_row_q8_0 (QK:1406-1455):
-// amax, d = amax/127 (1 if 0), id = 1/d, q = RNE(clamp(x*id, +-127)) with a
+// amax (in the reference's vmaxps order, which decides whether a NaN reaches
+// it), d = amax/127 (1 if 0), id = 1/d, q = RNE(clamp(x*id, +-127)) with a
 // NaN product clamped to -127 (maxps returns its second operand), scale
 // stored as fp16 RNE.
 __global__ void k_quantize_q8_0(const float *__restrict__ x, int T, int n_cols, uint8_t *__restrict__ q8_raw,
@@ -94,9 +95,7 @@ __global__ void k_quantize_q8_0(const float *__restrict__ x, int T, int n_cols, 
 #pragma unroll
         for (int k = 0; k < 32; k++) v[k] = s[k];
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) { float a = fabsf(v[k]); amax = (a > amax) ? a : amax; }
+    const float amax = mllm_q8_amax_ref([&](int k) { return fabsf(v[k]); });
     float d = amax / 127.0f;
     if (d == 0.0f) d = 1.0f;
     const float id = 1.0f / d;
@@ -821,6 +820,41 @@ __global__ void k_fill_f32(float *__restrict__ p, long n, float v)
     if (i < n) p[i] = v;
 }
 
+// Scale scan of n_mats packed matrices (tab, or the one view) of layout ly,
+// nblk blocks each: *flags |= 1 when a block scale is not finite (fp16
+// exponent 31, or an E8M0 byte of 255), |= 2 when an E8M0 byte is >= 178:
+// there 2^(E-127) times the largest fp16 Q8_0 scale (65504) can exceed 1e20,
+// where mxfp4_row_dot_q8 clamps the combined scale (QK:648-650), and from
+// E = 194 on mxfp4_batch_matmul's scale clamp to 1e20 (CE:454-456) gives
+// weights no longer exact in bf16.
+__global__ void k_scale_scan(const mllm_packed *__restrict__ tab, mllm_packed one, int ly, long nblk,
+                             int *__restrict__ flags)
+{
+    const mllm_packed v = tab ? tab[blockIdx.y] : one;
+    int f = 0;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nblk; i += (long)gridDim.x * blockDim.x) {
+        auto h = [&](int plane, int stride, int off) {
+            const uint8_t *q = v.p[plane] + i * stride + off;
+            return ((q[0] | (q[1] << 8)) & 0x7C00) == 0x7C00;
+        };
+        switch (ly) {
+        case LY_Q4_0: case LY_Q8_0: f |= h(1, 2, 0); break;
+        case LY_Q4_1: f |= h(1, 4, 0) | h(1, 4, 2); break;
+        case LY_Q5_0: f |= h(2, 2, 0); break;
+        case LY_Q4_K: f |= h(1, 16, 0) | h(1, 16, 2); break;
+        case LY_Q5_K_GGML: case LY_Q5_K_CE: f |= h(2, 16, 0) | h(2, 16, 2); break;
+        case LY_Q6_K: f |= h(3, 2, 0); break;
+        case LY_MXFP4: {
+            const uint8_t e = v.p[1][i];
+            f |= (e == 255 ? 1 : 0) | (e >= 178 ? 2 : 0);
+            break;
+        }
+        default: break;
+        }
+    }
+    if (f) atomicOr(flags, f);
+}
+
 // out[i] += add[i], i < n (the residual epilogue of launches that cannot fuse it).
 __global__ void k_add(float *__restrict__ out, const float *__restrict__ add, long n)
 {
@@ -1044,6 +1078,23 @@ hipError_t mllm_launch_fill(float *p, long n, float v, hipStream_t st)
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n, v);
     return hipGetLastError();
+}
+
+hipError_t mllm_launch_scale_scan(const mllm_packed *tab_dev, const mllm_packed *one, int n_mats, int sem, int n_rows,
+                                  int n_cols, int *flags, hipStream_t st)
+{
+    const int ly = mllm_sem_layout(sem);
+    const long nblk = (long)n_rows * (n_cols / mllm_layout_info(ly).block_elems);
+    if (n_mats <= 0 || nblk <= 0 || ly == LY_F32 || (!tab_dev && !one)) return hipSuccess;
+    const unsigned gx = (unsigned)std::min<long>((nblk + 255) / 256, 64);
+    hipLaunchKernelGGL(k_scale_scan, dim3(gx, tab_dev ? (unsigned)n_mats : 1u), dim3(256), 0, st, tab_dev,
+                       tab_dev ? mllm_packed{} : *one, ly, nblk, flags);
+    return hipGetLastError();
+}
+
+bool mllm_scales_need_gemv(int sem, int flags)
+{
+    return (flags & 1) || ((sem == SEM_MXFP4_Q8 || sem == SEM_MXFP4_CLAMP) && (flags & 2));
 }
 
 hipError_t mllm_launch_add(float *out, const float *add, long n, hipStream_t st)

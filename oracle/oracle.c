@@ -281,17 +281,30 @@ int orc_dequant_row(int sem, const uint8_t *row, float *w, int n_cols)
 
 /* --------------------------------------------- activation quantisation */
 
+/* maxps(a, b) (vmaxps): a if a > b, else b, so a NaN in either operand
+ * gives the second operand. */
+static float maxps(float a, float b) { return a > b ? a : b; }
+
 /* quantize_row_q8_0 (QK:1406-1455): per 32: amax, d = amax/127 (1 if 0),
  * id = 1/d, q = RNE(clamp(x*id, +-127)); stored scale fp16_RNE(d).
- * A NaN product clamps to -127 (maxps returns its second operand). */
+ * amax follows the reference's vector order, which only matters for NaN:
+ * eight lanes m_j fold |x_{8i+j}| for i = 0..3 as maxps(m_j, |x|)
+ * (QK:1417-1421), then the halves, pairs and neighbours combine as
+ * maxps(m_j, m_{j^4}), maxps(., j^2), maxps(., j^1) (QK:1423-1425), lane 0
+ * read.  A NaN product clamps to -127 (maxps returns its second operand). */
 int orc_quantize_row_q8_0(const float *x, uint8_t *q8, int n_cols)
 {
     int nb = n_cols / 32;
     for (int b = 0; b < nb; b++) {
         const float *s = x + 32 * b;
         uint8_t *dst = q8 + 34 * b;
-        float amax = 0.0f;
-        for (int i = 0; i < 32; i++) { float a = fabsf(s[i]); if (a > amax) amax = a; }
+        float m[8], t[8], u[8];
+        for (int j = 0; j < 8; j++) m[j] = 0.0f;
+        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 8; j++) m[j] = maxps(m[j], fabsf(s[8 * i + j]));
+        for (int j = 0; j < 8; j++) t[j] = maxps(m[j], m[j ^ 4]);
+        for (int j = 0; j < 8; j++) u[j] = maxps(t[j], t[j ^ 2]);
+        float amax = maxps(u[0], u[1]);
         float d = amax / 127.0f;
         if (d == 0.0f) d = 1.0f;
         float id = 1.0f / d;
@@ -363,6 +376,37 @@ static float dot_q5_0_q8_blk(const uint8_t *b, const uint8_t *q8blk)
 
 /* ------------------------------------------------------------- GEMV */
 
+/* q5_k_row_dot_avx2 (QK:249-344) on one super-block: per 32-element
+ * sub-block d1 * sum(q x) - m1 * sum(x) with d1 = d*sc, m1 = dmin*m in fp32
+ * (QK:266-269, 300, 338): the min term factored out of the sum, which is
+ * what decides the result when x holds an inf (inf - inf = NaN where a
+ * per-element w*x would give +-inf). */
+static double dot_q5_k_ggml_sb(const uint8_t *b, const float *x)
+{
+    float d = ld_f16(b), dm = ld_f16(b + 2);
+    const uint8_t *sc = b + 4, *qh = b + 16, *qs = b + 48;
+    double acc = 0.0;
+    for (int g = 0; g < 4; g++) {
+        int s1, m1, s2, m2;
+        k4_pair(2 * g, sc, &s1, &m1);
+        k4_pair(2 * g + 1, sc, &s2, &m2);
+        float d1 = d * (float)s1, mm1 = dm * (float)m1;
+        float d2 = d * (float)s2, mm2 = dm * (float)m2;
+        double qx1 = 0, sx1 = 0, qx2 = 0, sx2 = 0;
+        for (int k = 0; k < 32; k++) {
+            int lo = (qs[32 * g + k] & 15) + (((qh[k] >> (2 * g)) & 1) << 4);
+            int hi = (qs[32 * g + k] >> 4) + (((qh[k] >> (2 * g + 1)) & 1) << 4);
+            qx1 += (double)lo * x[64 * g + k];
+            sx1 += x[64 * g + k];
+            qx2 += (double)hi * x[64 * g + 32 + k];
+            sx2 += x[64 * g + 32 + k];
+        }
+        acc += (double)d1 * qx1 - (double)mm1 * sx1;
+        acc += (double)d2 * qx2 - (double)mm2 * sx2;
+    }
+    return acc;
+}
+
 void orc_gemv(int sem, const uint8_t *W, const float *x, float *out,
               int n_rows, int n_cols, int B)
 {
@@ -386,6 +430,16 @@ void orc_gemv(int sem, const uint8_t *W, const float *x, float *out,
             }
         }
         free(xq);
+        return;
+    }
+    if (sem == ORC_Q5_K_GGML) {
+        for (int r = 0; r < n_rows; r++)
+            for (int b = 0; b < B; b++) {
+                double acc = 0.0;
+                for (int s = 0; s < n_cols / 256; s++)
+                    acc += dot_q5_k_ggml_sb(W + (long)r * rb + 176L * s, x + (long)b * n_cols + 256L * s);
+                out[(long)b * n_rows + r] = (float)acc;
+            }
         return;
     }
     float *w = (float *)malloc((size_t)(n_cols > 0 ? n_cols : 1) * sizeof(float));

@@ -2,7 +2,8 @@
 (oracle/_ref/libref.so, compiled in place from /root/reference by
 oracle/Makefile) on small seeded inputs.
 
-Usage:  python tests/golden/make_golden.py        (from the repo root)
+Usage:  python tests/golden/make_golden.py [group]   (from the repo root;
+        group = gen_requant or gen_nonfinite writes that group only)
 
 Outputs (committed): tests/golden/*.npz.  Each file holds the inputs and the
 reference's outputs, so the tests need neither the reference tree nor
@@ -112,6 +113,37 @@ def gen_requant(ref):
         w[3 * rb:4 * rb] = 0          # row 3: d = dmin = 0 -> all-zero blocks
         out = te_requantize(ref, w, qt, R, C)
         np.savez_compressed(os.path.join(OUT, f"requant_q8_{qt}.npz"), W=w, out=out, qt=qt, n_rows=R, n_cols=C)
+
+
+def gen_nonfinite(ref):
+    """Non-finite activations: quantize_row_q8_0 with NaN / +-inf at every
+    block position (its vmaxps order decides when amax itself turns NaN),
+    and moe_forward_omp on tokens holding a NaN or an inf."""
+    rng = np.random.default_rng(73)
+    x = W.gen_x(rng, 1, 4096)[0].copy()
+    for b in range(96):
+        x[32 * b + b % 32] = (np.nan, np.inf, -np.inf)[b // 32]
+    for b in range(96, 128):
+        pos = rng.choice(32, size=int(rng.integers(2, 6)), replace=False)
+        x[32 * b + pos] = rng.choice([np.nan, np.inf, -np.inf], size=pos.size)
+    np.savez_compressed(os.path.join(OUT, "q8_0_nonfinite.npz"), x=x, q8=ref.quantize_q8_0(x))
+
+    for tag, qts, n_embd, n_ff in (("gptoss", (39, 39, 39), 192, 160), ("qwen", (12, 12, 14), 256, 256)):
+        E = 2
+        gates = [W.gen_weights(rng, qts[0], n_ff, n_embd) for _ in range(E)]
+        ups = [W.gen_weights(rng, qts[1], n_ff, n_embd) for _ in range(E)]
+        downs = [W.gen_weights(rng, qts[2], n_embd, n_ff) for _ in range(E)]
+        xs, outs = [], []
+        for pos, val in ((0, np.nan), (31, np.nan), (n_embd - 1, np.nan), (5, np.inf), (n_embd // 2, -np.inf)):
+            xt = W.gen_x(rng, 1, n_embd)[0].copy()
+            xt[pos] = val
+            xs.append(xt)
+            outs.append(ref.moe_forward(gates, ups, downs, xt, n_ff, n_embd, qts, np.array([1, 0], np.int32),
+                                        np.array([0.625, 0.375], np.float32)))
+        np.savez_compressed(os.path.join(OUT, f"moe_forward_nonfinite_{tag}.npz"), gates=np.stack(gates),
+                            ups=np.stack(ups), downs=np.stack(downs), x=np.stack(xs), out=np.stack(outs),
+                            top_idx=np.array([1, 0], np.int32), top_w=np.array([0.625, 0.375], np.float32),
+                            n_embd=n_embd, n_ff=n_ff, qts=np.array(qts))
 
 
 def main():
@@ -234,8 +266,15 @@ def main():
         np.savez_compressed(os.path.join(OUT, f"route_sel_{tag}.npz"), seed=seed, N=N, E=E, K=K, T=T, M=M,
                             crc=crc(router, xs), sel=sel, ffn=ffn)
     gen_requant(ref)
+    gen_nonfinite(ref)
     print("golden vectors written to", OUT)
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1:
+        # one group only, e.g. `make_golden.py gen_nonfinite`
+        _ref = RefLib()
+        _ref.so.set_num_threads(1)
+        globals()[sys.argv[1]](_ref)
+    else:
+        main()

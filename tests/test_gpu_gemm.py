@@ -48,6 +48,39 @@ def test_batch_matmul_gemm_vs_oracle(lib, orc, name, qt, B):
     assert O.norm_err(got, orc.gemv(orc.sem_for(1, qt), w, x, R, C, B)) < GEMM_TOL
 
 
+def same_nonfinite(got, ref, tol):
+    if not (np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])):
+        return False
+    fin = np.isfinite(ref)
+    return not fin.any() or O.norm_err(got[fin], ref[fin]) < tol
+
+
+@pytest.mark.parametrize("name,qt", [("q4_0", 2), ("q8_0", 8), ("q4_k", 12), ("q6_k", 14), ("q5_k", 13),
+                                     ("mxfp4", 39)])
+def test_batch_matmul_large_B_nonfinite_scales(lib, orc, name, qt):
+    """B = 16 with inf / NaN block scales (E8M0 255, or 194 where
+    mxfp4_batch_matmul's 1e20 clamp bites): the weight cache's scale scan keeps
+    such a matrix off the MFMA GEMM, whose bf16 weights would turn inf * 0
+    into NaN and would not apply the clamp; outputs match the oracle's
+    per-element weighting exactly in their NaN / inf pattern."""
+    rng = np.random.default_rng(930 + qt)
+    be, bb = W.BLOCK[qt]
+    R, C, B = 24, 768 if be == 256 else 800, 16
+    w = W.gen_weights(rng, qt, R, C).reshape(R, C // be, bb)
+    if qt == 39:
+        for row, blk, e in ((3, 1, 255), (6, 0, 194), (9, 2, 230)):
+            w[row, blk, 16] = e
+    else:
+        d_off = 208 if qt == W.QT_Q6_K else 0
+        for row, blk, bits in ((3, 1, 0x7C00), (6, 0, 0x7E00), (9, 2, 0xFC00)):
+            w[row, blk, d_off:d_off + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    w = np.ascontiguousarray(w.ravel())
+    x = W.gen_x(rng, B, C)
+    got = bmm(lib, name, w, x, R, C, B)
+    ref = orc.gemv(orc.sem_for(1, qt), w, x, R, C, B)
+    assert same_nonfinite(got, ref, GEMM_TOL)
+
+
 @pytest.mark.parametrize("sem", [K.Q4_0, K.Q4_1, K.Q5_0_F32, K.Q8_0, K.Q4_K_GGML, K.Q4_K_Q8, K.Q5_K_GGML, K.Q5_K_CE,
                                  K.Q6_K_GGML, K.Q6_K_LOWNIB, K.Q6_K_SEQ, K.MXFP4, K.MXFP4_CLAMP, K.MXFP4_Q8])
 def test_device_gemm_every_semantic(dev, orc, sem):

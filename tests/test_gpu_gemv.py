@@ -81,6 +81,15 @@ def test_golden_quantize_q8_0_bitexact(lib, golden):
     assert np.array_equal(q, g["q8"])
 
 
+def test_golden_quantize_q8_0_nonfinite_bitexact(lib, golden):
+    """NaN / +-inf activations: bit-exact with the reference, including the
+    blocks whose amax its vmaxps order turns NaN."""
+    g = golden("q8_0_nonfinite.npz")
+    q = np.zeros_like(g["q8"])
+    lib.quantize_row_q8_0(fp(g["x"]), up(q), g["x"].size)
+    assert np.array_equal(q, g["q8"])
+
+
 @pytest.mark.parametrize("name", ["q4_k", "q6_k", "q5_k", "q8_0"])
 def test_golden_dequantize_row_bitexact(lib, golden, name):
     g = golden(f"deq_{name}.npz")
@@ -162,6 +171,65 @@ def test_device_gemv_nonfinite_scales(dev, orc, sem, B):
     assert np.array_equal(got[inf], ref[inf])
     fin = np.isfinite(ref)
     assert O.norm_err(got[fin], ref[fin]) < GEMV_TOL, (K.SEM_NAMES[sem], B)
+
+
+@pytest.mark.parametrize("sem", [K.F32, K.Q4_0, K.Q4_1, K.Q5_0_F32, K.Q8_0, K.Q4_K_GGML, K.Q5_K_GGML, K.Q5_K_CE,
+                                 K.Q6_K_GGML, K.Q6_K_LOWNIB, K.Q6_K_SEQ, K.MXFP4, K.MXFP4_CLAMP])
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_device_gemv_nonfinite_activations(dev, orc, sem, B):
+    """fp32-activation semantics on tokens holding +-inf / NaN: a staged
+    16-element group keeps each element's class, and the per-element path
+    weighs it as the reference does (Q5_K ggml with its min term factored
+    out, QK:300,338), so NaN / inf land on the same outputs as the oracle's."""
+    import torch
+    rng = np.random.default_rng(95 + 16 * B + sem)
+    qt = SEM_QT[sem]
+    R, C = 40, 1024
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, B, C).copy()
+    for b in range(B):
+        if b % 3 == 0:
+            x[b, 5 + 64 * b] = np.inf
+        elif b % 3 == 1:
+            x[b, 200 + b] = -np.inf
+            x[b, 301] = np.inf
+        else:
+            x[b, 17] = np.nan
+    ref = orc.gemv(sem, w, x, R, C, B).reshape(B, R)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy().reshape(B, R)
+    if sem != K.Q5_K_GGML:   # there d1 * inf - m1 * inf is NaN whenever d1, m1 > 0
+        assert not np.all(np.isnan(ref)), "an inf token must give +-inf somewhere for the test to mean something"
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (K.SEM_NAMES[sem], B)
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf]), (K.SEM_NAMES[sem], B)
+
+
+@pytest.mark.parametrize("sem", [K.Q4_K_Q8, K.Q5_0_Q8, K.MXFP4_Q8])
+@pytest.mark.parametrize("B", [1, 4])
+def test_device_gemv_q8_activation_nonfinite(dev, orc, sem, B):
+    """Q8_0-activation semantics on activations holding NaN / +-inf at block
+    positions 0, 7, 24 and 31 (the vmaxps order makes only some of them reach
+    amax): NaN / inf pattern exact, finite outputs within tolerance."""
+    import torch
+    rng = np.random.default_rng(91 + 16 * B + sem)
+    qt = SEM_QT[sem]
+    R, C = 40, 1024
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, B, C).copy()
+    for b in range(B):
+        for blk, pos, val in ((1, 0, np.nan), (3, 31, np.nan), (5, 24, np.inf), (8, 7, -np.inf), (12, 31, np.inf)):
+            if (blk + b) % 3:
+                x[b, 32 * (blk + 4 * b) + pos] = val
+    ref = orc.gemv(sem, w, x, R, C, B).reshape(B, R)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy().reshape(B, R)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (K.SEM_NAMES[sem], B)
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf])
+    fin = np.isfinite(ref)
+    if fin.any():
+        assert O.norm_err(got[fin], ref[fin]) < GEMV_TOL, (K.SEM_NAMES[sem], B)
 
 
 @pytest.mark.parametrize("sem", [K.Q4_0, K.Q4_1, K.Q5_0_F32, K.Q8_0, K.Q4_K_GGML, K.Q5_K_GGML, K.Q5_K_CE,

@@ -118,6 +118,23 @@ def test_golden_moe_forward(lib, golden, tag):
     assert O.norm_err(got, g["out"]) < MOE_TOL, K.last_error(lib)
 
 
+@pytest.mark.parametrize("tag", ["qwen", "gptoss"])
+def test_golden_moe_forward_nonfinite(lib, golden, tag):
+    """Tokens holding a NaN or an inf: NaN / inf outputs where the reference
+    has them (its Q8_0 amax order, the +-80 clamp passing NaN), finite ones
+    within tolerance."""
+    g = golden(f"moe_forward_nonfinite_{tag}.npz")
+    qts = tuple(int(v) for v in g["qts"])
+    for i, (x, ref) in enumerate(zip(g["x"], g["out"])):
+        got = moe_forward(lib, list(g["gates"]), list(g["ups"]), list(g["downs"]), x, int(g["n_ff"]),
+                          int(g["n_embd"]), qts, g["top_idx"], g["top_w"])
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), (tag, i)
+        assert np.array_equal(np.isinf(got), np.isinf(ref)), (tag, i)
+        fin = np.isfinite(ref)
+        if fin.any():
+            assert O.norm_err(got[fin], ref[fin]) < moe_tol(qts), (tag, i)
+
+
 @pytest.mark.parametrize("tag", ["q4k", "mxfp4"])
 def test_golden_moe_ffn(lib, golden, tag):
     g = golden(f"moe_ffn_{tag}.npz")
@@ -195,12 +212,14 @@ def test_bucketing_stable_and_exact(dev):
     assert np.all(cover == 1)
 
 
-def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False):
+def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False, plant=None):
     import torch
     rng = np.random.default_rng(seed)
     gates = [W.gen_weights(rng, qts[0], M, N) for _ in range(E)]
     ups = [W.gen_weights(rng, qts[1], M, N) for _ in range(E)]
     downs = [W.gen_weights(rng, qts[2], N, M) for _ in range(E)]
+    if plant:
+        plant(gates, ups, downs)
     router = W.gen_router(rng, E, N)
     if skew:
         x, router, _, _ = W.skewed_tokens(rng, router, T)
@@ -217,6 +236,35 @@ def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False):
     assert np.max(np.abs(w.cpu().numpy() - rw) / np.abs(rw)) < 1e-6
     ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in range(T)])
     return got, ref
+
+
+def _plant_mxfp4_exponents(tensor, e_byte):
+    """Set the E8M0 byte of a few MXFP4 blocks in every expert of one tensor."""
+    def plant(gates, ups, downs):
+        for a in {"gate": gates, "down": downs}[tensor]:
+            a.reshape(-1, 17)[[3, 40, 77], 16] = e_byte
+    return plant
+
+
+@pytest.mark.parametrize("tensor,e_byte", [("down", 200), ("down", 255), ("gate", 255)])
+def test_moe_layer_batched_extreme_exponents(dev, orc, tensor, e_byte):
+    """T = 40 (the grouped-GEMM range) with MXFP4 exponents the GEMMs would not
+    reproduce: an inf scale (255), or a down-projection exponent where
+    mxfp4_row_dot_q8 clamps 2^(E-127) * d8 to +-1e20 (QK:648-650).  The layer's
+    setup-time scale scan keeps it on the per-token GEMV path: NaN / inf where
+    the oracle has them, finite outputs within tolerance."""
+    qts = (39, 39, 39)
+    # M = 2880 (GPT-OSS): one Q8_0 flip of h moves an output by ~3 / (127 sqrt(M)) of its max
+    got, ref = _moe_case(dev, orc, qts, N=256, M=2880, E=8, Kk=2, T=40, renorm=0, seed=e_byte,
+                         plant=_plant_mxfp4_exponents(tensor, e_byte))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf])
+    fin = np.isfinite(ref)
+    big = np.abs(ref) > 1e18
+    assert O.norm_err(got[fin & ~big], ref[fin & ~big]) < moe_tol(qts)
+    if (fin & big).any():
+        assert np.max(np.abs(got[fin & big] / ref[fin & big] - 1)) < 1e-3
 
 
 @pytest.mark.parametrize("qts", [(12, 12, 14), (39, 39, 39), (14, 14, 2)])

@@ -83,6 +83,30 @@ def test_golden_batch_qkv_and_gate_up(orc, golden):
         assert O.norm_err(got, o) < TOL
 
 
+def test_golden_quantize_q8_0_nonfinite_bitexact(orc, golden):
+    """NaN / +-inf at every block position: amax turns NaN only where the
+    reference's vmaxps order lets it (QK:1417-1425)."""
+    g = golden("q8_0_nonfinite.npz")
+    assert np.array_equal(orc.quantize_q8_0(g["x"]), g["q8"])
+
+
+def same_nonfinite(got, ref, tol):
+    """NaN and inf at the same places, finite values within tol (normalised)."""
+    if not (np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref))):
+        return False
+    fin = np.isfinite(ref)
+    return not fin.any() or O.norm_err(got[fin], ref[fin]) < tol
+
+
+@pytest.mark.parametrize("tag", ["qwen", "gptoss"])
+def test_golden_moe_forward_nonfinite(orc, golden, tag):
+    g = golden(f"moe_forward_nonfinite_{tag}.npz")
+    for x, out in zip(g["x"], g["out"]):
+        got = orc.moe_forward_token(list(g["gates"]), list(g["ups"]), list(g["downs"]), x, int(g["n_ff"]),
+                                    int(g["n_embd"]), tuple(int(v) for v in g["qts"]), g["top_idx"], g["top_w"])
+        assert same_nonfinite(got, out, TOL)
+
+
 @pytest.mark.parametrize("tag", ["qwen", "gptoss"])
 def test_golden_moe_forward(orc, golden, tag):
     g = golden(f"moe_forward_{tag}.npz")
@@ -183,6 +207,80 @@ def test_live_quantize_q8_0(orc, ref):
     rng = np.random.default_rng(7)
     x = (rng.standard_normal(1 << 16) * np.exp(rng.uniform(-8, 8, 1 << 16))).astype(np.float32)
     assert np.array_equal(orc.quantize_q8_0(x), ref.quantize_q8_0(x))
+
+
+def test_live_quantize_q8_0_nonfinite(orc, ref):
+    rng = np.random.default_rng(8)
+    x = W.gen_x(rng, 1, 32 * 2048)[0].copy()
+    pos = rng.choice(x.size, size=3000, replace=False)
+    x[pos] = rng.choice([np.nan, np.inf, -np.inf, 0.0, 3e38], size=pos.size)
+    assert np.array_equal(orc.quantize_q8_0(x), ref.quantize_q8_0(x))
+
+
+@pytest.mark.parametrize("qt", [2, 3, 6, 8, 12, 13, 14, 39])
+def test_live_nonfinite_block_scales(orc, ref, qt):
+    """inf / NaN fp16 scales and mins (E8M0 255 for MXFP4) through
+    quant_matmul_omp (B = 1) and *_batch_matmul (B = 3): NaN / inf at the same
+    outputs as the reference, finite outputs within tolerance."""
+    rng = np.random.default_rng(5 + qt)
+    be, bb = W.BLOCK[qt]
+    R, C = 24, 768 if be == 256 else 800
+    w = W.gen_weights(rng, qt, R, C).reshape(R, C // be, bb)
+    if qt == 39:
+        w[3, 1, 16] = w[6, 0, 16] = 255
+    else:
+        d_off = 208 if qt == W.QT_Q6_K else 0
+        for row, blk, bits in ((3, 1, 0x7C00), (6, 0, 0x7E00), (9, 2, 0xFC00)):
+            w[row, blk, d_off:d_off + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+        if qt in (3, 12, 13):
+            w[12, 1, 2:4] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)
+    w = np.ascontiguousarray(w.ravel())
+    x = W.gen_x(rng, 3, C)
+    for b in range(3):
+        assert same_nonfinite(orc.gemv(orc.sem_for(0, qt), w, x[b], R, C, 1)[0],
+                              ref.quant_matmul(w, x[b], R, C, qt), 1e-5), b
+    name = {2: "q4_0", 8: "q8_0", 12: "q4_k", 14: "q6_k", 13: "q5_k", 39: "mxfp4"}.get(qt)
+    if name:
+        assert same_nonfinite(orc.gemv(orc.sem_for(1, qt), w, x, R, C, 3).ravel(),
+                              ref.batch_matmul(name + "_batch_matmul", w, x, R, C, 3).ravel(), 1e-5)
+
+
+@pytest.mark.parametrize("qt", [0, 2, 3, 6, 8, 12, 13, 14, 39])
+def test_live_quant_matmul_nonfinite_activations(orc, ref, qt):
+    """inf / NaN activations: every quant_matmul_omp code (B = 1) and
+    *_batch_matmul (B = 3) give NaN / inf at the same outputs as the reference."""
+    rng = np.random.default_rng(60 + qt)
+    R, C = 32, 512
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, 3, C).copy()
+    x[0, 5], x[1, 200], x[1, 301], x[2, 17] = np.inf, -np.inf, np.inf, np.nan
+    for b in range(3):
+        got = orc.gemv(orc.sem_for(0, qt), w, x[b], R, C, 1)[0]
+        want = ref.quant_matmul(w, x[b], R, C, qt)
+        assert same_nonfinite(got, want, 1e-5), b
+    name = {2: "q4_0", 8: "q8_0", 12: "q4_k", 14: "q6_k", 13: "q5_k", 39: "mxfp4"}.get(qt)
+    if name:
+        got = orc.gemv(orc.sem_for(1, qt), w, x, R, C, 3)
+        want = ref.batch_matmul(name + "_batch_matmul", w, x, R, C, 3)
+        assert same_nonfinite(got.ravel(), want.ravel(), 1e-5)
+
+
+@pytest.mark.parametrize("qts", [(39, 39, 39), (12, 12, 14), (14, 14, 14), (39, 39, 14), (2, 2, 2), (6, 6, 14)])
+def test_live_moe_forward_nonfinite(orc, ref, qts):
+    rng = np.random.default_rng(sum(qts))
+    n_embd, n_ff = 512, 256
+    gates = [W.gen_weights(rng, qts[0], n_ff, n_embd) for _ in range(3)]
+    ups = [W.gen_weights(rng, qts[1], n_ff, n_embd) for _ in range(3)]
+    downs = [W.gen_weights(rng, qts[2], n_embd, n_ff) for _ in range(3)]
+    ti = np.array([2, 0], np.int32)
+    for pos in (0, 31, 100, 511):
+        for val in (np.nan, np.inf, -np.inf):
+            x = W.gen_x(rng, 1, n_embd)[0].copy()
+            x[pos] = val
+            for tw in (np.array([0.6, 0.4], np.float32), np.array([np.nan, np.nan], np.float32)):
+                a = ref.moe_forward(gates, ups, downs, x, n_ff, n_embd, qts, ti, tw)
+                b = orc.moe_forward_token(gates, ups, downs, x, n_ff, n_embd, qts, ti, tw)
+                assert same_nonfinite(b, a, 1e-4), (pos, val, tw)
 
 
 def test_live_moe_forward_null_q8_scratch_differs_only_for_mxfp4_down(orc, ref):

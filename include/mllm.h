@@ -99,6 +99,19 @@ MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_o
  * the reference's C library: the routine TE would call in place of its loop. */
 MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, int quant_type, uint8_t *out);
 
+/* gqa_attention.c:93 gqa_attention_decode: decode attention of one token.
+ * q [n_head][head_dim]; k_cache / v_cache [seq_len][n_kv_head][head_dim];
+ * query head h reads KV head h / (n_head / n_kv_head); out [n_head][head_dim].
+ * Scores (q . k) / sqrtf(head_dim); softmax_simd (gqa_attention.c:50-88):
+ * maximum from -1e30, the first floor(seq_len/8)*8 weights by the source's
+ * exp_ps_simd polynomial on (s - max) clamped to [-80, 80], the rest expf
+ * capped at 1e38, normalised by 1 / (sum + 1e-10).  workspace is not written
+ * (the reference keeps its weights there; nothing reads them back).  Host
+ * pointers: q, K and V are uploaded on every call, so the device entry
+ * mllm_gqa_decode is the fast path.  seq_len <= 0 gives zeros. */
+MLLM_API void gqa_attention_decode(const float *q, const float *k_cache, const float *v_cache, float *out, int seq_len,
+                                   int n_head, int n_kv_head, int head_dim, float *workspace);
+
 /* QK:1029-1030: accepted and ignored / number of compute units. */
 MLLM_API void set_num_threads(int n);
 MLLM_API int get_max_threads(void);
@@ -236,6 +249,62 @@ MLLM_API int mllm_moe_forward_noalloc(const mllm_moe_layer *layer, const float *
  * tiles = 3 arrays of (TK/64 + E + 1) ints (expert, begin, end) + count. */
 MLLM_API int mllm_moe_bucket(const int *idx, int TK, int E, int *off, int *perm, int *pos_of, int *tiles,
                              void *stream);
+
+/* ------------------------------------------------ decode attention, KV cache */
+/* A KV cache on the device.  Rows hold n_kv_head * head_dim floats; V mirrors
+ * K's layout.  Contiguous (block_tables == NULL): row s of sequence b at
+ * k + b * seq_stride + s * n_kv_head * head_dim (GO:158-161).  Paged
+ * (CE:160-214, PagedAttention): sequence b's logical page s / page_size maps
+ * through block_tables[b * max_blocks + s / page_size] to a physical page of
+ * page_size rows at k + page * page_size * n_kv_head * head_dim; CE keeps one
+ * such pool per layer, K then V ([2][L][n_pages][page_size][n_kv_head *
+ * head_dim], CE:164), so k / v point at the layer's K and V pools.  A row
+ * whose page is unmapped (< 0) or out of range reads as zeros (the
+ * reference's gather skips it, leaving stale workspace). */
+typedef struct {
+    float *k;
+    float *v;
+    long seq_stride;
+    const int *block_tables;
+    int max_blocks;
+    int page_size;
+    int n_pages;
+} mllm_kv_view;
+
+/* Decode attention of B sequences (one query token each) over their first
+ * seq_lens[b] cached rows (device array, each <= max_seq).
+ * mode 0: CE:141-158 gqa (expf weights, 1 / sum); mode 1: gqa_attention.c
+ * (see gqa_attention_decode).  q, out [B][NH * HD]; NH % NKH == 0,
+ * NH / NKH <= 16, HD <= 256.  Three launches on `stream`; weights and partial
+ * sums go to the workspace (mllm_gqa_workspace_size). */
+MLLM_API long mllm_gqa_workspace_size(int B, int NH, int HD, int max_seq);
+MLLM_API int mllm_gqa_decode(int mode, const float *q, const mllm_kv_view *kv, const int *seq_lens, int max_seq, int B,
+                             int NH, int NKH, int HD, float *out, void *workspace, long ws_bytes, void *stream);
+/* Row pos[b] (device array) of sequence b := k_new[b], v_new[b] [NKH * HD]
+ * (the KV store of CE:1363-1381 and GO:158-161); a row whose page is unmapped
+ * is skipped. */
+MLLM_API int mllm_kv_append(const mllm_kv_view *kv, const int *pos, const float *k_new, const float *v_new, int B,
+                            int NKH, int HD, void *stream);
+/* rope_apply (GO:37-51): in place on buf [T][NH * HD]; for each head the pairs
+ * (j, j + r/2), r = rope_dim (HD when <= 0), rotated by cos_t / sin_t rows
+ * [pos[t]][r/2] (pos a device array). */
+MLLM_API int mllm_rope(float *buf, int T, int NH, int HD, const int *pos, const float *cos_t, const float *sin_t,
+                       int rope_dim, void *stream);
+
+/* The page table of CE:160-201 (host side): a free list that hands out
+ * pages 0, 1, 2, ... in order, returned pages reused last-in first-out, and
+ * a logical -> physical map of MLLM_PAGE_TABLE_BLOCKS entries (MAX_BLOCKS,
+ * CE:23), -1 when unmapped.  Upload mllm_page_table_entries to the device as
+ * a sequence's block table. */
+#define MLLM_PAGE_TABLE_BLOCKS 1024
+typedef struct mllm_page_table mllm_page_table;
+MLLM_API mllm_page_table *mllm_page_table_create(int max_pages, int page_size);
+MLLM_API void mllm_page_table_destroy(mllm_page_table *pt);
+MLLM_API int mllm_page_table_alloc(mllm_page_table *pt);
+MLLM_API void mllm_page_table_free(mllm_page_table *pt, int page_id);
+MLLM_API void mllm_page_table_map(mllm_page_table *pt, int logical_page, int physical_page);
+MLLM_API int mllm_page_table_lookup(const mllm_page_table *pt, int logical_page);
+MLLM_API const int *mllm_page_table_entries(const mllm_page_table *pt);
 
 #ifdef __cplusplus
 }

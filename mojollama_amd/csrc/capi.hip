@@ -1127,6 +1127,47 @@ MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, in
     return rc;
 }
 
+// gqa_attention.c:93: one token's attention through mllm_gqa_decode (mode 1)
+// on uploaded copies of q, K and V; workspace is not written.
+MLLM_API void gqa_attention_decode(const float *q, const float *k_cache, const float *v_cache, float *out, int seq_len,
+                                   int n_head, int n_kv_head, int head_dim, float *workspace)
+{
+    API_GUARD;
+    (void)workspace;
+    if (n_head <= 0 || head_dim <= 0) return;
+    if (n_kv_head <= 0 || n_head % n_kv_head || n_head / n_kv_head > 16 || head_dim > 256) {
+        set_error("gqa_attention_decode: n_head %% n_kv_head == 0, n_head / n_kv_head <= 16 and head_dim <= 256 are "
+                  "served (output untouched)");
+        return;
+    }
+    const size_t qo = (size_t)n_head * head_dim * 4;
+    if (seq_len <= 0) { memset(out, 0, qo); return; }
+    thread_ctx &c = t_ctx;
+    if (c.init()) return;
+    const size_t kvb = (size_t)seq_len * n_kv_head * head_dim * 4;
+    const size_t o_k = align256(qo), o_v = o_k + align256(kvb), o_l = o_v + align256(kvb), in_b = o_l + 256;
+    const long ws = mllm_gqa_workspace_size(1, n_head, head_dim, seq_len);
+    if (c.d_in.ensure(in_b) || c.h_in.ensure(in_b) || c.d_out.ensure(qo) || c.h_out.ensure(qo) || c.d_scr.ensure(ws)) {
+        set_error("gqa_attention_decode: staging allocation failed");
+        return;
+    }
+    uint8_t *h = (uint8_t *)c.h_in.p, *d = (uint8_t *)c.d_in.p;
+    memcpy(h, q, qo);
+    memcpy(h + o_k, k_cache, kvb);
+    memcpy(h + o_v, v_cache, kvb);
+    memcpy(h + o_l, &seq_len, sizeof(int));
+    mllm_kv_view kv{(float *)(d + o_k), (float *)(d + o_v), 0, nullptr, 0, 0, 0};
+    if (hipMemcpyAsync(d, h, in_b, hipMemcpyHostToDevice, c.st) != hipSuccess ||
+        mllm_gqa_decode(1, (const float *)d, &kv, (const int *)(d + o_l), seq_len, 1, n_head, n_kv_head, head_dim,
+                        (float *)c.d_out.p, c.d_scr.p, ws, c.st) != 0 ||
+        hipMemcpyAsync(c.h_out.p, c.d_out.p, qo, hipMemcpyDeviceToHost, c.st) != hipSuccess ||
+        hipStreamSynchronize(c.st) != hipSuccess) {
+        set_error("gqa_attention_decode failed");
+        return;
+    }
+    memcpy(out, c.h_out.p, qo);
+}
+
 MLLM_API int mllm_read_probe(const void *dev, long bytes, void *sink, void *stream)
 {
     if (((uintptr_t)dev & 15) || (bytes & 15) || !sink) { set_error("mllm_read_probe: 16-byte aligned, multiple of 16"); return -1; }

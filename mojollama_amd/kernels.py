@@ -46,6 +46,15 @@ class GemvFusion(ctypes.Structure):
                 ("rms_eps", ctypes.c_float), ("rms_div", ci), ("out_add", cvp), ("x_ld", ci), ("silu_pair", ci)]
 
 
+class KVView(ctypes.Structure):
+    """mllm_kv_view (include/mllm.h): a contiguous or paged KV cache on the device."""
+    _fields_ = [("k", cvp), ("v", cvp), ("seq_stride", ctypes.c_long), ("block_tables", cvp), ("max_blocks", ci),
+                ("page_size", ci), ("n_pages", ci)]
+
+
+ATTN_CE, ATTN_GQA_C = 0, 1   # CE:141-158 gqa / gqa_attention.c:93 softmax
+
+
 _LIB = None
 
 
@@ -149,6 +158,32 @@ def load_kernels(path=LIB_PATH):
     so.mllm_moe_forward_noalloc.restype = ci
     so.mllm_moe_bucket.argtypes = [cvp, ci, ci, cvp, cvp, cvp, cvp, cvp]
     so.mllm_moe_bucket.restype = ci
+    # --- decode attention and the KV cache (TE:383-385 binds gqa_attention_decode so)
+    so.gqa_attention_decode.argtypes = [cf, cf, cf, cf, ci, ci, ci, ci, cf]
+    so.gqa_attention_decode.restype = None
+    so.mllm_gqa_workspace_size.argtypes = [ci, ci, ci, ci]
+    so.mllm_gqa_workspace_size.restype = ctypes.c_long
+    so.mllm_gqa_decode.argtypes = [ci, cvp, ctypes.POINTER(KVView), cvp, ci, ci, ci, ci, ci, cvp, cvp, ctypes.c_long,
+                                   cvp]
+    so.mllm_gqa_decode.restype = ci
+    so.mllm_kv_append.argtypes = [ctypes.POINTER(KVView), cvp, cvp, cvp, ci, ci, ci, cvp]
+    so.mllm_kv_append.restype = ci
+    so.mllm_rope.argtypes = [cvp, ci, ci, ci, cvp, cvp, cvp, ci, cvp]
+    so.mllm_rope.restype = ci
+    so.mllm_page_table_create.argtypes = [ci, ci]
+    so.mllm_page_table_create.restype = cvp
+    so.mllm_page_table_destroy.argtypes = [cvp]
+    so.mllm_page_table_destroy.restype = None
+    so.mllm_page_table_alloc.argtypes = [cvp]
+    so.mllm_page_table_alloc.restype = ci
+    so.mllm_page_table_free.argtypes = [cvp, ci]
+    so.mllm_page_table_free.restype = None
+    so.mllm_page_table_map.argtypes = [cvp, ci, ci]
+    so.mllm_page_table_map.restype = None
+    so.mllm_page_table_lookup.argtypes = [cvp, ci]
+    so.mllm_page_table_lookup.restype = ci
+    so.mllm_page_table_entries.argtypes = [cvp]
+    so.mllm_page_table_entries.restype = ctypes.POINTER(ci)
     if path == LIB_PATH:
         _LIB = so
     return so
@@ -264,6 +299,40 @@ class DeviceOps:
         return out
 
     # ------------------------------------------------------------ MoE layer
+    def kv_view(self, k, v, seq_stride=0, block_tables=None, page_size=0, n_pages=0):
+        """An mllm_kv_view over fp32 GPU tensors k, v (block_tables: int32 [B][max_blocks] GPU).
+        The view keeps the tensors alive."""
+        view = KVView(k.data_ptr(), v.data_ptr(), int(seq_stride),
+                      block_tables.data_ptr() if block_tables is not None else None,
+                      int(block_tables.shape[-1]) if block_tables is not None else 0, int(page_size), int(n_pages))
+        view._tensors = (k, v, block_tables)
+        return view
+
+    def gqa_decode(self, mode, q, kv, seq_lens, max_seq, NH, NKH, HD, out=None, ws=None):
+        """mllm_gqa_decode: q [B][NH*HD] fp32, seq_lens int32 [B] (GPU)."""
+        torch = self.torch
+        B = q.numel() // (NH * HD)
+        if out is None:
+            out = torch.empty((B, NH * HD), dtype=torch.float32, device=q.device)
+        n = self.so.mllm_gqa_workspace_size(B, NH, HD, max_seq)
+        if ws is None:
+            ws = torch.empty(n, dtype=torch.uint8, device=q.device)
+        self._check(self.so.mllm_gqa_decode(mode, q.data_ptr(), ctypes.byref(kv), seq_lens.data_ptr(), max_seq, B, NH,
+                                            NKH, HD, out.data_ptr(), ws.data_ptr(), ws.numel(), self._stream()),
+                    "mllm_gqa_decode")
+        return out
+
+    def kv_append(self, kv, pos, k_new, v_new, NKH, HD):
+        B = pos.numel()
+        self._check(self.so.mllm_kv_append(ctypes.byref(kv), pos.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), B,
+                                           NKH, HD, self._stream()), "mllm_kv_append")
+
+    def rope(self, buf, NH, HD, pos, cos_t, sin_t, rope_dim=0):
+        T = pos.numel()
+        self._check(self.so.mllm_rope(buf.data_ptr(), T, NH, HD, pos.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+                                      rope_dim, self._stream()), "mllm_rope")
+        return buf
+
     def moe_prepare(self, qts, N, M, E, K, gates, ups, downs, router, renorm):
         """gates/ups/downs: per-expert raw GGUF uint8 tensors (GPU) in the
         reference's layout; router: fp32 [E][N] (GPU).  Returns a MoELayer."""

@@ -656,3 +656,92 @@ int orc_requant_q8_0(int qt, const uint8_t *W, int n_rows, int n_cols, uint8_t *
     free(w);
     return 0;
 }
+
+/* ------------------------------------------------------------ attention */
+
+/* exp_ps_simd (gqa_attention.c:32-48), one lane: t = x*log2e, n = rne(t +
+ * 0.5) (cvtps_epi32 under the default MXCSR), f = t - n, then the FMA chain
+ * exactly as the source writes it (starting from 1 and adding the
+ * coefficients in ascending order), times 2^n built from the clamped biased
+ * exponent. */
+float orc_exp_ps_simd(float x)
+{
+    const float t = x * 1.4426950408889634f;
+    const int n = (int)nearbyintf(t + 0.5f);
+    const float f = t - (float)n;
+    float p = 1.0f;
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.0555041086648216f);
+    p = fmaf(p, f, 0.0096181291076285f);
+    p = fmaf(p, f, 0.0013333558146428f);
+    int biased = n + 127;
+    biased = biased < 0 ? 0 : biased > 255 ? 255 : biased;
+    uint32_t bits = (uint32_t)biased << 23;
+    float two_n;
+    memcpy(&two_n, &bits, 4);
+    return p * two_n;
+}
+
+void orc_gqa_decode(int mode, const float *q, const float *k, const float *v, long row_stride, int seq_len,
+                    int nh, int nkh, int hd, float *out)
+{
+    const int gr = nh / nkh;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *sc = (float *)malloc((size_t)(seq_len > 0 ? seq_len : 1) * sizeof(float));
+    for (int h = 0; h < nh; h++) {
+        const int j = h / gr;
+        const float *qh = q + (long)h * hd;
+        float mx = -1e30f;
+        for (int s = 0; s < seq_len; s++) {
+            const float *kr = k + (long)s * row_stride + (long)j * hd;
+            /* one fp32 FMA chain in element order: the reference's AVX2 lane
+             * order (CE:149-151) or sgemm blocking is not reproducible here,
+             * and any order is within fp32 rounding; a fixed order matters
+             * for exp_ps_simd, where a one-ulp change of a score can move its
+             * n = rne(t + 0.5) and so the weight by a step */
+            float dot = 0.0f;
+            for (int d = 0; d < hd; d++) dot = fmaf(qh[d], kr[d], dot);
+            sc[s] = dot * scale;                        /* CE:152 dot*=inv; sgemm alpha */
+            if (sc[s] > mx) mx = sc[s];
+        }
+        double sum = 0.0;
+        const int vec_end = mode == ORC_ATTN_GQA_C ? seq_len / 8 * 8 : 0;
+        for (int s = 0; s < seq_len; s++) {
+            float e;
+            if (s < vec_end) {                           /* gqa_attention.c:71-77 */
+                float z = sc[s] - mx;
+                z = z > -80.0f ? z : -80.0f;
+                z = z < 80.0f ? z : 80.0f;
+                e = orc_exp_ps_simd(z);
+            } else {
+                e = expf(sc[s] - mx);
+                if (mode == ORC_ATTN_GQA_C && e > 1e38f) e = 1e38f;
+            }
+            sc[s] = e;
+            sum += e;
+        }
+        const float inv = mode == ORC_ATTN_GQA_C ? 1.0f / ((float)sum + 1e-10f) : 1.0f / (float)sum;
+        for (int d = 0; d < hd; d++) {
+            double acc = 0.0;
+            for (int s = 0; s < seq_len; s++) acc += (double)(sc[s] * inv) * v[(long)s * row_stride + (long)j * hd + d];
+            out[(long)h * hd + d] = (float)acc;
+        }
+    }
+    free(sc);
+}
+
+void orc_rope(float *buf, int nh, int hd, int pos, const float *cos_t, const float *sin_t, int rope_dim)
+{
+    if (rope_dim <= 0) rope_dim = hd;
+    const int hd2 = rope_dim / 2;
+    const float *cr = cos_t + (long)pos * hd2, *sr = sin_t + (long)pos * hd2;
+    for (int h = 0; h < nh; h++) {
+        float *b = buf + (long)h * hd;
+        for (int j = 0; j < hd2; j++) {
+            const float a0 = b[j], a1 = b[j + hd2];
+            b[j] = a0 * cr[j] - a1 * sr[j];
+            b[j + hd2] = a1 * cr[j] + a0 * sr[j];
+        }
+    }
+}

@@ -101,6 +101,27 @@ int orc_requant_q8_0(int qt, const uint8_t *W, int n_rows, int n_cols, uint8_t *
 /* moe_ffn's expert strides (CE:593-605). */
 long orc_moe_ffn_stride(int which, int qt, int N, int M);
 
+/* Decode attention of one query token over seq_len cached positions.
+ * q [nh][hd]; row s of kv head j at k + s*row_stride + j*hd (likewise v);
+ * query head h reads kv head h / (nh/nkh); out [nh][hd].
+ * mode ORC_ATTN_CE     : CE:141-158 gqa: scores dot*(1/sqrtf(hd)), max from
+ *                        -1e30 by strict '>', expf(s - max), 1/sum.
+ * mode ORC_ATTN_GQA_C  : gqa_attention.c:93 gqa_attention_decode: the same
+ *                        scores; softmax_simd (gqa_attention.c:50-88): the
+ *                        first floor(seq_len/8)*8 weights by exp_ps_simd on
+ *                        (s - max) clamped to [-80, 80], the rest expf
+ *                        capped at 1e38, 1/(sum + 1e-10).
+ * Scores: one fp32 FMA chain per dot in element order, times the scale;
+ * the weighted V sum accumulates in double. */
+enum { ORC_ATTN_CE = 0, ORC_ATTN_GQA_C = 1 };
+void orc_gqa_decode(int mode, const float *q, const float *k, const float *v, long row_stride, int seq_len,
+                    int nh, int nkh, int hd, float *out);
+/* exp_ps_simd (gqa_attention.c:32-48) on one value, as written. */
+float orc_exp_ps_simd(float x);
+/* rope_apply (GO:37-51): pairs (j, j + rope_dim/2) of each head rotated by
+ * cos/sin rows [pos][rope_dim/2]. */
+void orc_rope(float *buf, int nh, int hd, int pos, const float *cos_t, const float *sin_t, int rope_dim);
+
 #ifdef __cplusplus
 }
 #endif

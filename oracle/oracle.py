@@ -48,6 +48,9 @@ def build():
     subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
 
 
+ATTN_CE, ATTN_GQA_C = 0, 1
+
+
 class Oracle:
     def __init__(self, path=ORACLE_SO):
         if not os.path.exists(path):
@@ -76,6 +79,12 @@ class Oracle:
         lib.orc_moe_forward_token.argtypes = [ctypes.POINTER(_cu)] * 3 + [_cf, _ci, _ci, _ci, _ci, _ci,
                                               ctypes.POINTER(ctypes.c_int), _cf, _ci, _ci, _cf]
         lib.orc_moe_forward_token.restype = None
+        lib.orc_gqa_decode.argtypes = [_ci, _cf, _cf, _cf, ctypes.c_long, _ci, _ci, _ci, _ci, _cf]
+        lib.orc_gqa_decode.restype = None
+        lib.orc_exp_ps_simd.argtypes = [ctypes.c_float]
+        lib.orc_exp_ps_simd.restype = ctypes.c_float
+        lib.orc_rope.argtypes = [_cf, _ci, _ci, _ci, _cf, _cf, _ci]
+        lib.orc_rope.restype = None
         lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
         lib.orc_f32_to_f16.restype = ctypes.c_uint16
         lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -134,6 +143,26 @@ class Oracle:
         if rc != 0:
             raise ValueError(f"no requantisation for type {qt}")
         return out
+
+    def gqa_decode(self, mode, q, k, v, seq_len, nh, nkh, hd):
+        """Decode attention (ATTN_CE: CE:141-158, ATTN_GQA_C: gqa_attention.c:93) of one
+        query [nh*hd] over k, v [>= seq_len][nkh*hd]; returns [nh*hd]."""
+        q = np.ascontiguousarray(q, np.float32)
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        out = np.zeros(nh * hd, np.float32)
+        self.lib.orc_gqa_decode(mode, fp(q), fp(k), fp(v), nkh * hd, seq_len, nh, nkh, hd, fp(out))
+        return out
+
+    def exp_ps_simd(self, x):
+        return self.lib.orc_exp_ps_simd(float(x))
+
+    def rope(self, buf, nh, hd, pos, cos_t, sin_t, rope_dim):
+        """rope_apply (GO:37-51) on a copy of buf [nh*hd]."""
+        b = np.array(buf, np.float32, copy=True)
+        self.lib.orc_rope(fp(b), nh, hd, pos, fp(np.ascontiguousarray(cos_t, np.float32)),
+                          fp(np.ascontiguousarray(sin_t, np.float32)), rope_dim)
+        return b
 
     def moe_ffn_stride(self, which, qt, N, M):
         return self.lib.orc_moe_ffn_stride(which, qt, N, M)

@@ -55,3 +55,37 @@ def test_bindings_mirror_reference_argtypes(libpath):
     assert so.f32_matmul_omp.argtypes == [cf, cf, cf, ci, ci]                # TE:253
     assert len(so.moe_forward_omp.argtypes) == 15                             # TE:363-377
     assert so.q4_k_batch_matmul.argtypes == [cu, cf, cf, ci, ci, ci]         # CE:256
+
+
+def test_gqa_binding_mirrors_te(libpath):
+    from mojollama_amd import kernels
+    so = kernels.load_kernels()
+    cf, ci = kernels.cf, kernels.ci
+    assert so.gqa_attention_decode.argtypes == [cf, cf, cf, cf, ci, ci, ci, ci, cf]   # TE:383-385
+
+
+def test_page_table_follows_ce(libpath):
+    """CE:173-201 (host code, no GPU): allocation hands out 0, 1, 2, ...; a freed
+    page is handed out next; exhaustion gives -1; the logical map has 1024
+    entries (MAX_BLOCKS, CE:23), -1 when unmapped, and ignores indices outside."""
+    from mojollama_amd import kernels
+    so = kernels.load_kernels()
+    pt = so.mllm_page_table_create(5, 64)
+    try:
+        assert [so.mllm_page_table_alloc(pt) for _ in range(3)] == [0, 1, 2]
+        so.mllm_page_table_free(pt, 1)
+        assert so.mllm_page_table_alloc(pt) == 1
+        assert [so.mllm_page_table_alloc(pt) for _ in range(3)] == [3, 4, -1]
+        so.mllm_page_table_map(pt, 7, 3)
+        so.mllm_page_table_map(pt, 1024, 2)
+        so.mllm_page_table_map(pt, -1, 2)
+        assert so.mllm_page_table_lookup(pt, 7) == 3
+        assert so.mllm_page_table_lookup(pt, 8) == -1
+        ent = so.mllm_page_table_entries(pt)
+        assert [ent[i] for i in range(1024)].count(-1) == 1023 and ent[7] == 3
+        for _ in range(10):
+            so.mllm_page_table_free(pt, 0)          # the free list never grows past n_pages
+        assert [so.mllm_page_table_alloc(pt) for _ in range(6)] == [0] * 5 + [-1]
+    finally:
+        so.mllm_page_table_destroy(pt)
+    assert so.mllm_page_table_create(0, 64) is None

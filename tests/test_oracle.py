@@ -461,3 +461,96 @@ def test_route_properties(orc):
     p = np.exp(logits - logits.max(1, keepdims=True))
     p /= p.sum(1, keepdims=True)
     assert np.allclose(np.take_along_axis(p, i0, 1), w0, rtol=1e-5)
+
+
+# ------------------------------------------------- decode attention, RoPE
+
+def _textbook_attention(q, k, v, nh, nkh, hd):
+    """Softmax attention in double precision (one query token)."""
+    S = k.shape[0]
+    kk = k.reshape(S, nkh, hd).astype(np.float64)
+    vv = v.reshape(S, nkh, hd).astype(np.float64)
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        j = h // (nh // nkh)
+        sc = (kk[:, j] @ q.reshape(nh, hd)[h].astype(np.float64)) / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        out[h] = (p / p.sum()) @ vv[:, j]
+    return out.ravel()
+
+
+@pytest.mark.parametrize("nh,nkh,hd,S", [(8, 2, 32, 1), (8, 2, 32, 40), (16, 4, 64, 300), (4, 4, 16, 7)])
+def test_attention_ce_is_textbook_softmax(orc, nh, nkh, hd, S):
+    """CE:141-158 is plain softmax attention with expf: the double-precision
+    closed form pins it (scores scaled by 1/sqrt(hd), GQA head grouping h // (nh/nkh))."""
+    rng = np.random.default_rng(S + hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    v = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    got = orc.gqa_decode(O.ATTN_CE, q, k, v, S, nh, nkh, hd)
+    assert O.norm_err(got, _textbook_attention(q, k, v, nh, nkh, hd)) < 1e-6
+
+
+@pytest.mark.parametrize("S", [1, 3, 7])
+def test_attention_gqa_c_below_eight_positions_is_textbook(orc, S):
+    """softmax_simd's vector loop covers floor(S/8)*8 positions: below 8 every
+    weight is the scalar tail's expf, so gqa_attention_decode is softmax attention."""
+    rng = np.random.default_rng(S)
+    nh, nkh, hd = 8, 2, 32
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    v = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    got = orc.gqa_decode(O.ATTN_GQA_C, q, k, v, S, nh, nkh, hd)
+    assert O.norm_err(got, _textbook_attention(q, k, v, nh, nkh, hd)) < 1e-6
+
+
+@pytest.mark.parametrize("S", [8, 13, 64, 100])
+def test_attention_gqa_c_equal_scores_closed_form(orc, S):
+    """q = 0 makes every score 0 = the maximum: the vector loop's weights are
+    exp_ps_simd(0), which the source's polynomial evaluates to its last
+    coefficient 0.0013333558146428f (t = 0, n = rne(0.5) = 0, f = 0), the tail's
+    expf(0) = 1, and out = (c sum_{s < 8k} v + sum_tail v) / (8k c + r + 1e-10).
+    A textbook exponential (weight 1 everywhere), a Horner order that yields
+    2^0 = 1, or a different vector/tail split all fail this."""
+    rng = np.random.default_rng(S)
+    nh, nkh, hd = 4, 2, 16
+    q = np.zeros(nh * hd, np.float32)
+    k = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    v = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    got = orc.gqa_decode(O.ATTN_GQA_C, q, k, v, S, nh, nkh, hd)
+    c = float(np.float32(0.0013333558146428))
+    vec = S // 8 * 8
+    vv = v.reshape(S, nkh, hd).astype(np.float64)
+    num = c * vv[:vec].sum(0) + vv[vec:].sum(0)
+    den = c * vec + (S - vec) + 1e-10
+    want = np.repeat(num / den, nh // nkh, axis=0).ravel()
+    assert O.norm_err(got, want) < 1e-5
+    assert orc.exp_ps_simd(0.0) == np.float32(0.0013333558146428)
+
+
+def test_attention_modes_differ_from_eight_positions(orc):
+    rng = np.random.default_rng(5)
+    nh, nkh, hd, S = 4, 1, 16, 16
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    v = rng.standard_normal((S, nkh * hd)).astype(np.float32)
+    a = orc.gqa_decode(O.ATTN_CE, q, k, v, S, nh, nkh, hd)
+    b = orc.gqa_decode(O.ATTN_GQA_C, q, k, v, S, nh, nkh, hd)
+    assert O.norm_err(a, b) > 1e-2
+
+
+def test_rope_is_a_rotation(orc):
+    """rope_apply (GO:37-51): each pair (j, j + r/2) rotated by angle theta_pj,
+    i.e. the complex product (a0 + i a1) e^{i theta}; lanes past rope_dim untouched."""
+    rng = np.random.default_rng(3)
+    nh, hd, r, P = 4, 64, 48, 9
+    theta = rng.uniform(-3, 3, (P, r // 2))
+    cos_t, sin_t = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    buf = rng.standard_normal(nh * hd).astype(np.float32)
+    for pos in (0, 5, 8):
+        got = orc.rope(buf, nh, hd, pos, cos_t, sin_t, r).reshape(nh, hd)
+        b = buf.reshape(nh, hd).astype(np.float64)
+        z = (b[:, :r // 2] + 1j * b[:, r // 2:r]) * np.exp(1j * theta[pos].astype(np.float32).astype(np.float64))
+        assert np.max(np.abs(got[:, :r // 2] - z.real)) < 1e-5
+        assert np.max(np.abs(got[:, r // 2:r] - z.imag)) < 1e-5
+        assert np.array_equal(got[:, r:], buf.reshape(nh, hd)[:, r:])

@@ -112,6 +112,31 @@ MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, in
 MLLM_API void gqa_attention_decode(const float *q, const float *k_cache, const float *v_cache, float *out, int seq_len,
                                    int n_head, int n_kv_head, int head_dim, float *workspace);
 
+/* gptoss_forward (GO:96-189): one decode token of gpt-oss through all
+ * layers, the reference's steps in its order (see mllm_gptoss_step), on the
+ * reference's host buffers: logits[outNR] written, K/V row kv_len[l] of each
+ * layer written into k_cache / v_cache ([L][max_ctx][NKH*HD]) and kv_len[l]
+ * incremented.  Weights are packed on the device on first use (cached by
+ * their pointers and a sampled fingerprint); the caches are mirrored on the
+ * device and only rows the mirror lacks (or rewritten rows) are uploaded.
+ * Q/K/V/O and the output projection are MXFP4 whatever *_quant says (GO
+ * calls mxfp4_matmul_omp for all of them); expert e of layer l is
+ * w_*_exps[l + e] (GO:179-181), so those arrays need L - 1 + n_experts
+ * entries.  workspace, moe_prealloc_* and gqa_ws are not written.  Refused
+ * (error, outputs untouched) when kv_len[l] >= max_ctx (the reference writes
+ * past its cache) or nQ/nK/nV/nO disagree with NH, NKH, HD, N. */
+MLLM_API void gptoss_forward(const int *token, int pos, const float *emb, int V, const uint8_t **wQ,
+                             const uint8_t **wK, const uint8_t **wV, const uint8_t **wO, const float **wAN,
+                             const float **wFN, const int *nQ, const int *nK, const int *nV, const int *nO,
+                             const int *q_quant, const int *k_quant, const int *v_quant, const int *o_quant,
+                             const uint8_t *wOut, int outNR, int outNC, int outQuant, float *k_cache, float *v_cache,
+                             int *kv_len, const float *cos_table, const float *sin_table, int max_ctx, int rope_dim,
+                             float *workspace, int ws_size, int L, int N, int NH, int NKH, int HD, int FF, float eps,
+                             int n_experts, int n_experts_per_tok, int moe_intermediate, const float **w_gate_inp,
+                             const uint8_t **w_gate_exps, const uint8_t **w_up_exps, const uint8_t **w_down_exps,
+                             int gate_exp_quant, int up_exp_quant, int down_exp_quant, float *logits,
+                             float *moe_prealloc_buf, uint8_t *moe_prealloc_q8, float *gqa_ws);
+
 /* QK:1029-1030: accepted and ignored / number of compute units. */
 MLLM_API void set_num_threads(int n);
 MLLM_API int get_max_threads(void);
@@ -290,6 +315,34 @@ MLLM_API int mllm_kv_append(const mllm_kv_view *kv, const int *pos, const float 
  * [pos[t]][r/2] (pos a device array). */
 MLLM_API int mllm_rope(float *buf, int T, int NH, int HD, const int *pos, const float *cos_t, const float *sin_t,
                        int rope_dim, void *stream);
+
+/* gptoss_forward's model on the device.  Host pointers to the raw GGUF
+ * weights (MXFP4 Q/K/V/O/output, fp32 norms and routers, experts of the given
+ * types indexed [l + e] as GO:179-181); create uploads and packs them (the
+ * Q/K/V rows of a layer stacked into one matrix) and builds one MoE layer per
+ * layer (mllm_moe_prepare, renormalised routing). */
+typedef struct {
+    int L, N, NH, NKH, HD, E, K, M, max_ctx, rope_dim, outNR;
+    float eps;
+    const uint8_t *const *wQ, *const *wK, *const *wV, *const *wO;
+    const float *const *wAN, *const *wFN;
+    const uint8_t *wOut;
+    const float *const *w_gate_inp;
+    const uint8_t *const *w_gate_exps, *const *w_up_exps, *const *w_down_exps;
+    int qt_gate, qt_up, qt_down;
+    const float *cos_t, *sin_t;        /* [max_ctx][rope_dim / 2] */
+} mllm_gptoss_desc;
+typedef struct mllm_gptoss mllm_gptoss;
+MLLM_API mllm_gptoss *mllm_gptoss_create(const mllm_gptoss_desc *desc);
+MLLM_API void mllm_gptoss_release(mllm_gptoss *m);
+/* Floats of one of the step's K / V caches: L * max_ctx * NKH * HD. */
+MLLM_API long mllm_gptoss_kv_floats(const mllm_gptoss *m);
+/* One token, device pointers only, no host synchronisation (14 launches per
+ * layer; capturable): x_emb the token's embedding row [N], pos the RoPE
+ * position [1], kv_len [L] (read, then incremented), caches [L][max_ctx][NKH *
+ * HD], logits [outNR]. */
+MLLM_API int mllm_gptoss_step(mllm_gptoss *m, const float *x_emb, const int *pos, int *kv_len, float *k_cache,
+                              float *v_cache, float *logits, void *stream);
 
 /* The page table of CE:160-201 (host side): a free list that hands out
  * pages 0, 1, 2, ... in order, returned pages reused last-in first-out, and

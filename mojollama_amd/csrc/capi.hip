@@ -907,6 +907,7 @@ MLLM_API void mllm_cache_clear(void)
     g_retired.clear();
     for (auto &kv : g_router_cache) (void)hipFree(kv.second.first);
     g_router_cache.clear();
+    mllm_gptoss_cache_clear();
 }
 
 // ====================================================== device-pointer ABI

@@ -1,0 +1,450 @@
+// gptoss.hip — gptoss_forward (GO:96-189) on the GPU: one decode token
+// through every layer with the weights resident in HBM.
+//
+// Per layer (14 launches, all on one stream, no host synchronisation, so a
+// step can be captured in a graph):
+//   qkv  = Wqkv (rms(x) * wAN)        one MXFP4 GEMV over the stacked q/k/v
+//                                     rows with the RMS norm in its prologue
+//   RoPE on the q and k heads          one launch over NH + NKH heads
+//   K/V row kv_len[l] := k, v          mllm_kv_append
+//   att  = attention over kv_len[l]+1  mllm_gqa_decode, gqa_attention.c softmax
+//   x2   = x + Wo att                  GEMV with the residual in its epilogue
+//   xn   = rms(x2) * wFN               the prologue kernel on its own (the
+//                                      router and the experts both read it)
+//   ffn  = MoE layer (route + experts) mllm_moe_forward, moe_forward_omp's
+//                                      semantics, GO's renormalised router
+//   x   += ffn                         x is still the layer's input: GO:186
+//                                      adds the FFN to res, not to x2
+// then logits = Wout xn (the last layer's xn, GO:189) and kv_len[l] += 1.
+#include <string.h>
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <vector>
+#include "gemv.h"
+#include "moe.h"
+
+namespace {
+
+__global__ void k_len_plus_one(const int *kv_len, int *len1, int L)
+{
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l < L) len1[l] = kv_len[l] + 1;
+}
+
+__global__ void k_len_increment(int *kv_len, int L)
+{
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l < L) kv_len[l] += 1;
+}
+
+long a256(long n) { return (n + 255) / 256 * 256; }
+
+} // namespace
+
+struct mllm_gptoss {
+    mllm_gptoss_desc d;
+    int inner, kvd;
+    std::vector<void *> allocs;                       // every device buffer the model owns
+    std::vector<uint8_t *> qkv, wo;                   // packed MXFP4 per layer
+    std::vector<float *> an, fn;                      // RMS weights per layer
+    std::vector<mllm_moe_layer *> moe;
+    uint8_t *wout = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    // step buffers
+    float *x = nullptr, *xn = nullptr, *x2 = nullptr, *qkvb = nullptr, *att = nullptr, *ffn = nullptr;
+    int *len1 = nullptr;
+    uint8_t *ws = nullptr;
+    long ws_gemv = 0, ws_attn = 0, ws_moe = 0;
+    long ws_bytes = 0;
+
+    void *dalloc(size_t bytes)
+    {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess) return nullptr;
+        allocs.push_back(p);
+        return p;
+    }
+    // raw host MXFP4 matrices (rows each, n_cols) stacked and packed; nullptr on failure
+    uint8_t *pack_stack(const uint8_t *const *hosts, const int *rows, int n, int n_cols)
+    {
+        const long rb = (long)(n_cols / 32) * 17;
+        long total_rows = 0;
+        for (int i = 0; i < n; i++) total_rows += rows[i];
+        uint8_t *raw = (uint8_t *)dalloc(total_rows * rb);
+        uint8_t *packed = (uint8_t *)dalloc(mllm_packed_bytes(LY_MXFP4, (int)total_rows, n_cols, nullptr));
+        if (!raw || !packed) return nullptr;
+        long off = 0;
+        for (int i = 0; i < n; i++) {
+            if (hipMemcpy(raw + off, hosts[i], rows[i] * rb, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+            off += rows[i] * rb;
+        }
+        if (mllm_launch_pack(LY_MXFP4, raw, packed, (int)total_rows, n_cols, nullptr) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess)
+            return nullptr;
+        allocs.pop_back();            // packed stays; the raw staging copy goes
+        allocs.pop_back();
+        allocs.push_back(packed);
+        (void)hipFree(raw);
+        return packed;
+    }
+    float *upload_f32(const float *h, long n)
+    {
+        float *p = (float *)dalloc(n * 4);
+        if (!p || hipMemcpy(p, h, n * 4, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+        return p;
+    }
+};
+
+extern "C" {
+
+MLLM_API void mllm_gptoss_release(mllm_gptoss *m)
+{
+    if (!m) return;
+    for (mllm_moe_layer *l : m->moe) mllm_moe_release(l);
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+MLLM_API mllm_gptoss *mllm_gptoss_create(const mllm_gptoss_desc *desc)
+{
+    if (!desc) return nullptr;
+    const mllm_gptoss_desc &d = *desc;
+    if (d.L <= 0 || d.N <= 0 || d.N % 32 || d.NH <= 0 || d.NKH <= 0 || d.NH % d.NKH || d.NH / d.NKH > 16 ||
+        d.HD <= 0 || d.HD > 256 || (d.NH * d.HD) % 32 || d.E <= 0 || d.K <= 0 || d.K > d.E || d.M <= 0 ||
+        d.max_ctx <= 0 || d.outNR <= 0) {
+        mllm_set_error("mllm_gptoss_create: unsupported shape (N and NH*HD multiples of 32, NH % NKH == 0, "
+                       "NH/NKH <= 16, HD <= 256, K <= E)");
+        return nullptr;
+    }
+    const int rd = d.rope_dim <= 0 ? d.HD : d.rope_dim;
+    if (rd > d.HD || (rd & 1)) { mllm_set_error("mllm_gptoss_create: rope_dim must be even and <= HD"); return nullptr; }
+    mllm_gptoss *m = new mllm_gptoss;
+    m->d = d;
+    m->inner = d.NH * d.HD;
+    m->kvd = d.NKH * d.HD;
+    const int N = d.N, inner = m->inner, kvd = m->kvd;
+    bool ok = true;
+    std::map<const void *, uint8_t *> experts;        // GO's [l + e] indexing shares matrices between layers
+    auto expert = [&](const uint8_t *h, int rows, int cols) -> uint8_t * {
+        auto it = experts.find(h);
+        if (it != experts.end()) return it->second;
+        uint8_t *p = m->pack_stack(&h, &rows, 1, cols);
+        experts[h] = p;
+        return p;
+    };
+    for (int l = 0; l < d.L && ok; l++) {
+        const uint8_t *qkv_h[3] = {d.wQ[l], d.wK[l], d.wV[l]};
+        const int qkv_r[3] = {inner, kvd, kvd};
+        m->qkv.push_back(m->pack_stack(qkv_h, qkv_r, 3, N));
+        const uint8_t *o_h = d.wO[l];
+        m->wo.push_back(m->pack_stack(&o_h, &N, 1, inner));
+        m->an.push_back(m->upload_f32(d.wAN[l], N));
+        m->fn.push_back(m->upload_f32(d.wFN[l], N));
+        std::vector<const void *> g(d.E), u(d.E), dn(d.E);
+        for (int e = 0; e < d.E && ok; e++) {          // GO:179-181: expert e of layer l is w_*_exps[l + e]
+            g[e] = expert(d.w_gate_exps[l + e], d.M, N);
+            u[e] = expert(d.w_up_exps[l + e], d.M, N);
+            dn[e] = expert(d.w_down_exps[l + e], N, d.M);
+            ok = g[e] && u[e] && dn[e];
+        }
+        float *router = ok ? m->upload_f32(d.w_gate_inp[l], (long)d.E * N) : nullptr;
+        mllm_moe_layer *ml = router ? mllm_moe_prepare(d.qt_gate, d.qt_up, d.qt_down, N, d.M, d.E, d.K, g.data(),
+                                                       u.data(), dn.data(), router, 1)
+                                    : nullptr;
+        m->moe.push_back(ml);
+        ok = ok && m->qkv.back() && m->wo.back() && m->an.back() && m->fn.back() && ml;
+    }
+    if (ok) {
+        const uint8_t *out_h = d.wOut;
+        m->wout = m->pack_stack(&out_h, &d.outNR, 1, N);
+        m->cos_t = m->upload_f32(d.cos_t, (long)d.max_ctx * (rd / 2));
+        m->sin_t = m->upload_f32(d.sin_t, (long)d.max_ctx * (rd / 2));
+        ok = m->wout && m->cos_t && m->sin_t;
+    }
+    if (ok) {
+        m->x = (float *)m->dalloc((size_t)N * 4);
+        m->xn = (float *)m->dalloc((size_t)N * 4);
+        m->x2 = (float *)m->dalloc((size_t)N * 4);
+        m->ffn = (float *)m->dalloc((size_t)N * 4);
+        m->qkvb = (float *)m->dalloc((size_t)(inner + 2 * kvd) * 4);
+        m->att = (float *)m->dalloc((size_t)inner * 4);
+        m->len1 = (int *)m->dalloc((size_t)d.L * 4);
+        mllm_gemv_fusion f{};
+        f.rms_w = m->an[0];
+        f.rms_eps = d.eps;
+        f.rms_div = 1;
+        long g1 = mllm_gemv_fused_workspace_size(SEM_MXFP4, inner + 2 * kvd, N, 1, &f);
+        mllm_gemv_fusion fo{};
+        fo.out_add = m->x;
+        long g2 = mllm_gemv_fused_workspace_size(SEM_MXFP4, N, inner, 1, &fo);
+        long g3 = mllm_gemv_workspace_size(SEM_MXFP4, d.outNR, N, 1);
+        m->ws_gemv = std::max(std::max(g1, g2), std::max(g3, 256L));
+        m->ws_attn = mllm_gqa_workspace_size(1, d.NH, d.HD, d.max_ctx);
+        m->ws_moe = mllm_moe_workspace_size(m->moe[0], 1);
+        m->ws_bytes = a256(m->ws_gemv) + a256(m->ws_attn) + a256(m->ws_moe);
+        m->ws = (uint8_t *)m->dalloc(m->ws_bytes);
+        ok = m->x && m->xn && m->x2 && m->ffn && m->qkvb && m->att && m->len1 && m->ws && g1 >= 0 && g2 >= 0 &&
+             g3 >= 0 && m->ws_moe > 0;
+    }
+    if (!ok) {
+        if (!*mllm_last_error()) mllm_set_error("mllm_gptoss_create: device allocation or upload failed");
+        mllm_gptoss_release(m);
+        return nullptr;
+    }
+    return m;
+}
+
+MLLM_API long mllm_gptoss_kv_floats(const mllm_gptoss *m)
+{
+    return m ? (long)m->d.L * m->d.max_ctx * m->kvd : 0;
+}
+
+MLLM_API int mllm_gptoss_step(mllm_gptoss *m, const float *x_emb, const int *pos, int *kv_len, float *k_cache,
+                              float *v_cache, float *logits, void *stream)
+{
+    if (!m || !x_emb || !pos || !kv_len || !k_cache || !v_cache || !logits) {
+        mllm_set_error("mllm_gptoss_step: null argument");
+        return -1;
+    }
+    const mllm_gptoss_desc &d = m->d;
+    const int N = d.N, inner = m->inner, kvd = m->kvd;
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t *ws_g = m->ws, *ws_a = m->ws + a256(m->ws_gemv), *ws_m = ws_a + a256(m->ws_attn);
+#define CK(e) do { if ((e) != hipSuccess) { mllm_set_error("mllm_gptoss_step: launch failed"); return -1; } } while (0)
+#define CKI(e) do { if ((e) != 0) return -1; } while (0)
+    CK(hipMemcpyAsync(m->x, x_emb, (size_t)N * 4, hipMemcpyDeviceToDevice, st));
+    hipLaunchKernelGGL(k_len_plus_one, dim3((d.L + 255) / 256), dim3(256), 0, st, kv_len, m->len1, d.L);
+    CK(hipGetLastError());
+    const long layer = (long)d.max_ctx * kvd;
+    for (int l = 0; l < d.L; l++) {
+        mllm_gemv_fusion fq{};
+        fq.rms_w = m->an[l];
+        fq.rms_eps = d.eps;
+        fq.rms_div = 1;
+        CKI(mllm_gemv_fused(SEM_MXFP4, m->qkv[l], m->x, m->qkvb, inner + 2 * kvd, N, 1, &fq, ws_g, st));
+        CKI(mllm_rope(m->qkvb, 1, d.NH + d.NKH, d.HD, pos, m->cos_t, m->sin_t, d.rope_dim, st));
+        mllm_kv_view kv{k_cache + l * layer, v_cache + l * layer, 0, nullptr, 0, 0, 0};
+        CKI(mllm_kv_append(&kv, kv_len + l, m->qkvb + inner, m->qkvb + inner + kvd, 1, d.NKH, d.HD, st));
+        CKI(mllm_gqa_decode(1, m->qkvb, &kv, m->len1 + l, d.max_ctx, 1, d.NH, d.NKH, d.HD, m->att, ws_a,
+                            m->ws_attn, st));
+        mllm_gemv_fusion fo{};
+        fo.out_add = m->x;
+        CKI(mllm_gemv_fused(SEM_MXFP4, m->wo[l], m->att, m->x2, N, inner, 1, &fo, ws_g, st));
+        CK(mllm_launch_act_prologue(m->x2, nullptr, nullptr, m->fn[l], d.eps, 1, nullptr, 1, 1, N, N, m->xn, st));
+        CKI(mllm_moe_forward(m->moe[l], m->xn, 1, m->ffn, ws_m, m->ws_moe, nullptr, nullptr, st));
+        CK(mllm_launch_add(m->x, m->ffn, N, st));
+    }
+    CKI(mllm_gemv(SEM_MXFP4, m->wout, m->xn, logits, d.outNR, N, 1, ws_g, st));
+    hipLaunchKernelGGL(k_len_increment, dim3((d.L + 255) / 256), dim3(256), 0, st, kv_len, d.L);
+    CK(hipGetLastError());
+#undef CK
+#undef CKI
+    return 0;
+}
+
+} // extern "C"
+
+// ============================================================ drop-in
+// gptoss_forward (GO:96-189) on host buffers.  The model is built once per
+// distinct set of weight pointers (checked by a sampled fingerprint of a few
+// matrices); the KV cache lives on the device as a mirror of the caller's
+// k_cache / v_cache: rows the caller's kv_len covers but the mirror lacks are
+// uploaded, a caller that rewrote rows (sampled rows differ) gets all its
+// rows uploaded again, and each call writes its new K/V row back to the
+// caller's arrays and increments kv_len, as the reference does.  workspace,
+// moe_prealloc_* and gqa_ws are not written.
+namespace {
+
+uint64_t fp_sample(const void *p, long n)
+{
+    const uint8_t *b = (const uint8_t *)p;
+    uint64_t h = 1469598103934665603ull ^ (uint64_t)n;
+    for (int i = 0; i < 32 && n > 0; i++) {
+        const long off = (long)((__int128)(n - 1) * i / 31);
+        h = (h ^ b[off]) * 1099511628211ull;
+    }
+    return h;
+}
+
+struct model_entry {
+    mllm_gptoss *m = nullptr;
+    uint64_t fp = 0;
+};
+
+struct kv_mirror {
+    float *k = nullptr, *v = nullptr;       // [L][max_ctx][kvd] on the device
+    int *len_d = nullptr, *pos_d = nullptr;
+    float *emb_d = nullptr, *logits_d = nullptr;
+    void *h_stage = nullptr;                // pinned: kv_len + pos in, logits + new rows out
+    size_t h_bytes = 0;
+    std::vector<int> rows;                  // rows per layer the device holds, equal to the caller's
+    std::vector<uint64_t> seal;             // fingerprint of sampled host rows at the end of the last call
+    int L = 0, max_ctx = 0, kvd = 0, outNR = 0, N = 0;
+};
+
+std::mutex g_go_mu;
+std::map<std::vector<uintptr_t>, model_entry> g_models;
+std::map<std::pair<const float *, const float *>, kv_mirror> g_mirrors;
+thread_local hipStream_t t_go_stream = nullptr;
+
+void free_mirror(kv_mirror &k)
+{
+    (void)hipFree(k.k); (void)hipFree(k.v); (void)hipFree(k.len_d); (void)hipFree(k.pos_d);
+    (void)hipFree(k.emb_d); (void)hipFree(k.logits_d);
+    if (k.h_stage) (void)hipHostFree(k.h_stage);
+}
+
+uint64_t rows_seal(const float *k_cache, const float *v_cache, int l, long layer, int kvd, int n)
+{
+    if (n <= 0) return 0;
+    const int pick[3] = {0, n / 2, n - 1};
+    uint64_t h = 0;
+    for (int r : pick) {
+        h = h * 31 + fp_sample(k_cache + l * layer + (long)r * kvd, (long)kvd * 4);
+        h = h * 31 + fp_sample(v_cache + l * layer + (long)r * kvd, (long)kvd * 4);
+    }
+    return h;
+}
+
+} // namespace
+
+void mllm_gptoss_cache_clear()
+{
+    std::lock_guard<std::mutex> lk(g_go_mu);
+    (void)hipDeviceSynchronize();
+    for (auto &e : g_models) mllm_gptoss_release(e.second.m);
+    g_models.clear();
+    for (auto &e : g_mirrors) free_mirror(e.second);
+    g_mirrors.clear();
+}
+
+extern "C" MLLM_API void gptoss_forward(
+    const int *token, int pos, const float *emb, int V, const uint8_t **wQ, const uint8_t **wK, const uint8_t **wV,
+    const uint8_t **wO, const float **wAN, const float **wFN, const int *nQ, const int *nK, const int *nV,
+    const int *nO, const int *q_quant, const int *k_quant, const int *v_quant, const int *o_quant,
+    const uint8_t *wOut, int outNR, int outNC, int outQuant, float *k_cache, float *v_cache, int *kv_len,
+    const float *cos_table, const float *sin_table, int max_ctx, int rope_dim, float *workspace, int ws_size, int L,
+    int N, int NH, int NKH, int HD, int FF, float eps, int n_experts, int n_experts_per_tok, int moe_intermediate,
+    const float **w_gate_inp, const uint8_t **w_gate_exps, const uint8_t **w_up_exps, const uint8_t **w_down_exps,
+    int gate_exp_quant, int up_exp_quant, int down_exp_quant, float *logits, float *moe_prealloc_buf,
+    uint8_t *moe_prealloc_q8, float *gqa_ws)
+{
+    (void)V; (void)q_quant; (void)k_quant; (void)v_quant; (void)o_quant; (void)outNC; (void)outQuant;
+    (void)workspace; (void)ws_size; (void)FF; (void)moe_prealloc_buf; (void)moe_prealloc_q8; (void)gqa_ws;
+    const int inner = NH * HD, kvd = NKH * HD, E = n_experts;
+    if (L <= 0 || N <= 0 || !token || !kv_len || !k_cache || !v_cache || !logits) return;
+    for (int l = 0; l < L; l++)
+        if (nQ[l] != inner || nK[l] != kvd || nV[l] != kvd || nO[l] != N) {
+            mllm_set_error("gptoss_forward: nQ/nK/nV/nO must be NH*HD, NKH*HD, NKH*HD and N (output untouched)");
+            return;
+        }
+    for (int l = 0; l < L; l++)
+        if (kv_len[l] < 0 || kv_len[l] >= max_ctx) {
+            mllm_set_error("gptoss_forward: kv_len must stay below max_ctx (the reference writes past its cache)");
+            return;
+        }
+    if (pos < 0 || pos >= max_ctx) { mllm_set_error("gptoss_forward: pos outside the RoPE tables"); return; }
+    std::lock_guard<std::mutex> lk(g_go_mu);
+    if (!t_go_stream && hipStreamCreateWithFlags(&t_go_stream, hipStreamNonBlocking) != hipSuccess) {
+        t_go_stream = nullptr;
+        mllm_set_error("gptoss_forward: hipStreamCreate failed");
+        return;
+    }
+    hipStream_t st = t_go_stream;
+    // ---- model
+    std::vector<uintptr_t> key = {(uintptr_t)wOut, (uintptr_t)cos_table, (uintptr_t)sin_table};
+    for (int v : {L, N, NH, NKH, HD, E, n_experts_per_tok, moe_intermediate, max_ctx, rope_dim, outNR, gate_exp_quant,
+                  up_exp_quant, down_exp_quant})
+        key.push_back((uintptr_t)(unsigned)v);
+    key.push_back((uintptr_t)__builtin_bit_cast(uint32_t, eps));
+    for (int l = 0; l < L; l++) {
+        for (const void *p : {(const void *)wQ[l], (const void *)wK[l], (const void *)wV[l], (const void *)wO[l],
+                              (const void *)wAN[l], (const void *)wFN[l], (const void *)w_gate_inp[l]})
+            key.push_back((uintptr_t)p);
+    }
+    for (int i = 0; i < L - 1 + E; i++) {             // GO:179-181 read w_*_exps[l + e]
+        key.push_back((uintptr_t)w_gate_exps[i]);
+        key.push_back((uintptr_t)w_up_exps[i]);
+        key.push_back((uintptr_t)w_down_exps[i]);
+    }
+    const long rb = (long)(N / 32) * 17;
+    uint64_t fp = fp_sample(wQ[0], (long)inner * rb) ^ (fp_sample(wOut, (long)outNR * rb) * 3) ^
+                  (fp_sample(w_down_exps[0], (long)N * (moe_intermediate / 32) * 17) * 7) ^
+                  (fp_sample(w_gate_inp[L - 1], (long)E * N * 4) * 11);
+    model_entry &me = g_models[key];
+    if (me.m && me.fp != fp) { mllm_gptoss_release(me.m); me.m = nullptr; }
+    if (!me.m) {
+        mllm_gptoss_desc d{};
+        d.L = L; d.N = N; d.NH = NH; d.NKH = NKH; d.HD = HD; d.E = E; d.K = n_experts_per_tok;
+        d.M = moe_intermediate; d.max_ctx = max_ctx; d.rope_dim = rope_dim; d.outNR = outNR; d.eps = eps;
+        d.wQ = wQ; d.wK = wK; d.wV = wV; d.wO = wO; d.wAN = wAN; d.wFN = wFN; d.wOut = wOut;
+        d.w_gate_inp = w_gate_inp; d.w_gate_exps = w_gate_exps; d.w_up_exps = w_up_exps; d.w_down_exps = w_down_exps;
+        d.qt_gate = gate_exp_quant; d.qt_up = up_exp_quant; d.qt_down = down_exp_quant;
+        d.cos_t = cos_table; d.sin_t = sin_table;
+        me.m = mllm_gptoss_create(&d);
+        me.fp = fp;
+        if (!me.m) { g_models.erase(key); return; }
+    }
+    // ---- KV mirror
+    const long layer = (long)max_ctx * kvd;
+    kv_mirror &km = g_mirrors[{k_cache, v_cache}];
+    if (km.k && (km.L != L || km.max_ctx != max_ctx || km.kvd != kvd || km.outNR != outNR || km.N != N)) {
+        free_mirror(km);
+        km = kv_mirror{};
+    }
+    if (!km.k) {
+        km.L = L; km.max_ctx = max_ctx; km.kvd = kvd; km.outNR = outNR; km.N = N;
+        km.h_bytes = (size_t)a256((L + 1) * 4) + (size_t)outNR * 4 + (size_t)2 * L * kvd * 4;
+        if (hipMalloc(&km.k, (size_t)L * layer * 4) != hipSuccess || hipMalloc(&km.v, (size_t)L * layer * 4) != hipSuccess ||
+            hipMalloc(&km.len_d, (size_t)L * 4) != hipSuccess || hipMalloc(&km.pos_d, 256) != hipSuccess ||
+            hipMalloc(&km.emb_d, (size_t)N * 4) != hipSuccess || hipMalloc(&km.logits_d, (size_t)outNR * 4) != hipSuccess ||
+            hipHostMalloc(&km.h_stage, km.h_bytes, hipHostMallocDefault) != hipSuccess) {
+            free_mirror(km);
+            g_mirrors.erase({k_cache, v_cache});
+            mllm_set_error("gptoss_forward: KV mirror allocation failed");
+            return;
+        }
+        km.rows.assign(L, 0);
+        km.seal.assign(L, 0);
+    }
+#define GO_CK(e) do { if ((e) != hipSuccess) { mllm_set_error("gptoss_forward: HIP call failed"); return; } } while (0)
+    for (int l = 0; l < L; l++) {
+        const int hl = kv_len[l];
+        int from = km.rows[l];
+        if (hl < from) from = hl;                                           // a shorter (restarted) sequence
+        if (from > 0 && rows_seal(k_cache, v_cache, l, layer, kvd, from) != km.seal[l]) from = 0;   // rewritten rows
+        if (hl > from) {
+            const size_t off = (size_t)l * layer + (size_t)from * kvd, n = (size_t)(hl - from) * kvd * 4;
+            GO_CK(hipMemcpyAsync(km.k + off, k_cache + off, n, hipMemcpyHostToDevice, st));
+            GO_CK(hipMemcpyAsync(km.v + off, v_cache + off, n, hipMemcpyHostToDevice, st));
+        }
+        km.rows[l] = hl;
+    }
+    int *h_len = (int *)km.h_stage;
+    memcpy(h_len, kv_len, (size_t)L * 4);
+    h_len[L] = pos;
+    GO_CK(hipMemcpyAsync(km.len_d, h_len, (size_t)L * 4, hipMemcpyHostToDevice, st));
+    GO_CK(hipMemcpyAsync(km.pos_d, h_len + L, 4, hipMemcpyHostToDevice, st));
+    GO_CK(hipMemcpyAsync(km.emb_d, emb + (long)(*token) * N, (size_t)N * 4, hipMemcpyHostToDevice, st));
+    if (mllm_gptoss_step(me.m, km.emb_d, km.pos_d, km.len_d, km.k, km.v, km.logits_d, st) != 0) return;
+    float *h_out = (float *)((uint8_t *)km.h_stage + a256((L + 1) * 4));
+    float *h_rows = h_out + outNR;
+    GO_CK(hipMemcpyAsync(h_out, km.logits_d, (size_t)outNR * 4, hipMemcpyDeviceToHost, st));
+    for (int l = 0; l < L; l++) {
+        const size_t off = (size_t)l * layer + (size_t)kv_len[l] * kvd;
+        GO_CK(hipMemcpyAsync(h_rows + (size_t)2 * l * kvd, km.k + off, (size_t)kvd * 4, hipMemcpyDeviceToHost, st));
+        GO_CK(hipMemcpyAsync(h_rows + (size_t)(2 * l + 1) * kvd, km.v + off, (size_t)kvd * 4, hipMemcpyDeviceToHost, st));
+    }
+    GO_CK(hipStreamSynchronize(st));
+#undef GO_CK
+    memcpy(logits, h_out, (size_t)outNR * 4);
+    for (int l = 0; l < L; l++) {
+        const size_t off = (size_t)l * layer + (size_t)kv_len[l] * kvd;
+        memcpy(k_cache + off, h_rows + (size_t)2 * l * kvd, (size_t)kvd * 4);
+        memcpy(v_cache + off, h_rows + (size_t)(2 * l + 1) * kvd, (size_t)kvd * 4);
+        kv_len[l]++;
+        km.rows[l] = kv_len[l];
+        km.seal[l] = rows_seal(k_cache, v_cache, l, layer, kvd, kv_len[l]);
+    }
+}

@@ -29,3 +29,6 @@ bool mllm_moe_batched_supported(int sem_g, int sem_u, int sem_d);
 
 // Record an error for mllm_last_error() (logged once to stderr).
 void mllm_set_error(const char *msg);
+
+// Frees the models and KV mirrors gptoss_forward keeps (part of mllm_cache_clear).
+void mllm_gptoss_cache_clear();

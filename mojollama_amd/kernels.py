@@ -55,6 +55,16 @@ class KVView(ctypes.Structure):
 ATTN_CE, ATTN_GQA_C = 0, 1   # CE:141-158 gqa / gqa_attention.c:93 softmax
 
 
+class GptOssDesc(ctypes.Structure):
+    """mllm_gptoss_desc (include/mllm.h): host pointers to gptoss_forward's weights."""
+    _fields_ = [(n, ci) for n in ("L", "N", "NH", "NKH", "HD", "E", "K", "M", "max_ctx", "rope_dim", "outNR")] + [
+        ("eps", ctypes.c_float), ("wQ", ctypes.POINTER(cu)), ("wK", ctypes.POINTER(cu)), ("wV", ctypes.POINTER(cu)),
+        ("wO", ctypes.POINTER(cu)), ("wAN", ctypes.POINTER(cf)), ("wFN", ctypes.POINTER(cf)), ("wOut", cu),
+        ("w_gate_inp", ctypes.POINTER(cf)), ("w_gate_exps", ctypes.POINTER(cu)), ("w_up_exps", ctypes.POINTER(cu)),
+        ("w_down_exps", ctypes.POINTER(cu)), ("qt_gate", ci), ("qt_up", ci), ("qt_down", ci), ("cos_t", cf),
+        ("sin_t", cf)]
+
+
 _LIB = None
 
 
@@ -170,6 +180,20 @@ def load_kernels(path=LIB_PATH):
     so.mllm_kv_append.restype = ci
     so.mllm_rope.argtypes = [cvp, ci, ci, ci, cvp, cvp, cvp, ci, cvp]
     so.mllm_rope.restype = ci
+    # gptoss_forward (GO:96-130 argument list)
+    pcu, pcf, pci = ctypes.POINTER(cu), ctypes.POINTER(cf), ctypes.POINTER(ci)
+    so.gptoss_forward.argtypes = ([pci, ci, cf, ci] + [pcu] * 4 + [pcf] * 2 + [pci] * 8 + [cu, ci, ci, ci, cf, cf, pci,
+                                  cf, cf, ci, ci, cf, ci] + [ci] * 6 + [ctypes.c_float] + [ci] * 3 + [pcf] +
+                                  [pcu] * 3 + [ci] * 3 + [cf, cf, cu, cf])
+    so.gptoss_forward.restype = None
+    so.mllm_gptoss_create.argtypes = [cvp]
+    so.mllm_gptoss_create.restype = cvp
+    so.mllm_gptoss_release.argtypes = [cvp]
+    so.mllm_gptoss_release.restype = None
+    so.mllm_gptoss_kv_floats.argtypes = [cvp]
+    so.mllm_gptoss_kv_floats.restype = ctypes.c_long
+    so.mllm_gptoss_step.argtypes = [cvp, cvp, cvp, cvp, cvp, cvp, cvp, cvp]
+    so.mllm_gptoss_step.restype = ci
     so.mllm_page_table_create.argtypes = [ci, ci]
     so.mllm_page_table_create.restype = cvp
     so.mllm_page_table_destroy.argtypes = [cvp]

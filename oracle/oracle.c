@@ -745,3 +745,53 @@ void orc_rope(float *buf, int nh, int hd, int pos, const float *cos_t, const flo
         }
     }
 }
+
+/* ----------------------------------------------------------- gptoss_forward */
+
+/* rms_norm (GO:29-34): (x / sqrtf(ss/N + eps)) * w, ss in double. */
+static void orc_rms_div(float *out, const float *x, const float *w, int n, float eps)
+{
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float r = sqrtf((float)(ss / n) + eps);
+    for (int i = 0; i < n; i++) out[i] = (x[i] / r) * w[i];
+}
+
+void orc_gptoss_forward(const orc_gptoss *m, int token, int pos, float *k_cache, float *v_cache, int *kv_len,
+                        float *logits)
+{
+    const int N = m->N, inner = m->NH * m->HD, kvd = m->NKH * m->HD;
+    float *x = (float *)malloc(sizeof(float) * N), *xn = (float *)malloc(sizeof(float) * N);
+    float *res = (float *)malloc(sizeof(float) * N), *ffn = (float *)malloc(sizeof(float) * N);
+    float *q = (float *)malloc(sizeof(float) * inner), *att = (float *)malloc(sizeof(float) * inner);
+    float *k = (float *)malloc(sizeof(float) * kvd), *v = (float *)malloc(sizeof(float) * kvd);
+    float *op = (float *)malloc(sizeof(float) * N);
+    int idx[64];
+    float w[64];
+    memcpy(x, m->emb + (long)token * N, sizeof(float) * N);
+    for (int l = 0; l < m->L; l++) {
+        memcpy(res, x, sizeof(float) * N);
+        orc_rms_div(xn, x, m->wAN[l], N, m->eps);
+        orc_gemv(ORC_MXFP4, m->wQ[l], xn, q, inner, N, 1);
+        orc_gemv(ORC_MXFP4, m->wK[l], xn, k, kvd, N, 1);
+        orc_gemv(ORC_MXFP4, m->wV[l], xn, v, kvd, N, 1);
+        orc_rope(q, m->NH, m->HD, pos, m->cos_t, m->sin_t, m->rope_dim);
+        orc_rope(k, m->NKH, m->HD, pos, m->cos_t, m->sin_t, m->rope_dim);
+        float *kc = k_cache + (long)l * m->max_ctx * kvd, *vc = v_cache + (long)l * m->max_ctx * kvd;
+        int sl = kv_len[l];
+        memcpy(kc + (long)sl * kvd, k, sizeof(float) * kvd);
+        memcpy(vc + (long)sl * kvd, v, sizeof(float) * kvd);
+        kv_len[l]++;
+        sl++;
+        orc_gqa_decode(ORC_ATTN_GQA_C, q, kc, vc, kvd, sl, m->NH, m->NKH, m->HD, att);
+        orc_gemv(ORC_MXFP4, m->wO[l], att, op, N, inner, 1);
+        for (int i = 0; i < N; i++) x[i] = res[i] + op[i];
+        orc_rms_div(xn, x, m->wFN[l], N, m->eps);
+        orc_route(m->w_gate_inp[l], xn, 1, N, m->E, m->K, 1, idx, w);
+        orc_moe_forward_token(m->w_gate_exps + l, m->w_up_exps + l, m->w_down_exps + l, xn, m->M, N, m->qt_gate,
+                              m->qt_up, m->qt_down, idx, w, m->K, 1, ffn);
+        for (int i = 0; i < N; i++) x[i] = res[i] + ffn[i];
+    }
+    orc_gemv(ORC_MXFP4, m->wOut, xn, logits, m->outNR, N, 1);
+    free(x); free(xn); free(res); free(ffn); free(q); free(att); free(k); free(v); free(op);
+}

@@ -122,6 +122,32 @@ float orc_exp_ps_simd(float x);
  * cos/sin rows [pos][rope_dim/2]. */
 void orc_rope(float *buf, int nh, int hd, int pos, const float *cos_t, const float *sin_t, int rope_dim);
 
+/* gptoss_forward (GO:96-189), one token, the reference's steps in order:
+ * x = emb[token]; per layer l: res = x; xn = (x / rms) * wAN[l] (rms_norm,
+ * GO:29-34); q, k, v = MXFP4 GEMVs (mxfp4_matmul_omp) of xn; RoPE on q and
+ * k at pos; K/V row kv_len[l] of layer l's cache := k, v and kv_len[l]++;
+ * att = gqa_attention_decode over kv_len[l] rows; x = res + Wo att; xn =
+ * rms_norm(x, wFN[l]); router_topk (GO:53-93: fp32 chain, softmax, top-k,
+ * renormalise); ffn = moe_forward_omp(w_*_exps + l, ...) -- expert e of
+ * layer l is the matrix at w_*_exps[l + e], as GO:179-181 index it; x =
+ * res + ffn (the attention output is not carried, GO:186).  Finally logits
+ * = MXFP4 GEMV of the last xn (GO:189: no output norm).  Caches are
+ * [L][max_ctx][nkh * hd]. */
+typedef struct {
+    int L, N, NH, NKH, HD, V, E, K, M, max_ctx, rope_dim, outNR;
+    float eps;
+    const float *emb;
+    const uint8_t *const *wQ, *const *wK, *const *wV, *const *wO;
+    const float *const *wAN, *const *wFN;
+    const uint8_t *wOut;
+    const float *const *w_gate_inp;
+    const uint8_t *const *w_gate_exps, *const *w_up_exps, *const *w_down_exps;
+    int qt_gate, qt_up, qt_down;
+    const float *cos_t, *sin_t;
+} orc_gptoss;
+void orc_gptoss_forward(const orc_gptoss *m, int token, int pos, float *k_cache, float *v_cache, int *kv_len,
+                        float *logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,20 @@ def build():
 ATTN_CE, ATTN_GQA_C = 0, 1
 
 
+class GptOss(ctypes.Structure):
+    """orc_gptoss (oracle.h): the weights and shapes orc_gptoss_forward reads."""
+    _pp = ctypes.POINTER(ctypes.POINTER(ctypes.c_uint8))
+    _pf = ctypes.POINTER(ctypes.POINTER(ctypes.c_float))
+    _fields_ = [(n, ctypes.c_int) for n in ("L", "N", "NH", "NKH", "HD", "V", "E", "K", "M", "max_ctx", "rope_dim",
+                                            "outNR")] + [
+        ("eps", ctypes.c_float), ("emb", ctypes.POINTER(ctypes.c_float)),
+        ("wQ", _pp), ("wK", _pp), ("wV", _pp), ("wO", _pp), ("wAN", _pf), ("wFN", _pf),
+        ("wOut", ctypes.POINTER(ctypes.c_uint8)), ("w_gate_inp", _pf),
+        ("w_gate_exps", _pp), ("w_up_exps", _pp), ("w_down_exps", _pp),
+        ("qt_gate", ctypes.c_int), ("qt_up", ctypes.c_int), ("qt_down", ctypes.c_int),
+        ("cos_t", ctypes.POINTER(ctypes.c_float)), ("sin_t", ctypes.POINTER(ctypes.c_float))]
+
+
 class Oracle:
     def __init__(self, path=ORACLE_SO):
         if not os.path.exists(path):
@@ -85,6 +99,8 @@ class Oracle:
         lib.orc_exp_ps_simd.restype = ctypes.c_float
         lib.orc_rope.argtypes = [_cf, _ci, _ci, _ci, _cf, _cf, _ci]
         lib.orc_rope.restype = None
+        lib.orc_gptoss_forward.argtypes = [ctypes.POINTER(GptOss), _ci, _ci, _cf, _cf, ctypes.POINTER(ctypes.c_int), _cf]
+        lib.orc_gptoss_forward.restype = None
         lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
         lib.orc_f32_to_f16.restype = ctypes.c_uint16
         lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -163,6 +179,11 @@ class Oracle:
         self.lib.orc_rope(fp(b), nh, hd, pos, fp(np.ascontiguousarray(cos_t, np.float32)),
                           fp(np.ascontiguousarray(sin_t, np.float32)), rope_dim)
         return b
+
+    def gptoss_forward(self, model, token, pos, k_cache, v_cache, kv_len, logits):
+        """orc_gptoss_forward on a GptOss struct; caches, kv_len and logits updated in place."""
+        self.lib.orc_gptoss_forward(ctypes.byref(model), token, pos, fp(k_cache), fp(v_cache),
+                                    kv_len.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), fp(logits))
 
     def moe_ffn_stride(self, which, qt, N, M):
         return self.lib.orc_moe_ffn_stride(which, qt, N, M)

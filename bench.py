@@ -427,12 +427,13 @@ def bench_moe(torch, dev, args, tag, sizes=(1, 1280)):
                       "note": f"{R} distinct tokens per replay, {Kk} experts each; the cycle's experts exceed the "
                               "256 MB Infinity Cache when bytes_per_cycle_MB > 256"}
     log(f"MoE {tag} T=1 cold: {per * 1e3:.1f} us ({touched} experts, {touched * wbytes_expert / 1e6:.0f} MB per cycle)")
-    # the drop-in host ABI: moe_forward_omp (host pointers) per call
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as Om
-    orc = Om.Oracle()
+    # the drop-in host ABI: moe_forward_omp (host pointers) per call, on the
+    # routing the layer itself computes for these tokens
     n_tok = 24
-    idx_h, w_h = orc.route(router_np, x_np[:n_tok], Kk, renorm=True)
+    idx_d = torch.empty(n_tok, Kk, dtype=torch.int32, device="cuda")
+    w_d = torch.empty(n_tok, Kk, dtype=torch.float32, device="cuda")
+    layer.forward(x[:n_tok].contiguous(), idx=idx_d, w=w_d)
+    idx_h, w_h = idx_d.cpu().numpy(), w_d.cpu().numpy()
     need = sorted(set(int(e) for e in idx_h.ravel()))
     host = {e: (gates[e].cpu().numpy(), ups[e].cpu().numpy(), downs[e].cpu().numpy()) for e in need}
     dummy = host[need[0]]
@@ -449,6 +450,113 @@ def bench_moe(torch, dev, args, tag, sizes=(1, 1280)):
     log(f"host-ABI moe_forward_omp ({tag}): {res['host_abi_moe_forward_omp_us']} us per call")
     del layer
     torch.cuda.empty_cache()
+    return res
+
+
+def bench_attention(torch, dev, args):
+    """Decode attention (gqa_attention.c semantics) at gpt-oss-20b's head layout
+    (64 query / 8 KV heads of 64) over 4096 cached positions: B=1 on a
+    contiguous cache and B=8 sequences on 64-row pages scattered by a random
+    page table.  Bytes = the K and V rows read + q and out; each replay cycles
+    over copies of the caches that together exceed the 256 MB Infinity Cache."""
+    nh, nkh, hd, S = 64, 8, 64, 4096
+    res = {}
+    for B, page in ((1, 0), (8, 64)):
+        row = nkh * hd
+        per = B * S * row * 4 * 2
+        R = max(2, -(-600_000_000 // per))
+        kvs = []
+        for _ in range(R):
+            k = torch.randn(B * S, row, device="cuda")
+            v = torch.randn(B * S, row, device="cuda")
+            if page:
+                n_pages = B * S // page
+                tables = torch.randperm(n_pages, device="cuda").to(torch.int32).view(B, S // page).contiguous()
+                kvs.append(dev.kv_view(k, v, block_tables=tables, page_size=page, n_pages=n_pages))
+            else:
+                kvs.append(dev.kv_view(k, v, seq_stride=S * row))
+        lens = torch.full((B,), S, dtype=torch.int32, device="cuda")
+        q = torch.randn(B, nh * hd, device="cuda")
+        out = torch.empty(B, nh * hd, device="cuda")
+        ws = torch.empty(dev.so.mllm_gqa_workspace_size(B, nh, hd, S), dtype=torch.uint8, device="cuda")
+        ms = time_region(torch, lambda: [dev.gqa_decode(K.ATTN_GQA_C, q, kv, lens, S, nh, nkh, hd, out=out, ws=ws)
+                                         for kv in kvs], max(5, args.steps // 2), args.warmup) / R
+        nbytes = per + B * nh * hd * 8
+        key = f"B{B}_{'paged' + str(page) if page else 'contiguous'}"
+        res[key] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "seq": S}
+        log(f"attention {key}: {ms * 1e3:.2f} us, {res[key]['GB/s']} GB/s")
+        del kvs
+        torch.cuda.empty_cache()
+    return res
+
+
+def bench_gptoss(torch, dev, args):
+    """gptoss_forward's device step (mllm_gptoss_step) at gpt-oss-20b shapes:
+    24 layers, N 2880, 64/8 heads of 64, MXFP4 q/k/v/o, 32 MXFP4 experts of
+    2880 (top-4, expert e of layer l = matrix l + e as GO:179-181 index them),
+    vocab 201088, with 512 positions already cached; one token per step,
+    replayed from a captured graph (each replay appends a row)."""
+    L, N, NH, NKH, HD, E, Kk, M, V, ctx = 24, 2880, 64, 8, 64, 32, 4, 2880, 201088, 1024
+    inner, kvd = NH * HD, NKH * HD
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    mx = lambda r, c: W.gen_weights_torch(gen, W.QT_MXFP4, r, c).cpu().numpy()  # noqa: E731
+    f32 = lambda *sh, sc=1.0: (torch.randn(*sh, generator=gen, device="cuda") * sc).cpu().numpy()  # noqa: E731
+    wq = [mx(inner, N) for _ in range(L)]
+    wk = [mx(kvd, N) for _ in range(L)]
+    wv = [mx(kvd, N) for _ in range(L)]
+    wo = [mx(N, inner) for _ in range(L)]
+    an = [1 + f32(N, sc=0.1) for _ in range(L)]
+    fn = [1 + f32(N, sc=0.1) for _ in range(L)]
+    router = [f32(E, N, sc=0.05) for _ in range(L)]
+    ge = [mx(M, N) for _ in range(L - 1 + E)]
+    ue = [mx(M, N) for _ in range(L - 1 + E)]
+    de = [mx(N, M) for _ in range(L - 1 + E)]
+    wout = mx(V, N)
+    theta = f32(ctx, HD // 2)
+    cos_t, sin_t = np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
+    arr_u = lambda xs: (K.cu * len(xs))(*[a.ctypes.data_as(K.cu) for a in xs])  # noqa: E731
+    arr_f = lambda xs: (K.cf * len(xs))(*[a.ctypes.data_as(K.cf) for a in xs])  # noqa: E731
+    keep = [arr_u(wq), arr_u(wk), arr_u(wv), arr_u(wo), arr_f(an), arr_f(fn), arr_f(router), arr_u(ge), arr_u(ue),
+            arr_u(de)]
+    d = K.GptOssDesc(L=L, N=N, NH=NH, NKH=NKH, HD=HD, E=E, K=Kk, M=M, max_ctx=ctx, rope_dim=HD, outNR=V, eps=1e-5,
+                     wQ=keep[0], wK=keep[1], wV=keep[2], wO=keep[3], wAN=keep[4], wFN=keep[5],
+                     wOut=wout.ctypes.data_as(K.cu), w_gate_inp=keep[6], w_gate_exps=keep[7], w_up_exps=keep[8],
+                     w_down_exps=keep[9], qt_gate=39, qt_up=39, qt_down=39, cos_t=cos_t.ctypes.data_as(K.cf),
+                     sin_t=sin_t.ctypes.data_as(K.cf))
+    h = dev.so.mllm_gptoss_create(ctypes.byref(d))
+    if not h:
+        raise RuntimeError("mllm_gptoss_create: " + K.last_error(dev.so))
+    try:
+        n = dev.so.mllm_gptoss_kv_floats(h)
+        kc = torch.randn(n, device="cuda")
+        vc = torch.randn(n, device="cuda")
+        lens = torch.full((L,), 512, dtype=torch.int32, device="cuda")
+        pos = torch.full((1,), 512, dtype=torch.int32, device="cuda")
+        x = torch.randn(N, device="cuda")
+        logits = torch.empty(V, device="cuda")
+
+        def step():
+            rc = dev.so.mllm_gptoss_step(h, x.data_ptr(), pos.data_ptr(), lens.data_ptr(), kc.data_ptr(),
+                                         vc.data_ptr(), logits.data_ptr(), dev._stream())
+            if rc:
+                raise RuntimeError("mllm_gptoss_step: " + K.last_error(dev.so))
+        steps = min(20, max(5, args.steps))
+        ms = time_region(torch, step, steps, 2)
+        fin = bool(torch.isfinite(logits).all())
+        seq = int(lens[0].item())
+    finally:
+        dev.so.mllm_gptoss_release(h)
+    wb = (L * (W.row_bytes(39, N) * (inner + 2 * kvd) + W.row_bytes(39, inner) * N +
+               Kk * (2 * W.row_bytes(39, N) * M + W.row_bytes(39, M) * N) + E * N * 4) + W.row_bytes(39, N) * V)
+    kvb = L * 2 * 512 * kvd * 4
+    res = {"ms_per_token": round(ms, 3), "tokens/s": round(1e3 / ms, 1),
+           "GB/s": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
+           "hbm_frac": round((wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes_per_token_MB": round((wb + kvb) / 1e6, 1), "logits_finite": fin, "kv_len_after": seq,
+           "note": "weights read per token: q/k/v/o, the 4 routed experts and the router of each layer, lm_head; "
+                   "KV rows at ~512 positions"}
+    log(f"gptoss step (24 layers, vocab {V}): {ms:.3f} ms/token, {res['GB/s']} GB/s, logits finite {fin}")
     return res
 
 
@@ -674,6 +782,8 @@ def main():
         extra["configs2_prefill_gemm"] = bench_prefill(torch, dev, args)
         extra["configs3_gptoss_moe"] = bench_moe(torch, dev, args, "gptoss")
         extra["configs4_qwen3_moe"] = bench_moe(torch, dev, args, "qwen3")
+        extra["decode_attention_gptoss_heads"] = bench_attention(torch, dev, args)
+        extra["gptoss_forward_step"] = bench_gptoss(torch, dev, args)
         if use_cpu:
             for key, leg in (("configs0_q8_0_gemv", "q8"), ("configs2_prefill_gemm", "prefill"),
                              ("configs3_gptoss_moe", "moe_gptoss"), ("configs4_qwen3_moe", "moe_qwen3")):

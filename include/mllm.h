@@ -108,7 +108,9 @@ MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, in
  * capped at 1e38, normalised by 1 / (sum + 1e-10).  workspace is not written
  * (the reference keeps its weights there; nothing reads them back).  Host
  * pointers: q, K and V are uploaded on every call, so the device entry
- * mllm_gqa_decode is the fast path.  seq_len <= 0 gives zeros. */
+ * mllm_gqa_decode is the fast path.  seq_len <= 0 gives zeros.  Served for
+ * n_head % n_kv_head == 0, n_head / n_kv_head <= 16, head_dim <= 256 and a
+ * multiple of 4; other shapes leave out untouched with an error. */
 MLLM_API void gqa_attention_decode(const float *q, const float *k_cache, const float *v_cache, float *out, int seq_len,
                                    int n_head, int n_kv_head, int head_dim, float *workspace);
 
@@ -300,7 +302,7 @@ typedef struct {
  * seq_lens[b] cached rows (device array, each <= max_seq).
  * mode 0: CE:141-158 gqa (expf weights, 1 / sum); mode 1: gqa_attention.c
  * (see gqa_attention_decode).  q, out [B][NH * HD]; NH % NKH == 0,
- * NH / NKH <= 16, HD <= 256.  Three launches on `stream`; weights and partial
+ * NH / NKH <= 16, HD <= 256 and a multiple of 4; K and V 16-byte aligned.  Three launches on `stream`; weights and partial
  * sums go to the workspace (mllm_gqa_workspace_size). */
 MLLM_API long mllm_gqa_workspace_size(int B, int NH, int HD, int max_seq);
 MLLM_API int mllm_gqa_decode(int mode, const float *q, const mllm_kv_view *kv, const int *seq_lens, int max_seq, int B,

@@ -52,6 +52,50 @@ __device__ __forceinline__ const float *kv_row(const float *base, const mllm_kv_
     return base + ((long)page * kv.page_size + s % kv.page_size) * rs + (long)j * HD;
 }
 
+// Offsets (floats from the pool base) of a chunk's rows for KV head j, -1
+// past the sequence or on an unmapped page; the first wave computes them.
+__device__ __forceinline__ void chunk_rows(long *ro, const mllm_kv_view &kv, int b, int s0, int rows, int NKH, int HD,
+                                           int j)
+{
+    if (threadIdx.x < kChunk) {
+        const int p = threadIdx.x;
+        long off = -1;
+        if (p < rows) {
+            const float *r = kv_row(kv.k, kv, b, s0 + p, NKH, HD, j);
+            if (r) off = r - kv.k;
+        }
+        ro[p] = off;
+    }
+}
+
+// The chunk's rows [kChunk][HD] from base + ro[p] into LDS rows of ld floats,
+// in 16-byte pieces (HD % 4 == 0, base 16-byte aligned); every load is issued
+// unconditionally (a missing row reads row 0 and stores zeros), so a thread's
+// pieces are all in flight at once.
+__device__ __forceinline__ void stage_chunk(float *dst, int ld, const float *__restrict__ base, const long *ro, int HD)
+{
+    const int hd4 = HD >> 2, n = kChunk * hd4;
+    float4 v[kMaxHD / 16];
+    bool ok[kMaxHD / 16];
+#pragma unroll
+    for (int k = 0; k < kMaxHD / 16; k++) {
+        const int i = threadIdx.x + 256 * k;
+        const int p = min(i, n - 1) / hd4, d4 = min(i, n - 1) - p * hd4;
+        const long off = ro[p];
+        ok[k] = i < n && off >= 0;
+        v[k] = *reinterpret_cast<const float4 *>(base + (off >= 0 ? off : 0) + 4 * d4);
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxHD / 16; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= n) break;
+        const int p = i / hd4, d4 = i - p * hd4;
+        const float4 w = ok[k] ? v[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float *o = dst + p * ld + 4 * d4;
+        o[0] = w.x; o[1] = w.y; o[2] = w.z; o[3] = w.w;
+    }
+}
+
 __device__ __forceinline__ int seq_len_of(const attn_args &a, int b)
 {
     const int n = a.seq_lens[b];
@@ -103,20 +147,15 @@ __global__ __launch_bounds__(256) void k_attn_scores(attn_args a)
     const int len = seq_len_of(a, b), s0 = c * kChunk;
     if (s0 >= len) return;
     const int HD = a.HD, G = a.NH / a.NKH, ld = HD + 1;
-    float *qs = lds;                  // [G][HD]
-    float *ks = lds + G * HD;         // [kChunk][HD + 1]
+    long *ro = reinterpret_cast<long *>(lds);     // [kChunk] row offsets
+    float *qs = lds + 2 * kChunk;                  // [G][HD]
+    float *ks = qs + G * HD;                       // [kChunk][HD + 1]
     const float *qb = a.q + (long)b * a.NH * HD + (long)j * G * HD;
-    for (int i = threadIdx.x; i < G * HD; i += 256) qs[i] = qb[i];
     const int rows = min(kChunk, len - s0);
-    for (int i = threadIdx.x; i < kChunk * HD; i += 256) {
-        const int p = i / HD, d = i - p * HD;
-        float val = 0.0f;
-        if (p < rows) {
-            const float *r = kv_row(a.kv.k, a.kv, b, s0 + p, a.NKH, HD, j);
-            if (r) val = r[d];
-        }
-        ks[p * ld + d] = val;
-    }
+    chunk_rows(ro, a.kv, b, s0, rows, a.NKH, HD, j);
+    for (int i = threadIdx.x; i < G * HD; i += 256) qs[i] = qb[i];
+    __syncthreads();
+    stage_chunk(ks, ld, a.kv.k, ro, HD);
     __syncthreads();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const float scale = 1.0f / sqrtf((float)HD);
@@ -145,18 +184,13 @@ __global__ __launch_bounds__(256) void k_attn_values(attn_args a)
     const int len = seq_len_of(a, b), s0 = c * kChunk;
     if (s0 >= len) return;
     const int HD = a.HD, G = a.NH / a.NKH;
-    float *wt = lds;                  // [G][kChunk]
-    float *vs = lds + G * kChunk;     // [kChunk][HD]
+    long *ro = reinterpret_cast<long *>(lds);     // [kChunk] row offsets (V mirrors K's layout)
+    float *wt = lds + 2 * kChunk;                  // [G][kChunk]
+    float *vs = wt + G * kChunk;                   // [kChunk][HD]
     const int rows = min(kChunk, len - s0), nc = (len + kChunk - 1) / kChunk;
-    for (int i = threadIdx.x; i < kChunk * HD; i += 256) {
-        const int p = i / HD, d = i - p * HD;
-        float val = 0.0f;
-        if (p < rows) {
-            const float *r = kv_row(a.kv.v, a.kv, b, s0 + p, a.NKH, HD, j);
-            if (r) val = r[d];
-        }
-        vs[p * HD + d] = val;
-    }
+    chunk_rows(ro, a.kv, b, s0, rows, a.NKH, HD, j);
+    __syncthreads();
+    stage_chunk(vs, HD, a.kv.v, ro, HD);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int vec_end = a.mode == 1 ? len / 8 * 8 : 0;
     for (int g = w; g < G; g += 4) {
@@ -196,20 +230,36 @@ __global__ __launch_bounds__(256) void k_attn_values(attn_args a)
 
 // out[b][h][d] = sum_c pout * 1 / (sum_c psum [+ 1e-10 in mode 1]); an empty
 // sequence gives zeros (the reference's products over no positions).
-// grid (NH, B), HD threads rounded up to a wave.
+// grid (NH, B), 256 threads: 256 / HD groups of HD lanes each take every
+// ng-th chunk (four loads in flight per lane), then group 0 adds the groups.
 __global__ __launch_bounds__(256) void k_attn_combine(attn_args a)
 {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    if (d >= a.HD) return;
+    __shared__ float part[256], spart[256];
+    const int h = blockIdx.x, b = blockIdx.y, HD = a.HD, ng = 256 / HD;
+    const int gi = threadIdx.x / HD, d = threadIdx.x - gi * HD;
     const int len = seq_len_of(a, b), nc = (len + kChunk - 1) / kChunk;
-    float *o = a.out + ((long)b * a.NH + h) * a.HD + d;
-    if (len == 0) { *o = 0.0f; return; }
     const float *ps = a.psum + ((long)b * a.NH + h) * a.n_chunks;
-    const float *po = a.pout + ((long)b * a.NH + h) * a.n_chunks * a.HD + d;
-    float sum = 0.0f, acc = 0.0f;
-    for (int c = 0; c < nc; c++) { sum += ps[c]; acc += po[(long)c * a.HD]; }
-    const float inv = a.mode == 1 ? 1.0f / (sum + 1e-10f) : 1.0f / sum;
-    *o = acc * inv;
+    const float *po = a.pout + ((long)b * a.NH + h) * a.n_chunks * HD + d;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (gi < ng) {
+        int c = gi;
+        for (; c + 3 * ng < nc; c += 4 * ng) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                acc[u] += po[(long)(c + u * ng) * HD];
+                sum[u] += ps[c + u * ng];
+            }
+        }
+        for (; c < nc; c += ng) { acc[0] += po[(long)c * HD]; sum[0] += ps[c]; }
+        part[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        spart[threadIdx.x] = (sum[0] + sum[1]) + (sum[2] + sum[3]);
+    }
+    __syncthreads();
+    if (gi != 0) return;
+    float o = 0.0f, s = 0.0f;
+    for (int g = 0; g < ng; g++) { o += part[g * HD + d]; s += spart[g * HD + d]; }
+    const float inv = a.mode == 1 ? 1.0f / (s + 1e-10f) : 1.0f / s;
+    a.out[((long)b * a.NH + h) * HD + d] = len == 0 ? 0.0f : o * inv;
 }
 
 // New K/V rows: token b's k/v [NKH*HD] to row pos[b] of its cache (CE:1363-1381,
@@ -264,7 +314,7 @@ long attn_ws(int B, int NH, int HD, int max_seq, attn_args *a, uint8_t *base)
 
 bool attn_shape_ok(int NH, int NKH, int HD)
 {
-    return NH > 0 && NKH > 0 && NH % NKH == 0 && NH / NKH <= kMaxRep && HD > 0 && HD <= kMaxHD;
+    return NH > 0 && NKH > 0 && NH % NKH == 0 && NH / NKH <= kMaxRep && HD > 0 && HD <= kMaxHD && HD % 4 == 0;
 }
 
 } // namespace
@@ -282,7 +332,12 @@ MLLM_API int mllm_gqa_decode(int mode, const float *q, const mllm_kv_view *kv, c
 {
     if ((mode != 0 && mode != 1) || !q || !kv || !kv->k || !kv->v || !seq_lens || !out || B <= 0 || max_seq < 0 ||
         !attn_shape_ok(NH, NKH, HD)) {
-        mllm_set_error("mllm_gqa_decode: bad arguments (mode 0/1, NH % NKH == 0, NH/NKH <= 16, HD <= 256)");
+        mllm_set_error("mllm_gqa_decode: bad arguments (mode 0/1, NH % NKH == 0, NH/NKH <= 16, HD <= 256 and a "
+                       "multiple of 4)");
+        return -1;
+    }
+    if (((uintptr_t)kv->k | (uintptr_t)kv->v) & 15) {
+        mllm_set_error("mllm_gqa_decode: K and V must be 16-byte aligned");
         return -1;
     }
     if (kv->block_tables && (kv->page_size <= 0 || kv->max_blocks <= 0 || kv->n_pages <= 0)) {
@@ -300,11 +355,11 @@ MLLM_API int mllm_gqa_decode(int mode, const float *q, const mllm_kv_view *kv, c
     attn_ws(B, NH, HD, a.max_seq, &a, (uint8_t *)workspace);
     const int G = NH / NKH;
     const dim3 grid(a.n_chunks, NKH, B);
-    const size_t lds1 = ((size_t)G * HD + (size_t)kChunk * (HD + 1)) * 4;
-    const size_t lds2 = ((size_t)G * kChunk + (size_t)kChunk * HD) * 4;
+    const size_t lds1 = (2 * (size_t)kChunk + (size_t)G * HD + (size_t)kChunk * (HD + 1)) * 4;
+    const size_t lds2 = (2 * (size_t)kChunk + (size_t)G * kChunk + (size_t)kChunk * HD) * 4;
     hipLaunchKernelGGL(k_attn_scores, grid, dim3(256), lds1, st, a);
     hipLaunchKernelGGL(k_attn_values, grid, dim3(256), lds2, st, a);
-    hipLaunchKernelGGL(k_attn_combine, dim3(NH, B), dim3((HD + 63) / 64 * 64), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(NH, B), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

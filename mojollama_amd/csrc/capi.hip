@@ -1136,9 +1136,9 @@ MLLM_API void gqa_attention_decode(const float *q, const float *k_cache, const f
     API_GUARD;
     (void)workspace;
     if (n_head <= 0 || head_dim <= 0) return;
-    if (n_kv_head <= 0 || n_head % n_kv_head || n_head / n_kv_head > 16 || head_dim > 256) {
-        set_error("gqa_attention_decode: n_head %% n_kv_head == 0, n_head / n_kv_head <= 16 and head_dim <= 256 are "
-                  "served (output untouched)");
+    if (n_kv_head <= 0 || n_head % n_kv_head || n_head / n_kv_head > 16 || head_dim > 256 || head_dim % 4) {
+        set_error("gqa_attention_decode: n_head %% n_kv_head == 0, n_head / n_kv_head <= 16 and head_dim <= 256, a "
+                  "multiple of 4, are served (output untouched)");
         return;
     }
     const size_t qo = (size_t)n_head * head_dim * 4;

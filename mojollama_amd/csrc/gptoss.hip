@@ -111,10 +111,10 @@ MLLM_API mllm_gptoss *mllm_gptoss_create(const mllm_gptoss_desc *desc)
     if (!desc) return nullptr;
     const mllm_gptoss_desc &d = *desc;
     if (d.L <= 0 || d.N <= 0 || d.N % 32 || d.NH <= 0 || d.NKH <= 0 || d.NH % d.NKH || d.NH / d.NKH > 16 ||
-        d.HD <= 0 || d.HD > 256 || (d.NH * d.HD) % 32 || d.E <= 0 || d.K <= 0 || d.K > d.E || d.M <= 0 ||
+        d.HD <= 0 || d.HD > 256 || d.HD % 4 || (d.NH * d.HD) % 32 || d.E <= 0 || d.K <= 0 || d.K > d.E || d.M <= 0 ||
         d.max_ctx <= 0 || d.outNR <= 0) {
         mllm_set_error("mllm_gptoss_create: unsupported shape (N and NH*HD multiples of 32, NH % NKH == 0, "
-                       "NH/NKH <= 16, HD <= 256, K <= E)");
+                       "NH/NKH <= 16, HD <= 256 and a multiple of 4, K <= E)");
         return nullptr;
     }
     const int rd = d.rope_dim <= 0 ? d.HD : d.rope_dim;

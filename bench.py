@@ -75,10 +75,12 @@ from mojollama_amd import workloads as W  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 EPS = 1e-5
-# HBM bytes per launch of the roofline kernel from FETCH_SIZE / WRITE_SIZE
-# counter runs calibrated on a copy of known size (bench.py --kernel ...):
-# profiles/gemv_down_q6k_chain_traffic.md gives the commands and raw values.
-ROOFLINE_TRAFFIC_BYTES = None
+# HBM bytes per launch of a decode-chain GEMV kind, from FETCH_SIZE /
+# WRITE_SIZE counter runs (bench.py --kernel gate_up) calibrated on a copy of
+# known size (bench.py --kernel copy): FETCH 6526.2 KiB x 1.99982 + WRITE
+# 22.0 KiB for the fused gate+up launch.  profiles/gemv_gate_up_q4k_traffic.md
+# gives the commands and raw values; re-measure after any change to that kernel.
+ROOFLINE_TRAFFIC_BYTES = {"gate_up": 13386967}
 
 
 def parse():
@@ -89,7 +91,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU reference timing")
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
-    ap.add_argument("--kernel", choices=("gate_up", "down", "copy"),
+    ap.add_argument("--kernel", choices=("gate_up", "down", "copy", "gemm_gate", "gemm_down", "moe_gptoss",
+                                         "moe_qwen3"),
                     help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
                          "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
     return ap.parse_args()
@@ -240,6 +243,27 @@ def kernel_only(torch, dev, which):
         torch.cuda.synchronize()
         for _ in range(50):
             b.copy_(a)
+    elif which in ("gemm_gate", "gemm_down"):
+        # configs[2] prefill at M = 1280: the Q4_K gate (5632x2048) or the Q6_K down (2048x5632), 10 launches
+        gen = torch.Generator(device="cuda").manual_seed(3)
+        sem, qt, R, C = (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048) if which == "gemm_gate" else \
+            (K.Q6_K_SEQ, W.QT_Q6_K, 2048, 5632)
+        packed = dev.pack(sem, W.gen_weights_torch(gen, qt, R, C), R, C)
+        x = torch.randn(1280, C, device="cuda", generator=gen).bfloat16().float()
+        o = torch.empty(1280, R, device="cuda")
+        ws = dev.workspace(sem, C, 1280, x.device, R)
+        for _ in range(10):
+            dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
+    elif which in ("moe_gptoss", "moe_qwen3"):
+        # the MoE layer at T = 1280, 5 forwards
+        wl = W.moe_workload(which[4:], 1280)
+        c = wl["cfg"]
+        layer = dev.moe_prepare(wl["qts"], c["N"], c["M"], c["E"], c["K"], wl["gates"], wl["ups"], wl["downs"],
+                                torch.from_numpy(wl["router"]).cuda(), 1)
+        x = torch.from_numpy(wl["x"]).cuda()
+        o = torch.empty(1280, c["N"], device="cuda")
+        for _ in range(5):
+            layer.forward(x, out=o)
     else:
         layers, lm, on = build_tinyllama(dev, np.random.default_rng(2), 1)
         ch = DecodeChain(torch, dev, layers, lm, on, 1)
@@ -818,7 +842,7 @@ def main():
                                             "note": "the same 89 GEMVs with independent inputs, no prologue"},
                    "per_kind_B1": kinds},
         "roofline": {"bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kd["GB/s"] / HBM_PEAK_GBS, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
+                     "frac": round(kd["GB/s"] / HBM_PEAK_GBS, 4), "traffic": ROOFLINE_TRAFFIC_BYTES.get(dom),
                      "kernel": f"{dom_names[dom]} ({kd['bytes']:,} algorithmic B/launch, {kd['us']} us/launch)",
                      "frac_of_plain_read": kd["frac_of_plain_read"]},
         "cpu_baseline": cpu,

@@ -456,11 +456,24 @@ size_t planes_bytes(int sem, long rows, int n_cols)
 // Scratch of run_gemv's GEMM path (B > 8): Q8_0 activation pack, split
 // planes, split-K partials.  The GEMV path needs none (Q8_0 activations are
 // quantised by the GEMV workgroups).
-size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
+size_t gemv_required_bytes(int sem, int n_rows, int n_cols, int B)
 {
     if (!(B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem))) return 0;
     return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0) +
            align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4);
+}
+
+// Optional scratch of the batch 2..8 MFMA GEMV: its split-K partials (without
+// them short matrices run unsplit, or on the VALU kernel).
+size_t gemv_mf_bytes(int sem, int n_rows, int n_cols, int B, bool pro = false, bool pair = false)
+{
+    if (B < 2 || B > 8) return 0;
+    return align256((size_t)mllm_gemv_mf_part_floats(sem, n_rows, n_cols, B, pro, pair) * 4);
+}
+
+size_t gemv_scratch_bytes(int sem, int n_rows, int n_cols, int B)
+{
+    return std::max(gemv_required_bytes(sem, n_rows, n_cols, B), gemv_mf_bytes(sem, n_rows, n_cols, B));
 }
 
 // Queue GEMV(s) over B tokens (any B: split into groups of 8) on device data;
@@ -506,6 +519,8 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
         a.ldo = n_rows;
         a.n_rows = n_rows; a.n_cols = n_cols; a.B = B - b0 < 8 ? B - b0 : 8;
         a.out_add = out_add ? out_add + (long)b0 * n_rows : nullptr;
+        // scratch sized by gemv_scratch_bytes holds the MFMA GEMV's partials at B <= 8
+        if (B <= 8 && scratch && gemv_mf_bytes(sem, n_rows, n_cols, B)) a.mf_part = (float *)scratch;
         HIP_OK(mllm_launch_gemv(sem, a, 1, st));
     }
     return 0;
@@ -945,7 +960,7 @@ MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, floa
 {
     if (sem < 0 || sem >= SEM_COUNT) { set_error("mllm_gemv: bad semantic %d", sem); return -1; }
     if (((uintptr_t)x_dev & 15) || ((uintptr_t)packed_dev & 255)) { set_error("mllm_gemv: misaligned pointer"); return -1; }
-    if (gemv_scratch_bytes(sem, n_rows, n_cols, B) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
+    if (gemv_required_bytes(sem, n_rows, n_cols, B) && !workspace) { set_error("mllm_gemv: semantic %d needs a workspace", sem); return -1; }
     mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
     return run_gemv(sem, view, x_dev, out_dev, n_rows, n_cols, B, workspace, (hipStream_t)stream);
 }
@@ -959,23 +974,29 @@ static bool fusion_pair(const mllm_gemv_fusion *f) { return f && f->silu_pair; }
 // activation is formed by its own kernel into the workspace, paired rows run
 // as one GEMV over both halves followed by the SiLU product, and on the MFMA
 // path the residual is added after the GEMM.
-static bool fusion_direct(int sem, int n_cols, int B, const mllm_gemv_fusion *f)
+static bool fusion_direct(int sem, int n_rows, int n_cols, int B, const mllm_gemv_fusion *f)
 {
     if (B > 8 || sem == SEM_F32 || n_cols < mllm_sem_block_elems(sem)) return false;
     const bool pro = fusion_has_pro(f), pair = fusion_pair(f);
-    if (pair && B != 1) return false;
     if (pro && (n_cols % 4 || fusion_ld(f, n_cols) % 4)) return false;
+    // batch 2..8 on the matrix cores: prologue, paired rows and residual in one launch
+    if (B >= 2 && !(f && f->x_up) && mllm_gemv_mf_fits(sem, n_rows, n_cols, B, pro, pair, true)) return true;
+    if (pair && B != 1) return false;
     if (pro || pair) return mllm_gemv_fused_fits(sem, n_cols, B, pro);
     if (f && f->x_up) return mllm_sem_uses_q8(sem) || B == 1;
     return true;
 }
 
-// workspace: [activation B x n_cols] [residual copy B x n_rows] [pair output B x 2 n_rows] [GEMV scratch]
+// workspace: [activation B x n_cols] [residual copy B x n_rows] [pair output B x 2 n_rows] [GEMV scratch];
+// on the one-launch path only the MFMA GEMV's split-K partials
 struct fused_ws { size_t keep, pair, gemv, total; };
 static fused_ws fused_layout(int sem, int n_rows, int n_cols, int B, const mllm_gemv_fusion *f)
 {
     fused_ws w{0, 0, 0, 0};
-    if (fusion_direct(sem, n_cols, B, f)) return w;
+    if (fusion_direct(sem, n_rows, n_cols, B, f)) {
+        w.total = gemv_mf_bytes(sem, n_rows, n_cols, B, fusion_has_pro(f), fusion_pair(f));
+        return w;
+    }
     const bool pair = fusion_pair(f);
     size_t o = 0;
     if (f && (fusion_has_pro(f) || f->x_up)) o += align256((size_t)B * n_cols * 4);
@@ -1023,14 +1044,23 @@ MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev
         if (overlaps(x_dev) || overlaps(f->x_res)) { set_error("mllm_gemv_fused: res_out overlaps x or x_res"); return -1; }
     }
     const fused_ws L = fused_layout(sem, n_rows, n_cols, B, f);
-    if (L.total && !workspace) { set_error("mllm_gemv_fused: needs a workspace of %zu bytes", L.total); return -1; }
+    const bool direct = fusion_direct(sem, n_rows, n_cols, B, f);
+    // one launch: the MFMA GEMV's partials are optional where it also runs unsplit,
+    // or where the VALU kernel takes the same fusion
+    const bool ws_optional = direct && (mllm_gemv_mf_fits(sem, n_rows, n_cols, B, pro, pair, false) ||
+                                        !(pair && B != 1));
+    if (L.total && !workspace && !ws_optional) {
+        set_error("mllm_gemv_fused: needs a workspace of %zu bytes", L.total);
+        return -1;
+    }
     hipStream_t st = (hipStream_t)stream;
     const int mrows = pair ? 2 * n_rows : n_rows;   // rows of the matrix (the stacked gate/up pair)
     mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, mrows, n_cols);
     const float *out_add = f ? f->out_add : nullptr;
-    if (fusion_direct(sem, n_cols, B, f)) {
+    if (direct) {
         mllm_gemv_args a{};
         a.W = view;
+        a.mf_part = L.total ? (float *)workspace : nullptr;
         a.x = x_dev; a.ldx = ldx;
         a.out = out_dev; a.ldo = n_rows;
         a.n_rows = n_rows; a.n_cols = n_cols; a.B = B;

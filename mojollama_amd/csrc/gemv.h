@@ -55,6 +55,9 @@ struct mllm_gemv_args {
     // r + n_rows of the matrix, or with table2 row r of table2's matrix for the
     // job's expert: gate, up and the SiLU product in one launch.
     int silu_pair;
+    // Split-K partials of the batch 2..8 MFMA GEMV (mllm_gemv_mf_part_floats
+    // floats; optional: without it that kernel runs unsplit or not at all).
+    float *mf_part;
 };
 
 // moe_forward_omp's SiLU product (QK:2157-2164): the gate clamped to +-80,
@@ -111,6 +114,15 @@ int mllm_sem_block_elems(int sem);
 // Whether mllm_launch_gemv takes the fused prologue for this shape (the
 // persistent kernel stages all of K; else the caller runs the prologue first).
 bool mllm_gemv_prologue_fits(int sem, int n_cols, int B);
+
+// The batch 2..8 decode GEMV on the matrix cores (gemv_mf.h): Q4_K ggml and
+// Q6_K sequential weights, fp32 activations, with the prologue, the paired
+// gate/up rows and out_add fused.  have_part: an mf_part buffer of
+// mllm_gemv_mf_part_floats floats is given (short matrices then split K).
+bool mllm_gemv_mf_fits(int sem, int n_rows, int n_cols, int B, bool pro, bool pair, bool have_part);
+long mllm_gemv_mf_part_floats(int sem, int n_rows, int n_cols, int B, bool pro, bool pair);
+// hipErrorNotSupported: this launch has no MFMA form (the caller takes the VALU kernel).
+hipError_t mllm_launch_gemv_mf(int sem, const mllm_gemv_args &a, hipStream_t st);
 
 // Repack raw GGUF blocks (device) into the plane layout `ly`.
 hipError_t mllm_launch_pack(int ly, const uint8_t *raw, uint8_t *packed, int n_rows, int n_cols, hipStream_t st);

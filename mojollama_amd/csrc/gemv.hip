@@ -81,6 +81,11 @@ hipError_t mllm_launch_gemv(int sem, const mllm_gemv_args &a, int n_jobs, hipStr
     if (a.x_up && (sem == SEM_F32 || (mllm_sem_uses_q8(sem) ? a.xq.q != nullptr : a.B != 1)))
         return hipErrorInvalidValue;
     if (a.job_split > 0 && (a.job_split >= n_jobs || !a.out2 || (a.table && !a.table2))) return hipErrorInvalidValue;
+    // batch 2..8 of one matrix: the MFMA form where the semantic has one
+    if (a.B >= 2 && n_jobs == 1 && a.n_cols >= mllm_sem_block_elems(sem)) {
+        const hipError_t r = mllm_launch_gemv_mf(sem, a, st);
+        if (r != hipErrorNotSupported) return r;
+    }
     // the fused forms run in the persistent kernel only: the prologue on one
     // matrix with a fp32 activation (or one the kernel quantises itself),
     // paired rows at batch 1

@@ -208,8 +208,8 @@ MLLM_DEV void prologue8(float (&v)[8], const float4 (&r)[2], const float4 (&w)[2
 }
 
 // Residual and RMS-weight loads of the half-groups stage_load loads (same
-// indices, clamped the same way).
-MLLM_DEV void pro_load(pro_regs &pr, const mllm_gemv_args &a, int B, int kn, int pass)
+// indices, clamped the same way; elements from k0 on).
+MLLM_DEV void pro_load(pro_regs &pr, const mllm_gemv_args &a, int B, int kn, int pass, int k0 = 0)
 {
     const int nh = kn >> 3, n = B * nh;
 #pragma unroll
@@ -219,13 +219,13 @@ MLLM_DEV void pro_load(pro_regs &pr, const mllm_gemv_args &a, int B, int kn, int
         const int idx = min(base + (int)threadIdx.x, n - 1);
         const int b = idx / nh, h = idx - b * nh;
         if (a.x_res) {
-            const float *src = a.x_res + (long)b * a.ldx + 8 * h;
+            const float *src = a.x_res + (long)b * a.ldx + k0 + 8 * h;
             pr.r[q][0] = gld<float4>(src);
             pr.r[q][1] = gld<float4>(src + 4);
         }
         if (a.rms_w) {
-            pr.w[q][0] = gld<float4>(a.rms_w + 8 * h);
-            pr.w[q][1] = gld<float4>(a.rms_w + 8 * h + 4);
+            pr.w[q][0] = gld<float4>(a.rms_w + k0 + 8 * h);
+            pr.w[q][1] = gld<float4>(a.rms_w + k0 + 8 * h + 4);
         }
     }
 }

@@ -1,0 +1,141 @@
+"""GPU parity of the batch 2..8 decode GEMV on the matrix cores (gemv_mf.h)
+at the TinyLlama decode shapes bench.py times (configs[1], B in {4, 8}) and
+at odd batch widths, against the oracle's q4_k_batch_matmul (CE:255-313) /
+q6_k_batch_matmul (CE:315-378) on the activation formed in float64 from the
+reference's formulas (RMSNorm TE:1516,1641; SiLU product; residual adds).
+
+Every output row and token is compared: the kernel's tiles (32 rows, or 16
+gate + 16 up rows), its K splits across workgroups (short matrices) and the
+four waves' K quarters all land in the checked outputs.  Reported: the
+normalised error max|d| / max|ref| (bound GEMV_TOL) and the per-element
+relative error over outputs with |ref| >= 1e-3 max|ref|.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import GEMV_TOL
+from mojollama_amd import kernels as K
+from mojollama_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+QT = {K.Q4_K_GGML: W.QT_Q4_K, K.Q6_K_SEQ: W.QT_Q6_K}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return K.DeviceOps(K.load_kernels())
+
+
+def rms_np(v, w, eps):
+    v = v.astype(np.float64)
+    return v * (1.0 / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + eps)) * w
+
+
+def silu_np(g, u):
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g)) * u
+
+
+def rel_err(got, ref):
+    big = np.abs(ref) >= 1e-3 * np.abs(ref).max()
+    return float(np.max(np.abs(got[big] - ref[big]) / np.abs(ref[big])))
+
+
+def check(name, got, ref):
+    err, rel = O.norm_err(got, ref), rel_err(got, ref)
+    print(f"[parity] mfma gemv {name}: norm {err:.3e} max rel {rel:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), name
+    assert err < GEMV_TOL, name
+
+
+CASES = [
+    # name, sem, rows (output), cols, mode
+    ("qkv", K.Q4_K_GGML, 2560, 2048, "rms"),
+    ("o", K.Q4_K_GGML, 2048, 2048, "add"),
+    ("gate_up", K.Q4_K_GGML, 5632, 2048, "pair_rms"),
+    ("down", K.Q6_K_SEQ, 2048, 5632, "add"),
+    ("lm_head", K.Q6_K_SEQ, 32000, 2048, "rms"),
+]
+
+
+@pytest.mark.parametrize("B", [4, 8])
+@pytest.mark.parametrize("name,sem,R,C,mode", CASES)
+def test_mfma_decode_shapes(dev, orc, name, sem, R, C, mode, B):
+    import torch
+    rng = np.random.default_rng(zlib.crc32(f"{name}{B}".encode()))
+    mrows = 2 * R if mode.startswith("pair") else R
+    w = W.gen_weights(rng, QT[sem], mrows, C)
+    x = W.gen_x(rng, B, C)
+    g = (rng.standard_normal(C) * 0.5 + 1.0).astype(np.float32)
+    add = W.gen_x(rng, B, R)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    packed = dev.pack(sem, cu(w), mrows, C)
+    gt, addt = cu(g), cu(add)
+    eps = 1e-5
+    if mode == "rms":
+        f, xe = dev.fusion(rms_w=gt, rms_eps=eps), rms_np(x, g, eps)
+    elif mode == "pair_rms":
+        f, xe = dev.fusion(rms_w=gt, rms_eps=eps, silu_pair=True, silu_clamp=False), rms_np(x, g, eps)
+    else:
+        f, xe = dev.fusion(out_add=addt), x
+    got = dev.gemv_fused(sem, packed, cu(x), R, C, f).cpu().numpy()
+    y = orc.gemv(sem, w, np.ascontiguousarray(xe, np.float32), mrows, C, B).astype(np.float64)
+    if mode == "pair_rms":
+        ref = silu_np(y[:, :R], y[:, R:])
+    elif mode == "add":
+        ref = y + add
+    else:
+        ref = y
+    check(f"{name} {R}x{C} B={B} {mode}", got, ref)
+
+
+@pytest.mark.parametrize("B", [2, 3, 5, 7])
+@pytest.mark.parametrize("sem,R,C", [(K.Q4_K_GGML, 2560, 2048), (K.Q6_K_SEQ, 2048, 5632), (K.Q4_K_GGML, 45, 768)])
+def test_mfma_gemv_odd_batches(dev, orc, sem, R, C, B):
+    """mllm_gemv at every batch-width class (tokens past B padded in the tile)."""
+    import torch
+    rng = np.random.default_rng(R + C + B)
+    w = W.gen_weights(rng, QT[sem], R, C)
+    x = W.gen_x(rng, B, C)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy()
+    check(f"{K.SEM_NAMES[sem]} {R}x{C} B={B}", got, orc.gemv(sem, w, x, R, C, B))
+
+
+@pytest.mark.parametrize("sem,R,C", [(K.Q4_K_GGML, 2048, 2048), (K.Q6_K_SEQ, 300, 1024)])
+def test_mfma_gemv_without_workspace(dev, orc, sem, R, C):
+    """No partials buffer: the K range is not split (one workgroup per row
+    tile over all of K) and the result is the same to tolerance."""
+    import torch
+    rng = np.random.default_rng(5 + R)
+    B = 8
+    w = W.gen_weights(rng, QT[sem], R, C)
+    x = W.gen_x(rng, B, C)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    out = torch.empty(B, R, device="cuda")
+    xt = torch.from_numpy(x).cuda()
+    dev._check(dev.so.mllm_gemv(sem, packed.data_ptr(), xt.data_ptr(), out.data_ptr(), R, C, B, None, dev._stream()),
+               "mllm_gemv")
+    check(f"{K.SEM_NAMES[sem]} {R}x{C} B={B} no workspace", out.cpu().numpy(), orc.gemv(sem, w, x, R, C, B))
+
+
+def test_mfma_gemv_strided_x(dev, orc):
+    """The o projection of bench.py's chain reads q from the qkv rows (x_ld 2560)."""
+    import torch
+    rng = np.random.default_rng(11)
+    B, R, C = 8, 2048, 2048
+    w = W.gen_weights(rng, W.QT_Q4_K, R, C)
+    qkv = W.gen_x(rng, B, 2560)
+    add = W.gen_x(rng, B, R)
+    packed = dev.pack(K.Q4_K_GGML, torch.from_numpy(w).cuda(), R, C)
+    qt, addt = torch.from_numpy(qkv).cuda(), torch.from_numpy(add).cuda()
+    f = dev.fusion(out_add=addt, x_ld=2560)
+    got = dev.gemv_fused(K.Q4_K_GGML, packed, qt.data_ptr(), R, C, f, B=B).cpu().numpy()
+    ref = orc.gemv(K.Q4_K_GGML, w, np.ascontiguousarray(qkv[:, :C]), R, C, B) + add
+    check("o strided x B=8", got, ref)

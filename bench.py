@@ -91,8 +91,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU reference timing")
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
-    ap.add_argument("--kernel", choices=("gate_up", "down", "copy", "gemm_gate", "gemm_down", "moe_gptoss",
-                                         "moe_qwen3"),
+    ap.add_argument("--kernel", choices=("gate_up", "down", "gate_up_b8", "down_b8", "copy", "gemm_gate",
+                                         "gemm_down", "moe_gptoss", "moe_qwen3"),
                     help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
                          "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
     return ap.parse_args()
@@ -265,13 +265,15 @@ def kernel_only(torch, dev, which):
         for _ in range(5):
             layer.forward(x, out=o)
     else:
+        # the decode chain's fused gate+up or down GEMV; *_b8: at batch 8 (the integer-MFMA kernel)
+        B = 8 if which.endswith("_b8") else 1
         layers, lm, on = build_tinyllama(dev, np.random.default_rng(2), 1)
-        ch = DecodeChain(torch, dev, layers, lm, on, 1)
+        ch = DecodeChain(torch, dev, layers, lm, on, B)
         ch.run()
         torch.cuda.synchronize()
         L = layers[0]
         for _ in range(50):
-            if which == "gate_up":
+            if which.startswith("gate_up"):
                 dev.gemv_fused(L["gate_up"].sem, L["gate_up"].packed, ch.xb, 5632, 2048, ch.f_gu[0], out=ch.h,
                                ws=ch.ws)
             else:

@@ -53,6 +53,7 @@ constexpr int kMfMaxSplits = 8;
 constexpr int kMfLdsCap = 80 * 1024;   // per workgroup: two per CU
 constexpr int kMfWaves = 8;            // waves per workgroup, splitting the K range's chunk pairs
 constexpr int kMfThreads = 64 * kMfWaves;
+static_assert(kMfWaves >= 8, "wave b computes token b's RMS scale");
 
 // LDS of one workgroup staging kn elements of BM tokens.
 struct mf_geom {
@@ -136,7 +137,7 @@ MLLM_DEV void mf_epilogue(const mf_v16i &C, float s, float o, const float *rec, 
 {
 #pragma unroll
     for (int j = 0; j < JT; j++) {
-        const int I = C[4 * j] * 16384 + C[4 * j + 1] * 128 + C[4 * j + 2];
+        const int I = (((C[4 * j] << 7) + C[4 * j + 1]) << 7) + C[4 * j + 2];   // two v_lshl_add
         acc[j] = fmaf((float)I, s * rec[2 * j], acc[j]);
         acc[j] = fmaf(o, rec[2 * j + 1], acc[j]);
     }
@@ -504,25 +505,24 @@ __global__ __launch_bounds__(kMfThreads) void k_gemv_mf(mllm_gemv_args a)
     }
     __syncthreads();
     if constexpr (PRO) {
-        if (a.rms_w && wave == 0) {
-            // sum of squares of the staged pieces per token, in one fixed order
-            const int nh = kn >> 3;
+        // wave b sums token b's squares of the staged pieces in one fixed order;
+        // the scale is read after the barrier of the first tile's end, so the
+        // other waves go on meanwhile
+        if (a.rms_w && wave < a.B) {
+            const int nh = kn >> 3, b = wave;
             const float *ssq = reinterpret_cast<const float *>(lds + g.ssq);
-            for (int b = 0; b < a.B; b++) {
-                float t = 0.0f;
-                for (int e = lane; e < nh; e += 64) t += ssq[b * nh + e];
-                t = group_sum<64>(t);
-                if (S == 1) {
-                    const float r = sqrtf(t / (float)a.n_cols + a.rms_eps);
-                    if (lane == 0) scl[b] = a.rms_div ? r : 1.0f / r;
-                } else if (blockIdx.x == 0 && lane == 0) {
-                    // the split's share, summed by the reduction kernel
-                    const int nre = PAIR ? 2 * n_rows : n_rows;
-                    a.mf_part[(long)S * a.B * nre + s * a.B + b] = t;
-                }
+            float t = 0.0f;
+            for (int e = lane; e < nh; e += 64) t += ssq[b * nh + e];
+            t = group_sum<64>(t);
+            if (S == 1) {
+                const float r = sqrtf(t / (float)a.n_cols + a.rms_eps);
+                if (lane == 0) scl[b] = a.rms_div ? r : 1.0f / r;
+            } else if (blockIdx.x == 0 && lane == 0) {
+                // the split's share, summed by the reduction kernel
+                const int nre = PAIR ? 2 * n_rows : n_rows;
+                a.mf_part[(long)S * a.B * nre + s * a.B + b] = t;
             }
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int j = 0; j < JT; j++) acc[j] = 0.0f;

@@ -371,10 +371,14 @@ MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, con
                            const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B, int k0, int kn,
                            bool clamp = true)
 {
+    // pass 0 stays out of the pass loop: there the wait before the digits
+    // covers the activation loads only, not weight loads the caller issued
+    // behind them (at a loop head the wait would cover every load in flight)
     const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
-    bool bad = false;
-    for (int pass = 0; pass < passes; pass++) {
-        if (pass || !load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
+    if (!load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, 0);
+    bool bad = stage_store<SEM, SILU>(st, lds, dg, B, kn, 0, clamp);
+    for (int pass = 1; pass < passes; pass++) {
+        stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
         bad |= stage_store<SEM, SILU>(st, lds, dg, B, kn, pass, clamp);
     }
     if (__any(bad)) stage_fix<SEM>(lds, dg, x, SILU ? xu : nullptr, nullptr, ldx, B, k0, kn, clamp);
@@ -998,13 +1002,13 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             pro_regs pr;
             pro_load(pr, a, B, kused, 0);
             fetch_step(min(rg, nrg - 1), it, bufA);
+            // pass 0 out of the pass loop (see stage_digits)
             const int passes = (B * (kused >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
-            bool bad = false;
-            for (int pass = 0; pass < passes; pass++) {
-                if (pass) {
-                    stage_load<false>(xst, xj, nullptr, a.ldx, B, 0, kused, pass);
-                    pro_load(pr, a, B, kused, pass);
-                }
+            bool bad = stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, 0, true, &pr,
+                                                     &a, part);
+            for (int pass = 1; pass < passes; pass++) {
+                stage_load<false>(xst, xj, nullptr, a.ldx, B, 0, kused, pass);
+                pro_load(pr, a, B, kused, pass);
                 bad |= stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, pass, true,
                                                      &pr, &a, part);
             }

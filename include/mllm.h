@@ -169,10 +169,10 @@ MLLM_API int mllm_pack(int sem, const void *raw_dev, void *packed_dev, int n_row
 /* out[b][r] = row r of W applied to x[b], b < B (any B), under semantic `sem`.
  * Q8_0-activation semantics, and B > 8 (run as an MFMA GEMM over split bf16
  * activation planes), need `workspace` of mllm_gemv_workspace_size bytes.
- * At 2 <= B <= 8 the Q4_K (q4_k_batch_matmul) and Q6_K (q6_k_batch_matmul)
- * semantics run on the matrix cores; given the workspace, short matrices
- * there also split K over more workgroups (optional: NULL runs unsplit or
- * on the vector kernel). */
+ * At 2 <= B <= 8 the Q4_K, Q6_K, Q8_0, Q4_0 and MXFP4 batch semantics run on
+ * the matrix cores from the batch where that is faster; given the workspace,
+ * short matrices there also split K over more workgroups (optional: NULL
+ * runs unsplit or on the vector kernel). */
 MLLM_API long mllm_gemv_workspace_size(int sem, int n_rows, int n_cols, int B);
 MLLM_API int mllm_gemv(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols,
                        int B, void *workspace, void *stream);

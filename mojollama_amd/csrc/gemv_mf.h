@@ -1,4 +1,5 @@
-// gemv_mf.h — decode GEMV at batch 2..8 on the matrix cores.
+// gemv_mf.h — decode GEMV at batch 2..8 on the matrix cores (Q4_K ggml, Q6_K
+// sequential, Q8_0, Q4_0, MXFP4 with and without the scale clamp).
 //
 // The batch-1 kernel (gemv_impl.h) dots every weight code with three int8
 // digit planes of each token on the VALU; at B tokens that is 3·B v_dot4 per
@@ -9,14 +10,15 @@
 //   A row m = token t (m / 4) x digit plane p (m % 4; plane 3 is zero),
 //   B column n = one weight row, k = 16 consecutive elements of one scale
 //   group (a "run"; the codes are the format's unsigned codes u, as the
-//   batch-1 kernel uses them).
+//   batch-1 kernel uses them, or Q8_0's signed quants).
 //
 // Lane l of the result holds column n = l % 32 and rows 8j + 4(l / 32) + i,
 // i.e. the three planes of token t = 2j + l / 32 in consecutive registers, so
 // I = (I0·2^7 + I1)·2^7 + I2 is formed in-lane and the run's fp32 epilogue
 // is   acc_t += (s·P'_t)·I + o'·sum_t   (P'_t = P_t·2^-14, o' = o - s·bias).
-// |I| < 2^31 for every form here: Q4_K codes <= 15 over 32 elements and Q6_K
-// codes <= 63 over 16 elements, digits |d| <= 64.
+// |I| < 2^31 for the unsigned-code forms: codes <= 15 (Q4_K, Q4_0, MXFP4)
+// over 32 elements and Q6_K codes <= 63 over 16 elements, digits |d| <= 64
+// (Q8_0 combines its planes in fp32).
 //
 // Activation digits are those of the batch-1 kernel (x = P·(d0 + d1/2^7 +
 // d2/2^14), P a power of two with max|x| / P in [32, 64)), with one P per
@@ -45,8 +47,14 @@ namespace mllm_gemv {
 typedef int mf_v16i __attribute__((ext_vector_type(16)));
 
 template <int SEM> struct mf_traits {
-    static constexpr bool kOk = SEM == SEM_Q4_K_GGML || SEM == SEM_Q6_K_SEQ;
-    static constexpr int kG = SEM == SEM_Q4_K_GGML ? 32 : 16;   // elements per activation scale P
+    static constexpr bool kKQ = SEM == SEM_Q4_K_GGML || SEM == SEM_Q6_K_SEQ;
+    static constexpr bool kOk = kKQ || SEM == SEM_Q8_0 || SEM == SEM_Q4_0 || SEM == SEM_MXFP4 ||
+                                SEM == SEM_MXFP4_CLAMP;
+    static constexpr int kG = SEM == SEM_Q6_K_SEQ ? 16 : 32;   // elements per activation scale P
+    static constexpr int kBE = kKQ ? 256 : 32;                 // elements per quant block
+    // elements per unit, the step of one lane pair of a row: a K-quant chunk
+    // pair (64), one 32-element block of the others
+    static constexpr int kUE = kKQ ? 64 : 32;
 };
 
 constexpr int kMfMaxSplits = 8;
@@ -85,9 +93,12 @@ __host__ __device__ inline mf_geom mf_geom_for(int BM, int G, int kn, bool pro)
     return g;
 }
 
-// One chunk pair's loads for lane (n, h): 16 bytes of chunk 2q + h of row n
-// and the side data of the pair (Q4_K: the block's d, dmin and scales;
+// One unit's loads for lane (n, h) of row n.  K-quants: 16 bytes of chunk
+// 2q + h and the pair's side data (Q4_K: the block's d, dmin and scales;
 // Q6_K: the qh bytes of both chunks, their four scales, the block's d).
+// Q8_0: bytes 8h .. 8h+7 of each 16-element run (a.xy, a.zw) and d (m.x);
+// Q4_0: bytes 8h .. 8h+7 of the 16 code bytes (a.xy) and d; MXFP4: the 16
+// code bytes and the E8M0 byte.
 template <int SEM> struct mf_pair {
     uint4 a;
     uint4 m;
@@ -98,16 +109,29 @@ template <> struct mf_pair<SEM_Q6_K_SEQ> {
     uint32_t sc, d;
 };
 
+// bi: block index (row * blocks per row + block); q: chunk pair of a K-quant block.
 template <int SEM>
 MLLM_DEV void mf_fetch(const mllm_packed &P, long bi, int q, int h, mf_pair<SEM> &r)
 {
-    r.a = ld16(P.p[0] + bi * 128 + 16 * (2 * q + h));
     if constexpr (SEM == SEM_Q4_K_GGML) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * (2 * q + h));
         r.m = ld16c(P.p[1] + bi * 16);
-    } else {
+    } else if constexpr (SEM == SEM_Q6_K_SEQ) {
+        r.a = ld16(P.p[0] + bi * 128 + 16 * (2 * q + h));
         r.qh = ld16c(P.p[1] + bi * 64 + 16 * q);
         r.sc = gld<uint32_t>(P.p[2] + bi * 16 + 4 * q);
         r.d = gld<uint16_t>(P.p[3] + bi * 2);
+    } else if constexpr (SEM == SEM_Q8_0) {
+        const uint2 lo = gld<uint2>(P.p[0] + bi * 32 + 8 * h), hi = gld<uint2>(P.p[0] + bi * 32 + 16 + 8 * h);
+        r.a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        r.m.x = gld<uint16_t>(P.p[1] + bi * 2);
+    } else if constexpr (SEM == SEM_Q4_0) {
+        const uint2 v = gld<uint2>(P.p[0] + bi * 16 + 8 * h);
+        r.a = make_uint4(v.x, v.y, 0u, 0u);
+        r.m.x = gld<uint16_t>(P.p[1] + bi * 2);
+    } else {
+        r.a = ld16(P.p[0] + bi * 16);
+        r.m.x = gld<uint8_t>(P.p[1] + bi);
     }
 }
 
@@ -140,6 +164,19 @@ MLLM_DEV void mf_epilogue(const mf_v16i &C, float s, float o, const float *rec, 
         const int I = (((C[4 * j] << 7) + C[4 * j + 1]) << 7) + C[4 * j + 2];   // two v_lshl_add
         acc[j] = fmaf((float)I, s * rec[2 * j], acc[j]);
         acc[j] = fmaf(o, rec[2 * j + 1], acc[j]);
+    }
+}
+
+// Q8_0's signed codes reach -128 and 32 elements: a plane's integer stays
+// below 2^18 but the shifted combination would pass 2^31, so the planes
+// combine in fp32 (as the batch-1 kernel's three accumulators do); no offset.
+template <int JT>
+MLLM_DEV void mf_epilogue_f(const mf_v16i &C, float s, const float *rec, float (&acc)[JT])
+{
+#pragma unroll
+    for (int j = 0; j < JT; j++) {
+        const float t = fmaf((float)C[4 * j], 16384.0f, fmaf((float)C[4 * j + 1], 128.0f, (float)C[4 * j + 2]));
+        acc[j] = fmaf(t, s * rec[2 * j], acc[j]);
     }
 }
 
@@ -271,15 +308,15 @@ MLLM_DEV void mf_stage_store(const x_stage<false> &st, const pro_regs &pr, uint8
 // w = s * (u - bias) + o, x = P * (d0 + d1/2^7 + d2/2^14), t += w * x in
 // chunk order (decode.h codes, the batch-1 kernel's rare path).
 template <int SEM, int BM>
-MLLM_DEV float mf_slow(const mllm_packed &W, int nb, int row, int kb0, int nbk, int wave, int tok, const uint8_t *lds,
+MLLM_DEV float mf_slow(const mllm_packed &W, int nb, int row, int n_units, int wave, int tok, const uint8_t *lds,
                        const mf_geom &g, int k0)
 {
-    constexpr int G = mf_traits<SEM>::kG;
-    constexpr float bias = (float)sem_traits<SEM>::kBias;
+    constexpr int G = mf_traits<SEM>::kG, CU = mf_traits<SEM>::kUE / 32;   // 32-element chunks per unit
+    constexpr float bias = (float)digit_bias<SEM>();
     float t = 0.0f;
-    for (int p = wave; p < 4 * nbk; p += kMfWaves) {
-        for (int cc = 2 * (p & 3); cc < 2 * (p & 3) + 2; cc++) {
-            const int c = (kb0 + p / 4) * 8 + cc;
+    for (int p = wave; p < n_units; p += kMfWaves) {
+        for (int i = 0; i < CU; i++) {
+            const int c = k0 / 32 + p * CU + i;   // decode.h's chunk index (a K-quant pair is chunks 2q, 2q+1)
             raw_chunk raw;
             fetch<SEM>(W, nb, row, c, raw);
             chunk_codes k;
@@ -296,8 +333,8 @@ MLLM_DEV float mf_slow(const mllm_packed &W, int nb, int row, int kb0, int nbk, 
                 const uint8_t *d1 = lds + (e1 >> 4) * g.gs + (j >> 1) * (3 * BM * 8) + tok * 24 + (j & 1) * 4;
 #pragma unroll
                 for (int qb = 0; qb < 4; qb++) {
-                    const float w0 = fmaf(k.s0, ubyte_f(k.U[j], qb) - bias, k.o0);
-                    const float w1 = fmaf(k.s1, ubyte_f(k.U[4 + j], qb) - bias, k.o1);
+                    const float w0 = fmaf(k.s0, code_f<SEM>(k.U[j], qb) - bias, k.o0);
+                    const float w1 = fmaf(k.s1, code_f<SEM>(k.U[4 + j], qb) - bias, k.o1);
                     const float x0 = fmaf((float)(int8_t)d0[16 + qb], 0x1p-14f,
                                           fmaf((float)(int8_t)d0[8 + qb], 0x1p-7f, (float)(int8_t)d0[qb]));
                     const float x1 = fmaf((float)(int8_t)d1[16 + qb], 0x1p-14f,
@@ -319,21 +356,21 @@ __global__ __launch_bounds__(kMfThreads) void k_gemv_mf(mllm_gemv_args a)
 {
     static_assert(mf_traits<SEM>::kOk, "no MFMA decode form for this semantic");
     constexpr int JT = BM / 2;
-    constexpr int G = mf_traits<SEM>::kG;
+    constexpr int G = mf_traits<SEM>::kG, BE = mf_traits<SEM>::kBE, UE = mf_traits<SEM>::kUE;
     constexpr int NW = kMfWaves;
     extern __shared__ __align__(16) uint8_t lds[];
     const mllm_packed W = a.W;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 31, h = lane >> 5;
-    const int nb = a.n_cols / 256;
+    const int nb = a.n_cols / BE;
     const int S = gridDim.y, s = blockIdx.y;
     const int kb0 = (int)((long)nb * s / S), nbk = (int)((long)nb * (s + 1) / S) - kb0;
-    const int k0 = kb0 * 256, kn = nbk * 256;
+    const int k0 = kb0 * BE, kn = nbk * BE;
     const mf_geom g = mf_geom_for(BM, G, kn, PRO);
     const int n_rows = a.n_rows;
     const int n_tiles = PAIR ? (n_rows + 15) / 16 : (n_rows + 31) / 32;
-    // this wave's chunk pairs of the K range: wave, wave + NW, ...
-    const int npr = 4 * nbk;
+    // this wave's units of the K range: wave, wave + NW, ...
+    const int npr = kn / UE;
     const int nw = wave < npr ? (npr - wave + NW - 1) / NW : 0;
 
     auto row_of = [&](int T, int n) __attribute__((always_inline)) {
@@ -347,8 +384,10 @@ __global__ __launch_bounds__(kMfThreads) void k_gemv_mf(mllm_gemv_args a)
     // every fetch is issued, clamped to a valid tile and pair, so the loads in
     // flight are the same on every path and each wait covers only the older buffers
     auto fetch_pair = [&](int T, int i, mf_pair<SEM> &r) __attribute__((always_inline)) {
-        const int p = min(wave + NW * min(i, nw - 1), npr - 1);
-        mf_fetch<SEM>(W, (long)row_of(min(T, n_tiles - 1), nl) * nb + kb0 + max(p, 0) / 4, max(p, 0) & 3, h, r);
+        const int p = max(min(wave + NW * min(i, nw - 1), npr - 1), 0);
+        const long rb = (long)row_of(min(T, n_tiles - 1), nl) * nb + kb0;
+        if constexpr (mf_traits<SEM>::kKQ) mf_fetch<SEM>(W, rb + p / 4, p & 3, h, r);
+        else mf_fetch<SEM>(W, rb + p, 0, h, r);
     };
     auto adv = [&](int &T, int &i) __attribute__((always_inline)) {
         if (++i >= nw) { i = 0; T += gridDim.x; }
@@ -366,12 +405,36 @@ __global__ __launch_bounds__(kMfThreads) void k_gemv_mf(mllm_gemv_args a)
     float acc[JT];
     auto run_pair = [&](int i, const mf_pair<SEM> &r) __attribute__((always_inline)) {
         const int p = wave + NW * i;
-        const int gq = 4 * p;   // first 16-element group of the chunk pair
+        const int gq = p * (UE / 16);   // first 16-element group of the unit
         const uint32_t L4 = 0x0F0F0F0Fu;
         const mf_v16i z = {};
         uint32_t w0 = r.a.x, w1 = r.a.y, w2 = r.a.z, w3 = r.a.w;
         float rec[2 * JT];
-        if constexpr (SEM == SEM_Q4_K_GGML) {
+        if constexpr (SEM == SEM_Q8_0) {
+            // lane half h: bytes 8h .. 8h+7 of run 0 (w0, w1) and of run 1 (w2, w3), signed codes
+            mf_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq), mf_pack(w0, w1), z, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq + 1), mf_pack(w2, w3), c, 0, 0, 0);
+            mf_rec<JT>(lds, g, p, h, rec);
+            mf_epilogue_f<JT>(c, h2f(r.m.x), rec, acc);
+        } else if constexpr (SEM == SEM_Q4_0) {
+            // lane half h: bytes 8h .. 8h+7; low nibbles run 0, high nibbles run 1
+            mf_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq), mf_pack(w0 & L4, w1 & L4), z, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq + 1), mf_pack((w0 >> 4) & L4, (w1 >> 4) & L4), c,
+                                                      0, 0, 0);
+            const float d = h2f(r.m.x);
+            mf_rec<JT>(lds, g, p, h, rec);
+            mf_epilogue<JT>(c, d, -8.0f * d, rec, acc);
+        } else if constexpr (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_CLAMP) {
+            // word m holds elements 8m .. 8m+7 (even ones in the low nibbles): lane half
+            // h takes word h (run 0) and word 2 + h (run 1); u = n ^ 8 = v + 8
+            const uint32_t u0 = (h ? w1 : w0) ^ 0x88888888u, u1 = (h ? w3 : w2) ^ 0x88888888u;
+            mf_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq), mf_pack(u0 & L4, (u0 >> 4) & L4), z, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_32x32x16_i8(opA(gq + 1), mf_pack(u1 & L4, (u1 >> 4) & L4), c, 0, 0, 0);
+            float sc = e8m0f(r.m.x);
+            if constexpr (SEM == SEM_MXFP4_CLAMP) sc = fminf(sc, 1e20f);
+            mf_rec<JT>(lds, g, p, h, rec);
+            mf_epilogue<JT>(c, sc, -8.0f * sc, rec, acc);
+        } else if constexpr (SEM == SEM_Q4_K_GGML) {
             // lane half h: words 2h, 2h+1 of chunk 2q (w0, w1) and of chunk 2q+1 (w2, w3)
             mf_swap(w0, w2);
             mf_swap(w1, w3);
@@ -427,7 +490,7 @@ __global__ __launch_bounds__(kMfThreads) void k_gemv_mf(mllm_gemv_args a)
 #pragma unroll
             for (int j = 0; j < JT; j++)
                 if (!isfinite(acc[j]))
-                    acc[j] = mf_slow<SEM, BM>(W, nb, row, kb0, nbk, wave, 2 * j + h, lds, g, k0);
+                    acc[j] = mf_slow<SEM, BM>(W, nb, row, npr, wave, 2 * j + h, lds, g, k0);
         }
 #pragma unroll
         for (int j = 0; j < JT; j++) red[(wave * JT + j) * 64 + lane] = acc[j];

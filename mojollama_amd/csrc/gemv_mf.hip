@@ -16,7 +16,23 @@ struct mf_plan {
     size_t lds;
 };
 
-int mf_group(int sem) { return sem == SEM_Q4_K_GGML ? 32 : 16; }
+bool mf_sem_ok(int sem)
+{
+    return sem == SEM_Q4_K_GGML || sem == SEM_Q6_K_SEQ || sem == SEM_Q8_0 || sem == SEM_Q4_0 || sem == SEM_MXFP4 ||
+           sem == SEM_MXFP4_CLAMP;
+}
+int mf_group(int sem) { return sem == SEM_Q6_K_SEQ ? 16 : 32; }
+
+// Batch from which the MFMA form beats the VALU kernel on its own (measured on
+// MI355X over TinyLlama / GPT-OSS shapes: the MFMA kernel's time hardly grows
+// with B, the VALU kernel's grows per token).  Paired gate/up rows at B > 1
+// exist only here.
+int mf_min_batch(int sem, int n_rows)
+{
+    if (sem == SEM_Q6_K_SEQ && n_rows <= 4096) return 3;   // the down projection; not the 32000-row lm_head
+    return sem == SEM_Q8_0 ? 7 : 5;
+}
+int mf_block(int sem) { return (sem == SEM_Q4_K_GGML || sem == SEM_Q6_K_SEQ) ? 256 : 32; }
 
 // S: the fewest K splits whose range fits the LDS budget, raised (up to 8
 // and one 256-element block per split) until rows x splits give a tile per
@@ -24,14 +40,14 @@ int mf_group(int sem) { return sem == SEM_Q4_K_GGML ? 32 : 16; }
 mf_plan mf_plan_for(int sem, int n_rows, int n_cols, int B, bool pro, bool pair, bool have_part)
 {
     mf_plan p{};
-    if ((sem != SEM_Q4_K_GGML && sem != SEM_Q6_K_SEQ) || B < 2 || B > 8 || n_rows <= 0) return p;
-    const int nb = n_cols / 256;
+    if (!mf_sem_ok(sem) || B < 2 || B > 8 || n_rows <= 0 || (!pair && B < mf_min_batch(sem, n_rows))) return p;
+    const int BE = mf_block(sem), nb = n_cols / BE;
     if (nb < 1) return p;
     p.BM = B <= 2 ? 2 : B <= 4 ? 4 : 8;
     p.n_tiles = pair ? (n_rows + 15) / 16 : (n_rows + 31) / 32;
     const int cus = device_cus();
     auto lds_for = [&](int S) {
-        const int kn = (nb + S - 1) / S * 256;
+        const int kn = (nb + S - 1) / S * BE;
         return (size_t)mf_geom_for(p.BM, mf_group(sem), kn, pro).total;
     };
     int S = 1;
@@ -69,12 +85,19 @@ hipError_t mllm_launch_gemv_mf(int sem, const mllm_gemv_args &a, hipStream_t st)
     const bool pro = mllm_has_prologue(a), pair = a.silu_pair != 0;
     if (a.table || a.x_up || a.xq.q || a.job_split > 0) return hipErrorNotSupported;
     // the prologue's norm covers whole blocks
-    if (pro && a.n_cols % 256) return hipErrorNotSupported;
+    if (!mf_sem_ok(sem) || (pro && a.n_cols % mf_block(sem))) return hipErrorNotSupported;
     if ((a.ldx & 3) || ((uintptr_t)a.x & 15)) return hipErrorNotSupported;
     const mf_plan p = mf_plan_for(sem, a.n_rows, a.n_cols, a.B, pro, pair, a.mf_part != nullptr);
     if (!p.ok) return hipErrorNotSupported;
-    hipError_t r = sem == SEM_Q4_K_GGML ? gemv_mf_sem<SEM_Q4_K_GGML>(a, p.BM, p.n_tiles, p.S, p.lds, st)
-                                        : gemv_mf_sem<SEM_Q6_K_SEQ>(a, p.BM, p.n_tiles, p.S, p.lds, st);
+    hipError_t r;
+    switch (sem) {
+    case SEM_Q4_K_GGML: r = gemv_mf_sem<SEM_Q4_K_GGML>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    case SEM_Q6_K_SEQ: r = gemv_mf_sem<SEM_Q6_K_SEQ>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    case SEM_Q8_0: r = gemv_mf_sem<SEM_Q8_0>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    case SEM_Q4_0: r = gemv_mf_sem<SEM_Q4_0>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    case SEM_MXFP4: r = gemv_mf_sem<SEM_MXFP4>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    default: r = gemv_mf_sem<SEM_MXFP4_CLAMP>(a, p.BM, p.n_tiles, p.S, p.lds, st); break;
+    }
     if (r != hipSuccess) return r;
     if (p.S > 1) {
         const dim3 rg((unsigned)(((long)a.B * a.n_rows + 255) / 256));

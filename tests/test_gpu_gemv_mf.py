@@ -1,8 +1,10 @@
 """GPU parity of the batch 2..8 decode GEMV on the matrix cores (gemv_mf.h)
 at the TinyLlama decode shapes bench.py times (configs[1], B in {4, 8}) and
 at odd batch widths, against the oracle's q4_k_batch_matmul (CE:255-313) /
-q6_k_batch_matmul (CE:315-378) on the activation formed in float64 from the
-reference's formulas (RMSNorm TE:1516,1641; SiLU product; residual adds).
+q6_k_batch_matmul (CE:315-378) / q8_0 and q4_0 batch matmuls (CE:216-253,
+CE:68-110) / mxfp4 (QK:683-720, clamped CE:427-534) on the activation formed
+in float64 from the reference's formulas (RMSNorm TE:1516,1641; SiLU
+product; residual adds).
 
 Every output row and token is compared: the kernel's tiles (32 rows, or 16
 gate + 16 up rows), its K splits across workgroups (short matrices) and the
@@ -22,7 +24,8 @@ from mojollama_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
-QT = {K.Q4_K_GGML: W.QT_Q4_K, K.Q6_K_SEQ: W.QT_Q6_K}
+QT = {K.Q4_K_GGML: W.QT_Q4_K, K.Q6_K_SEQ: W.QT_Q6_K, K.Q8_0: W.QT_Q8_0, K.Q4_0: W.QT_Q4_0, K.MXFP4: W.QT_MXFP4,
+      K.MXFP4_CLAMP: W.QT_MXFP4}
 
 
 @pytest.fixture(scope="module")
@@ -96,7 +99,9 @@ def test_mfma_decode_shapes(dev, orc, name, sem, R, C, mode, B):
 
 
 @pytest.mark.parametrize("B", [2, 3, 5, 7])
-@pytest.mark.parametrize("sem,R,C", [(K.Q4_K_GGML, 2560, 2048), (K.Q6_K_SEQ, 2048, 5632), (K.Q4_K_GGML, 45, 768)])
+@pytest.mark.parametrize("sem,R,C", [(K.Q4_K_GGML, 2560, 2048), (K.Q6_K_SEQ, 2048, 5632), (K.Q4_K_GGML, 45, 768),
+                                     (K.Q8_0, 5632, 2048), (K.Q4_0, 300, 2080), (K.MXFP4, 2880, 2880),
+                                     (K.MXFP4_CLAMP, 333, 800)])
 def test_mfma_gemv_odd_batches(dev, orc, sem, R, C, B):
     """mllm_gemv at every batch-width class (tokens past B padded in the tile)."""
     import torch
@@ -139,3 +144,37 @@ def test_mfma_gemv_strided_x(dev, orc):
     got = dev.gemv_fused(K.Q4_K_GGML, packed, qt.data_ptr(), R, C, f, B=B).cpu().numpy()
     ref = orc.gemv(K.Q4_K_GGML, w, np.ascontiguousarray(qkv[:, :C]), R, C, B) + add
     check("o strided x B=8", got, ref)
+
+
+@pytest.mark.parametrize("B", [4, 8])
+@pytest.mark.parametrize("sem,R,C", [(K.Q8_0, 5632, 2048), (K.MXFP4, 2880, 2880), (K.Q4_0, 1024, 2048)])
+@pytest.mark.parametrize("mode", ["rms", "pair_rms", "add"])
+def test_mfma_block32_fused(dev, orc, sem, R, C, mode, B):
+    """The 32-element block formats (one unit = one block) with the fused
+    prologue, paired rows and residual, as the decode chain uses them."""
+    import torch
+    rng = np.random.default_rng(zlib.crc32(f"{sem}{R}{mode}{B}".encode()))
+    mrows = 2 * R if mode.startswith("pair") else R
+    w = W.gen_weights(rng, QT[sem], mrows, C)
+    x = W.gen_x(rng, B, C)
+    g = (rng.standard_normal(C) * 0.5 + 1.0).astype(np.float32)
+    add = W.gen_x(rng, B, R)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    packed = dev.pack(sem, cu(w), mrows, C)
+    gt, addt = cu(g), cu(add)
+    eps = 1e-5
+    if mode == "rms":
+        f, xe = dev.fusion(rms_w=gt, rms_eps=eps), rms_np(x, g, eps)
+    elif mode == "pair_rms":
+        f, xe = dev.fusion(rms_w=gt, rms_eps=eps, silu_pair=True, silu_clamp=True), rms_np(x, g, eps)
+    else:
+        f, xe = dev.fusion(out_add=addt), x
+    got = dev.gemv_fused(sem, packed, cu(x), R, C, f).cpu().numpy()
+    y = orc.gemv(sem, w, np.ascontiguousarray(xe, np.float32), mrows, C, B).astype(np.float64)
+    if mode == "pair_rms":
+        ref = silu_np(np.clip(y[:, :R], -80, 80), y[:, R:])
+    elif mode == "add":
+        ref = y + add
+    else:
+        ref = y
+    check(f"{K.SEM_NAMES[sem]} {R}x{C} B={B} {mode}", got, ref)

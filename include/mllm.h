@@ -277,6 +277,14 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
                                           const void *const *gate_packed, const void *const *up_packed,
                                           const void *const *down_packed, const float *router_dev, int renorm);
 MLLM_API void mllm_moe_release(mllm_moe_layer *layer);
+/* Load-time bf16 copies of the layer's expert matrices whose weights are exact
+ * in bf16 (the MXFP4 forms: gate/up of one semantic, down), which the batched
+ * path (T > 24) then copies into its tiles instead of decoding; results are
+ * bit-identical.  2 bytes per weight (3.8x MXFP4), freed with the layer.
+ * Returns the bytes allocated (0: nothing qualifies, or already made), -1 on
+ * error; synchronises `stream`.  No reference counterpart: the memory-for-
+ * speed trade of moe_forward_omp's experts (QK:2066-2250) on 288 GB HBM. */
+MLLM_API long mllm_moe_dense_experts(mllm_moe_layer *layer, void *stream);
 MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *layer, int T);
 /* out[T][N]; idx_out/w_out (optional, device [T][K]) receive the routing. */
 MLLM_API int mllm_moe_forward(const mllm_moe_layer *layer, const float *x, int T, float *out, void *workspace,

@@ -52,6 +52,10 @@ struct qgemm_args {
     // the ksplit partials in order into out.
     int ksplit;
     float *part;
+    // dense_ld > 0: W / W2 / table entries hold p[0] = bf16 rows of that stride
+    // (a multiple of 64, zero padded; a load-time copy of weights exact in
+    // bf16, the MXFP4 forms), copied into the tiles instead of decoded.
+    int dense_ld;
 };
 
 hipError_t mllm_launch_qgemm(int sem, int xmode, bool dual, const qgemm_args &a, int max_tiles, hipStream_t st);

@@ -24,6 +24,7 @@
 // loads run two K-steps ahead of the MFMAs (register double buffer).
 #include <algorithm>
 #include "decode.h"
+#include <type_traits>
 #include "gemm.h"
 
 namespace {
@@ -285,6 +286,35 @@ MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, in
     }
 }
 
+// Dense bf16 weights (dense_ld > 0): a step is TN_ rows x 64 columns, eight
+// 16-byte pieces per row, copied into the tile as they are (rows past the
+// matrix clamped to its last row, whose outputs are never stored).
+template <int TN_> struct wdense {
+    static constexpr int NP = TN_ * 8 / 256;
+    uint4 p[NP];
+};
+
+template <int TN_>
+MLLM_DEV void fetch_wd(const mllm_packed &W, int n_rows, int ldw, int n0, int k0, wdense<TN_> &wd)
+{
+    const __bf16 *base = reinterpret_cast<const __bf16 *>(W.p[0]);
+#pragma unroll
+    for (int i = 0; i < wdense<TN_>::NP; i++) {
+        const int q = threadIdx.x + 256 * i, row = min(n0 + (q >> 3), n_rows - 1);
+        wd.p[i] = gld<uint4>(base + (long)row * ldw + k0 + 8 * (q & 7));
+    }
+}
+
+template <int TN_, bool SWZ, int LDA>
+MLLM_DEV void put_wd(const wdense<TN_> &wd, __bf16 *A)
+{
+#pragma unroll
+    for (int i = 0; i < wdense<TN_>::NP; i++) {
+        const int q = threadIdx.x + 256 * i;
+        *reinterpret_cast<uint4 *>(A + tile_off<SWZ, LDA>(q >> 3, 8 * (q & 7))) = wd.p[i];
+    }
+}
+
 // Activation task of thread tid.  XM_PLANES: TM_/32 16-byte pieces per plane
 // (entry q/8, columns 8*(q%8) .. +8 of the step, q = tid + 256*i), planes
 // p < npl only (the lower plane of a tile whose activations are all exact in
@@ -395,7 +425,7 @@ template <int SEM, int XM, bool DUAL, int TM> constexpr int qgemm_wgs_per_cu()
     return n < 1 ? 1 : n > cap ? cap : n;
 }
 
-template <int SEM, int XM, bool DUAL, int TM>
+template <int SEM, int XM, bool DUAL, int TM, bool DW>
 __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void k_qgemm(qgemm_args a)
 {
     using C = gemm_cfg<SEM, XM>;
@@ -488,20 +518,32 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         else return (base + li) * LDA + ks + lk;
     };
 
+    static_assert(!DW || (NA == 1 && !C::A4 && KS == 64), "dense bf16 weights: one exact plane, 64-column steps");
+    using WB = typename std::conditional<DW, wdense<TN>, wraw<SEM, XM, TN>>::type;
     struct stepbuf {
-        wraw<SEM, XM, TN> w, u;
+        WB w, u;
         araw<TM, NB> x;
     };
     auto fetch_step = [&](int s, stepbuf &b) __attribute__((always_inline)) {
         const int k0 = min(s, s_end - 1) * KS;   // past the end: refetch the last step (unused)
-        fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w, 0);
-        if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u, 128);
+        if constexpr (DW) {
+            fetch_wd<TN>(W, a.n_rows, a.dense_ld, n0, k0, b.w);
+            if constexpr (DUAL) fetch_wd<TN>(W2, a.n_rows, a.dense_ld, n0, k0, b.u);
+        } else {
+            fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w, 0);
+            if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u, 128);
+        }
         fetch_a<SEM, XM, TM>(a, s_row, n_ent, k0, kused, b.x, pb_end);
     };
     auto put_step = [&](int s, const stepbuf &b) __attribute__((always_inline)) {
         const int k0 = s * KS;
-        put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr, 0);
-        if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr, 128);
+        if constexpr (DW) {
+            put_wd<TN, C::SWZ, LDA>(b.w, s_a);
+            if constexpr (DUAL) put_wd<TN, C::SWZ, LDA>(b.u, s_u);
+        } else {
+            put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr, 0);
+            if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr, 128);
+        }
         put_a<SEM, XM, TM>(b.x, n_ent, k0, kused, s_b, (C::A4 || XM == XM_Q8D) ? s_tsum : nullptr, pb_end);
     };
     auto mfma_step = [&]() __attribute__((always_inline)) {
@@ -667,7 +709,7 @@ __global__ void k_ksum(const float *__restrict__ part, int ks, long plane, int n
     out[e * ldo + n] = v;
 }
 
-template <int SEM, int XM, bool DUAL, int TM>
+template <int SEM, int XM, bool DUAL, int TM, bool DW = false>
 hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
 {
     constexpr int TN = tile_cfg<DUAL, TM>::TN;
@@ -676,7 +718,7 @@ hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
     if (grid.y == 0) return hipSuccess;
     qgemm_args b = a;
     b.ksplit = ks;
-    hipLaunchKernelGGL((k_qgemm<SEM, XM, DUAL, TM>), grid, dim3(256), 0, st, b);
+    hipLaunchKernelGGL((k_qgemm<SEM, XM, DUAL, TM, DW>), grid, dim3(256), 0, st, b);
     if (ks > 1) {
         const long plane = (long)a.n_entries * a.n_rows;
         hipLaunchKernelGGL(k_ksum, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part, ks, plane,
@@ -692,6 +734,20 @@ hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
 // entries to fill them.
 hipError_t mllm_launch_qgemm(int sem, int xmode, bool dual, const qgemm_args &a, int max_tiles, hipStream_t st)
 {
+    if (a.dense_ld > 0) {
+        // dense bf16 copies: the weight-exact (MXFP4) forms, 64-entry tiles
+        if (a.dense_ld % 64 || a.dense_ld < a.n_cols) return hipErrorInvalidValue;
+        if (sem == SEM_MXFP4 && xmode == XM_PLANES)
+            return dual ? launch<SEM_MXFP4, XM_PLANES, true, 64, true>(a, max_tiles, st)
+                        : launch<SEM_MXFP4, XM_PLANES, false, 64, true>(a, max_tiles, st);
+        if (sem == SEM_MXFP4_CLAMP && xmode == XM_PLANES)
+            return dual ? launch<SEM_MXFP4_CLAMP, XM_PLANES, true, 64, true>(a, max_tiles, st)
+                        : launch<SEM_MXFP4_CLAMP, XM_PLANES, false, 64, true>(a, max_tiles, st);
+        if (sem == SEM_MXFP4_Q8 && xmode == XM_Q8D)
+            return dual ? launch<SEM_MXFP4_Q8, XM_Q8D, true, 64, true>(a, max_tiles, st)
+                        : launch<SEM_MXFP4_Q8, XM_Q8D, false, 64, true>(a, max_tiles, st);
+        return hipErrorInvalidValue;
+    }
     const bool wide = !dual && !a.tile_expert && a.n_entries >= 512;
 #define QGP(S)                                                                        \
     if (sem == S && xmode == XM_PLANES) {                                             \

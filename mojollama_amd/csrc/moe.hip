@@ -219,6 +219,12 @@ struct mllm_moe_layer {
     int owns_router, owns_tab;
     float *router_p;    // device, routing layout (mllm_router_pack); freed with the layer when owned
     mllm_packed *tab;   // device: [E] gate, [E] up, [E] down; freed with the layer when owned
+    // load-time bf16 copies of the bf16-exact expert matrices (mllm_moe_dense_experts):
+    // dtab as tab with p[0] = bf16 rows of stride ld_gu (gate/up) or ld_d (down);
+    // dense_gu / dense_d: the batched path reads them
+    mllm_packed *dtab;
+    void *dmem;
+    int dense_gu, dense_d, ld_gu, ld_d;
 };
 
 struct moe_ws {
@@ -288,6 +294,9 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
     L->router_p = nullptr;
     L->tab = nullptr;
     L->gemv_only = 0;
+    L->dtab = nullptr;
+    L->dmem = nullptr;
+    L->dense_gu = L->dense_d = L->ld_gu = L->ld_d = 0;
     std::vector<mllm_packed> tab(3 * (size_t)E);
     for (int e = 0; e < E; e++) {
         if (L->sem_g >= 0) tab[e] = mllm_packed_view(mllm_sem_layout(L->sem_g), (const uint8_t *)gate_packed[e], M, N);
@@ -311,8 +320,83 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *L)
 {
     if (!L) return;
     if (L->tab && L->owns_tab) (void)hipFree(L->tab);
+    if (L->dtab) (void)hipFree(L->dtab);
+    if (L->dmem) (void)hipFree(L->dmem);
     if (L->router_p && L->owns_router) (void)hipFree(L->router_p);
     delete L;
+}
+
+// The MXFP4 forms' weights, sext4(n) * 2^(E-127), are exact in bf16 (the
+// GEMM's tiles hold exactly these values): a load-time copy lets the batched
+// path copy tiles instead of decoding them, with bit-identical results.
+static bool dense_exact(int sem) { return sem == SEM_MXFP4 || sem == SEM_MXFP4_CLAMP || sem == SEM_MXFP4_Q8; }
+
+__global__ void k_bf16_rows(const float *__restrict__ w, int rows, int cols, int ld, __bf16 *__restrict__ out)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * ld) return;
+    const int r = (int)(i / ld), c = (int)(i % ld);
+    out[i] = c < cols ? (__bf16)w[(long)r * cols + c] : (__bf16)0.0f;
+}
+
+MLLM_API long mllm_moe_dense_experts(mllm_moe_layer *L, void *stream)
+{
+    if (!L) return -1;
+    if (L->dmem) return 0;
+    const bool gu = !L->gemv_only && L->sem_g >= 0 && L->sem_g == L->sem_u && dense_exact(L->sem_g);
+    const bool dn = !L->gemv_only && L->sem_d >= 0 && dense_exact(L->sem_d);
+    if (!gu && !dn) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const int E = L->E, N = L->N, M = L->M;
+    const int ld_gu = (N + 63) / 64 * 64, ld_d = (M + 63) / 64 * 64;
+    const size_t mgu = (size_t)M * ld_gu, md = (size_t)N * ld_d;   // elements per matrix
+    const size_t total = (gu ? 2 * E * mgu : 0) + (dn ? E * md : 0);
+    std::vector<mllm_packed> tab(3 * (size_t)E), dtab(3 * (size_t)E);
+    float *tmp = nullptr;
+    __bf16 *mem = nullptr;
+    if (hipMemcpy(tab.data(), L->tab, tab.size() * sizeof(mllm_packed), hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMalloc(&mem, total * 2) != hipSuccess ||
+        hipMalloc(&tmp, std::max(mgu, md) * 4) != hipSuccess) {
+        (void)hipFree(mem);
+        return -1;
+    }
+    size_t at = 0;
+    bool ok = true;
+    auto copy = [&](int which, int sem, int rows, int cols, int ld) {
+        for (int e = 0; e < E && ok; e++) {
+            __bf16 *dst = mem + at;
+            at += (size_t)rows * ld;
+            // the dequantised values of the MXFP4 layout (the Q8-activation form has the same weights)
+            const int dsem = sem == SEM_MXFP4_Q8 ? SEM_MXFP4 : sem;
+            const long n = (long)rows * ld;
+            ok = mllm_launch_dequant(dsem, tab[(size_t)which * E + e], rows, cols, tmp, st) == 0;
+            if (ok) {
+                hipLaunchKernelGGL(k_bf16_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, tmp, rows, cols,
+                                   ld, dst);
+                ok = hipGetLastError() == hipSuccess;
+            }
+            dtab[(size_t)which * E + e].p[0] = reinterpret_cast<const uint8_t *>(dst);
+        }
+    };
+    if (gu) { copy(0, L->sem_g, M, N, ld_gu); copy(1, L->sem_u, M, N, ld_gu); }
+    if (dn) copy(2, L->sem_d, N, M, ld_d);
+    ok = ok && hipStreamSynchronize(st) == hipSuccess;
+    (void)hipFree(tmp);
+    if (ok && (hipMalloc(&L->dtab, dtab.size() * sizeof(mllm_packed)) != hipSuccess ||
+               hipMemcpy(L->dtab, dtab.data(), dtab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess))
+        ok = false;
+    if (!ok) {
+        (void)hipFree(mem);
+        if (L->dtab) (void)hipFree(L->dtab);
+        L->dtab = nullptr;
+        return -1;
+    }
+    L->dmem = mem;
+    L->dense_gu = gu;
+    L->dense_d = dn;
+    L->ld_gu = ld_gu;
+    L->ld_d = ld_d;
+    return (long)(total * 2);
 }
 
 MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *L, int T)
@@ -353,6 +437,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
         // gate + up (+ SiLU) in bucket order
         qgemm_args a{};
         a.table = L->tab; a.table2 = L->tab + E;
+        if (L->dense_gu) { a.table = L->dtab; a.table2 = L->dtab + E; a.dense_ld = L->ld_gu; }
         a.xq = xqx;
         if (xmode_of(L->sem_g) == XM_PLANES || xmode_of(L->sem_u) == XM_PLANES) {
             const long pe = act_planes_elems(T, N);
@@ -371,7 +456,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
         } else {
             a.out = s.g; a.ldo = M;
             CK(mllm_launch_qgemm(L->sem_g, xmode_of(L->sem_g), false, a, max_tiles, st));
-            a.table = L->tab + E; a.out = s.u;
+            a.table = (L->dense_gu ? L->dtab : L->tab) + E; a.out = s.u;
             CK(mllm_launch_qgemm(L->sem_u, xmode_of(L->sem_u), false, a, max_tiles, st));
             CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, L->clamp, st));
         }
@@ -380,6 +465,7 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
             if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
             qgemm_args b{};
             b.table = L->tab + 2 * E;
+            if (L->dense_d) { b.table = L->dtab + 2 * E; b.dense_ld = L->ld_d; }
             b.xq = xqh;
             if (xmode_of(L->sem_d) == XM_PLANES) {
                 const long pe = act_planes_elems((long)TK, M);

@@ -155,6 +155,8 @@ def load_kernels(path=LIB_PATH):
     so.mllm_route.restype = ci
     so.mllm_dequant.argtypes = [ci, cvp, ci, ci, cvp, cvp]
     so.mllm_dequant.restype = ci
+    so.mllm_moe_dense_experts.argtypes = [cvp, cvp]
+    so.mllm_moe_dense_experts.restype = ctypes.c_long
     so.mllm_dense16_size.argtypes = [ci, ci]
     so.mllm_dense16_size.restype = ctypes.c_long
     so.mllm_dense16_make.argtypes = [ci, cvp, ci, ci, cvp, cvp]
@@ -429,6 +431,14 @@ class MoELayer:
         if not self.h:
             raise RuntimeError("mllm_moe_prepare failed")
         self._ws = None
+
+    def dense_experts(self):
+        """Load-time bf16 copies of the bf16-exact expert matrices (mllm_moe_dense_experts);
+        returns the bytes they take (0: no matrix of this layer qualifies)."""
+        n = self.ops.so.mllm_moe_dense_experts(self.h, self.ops._stream())
+        if n < 0:
+            raise RuntimeError("mllm_moe_dense_experts failed: " + last_error(self.ops.so))
+        return n
 
     def workspace(self, T):
         n = self.ops.so.mllm_moe_workspace_size(self.h, T)

@@ -92,7 +92,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
     ap.add_argument("--kernel", choices=("gate_up", "down", "gate_up_b8", "down_b8", "copy", "gemm_gate",
-                                         "gemm_down", "moe_gptoss", "moe_qwen3"),
+                                         "gemm_down", "moe_gptoss", "moe_qwen3", "moe_gptoss_dense"),
                     help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
                          "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
     return ap.parse_args()
@@ -254,12 +254,14 @@ def kernel_only(torch, dev, which):
         ws = dev.workspace(sem, C, 1280, x.device, R)
         for _ in range(10):
             dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
-    elif which in ("moe_gptoss", "moe_qwen3"):
-        # the MoE layer at T = 1280, 5 forwards
-        wl = W.moe_workload(which[4:], 1280)
+    elif which in ("moe_gptoss", "moe_qwen3", "moe_gptoss_dense"):
+        # the MoE layer at T = 1280, 5 forwards (_dense: over bf16 expert copies)
+        wl = W.moe_workload(which.split("_")[1], 1280)
         c = wl["cfg"]
         layer = dev.moe_prepare(wl["qts"], c["N"], c["M"], c["E"], c["K"], wl["gates"], wl["ups"], wl["downs"],
                                 torch.from_numpy(wl["router"]).cuda(), 1)
+        if which.endswith("_dense"):
+            layer.dense_experts()
         x = torch.from_numpy(wl["x"]).cuda()
         o = torch.empty(1280, c["N"], device="cuda")
         for _ in range(5):

@@ -222,9 +222,9 @@ struct mllm_moe_layer {
     // load-time bf16 copies of the bf16-exact expert matrices (mllm_moe_dense_experts):
     // dtab as tab with p[0] = bf16 rows of stride ld_gu (gate/up) or ld_d (down);
     // dense_gu / dense_d: the batched path reads them
-    mllm_packed *dtab;
-    void *dmem;
-    int dense_gu, dense_d, ld_gu, ld_d;
+    mllm_packed *dtab = nullptr;
+    void *dmem = nullptr;
+    int dense_gu = 0, dense_d = 0, ld_gu = 0, ld_d = 0;
 };
 
 struct moe_ws {
@@ -294,9 +294,6 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
     L->router_p = nullptr;
     L->tab = nullptr;
     L->gemv_only = 0;
-    L->dtab = nullptr;
-    L->dmem = nullptr;
-    L->dense_gu = L->dense_d = L->ld_gu = L->ld_d = 0;
     std::vector<mllm_packed> tab(3 * (size_t)E);
     for (int e = 0; e < E; e++) {
         if (L->sem_g >= 0) tab[e] = mllm_packed_view(mllm_sem_layout(L->sem_g), (const uint8_t *)gate_packed[e], M, N);

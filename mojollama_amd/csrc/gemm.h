@@ -52,9 +52,9 @@ struct qgemm_args {
     // the ksplit partials in order into out.
     int ksplit;
     float *part;
-    // dense_ld > 0: W / W2 / table entries hold p[0] = bf16 rows of that stride
-    // (a multiple of 64, zero padded; a load-time copy of weights exact in
-    // bf16, the MXFP4 forms), copied into the tiles instead of decoded.
+    // dense_ld > 0: W / W2 / table entries hold p[0] = the matrix's bf16 planes
+    // (mllm_launch_dense_planes: [planes][n_rows][dense_ld], dense_ld a
+    // multiple of 64, zero padded), copied into the tiles instead of decoded.
     int dense_ld;
 };
 
@@ -67,3 +67,10 @@ inline long mllm_qgemm_part_floats(int sem, int n_rows, int n_cols, int n_entrie
     return ks > 1 ? (long)ks * n_entries * n_rows : 0;
 }
 bool mllm_qgemm_supported(int sem);
+// Dense bf16 copies for the tiles (qgemm_args.dense_ld): the number of planes
+// a semantic's copy holds (0: not offered), and the copy itself, [planes]
+// [n_rows][ldw] (ldw a multiple of 64 >= n_cols; columns past the last block
+// are not written: clear the buffer first).
+int mllm_dense_planes(int sem);
+hipError_t mllm_launch_dense_planes(int sem, const mllm_packed &W, int n_rows, int n_cols, int ldw, __bf16 *out,
+                                    hipStream_t st);

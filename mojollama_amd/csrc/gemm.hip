@@ -289,29 +289,68 @@ MLLM_DEV void put_w(const wraw<SEM, XM, TN_> &wr, int n_rows, int nb, int n0, in
 // Dense bf16 weights (dense_ld > 0): a step is TN_ rows x 64 columns, eight
 // 16-byte pieces per row, copied into the tile as they are (rows past the
 // matrix clamped to its last row, whose outputs are never stored).
-template <int TN_> struct wdense {
+template <int TN_, int NA> struct wdense {
     static constexpr int NP = TN_ * 8 / 256;
-    uint4 p[NP];
+    uint4 p[NA][NP];
 };
 
-template <int TN_>
-MLLM_DEV void fetch_wd(const mllm_packed &W, int n_rows, int ldw, int n0, int k0, wdense<TN_> &wd)
+// Plane p of the copy starts p * plane elements after W.p[0].
+template <int TN_, int NA>
+MLLM_DEV void fetch_wd(const mllm_packed &W, int n_rows, int ldw, long plane, int n0, int k0, wdense<TN_, NA> &wd)
 {
     const __bf16 *base = reinterpret_cast<const __bf16 *>(W.p[0]);
 #pragma unroll
-    for (int i = 0; i < wdense<TN_>::NP; i++) {
+    for (int i = 0; i < wdense<TN_, NA>::NP; i++) {
         const int q = threadIdx.x + 256 * i, row = min(n0 + (q >> 3), n_rows - 1);
-        wd.p[i] = gld<uint4>(base + (long)row * ldw + k0 + 8 * (q & 7));
+#pragma unroll
+        for (int p = 0; p < NA; p++) wd.p[p][i] = gld<uint4>(base + p * plane + (long)row * ldw + k0 + 8 * (q & 7));
     }
 }
 
-template <int TN_, bool SWZ, int LDA>
-MLLM_DEV void put_wd(const wdense<TN_> &wd, __bf16 *A)
+template <int TN_, int NA, bool SWZ, int LDA>
+MLLM_DEV void put_wd(const wdense<TN_, NA> &wd, __bf16 *A)
 {
 #pragma unroll
-    for (int i = 0; i < wdense<TN_>::NP; i++) {
+    for (int i = 0; i < wdense<TN_, NA>::NP; i++) {
         const int q = threadIdx.x + 256 * i;
-        *reinterpret_cast<uint4 *>(A + tile_off<SWZ, LDA>(q >> 3, 8 * (q & 7))) = wd.p[i];
+#pragma unroll
+        for (int p = 0; p < NA; p++)
+            *reinterpret_cast<uint4 *>(A + p * TN_ * LDA + tile_off<SWZ, LDA>(q >> 3, 8 * (q & 7))) = wd.p[p][i];
+    }
+}
+
+// The weights of a packed matrix exactly as the tiles hold them (put_w's
+// chunk_weights and plane split): NA bf16 planes [NA][n_rows][ldw], plane p
+// the bf16 rounding of what planes < p leave; columns past the last block are
+// left as they are (the caller clears the buffer).  One thread per chunk.
+template <int SEM>
+__global__ __launch_bounds__(256) void k_dense_planes(mllm_packed W, int n_rows, int n_cols, int ldw, __bf16 *out)
+{
+    constexpr int NA = gemm_cfg<SEM, XM_PLANES>::NA;
+    constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
+    const int nb = n_cols / sem_traits<SEM>::kBlockElems, nch = nb * CPB;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n_rows * nch) return;
+    const int row = (int)(i / nch), c = (int)(i % nch);
+    raw_chunk raw;
+    fetch<SEM>(W, nb, row, c, raw);
+    float w[2][16];
+    int x[2];
+    chunk_weights<SEM>(raw, c, w[0], w[1], x[0], x[1]);
+    const long plane = (long)n_rows * ldw;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        __bf16 *o = out + (long)row * ldw + x[h];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            float r = w[h][e];
+#pragma unroll
+            for (int p = 0; p < NA; p++) {
+                const float t = (float)(__bf16)r;
+                r -= t;
+                o[p * plane + e] = (__bf16)t;
+            }
+        }
     }
 }
 
@@ -412,7 +451,7 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
 // Workgroups per CU the tile's LDS allows (160 KB per CU), at most 3 (2 for
 // the Q8D form, whose registers do not fit a third); the compiler then
 // budgets registers for that many.
-template <int SEM, int XM, bool DUAL, int TM> constexpr int qgemm_wgs_per_cu()
+template <int SEM, int XM, bool DUAL, int TM, bool DW = false> constexpr int qgemm_wgs_per_cu()
 {
     using C = gemm_cfg<SEM, XM>;
     constexpr int TN = tile_cfg<DUAL, TM>::TN;
@@ -420,13 +459,14 @@ template <int SEM, int XM, bool DUAL, int TM> constexpr int qgemm_wgs_per_cu()
     // unpadded tiles would admit a third workgroup whose register budget spills
     constexpr int RW = DUAL ? C::KE + 8 : C::LDA;
     constexpr int lds = 2 * (C::NA * TN * RW * (DUAL ? 2 : 1) + C::NB * TM * RW) + 4 * TM + 4 * 3 * TN + 8 * TM + 64;
-    constexpr int cap = XM == XM_Q8D ? 2 : 3;
+    // (two-plane dense-weight tiles: their copied planes' registers do not fit a third either)
+    constexpr int cap = (XM == XM_Q8D || (DW && C::NA == 2)) ? 2 : 3;
     constexpr int n = 163840 / lds;
     return n < 1 ? 1 : n > cap ? cap : n;
 }
 
 template <int SEM, int XM, bool DUAL, int TM, bool DW>
-__global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void k_qgemm(qgemm_args a)
+__global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM, DW>())) void k_qgemm(qgemm_args a)
 {
     using C = gemm_cfg<SEM, XM>;
     using G = tile_cfg<DUAL, TM>;
@@ -518,8 +558,8 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
         else return (base + li) * LDA + ks + lk;
     };
 
-    static_assert(!DW || (NA == 1 && !C::A4 && KS == 64), "dense bf16 weights: one exact plane, 64-column steps");
-    using WB = typename std::conditional<DW, wdense<TN>, wraw<SEM, XM, TN>>::type;
+    static_assert(!DW || (!C::A4 && KS == 64), "dense bf16 weights: plane-split forms, 64-column steps");
+    using WB = typename std::conditional<DW, wdense<TN, NA>, wraw<SEM, XM, TN>>::type;
     struct stepbuf {
         WB w, u;
         araw<TM, NB> x;
@@ -527,8 +567,8 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
     auto fetch_step = [&](int s, stepbuf &b) __attribute__((always_inline)) {
         const int k0 = min(s, s_end - 1) * KS;   // past the end: refetch the last step (unused)
         if constexpr (DW) {
-            fetch_wd<TN>(W, a.n_rows, a.dense_ld, n0, k0, b.w);
-            if constexpr (DUAL) fetch_wd<TN>(W2, a.n_rows, a.dense_ld, n0, k0, b.u);
+            fetch_wd<TN, NA>(W, a.n_rows, a.dense_ld, (long)a.n_rows * a.dense_ld, n0, k0, b.w);
+            if constexpr (DUAL) fetch_wd<TN, NA>(W2, a.n_rows, a.dense_ld, (long)a.n_rows * a.dense_ld, n0, k0, b.u);
         } else {
             fetch_w<SEM, XM, TN>(W, a.n_rows, nb, n0, k0, b.w, 0);
             if constexpr (DUAL) fetch_w<SEM, XM, TN>(W2, a.n_rows, nb, n0, k0, b.u, 128);
@@ -538,8 +578,8 @@ __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM>())) void 
     auto put_step = [&](int s, const stepbuf &b) __attribute__((always_inline)) {
         const int k0 = s * KS;
         if constexpr (DW) {
-            put_wd<TN, C::SWZ, LDA>(b.w, s_a);
-            if constexpr (DUAL) put_wd<TN, C::SWZ, LDA>(b.u, s_u);
+            put_wd<TN, NA, C::SWZ, LDA>(b.w, s_a);
+            if constexpr (DUAL) put_wd<TN, NA, C::SWZ, LDA>(b.u, s_u);
         } else {
             put_w<SEM, XM, TN>(b.w, a.n_rows, nb, n0, k0, s_a, C::A4 ? s_dmin : nullptr, 0);
             if constexpr (DUAL) put_w<SEM, XM, TN>(b.u, a.n_rows, nb, n0, k0, s_u, C::A4 ? s_dmin2 : nullptr, 128);
@@ -735,17 +775,15 @@ hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
 hipError_t mllm_launch_qgemm(int sem, int xmode, bool dual, const qgemm_args &a, int max_tiles, hipStream_t st)
 {
     if (a.dense_ld > 0) {
-        // dense bf16 copies: the weight-exact (MXFP4) forms, 64-entry tiles
-        if (a.dense_ld % 64 || a.dense_ld < a.n_cols) return hipErrorInvalidValue;
-        if (sem == SEM_MXFP4 && xmode == XM_PLANES)
-            return dual ? launch<SEM_MXFP4, XM_PLANES, true, 64, true>(a, max_tiles, st)
-                        : launch<SEM_MXFP4, XM_PLANES, false, 64, true>(a, max_tiles, st);
-        if (sem == SEM_MXFP4_CLAMP && xmode == XM_PLANES)
-            return dual ? launch<SEM_MXFP4_CLAMP, XM_PLANES, true, 64, true>(a, max_tiles, st)
-                        : launch<SEM_MXFP4_CLAMP, XM_PLANES, false, 64, true>(a, max_tiles, st);
-        if (sem == SEM_MXFP4_Q8 && xmode == XM_Q8D)
-            return dual ? launch<SEM_MXFP4_Q8, XM_Q8D, true, 64, true>(a, max_tiles, st)
-                        : launch<SEM_MXFP4_Q8, XM_Q8D, false, 64, true>(a, max_tiles, st);
+        // dense bf16 plane copies (mllm_launch_dense_planes) of the MoE layer's
+        // semantics, 64-entry tiles
+        if (a.dense_ld % 64 || a.dense_ld < a.n_cols || mllm_dense_planes(sem) == 0) return hipErrorInvalidValue;
+#define QGD(S, X)                                                                           \
+    if (sem == S && xmode == X) return dual ? launch<S, X, true, 64, true>(a, max_tiles, st) \
+                                            : launch<S, X, false, 64, true>(a, max_tiles, st);
+        QGD(SEM_MXFP4, XM_PLANES)
+        QGD(SEM_MXFP4_Q8, XM_Q8D)
+#undef QGD
         return hipErrorInvalidValue;
     }
     const bool wide = !dual && !a.tile_expert && a.n_entries >= 512;
@@ -847,5 +885,27 @@ hipError_t mllm_launch_act_split(const float *x, int ldx, int rows, int K, int n
         hipLaunchKernelGGL(k_act_split<2>, dim3(rows), dim3(256), 0, st, x, ldx, K, base, plane, act_planes_ld(K), lo_nz);
     else
         hipLaunchKernelGGL(k_act_split<3>, dim3(rows), dim3(256), 0, st, x, ldx, K, base, plane, act_planes_ld(K), lo_nz);
+    return hipGetLastError();
+}
+
+// bf16 planes of a packed matrix for the GEMM's dense-weight tiles; 0: not
+// offered for this semantic.  Offered for the MXFP4 forms (one exact plane).
+// Two-plane copies (the Q6_K / Q4_0 expert forms) ran no faster: Qwen3's Q6_K
+// down over them measured 714.6 -> 708.5 us per layer, the copied planes'
+// registers leaving two workgroups per CU instead of three.
+int mllm_dense_planes(int sem)
+{
+    return (sem == SEM_MXFP4 || sem == SEM_MXFP4_Q8) ? gemm_cfg<SEM_MXFP4, XM_PLANES>::NA : 0;
+}
+
+hipError_t mllm_launch_dense_planes(int sem, const mllm_packed &W, int n_rows, int n_cols, int ldw, __bf16 *out,
+                                    hipStream_t st)
+{
+    const long nch = (long)n_rows * (n_cols / 32);   // chunks of 32 weights
+    if (nch == 0) return hipSuccess;
+    const dim3 g((unsigned)((nch + 255) / 256));
+    if (mllm_dense_planes(sem) == 0) return hipErrorInvalidValue;
+    // MXFP4 and MXFP4_Q8: one layout and the same weights, sext4(n) * 2^(E-127)
+    hipLaunchKernelGGL(k_dense_planes<SEM_MXFP4>, g, dim3(256), 0, st, W, n_rows, n_cols, ldw, out);
     return hipGetLastError();
 }

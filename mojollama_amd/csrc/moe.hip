@@ -323,62 +323,41 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *L)
     delete L;
 }
 
-// The MXFP4 forms' weights, sext4(n) * 2^(E-127), are exact in bf16 (the
-// GEMM's tiles hold exactly these values): a load-time copy lets the batched
-// path copy tiles instead of decoding them, with bit-identical results.
-static bool dense_exact(int sem) { return sem == SEM_MXFP4 || sem == SEM_MXFP4_CLAMP || sem == SEM_MXFP4_Q8; }
-
-__global__ void k_bf16_rows(const float *__restrict__ w, int rows, int cols, int ld, __bf16 *__restrict__ out)
-{
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)rows * ld) return;
-    const int r = (int)(i / ld), c = (int)(i % ld);
-    out[i] = c < cols ? (__bf16)w[(long)r * cols + c] : (__bf16)0.0f;
-}
-
+// Load-time bf16 plane copies of the expert matrices (mllm_launch_dense_planes:
+// the values put_w would write into the tiles, so results are bit-identical);
+// gate and up take them when they share a semantic.
 MLLM_API long mllm_moe_dense_experts(mllm_moe_layer *L, void *stream)
 {
     if (!L) return -1;
     if (L->dmem) return 0;
-    const bool gu = !L->gemv_only && L->sem_g >= 0 && L->sem_g == L->sem_u && dense_exact(L->sem_g);
-    const bool dn = !L->gemv_only && L->sem_d >= 0 && dense_exact(L->sem_d);
+    const int pg = L->sem_g >= 0 ? mllm_dense_planes(L->sem_g) : 0;
+    const int pd = L->sem_d >= 0 ? mllm_dense_planes(L->sem_d) : 0;
+    const bool gu = !L->gemv_only && pg > 0 && L->sem_g == L->sem_u;
+    const bool dn = !L->gemv_only && pd > 0;
     if (!gu && !dn) return 0;
     hipStream_t st = (hipStream_t)stream;
     const int E = L->E, N = L->N, M = L->M;
     const int ld_gu = (N + 63) / 64 * 64, ld_d = (M + 63) / 64 * 64;
-    const size_t mgu = (size_t)M * ld_gu, md = (size_t)N * ld_d;   // elements per matrix
+    const size_t mgu = (size_t)pg * M * ld_gu, md = (size_t)pd * N * ld_d;   // elements per matrix copy
     const size_t total = (gu ? 2 * E * mgu : 0) + (dn ? E * md : 0);
     std::vector<mllm_packed> tab(3 * (size_t)E), dtab(3 * (size_t)E);
-    float *tmp = nullptr;
     __bf16 *mem = nullptr;
     if (hipMemcpy(tab.data(), L->tab, tab.size() * sizeof(mllm_packed), hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMalloc(&mem, total * 2) != hipSuccess ||
-        hipMalloc(&tmp, std::max(mgu, md) * 4) != hipSuccess) {
-        (void)hipFree(mem);
+        hipMalloc(&mem, total * 2) != hipSuccess)
         return -1;
-    }
+    bool ok = hipMemsetAsync(mem, 0, total * 2, st) == hipSuccess;
     size_t at = 0;
-    bool ok = true;
-    auto copy = [&](int which, int sem, int rows, int cols, int ld) {
+    auto copy = [&](int which, int sem, int rows, int cols, int ld, size_t elems) {
         for (int e = 0; e < E && ok; e++) {
             __bf16 *dst = mem + at;
-            at += (size_t)rows * ld;
-            // the dequantised values of the MXFP4 layout (the Q8-activation form has the same weights)
-            const int dsem = sem == SEM_MXFP4_Q8 ? SEM_MXFP4 : sem;
-            const long n = (long)rows * ld;
-            ok = mllm_launch_dequant(dsem, tab[(size_t)which * E + e], rows, cols, tmp, st) == 0;
-            if (ok) {
-                hipLaunchKernelGGL(k_bf16_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, tmp, rows, cols,
-                                   ld, dst);
-                ok = hipGetLastError() == hipSuccess;
-            }
+            at += elems;
+            ok = mllm_launch_dense_planes(sem, tab[(size_t)which * E + e], rows, cols, ld, dst, st) == hipSuccess;
             dtab[(size_t)which * E + e].p[0] = reinterpret_cast<const uint8_t *>(dst);
         }
     };
-    if (gu) { copy(0, L->sem_g, M, N, ld_gu); copy(1, L->sem_u, M, N, ld_gu); }
-    if (dn) copy(2, L->sem_d, N, M, ld_d);
+    if (gu) { copy(0, L->sem_g, M, N, ld_gu, mgu); copy(1, L->sem_u, M, N, ld_gu, mgu); }
+    if (dn) copy(2, L->sem_d, N, M, ld_d, md);
     ok = ok && hipStreamSynchronize(st) == hipSuccess;
-    (void)hipFree(tmp);
     if (ok && (hipMalloc(&L->dtab, dtab.size() * sizeof(mllm_packed)) != hipSuccess ||
                hipMemcpy(L->dtab, dtab.data(), dtab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice) != hipSuccess))
         ok = false;

@@ -1,18 +1,18 @@
 """GPU tests of the MoE layer's load-time bf16 expert copies
-(mllm_moe_dense_experts): the batched path over the copies gives results
-bit-identical to the per-tile decode (same bf16 tile values, same MFMA
-sequence), checked at configs[3]'s full GPT-OSS shape and at small shapes
-against the oracle, and layers whose weights are not exact in bf16 make no
-copy."""
+(mllm_moe_dense_experts, the MXFP4 forms): the batched path over the copies
+gives results bit-identical to the per-tile decode (same bf16 tile values,
+same MFMA sequence), checked at configs[3]'s full shape and at small shapes
+against the oracle (helpers.moe_tol: 1e-4, or 1e-3 where an MXFP4
+down requantises h to Q8_0)."""
 import numpy as np
 import pytest
 
 import oracle as O
+from helpers import MOE_Q8H_TOL, moe_tol
 from mojollama_amd import kernels as K
 from mojollama_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
-MOE_TOL_MX = 1e-3   # MXFP4 down: h requantised to Q8_0 (as in test_gpu_moe)
 
 
 @pytest.fixture(scope="module")
@@ -70,22 +70,46 @@ def test_dense_experts_small_vs_oracle(dev, orc, N, M, E, Kk, T):
     assert torch.equal(a, b)
     ri, rw = orc.route(router, x, Kk, 1)
     ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in range(T)])
-    assert O.norm_err(b.cpu().numpy(), ref) < MOE_TOL_MX
+    assert O.norm_err(b.cpu().numpy(), ref) < MOE_Q8H_TOL
 
 
-def test_dense_experts_not_exact_formats(dev):
-    """Q4_K / Q6_K experts are not exact in one bf16: no copy is made and the
-    layer runs as before."""
+def test_dense_experts_qwen3_config(dev):
+    """configs[4] (Q4_K x Q8_0 gate/up, Q6_K down: no one-plane form): no copy is
+    made and the layer runs as before."""
     import torch
-    qts = (12, 12, 14)
-    N, M, E, Kk, T = 256, 256, 8, 2, 30
-    rng = np.random.default_rng(2200)
-    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
-    gates = [cu(W.gen_weights(rng, 12, M, N)) for _ in range(E)]
-    ups = [cu(W.gen_weights(rng, 12, M, N)) for _ in range(E)]
-    downs = [cu(W.gen_weights(rng, 14, N, M)) for _ in range(E)]
-    router = cu(W.gen_router(rng, E, N))
-    x = cu(W.gen_x(rng, T, N))
-    plain, dense = _layers(dev, qts, N, M, E, Kk, gates, ups, downs, router, 0)
+    wl = W.moe_workload("qwen3", 300)
+    c = wl["cfg"]
+    N, M, E, Kk = c["N"], c["M"], c["E"], c["K"]
+    router = torch.from_numpy(wl["router"]).cuda()
+    plain, dense = _layers(dev, wl["qts"], N, M, E, Kk, wl["gates"], wl["ups"], wl["downs"], router, 1)
     assert dense.dense_experts() == 0
+    x = torch.from_numpy(wl["x"]).cuda()
     assert torch.equal(plain.forward(x), dense.forward(x))
+
+
+@pytest.mark.parametrize("qts", [(39, 39, 39), (12, 12, 39)])
+def test_dense_experts_formats_vs_oracle(dev, orc, qts):
+    """MXFP4 experts with and without MXFP4 gate/up (a down-only copy beside
+    the decoded Q4_K x Q8_0 gate/up tiles), vs the oracle and bit-equal to the
+    decoding layer.  (Gate/up products exact in both cases: at this small M a
+    single one-step flip of a Q8_0 code of h already moves an output by
+    3 / (127 sqrt(M)) ~ 1.5e-3 of its max.)"""
+    import torch
+    N, M, E, Kk, T = 512, 256, 8, 2, 60
+    rng = np.random.default_rng(2300 + sum(qts))
+    gates = [W.gen_weights(rng, qts[0], M, N) for _ in range(E)]
+    ups = [W.gen_weights(rng, qts[1], M, N) for _ in range(E)]
+    downs = [W.gen_weights(rng, qts[2], N, M) for _ in range(E)]
+    router = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, T, N)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    plain, dense = _layers(dev, qts, N, M, E, Kk, [cu(g) for g in gates], [cu(u) for u in ups],
+                           [cu(d) for d in downs], cu(router), 0)
+    ld_gu, ld_d = (N + 63) // 64 * 64, (M + 63) // 64 * 64
+    assert dense.dense_experts() == (2 * E * M * ld_gu if qts[0] == 39 else 0) * 2 + E * N * ld_d * 2
+    a = plain.forward(cu(x))
+    b = dense.forward(cu(x))
+    assert torch.equal(a, b)
+    ri, rw = orc.route(router, x, Kk, 0)
+    ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in range(T)])
+    assert O.norm_err(b.cpu().numpy(), ref) < moe_tol(qts)

@@ -11,7 +11,10 @@
 // 2^-11 each, so y = W.x keeps ~3e-4 of the output scale.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
+#include <algorithm>
+#include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 #include "gemv.h"
@@ -133,19 +136,20 @@ __global__ __launch_bounds__(256) void k_x16_cvt(const float *__restrict__ x, in
 
 constexpr int kAlgoCands = 8;   // heuristic candidates timed at plan time
 
+// A shape's GEMM: its descriptors and the heuristic's candidates (fixed once
+// made); `chosen` is the candidate calls use, -1 until timed (calls then use
+// the heuristic's first), published once by the timing call.
 struct plan {
     hipblasLtMatmulDesc_t op;
     hipblasLtMatrixLayout_t a, b, d;
-    hipblasLtMatmulAlgo_t algo;
-    size_t ws;
     hipblasLtMatmulHeuristicResult_t cand[kAlgoCands];
     int n_cand;
-    bool timed;
+    std::atomic<int> chosen{-1};
 };
 
 std::mutex g_mu, g_tune_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
-std::map<std::tuple<int, int, int, int, int>, plan> g_plans;
+std::map<std::tuple<int, int, int, int, int>, std::unique_ptr<plan>> g_plans;
 
 int device_cus_d16()
 {
@@ -165,7 +169,7 @@ plan *get_plan(int N, int K, int M, int ldo, std::string &err)
     std::lock_guard<std::mutex> lk(g_mu);
     const auto key = std::make_tuple(dev, N, K, M, ldo);
     auto it = g_plans.find(key);
-    if (it != g_plans.end()) return &it->second;
+    if (it != g_plans.end()) return it->second.get();
     hipblasLtHandle_t h;
     auto hi = g_handles.find(dev);
     if (hi == g_handles.end()) {
@@ -174,7 +178,8 @@ plan *get_plan(int N, int K, int M, int ldo, std::string &err)
     } else {
         h = hi->second;
     }
-    plan p{};
+    auto pp = std::make_unique<plan>();
+    plan &p = *pp;
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
     const int32_t pm = HIPBLASLT_POINTER_MODE_ALPHA_DEVICE_VECTOR_BETA_HOST;
     const uint64_t wsmax = kBlasWs;
@@ -199,9 +204,7 @@ plan *get_plan(int N, int K, int M, int ldo, std::string &err)
         return nullptr;
     }
     p.n_cand = n;
-    p.algo = p.cand[0].algo;
-    p.ws = p.cand[0].workspaceSize;
-    return &g_plans.emplace(key, p).first->second;
+    return g_plans.emplace(key, std::move(pp)).first->second.get();
 }
 
 hipblasLtHandle_t handle_for_current()
@@ -212,21 +215,24 @@ hipblasLtHandle_t handle_for_current()
     return g_handles[dev];
 }
 
-// The heuristic's candidates timed on the call's own operands (3 runs each
-// after a warm-up) the first time a shape runs outside a graph capture; the
-// fastest is kept.  Every candidate computes the same product.
+// The heuristic's candidates timed on the call's own operands (the better of
+// two rounds of 5 runs, after a warm-up) the first time a shape runs outside a
+// graph capture; the fastest is kept, the heuristic's first unless another is
+// 3% faster.  Every candidate computes the same product.
 void time_candidates(plan *p, hipblasLtHandle_t h, const float *alpha, const void *w16, const void *x16, float *out,
                      void *bws, hipStream_t st)
 {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
-    p->timed = true;
-    if (p->n_cand < 2) return;
-    hipEvent_t e0, e1;
-    if (hipEventCreate(&e0) != hipSuccess) return;
-    if (hipEventCreate(&e1) != hipSuccess) { (void)hipEventDestroy(e0); return; }
-    const float beta = 0.f;
+    int best_c = 0;
     float best = 1e30f;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (p->n_cand < 2 || hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        if (e0) (void)hipEventDestroy(e0);
+        p->chosen.store(0, std::memory_order_release);
+        return;
+    }
+    const float beta = 0.f;
     for (int c = 0; c < p->n_cand; c++) {
         const hipblasLtMatmulHeuristicResult_t &r = p->cand[c];
         if (r.state != HIPBLAS_STATUS_SUCCESS || r.workspaceSize > kBlasWs) continue;
@@ -235,20 +241,26 @@ void time_candidates(plan *p, hipblasLtHandle_t h, const float *alpha, const voi
                                    r.workspaceSize, st) == HIPBLAS_STATUS_SUCCESS;
         };
         if (!run()) continue;
-        bool ok = hipEventRecord(e0, st) == hipSuccess;
-        for (int k = 0; k < 3 && ok; k++) ok = run();
-        float ms = 0.f;
-        if (!ok || hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
-            hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
-            continue;
-        if (ms < best) {
+        float ms = 1e30f;
+        bool ok = true;
+        for (int round = 0; round < 2 && ok; round++) {
+            ok = hipEventRecord(e0, st) == hipSuccess;
+            for (int k = 0; k < 5 && ok; k++) ok = run();
+            float t = 0.f;
+            ok = ok && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                 hipEventElapsedTime(&t, e0, e1) == hipSuccess;
+            if (ok) ms = std::min(ms, t);
+        }
+        if (!ok) continue;
+        // the heuristic's first candidate unless another is clearly faster
+        if (c == 0 ? ms < best : ms < 0.97f * best) {
             best = ms;
-            p->algo = r.algo;
-            p->ws = r.workspaceSize;
+            best_c = c;
         }
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    p->chosen.store(best_c, std::memory_order_release);
 }
 
 } // namespace
@@ -316,13 +328,14 @@ int mllm_d16_gemm(const void *w16, const float *x, int ldx, int M, float *out, i
     hipLaunchKernelGGL(k_x16_cvt, dim3(gc), dim3(256), 0, st, x, n_cols, ldx, n4, part, np, x16, alpha, n_rows);
     if (hipGetLastError() != hipSuccess) { err = "activation conversion launch failed"; return -1; }
     const hipblasLtHandle_t h = handle_for_current();
-    if (!p->timed) {
+    if (p->chosen.load(std::memory_order_acquire) < 0) {
         std::lock_guard<std::mutex> lk(g_tune_mu);
-        if (!p->timed) time_candidates(p, h, alpha, w16, x16, out, bws, st);
+        if (p->chosen.load(std::memory_order_acquire) < 0) time_candidates(p, h, alpha, w16, x16, out, bws, st);
     }
+    const int c = std::max(0, p->chosen.load(std::memory_order_acquire));
     const float beta = 0.f;
     const hipblasStatus_t s = hipblasLtMatmul(h, p->op, alpha, w16, p->a, x16, p->b, &beta, out, p->d, out, p->d,
-                                              &p->algo, bws, p->ws, st);
+                                              &p->cand[c].algo, bws, p->cand[c].workspaceSize, st);
     if (s != HIPBLAS_STATUS_SUCCESS) { err = "hipblasLtMatmul failed"; return -1; }
     return 0;
 }

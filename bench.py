@@ -92,7 +92,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
     ap.add_argument("--kernel", choices=("gate_up", "down", "gate_up_b8", "down_b8", "copy", "gemm_gate",
-                                         "gemm_down", "moe_gptoss", "moe_qwen3", "moe_gptoss_dense"),
+                                         "gemm_down", "gemm16_gate", "gemm16_down", "moe_gptoss", "moe_qwen3",
+                                         "moe_gptoss_dense"),
                     help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
                          "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
     return ap.parse_args()
@@ -243,17 +244,26 @@ def kernel_only(torch, dev, which):
         torch.cuda.synchronize()
         for _ in range(50):
             b.copy_(a)
-    elif which in ("gemm_gate", "gemm_down"):
+    elif which in ("gemm_gate", "gemm_down", "gemm16_gate", "gemm16_down"):
         # configs[2] prefill at M = 1280: the Q4_K gate (5632x2048) or the Q6_K down (2048x5632), 10 launches
+        # (gemm16_*: over the load-time fp16 copy, mllm_gemm16)
         gen = torch.Generator(device="cuda").manual_seed(3)
-        sem, qt, R, C = (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048) if which == "gemm_gate" else \
+        sem, qt, R, C = (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048) if which.endswith("gate") else \
             (K.Q6_K_SEQ, W.QT_Q6_K, 2048, 5632)
         packed = dev.pack(sem, W.gen_weights_torch(gen, qt, R, C), R, C)
         x = torch.randn(1280, C, device="cuda", generator=gen).bfloat16().float()
         o = torch.empty(1280, R, device="cuda")
-        ws = dev.workspace(sem, C, 1280, x.device, R)
-        for _ in range(10):
-            dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
+        if which.startswith("gemm16"):
+            w16 = dev.dense16(sem, packed, R, C)
+            ws = dev.gemm16_workspace(R, C, 1280, x.device)
+            dev.gemm16(w16, x, R, C, out=o, ws=ws)   # the plan (and its timed choice) outside the counted launches
+            torch.cuda.synchronize()
+            for _ in range(10):
+                dev.gemm16(w16, x, R, C, out=o, ws=ws)
+        else:
+            ws = dev.workspace(sem, C, 1280, x.device, R)
+            for _ in range(10):
+                dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
     elif which in ("moe_gptoss", "moe_qwen3", "moe_gptoss_dense"):
         # the MoE layer at T = 1280, 5 forwards (_dense: over bf16 expert copies)
         wl = W.moe_workload(which.split("_")[1], 1280)

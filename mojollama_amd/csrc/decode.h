@@ -121,9 +121,13 @@ MLLM_DEV void kq_pairs(const uint4 &m, int j0, int &s_a, int &m_a, int &s_b, int
 {
     // S occupies bits [0, 48) of m.y:m.z, M bits [48, 96) of m.y:m.z:m.w.
     // 32-bit funnel shifts only: 64-bit shifts would need register pairs.
+    // The word pair is selected, not branched on (j0 differs between the lanes
+    // of a wave): a funnel from m.w:m.z past bit 32 keeps the low 12 bits of
+    // m.z >> (so - 32) since so + 12 <= 64, and 0:m.w gives m.w >> (mo - 64).
     const int so = 6 * j0, mo = 48 + 6 * j0;              // so < 48, 48 <= mo < 96
-    const uint32_t sv = so < 32 ? funnel(m.z, m.y, so) : (m.z >> (so - 32));
-    const uint32_t mv = mo < 64 ? funnel(m.w, m.z, mo - 32) : (m.w >> (mo - 64));
+    const bool s_lo = so < 32, m_lo = mo < 64;
+    const uint32_t sv = funnel(s_lo ? m.z : m.w, s_lo ? m.y : m.z, (uint32_t)so & 31);
+    const uint32_t mv = funnel(m_lo ? m.w : 0u, m_lo ? m.z : m.w, (uint32_t)mo & 31);
     s_a = sv & 63; s_b = (sv >> 6) & 63;
     m_a = mv & 63; m_b = (mv >> 6) & 63;
 }
@@ -132,7 +136,7 @@ template <int SEM>
 MLLM_DEV void fetch(const mllm_packed &P, int nb, int row, int c, raw_chunk &r)
 {
     constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
-    const int blk = c / CPB, cc = c % CPB;
+    const int blk = (int)((unsigned)c / CPB), cc = (int)((unsigned)c % CPB);   // c >= 0
     const long bi = (long)row * nb + blk;
     if constexpr (SEM == SEM_Q8_0) {
         r.a = ld16(P.p[0] + bi * 32);

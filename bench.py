@@ -348,6 +348,38 @@ def bench_kinds(torch, dev, layers, lm, out_norm, args):
     return res
 
 
+def bench_long_gemv(torch, dev, args):
+    """The batch-1 decode GEMV on one long matrix per format (16384 x 16384,
+    143-285 MB: a launch long enough for its steady rate to show), against a
+    plain read of the same bytes."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    sink = torch.empty(64, dtype=torch.uint8, device="cuda")
+    res = {}
+    R = C = 16384
+    for name, sem, qt in (("Q4_K", K.Q4_K_GGML, W.QT_Q4_K), ("Q6_K", K.Q6_K_SEQ, W.QT_Q6_K),
+                          ("Q8_0", K.Q8_0, W.QT_Q8_0), ("MXFP4", K.MXFP4, W.QT_MXFP4)):
+        raw = W.gen_weights_torch(gen, qt, R, C)
+        nbytes = raw.numel()
+        packed = dev.pack(sem, raw, R, C)
+        del raw
+        x = torch.randn(1, C, device="cuda")
+        o = torch.empty(1, R, device="cuda")
+        ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o), max(5, args.steps), args.warmup)
+        rd = time_region(torch, lambda: dev.so.mllm_read_probe(packed.data_ptr(), packed.numel() // 16 * 16,
+                                                                sink.data_ptr(), dev._stream()),
+                         max(5, args.steps), args.warmup)
+        gbs = (nbytes + 4 * (R + C)) / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "plain_read_us": round(rd * 1e3, 1), "frac_of_plain_read": round(rd / ms, 3),
+                     "MB": round(nbytes / 1e6, 1)}
+        log(f"long GEMV {name} {R}x{C} B=1: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); "
+            f"plain read {rd * 1e3:.1f} us")
+        del packed
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_q8(torch, dev, args):
     """Q8_0 GEMV 5632x2048 B=1 rotated over 24 copies (295 MB)."""
     sink = torch.empty(64, dtype=torch.uint8, device="cuda")
@@ -848,6 +880,7 @@ def main():
     extra = {}
     if not args.no_extra:
         extra["configs0_q8_0_gemv"] = bench_q8(torch, dev, args)
+        extra["long_gemv_b1"] = bench_long_gemv(torch, dev, args)
         extra["configs2_prefill_gemm"] = bench_prefill(torch, dev, args)
         extra["configs3_gptoss_moe"] = bench_moe(torch, dev, args, "gptoss")
         extra["configs4_qwen3_moe"] = bench_moe(torch, dev, args, "qwen3")

@@ -270,7 +270,7 @@ long mllm_d16_bytes(int n_rows, int n_cols) { return (long)n_rows * n_cols * 2; 
 int mllm_d16_make(int sem, const mllm_packed &W, int n_rows, int n_cols, void *w16, hipStream_t st, std::string &err)
 {
     const long n = (long)n_rows * n_cols;
-    if (n <= 0 || n_cols % 32) { err = "n_cols must be a positive multiple of the block size"; return -1; }
+    if (n <= 0 || n_cols % 4) { err = "n_cols must be a positive multiple of 4"; return -1; }
     float *tmp = nullptr;
     int *bad = nullptr;
     int bad_h = 0;
@@ -280,7 +280,9 @@ int mllm_d16_make(int sem, const mllm_packed &W, int n_rows, int n_cols, void *w
         return -1;
     }
     int rc = -1;
-    if (hipMemsetAsync(bad, 0, 4, st) != hipSuccess) err = "hipMemsetAsync failed";
+    // columns past the last whole block stay zero (the reference ignores a ragged tail)
+    if (hipMemsetAsync(bad, 0, 4, st) != hipSuccess || hipMemsetAsync(tmp, 0, n * 4, st) != hipSuccess)
+        err = "hipMemsetAsync failed";
     else if (mllm_launch_dequant(sem, W, n_rows, n_cols, tmp, st) != 0) err = "semantic has no fp32 weight form";
     else {
         const long n4 = n / 4;

@@ -136,6 +136,24 @@ def test_gemm16_strided(dev, orc):
     assert O.norm_err(o[:, :R], ref) < D16_TOL
 
 
+@pytest.mark.parametrize("qt,sem,C", [(12, K.Q4_K_GGML, 2048 + 32), (39, K.MXFP4, 800 + 4)])
+def test_gemm16_ragged_columns(dev, orc, qt, sem, C):
+    """Columns past the last whole block contribute nothing, as in the reference."""
+    import torch
+    rng = np.random.default_rng(1806 + qt)
+    R, M = 80, 20
+    be, bb = W.BLOCK[qt]
+    nb = C // be
+    w = W.gen_weights(rng, qt, R, nb * be)   # whole blocks only: the ragged tail has no bytes
+    x = W.gen_x(rng, M, C)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    w16 = dev.dense16(sem, packed, R, C)
+    assert np.all(w16.cpu().numpy()[:, nb * be:] == 0)
+    got = gemm(dev, w16, x, R, C)
+    ref = orc.gemv(sem, w, np.ascontiguousarray(x[:, :nb * be]), R, nb * be, M)
+    assert O.norm_err(got, ref) < D16_TOL
+
+
 def test_gemm16_nonfinite_activations(dev, orc):
     """inf / NaN activations give the oracle's inf / NaN outputs; the scale
     ignores them, so the other tokens keep their precision."""

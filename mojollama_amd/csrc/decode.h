@@ -197,7 +197,7 @@ template <int SEM, bool SIGNED_Q8 = false>
 MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
 {
     constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
-    const int blk = c / CPB, cc = c % CPB;
+    const int blk = (int)((unsigned)c / CPB), cc = (int)((unsigned)c % CPB);   // c >= 0
     const uint32_t A[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
     const uint32_t L4 = 0x0F0F0F0Fu;
     k.o0 = k.o1 = 0.0f;

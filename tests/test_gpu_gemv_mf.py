@@ -178,3 +178,63 @@ def test_mfma_block32_fused(dev, orc, sem, R, C, mode, B):
     else:
         ref = y
     check(f"{K.SEM_NAMES[sem]} {R}x{C} B={B} {mode}", got, ref)
+
+
+@pytest.mark.parametrize("B", [4, 8])
+def test_mfma_split_arrival_graph_replay(dev, orc, B):
+    """K split over workgroups (the o and down projections at these shapes,
+    their partials added by the reduction launch) and the unsplit paired
+    gate/up sharing one workspace that starts as garbage, captured once in a
+    graph and replayed with new activations written eagerly between replays:
+    every replay equals the eager calls bit for bit, and the eager o
+    projection matches the oracle."""
+    import ctypes
+    import torch
+    rng = np.random.default_rng(77 + B)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    w_o = W.gen_weights(rng, W.QT_Q4_K, 2048, 2048)
+    w_gu = W.gen_weights(rng, W.QT_Q4_K, 2 * 5632, 2048)
+    w_d = W.gen_weights(rng, W.QT_Q6_K, 2048, 5632)
+    p_o = dev.pack(K.Q4_K_GGML, cu(w_o), 2048, 2048)
+    p_gu = dev.pack(K.Q4_K_GGML, cu(w_gu), 2 * 5632, 2048)
+    p_d = dev.pack(K.Q6_K_SEQ, cu(w_d), 2048, 5632)
+    g = cu((rng.standard_normal(2048) * 0.5 + 1.0).astype(np.float32))
+    f_o, f_d = dev.fusion(), dev.fusion()
+    f_gu = dev.fusion(rms_w=g, rms_eps=1e-5, silu_pair=True, silu_clamp=False)
+    n = max(dev.so.mllm_gemv_fused_workspace_size(K.Q4_K_GGML, 2048, 2048, B, ctypes.byref(f_o)),
+            dev.so.mllm_gemv_fused_workspace_size(K.Q4_K_GGML, 5632, 2048, B, ctypes.byref(f_gu)),
+            dev.so.mllm_gemv_fused_workspace_size(K.Q6_K_SEQ, 2048, 5632, B, ctypes.byref(f_d)), 256)
+    ws = torch.full((n,), 0xA5, dtype=torch.uint8, device="cuda")
+    x = cu(W.gen_x(rng, B, 2048))
+    y_o = torch.empty(B, 2048, device="cuda")
+    h = torch.empty(B, 5632, device="cuda")
+    y_d = torch.empty(B, 2048, device="cuda")
+
+    def run():
+        dev.gemv_fused(K.Q4_K_GGML, p_o, x, 2048, 2048, f_o, out=y_o, ws=ws)
+        dev.gemv_fused(K.Q4_K_GGML, p_gu, y_o, 5632, 2048, f_gu, out=h, ws=ws)
+        dev.gemv_fused(K.Q6_K_SEQ, p_d, h, 2048, 5632, f_d, out=y_d, ws=ws)
+
+    run()
+    torch.cuda.synchronize()
+    check(f"o {2048}x{2048} B={B} split", y_o.cpu().numpy(), orc.gemv(K.Q4_K_GGML, w_o, x.cpu().numpy(), 2048, 2048, B))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for i in range(4):
+        x.copy_(cu(W.gen_x(rng, B, 2048)))
+        run()
+        torch.cuda.synchronize()
+        want = [t.clone() for t in (y_o, h, y_d)]
+        for t in (y_o, h, y_d):
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("o", "gate_up", "down"), (y_o, h, y_d), want):
+            assert torch.equal(got, ref), f"replay {i} {name}"

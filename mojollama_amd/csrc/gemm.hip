@@ -62,18 +62,23 @@ template <int SEM, int XM> struct gemm_cfg {
 // (measured on the MoE layers at T = 1280: GPT-OSS MXFP4 gate+up 1272 -> 1217
 // us per layer decoded, 1098 -> 964 us over bf16 copies; Qwen3's Q4_K x Q8_0
 // unchanged).
-template <int SEM, int XM, bool DUAL, bool DW> constexpr bool wide_tile()
+// Tile kinds: 0 the default; 1 wide (above); 2 narrow: 64 rows of two-plane
+// weights against 64-entry tiles (the grouped expert GEMMs), 2 x 2 waves
+// (Qwen3's Q6_K down at T = 1280: 745 -> 664 us per layer; the 128-entry
+// dense prefill tiles keep 128 rows, measured faster there).
+template <int SEM, int XM, bool DUAL, bool DW, int TM> constexpr int tile_kind()
 {
-    return DW || (DUAL && gemm_cfg<SEM, XM>::NA == 1);
+    if (!DUAL && TM == 64 && gemm_cfg<SEM, XM>::NA == 2) return 2;
+    return (DW || (DUAL && gemm_cfg<SEM, XM>::NA == 1)) ? 1 : 0;
 }
 
 // Tile of TN weight rows x TM_ entries; 4 waves in a WR x WE grid, each owning
 // IT x JT MFMA 16x16 outputs.
 // WIDE: 128 weight rows also for the fused gate+up tiles (each matrix's tile
 // one bf16 plane: its LDS still admits two workgroups per CU), waves 2 x 2.
-template <bool DUAL, int TM_, bool WIDE> struct tile_cfg {
-    static constexpr int TN = (DUAL && !WIDE) ? 64 : 128;
-    static constexpr int WR = (TN == 128 && TM_ == 64 && !WIDE) ? 4 : 2;
+template <bool DUAL, int TM_, int KIND> struct tile_cfg {
+    static constexpr int TN = (KIND == 2 || (DUAL && KIND == 0)) ? 64 : 128;
+    static constexpr int WR = (TN == 128 && TM_ == 64 && KIND == 0) ? 4 : 2;
     static constexpr int WE = 4 / WR;
     static constexpr int IT = TN / WR / 16;
     static constexpr int JT = TM_ / WE / 16;
@@ -465,13 +470,12 @@ MLLM_DEV void put_a(const araw<TM_, gemm_cfg<SEM, XM>::NB> &ar, int n_ent, int k
 template <int SEM, int XM, bool DUAL, int TM, bool DW = false> constexpr int qgemm_wgs_per_cu()
 {
     using C = gemm_cfg<SEM, XM>;
-    constexpr int TN = tile_cfg<DUAL, TM, wide_tile<SEM, XM, DUAL, DW>()>::TN;
+    constexpr int TN = tile_cfg<DUAL, TM, tile_kind<SEM, XM, DUAL, DW, TM>()>::TN;
     // fused gate+up tiles are sized with padded rows (KE + 8 columns): their
     // unpadded tiles would admit a third workgroup whose register budget spills
     constexpr int RW = DUAL ? C::KE + 8 : C::LDA;
     constexpr int lds = 2 * (C::NA * TN * RW * (DUAL ? 2 : 1) + C::NB * TM * RW) + 4 * TM + 4 * 3 * TN + 8 * TM + 64;
-    // (two-plane dense-weight tiles: their copied planes' registers do not fit a third either)
-    constexpr int cap = (XM == XM_Q8D || (DW && C::NA == 2)) ? 2 : 3;
+    constexpr int cap = XM == XM_Q8D ? 2 : 3;
     constexpr int n = 163840 / lds;
     return n < 1 ? 1 : n > cap ? cap : n;
 }
@@ -480,7 +484,7 @@ template <int SEM, int XM, bool DUAL, int TM, bool DW>
 __global__ __launch_bounds__(256, (qgemm_wgs_per_cu<SEM, XM, DUAL, TM, DW>())) void k_qgemm(qgemm_args a)
 {
     using C = gemm_cfg<SEM, XM>;
-    using G = tile_cfg<DUAL, TM, wide_tile<SEM, XM, DUAL, DW>()>;
+    using G = tile_cfg<DUAL, TM, tile_kind<SEM, XM, DUAL, DW, TM>()>;
     constexpr int NA = C::NA, NB = C::NB, LDA = C::LDA, KE = C::KE, KS = C::KS, MAXT = C::MAXT;
     // 128 weight rows per tile; 64 when gate and up share a tile of two-plane weights (LDS budget)
     constexpr int TN = G::TN, IT = G::IT, JT = G::JT;
@@ -763,7 +767,7 @@ __global__ void k_ksum(const float *__restrict__ part, int ks, long plane, int n
 template <int SEM, int XM, bool DUAL, int TM, bool DW = false>
 hipError_t launch(const qgemm_args &a, int max_tiles, hipStream_t st)
 {
-    constexpr int TN = tile_cfg<DUAL, TM, wide_tile<SEM, XM, DUAL, DW>()>::TN;
+    constexpr int TN = tile_cfg<DUAL, TM, tile_kind<SEM, XM, DUAL, DW, TM>()>::TN;
     const int ks = (a.ksplit > 1 && !DUAL && !a.tile_expert && !a.out_row) ? a.ksplit : 1;
     dim3 grid((a.n_rows + TN - 1) / TN, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
     if (grid.y == 0) return hipSuccess;
@@ -901,9 +905,9 @@ hipError_t mllm_launch_act_split(const float *x, int ldx, int rows, int K, int n
 
 // bf16 planes of a packed matrix for the GEMM's dense-weight tiles; 0: not
 // offered for this semantic.  Offered for the MXFP4 forms (one exact plane).
-// Two-plane copies (the Q6_K / Q4_0 expert forms) ran no faster: Qwen3's Q6_K
-// down over them measured 714.6 -> 708.5 us per layer, the copied planes'
-// registers leaving two workgroups per CU instead of three.
+// Two-plane copies (the Q6_K / Q4_0 expert forms) ran no faster than the
+// decoding narrow tiles: Qwen3's Q6_K down layer 677 us over them, 664 us
+// decoded.
 int mllm_dense_planes(int sem)
 {
     return (sem == SEM_MXFP4 || sem == SEM_MXFP4_Q8) ? gemm_cfg<SEM_MXFP4, XM_PLANES>::NA : 0;

@@ -125,18 +125,26 @@ struct dev_buf {
 
 struct host_buf {
     void *p = nullptr;
+    void *dp = nullptr;   // the same memory as a device address (kernels write it over PCIe), or null
     size_t n = 0;
     int ensure(size_t bytes)
     {
         if (bytes <= n) return 0;
         if (p) (void)hipHostFree(p);
-        p = nullptr; n = 0;
+        p = dp = nullptr; n = 0;
         size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
         if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) { p = nullptr; return -1; }
+        if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess) dp = nullptr;
         n = want;
         return 0;
     }
 };
+
+// Drop-in results up to this size are written by the kernels straight into the
+// pinned staging buffer (posted PCIe writes) instead of device memory plus a
+// device-to-host copy: one DMA transfer fewer per call (Q8_0 5632x2048 B=1:
+// ~31 -> ~19 us per quant_matmul_omp call on MI355X).
+constexpr size_t kDirectOutMax = 256u << 10;
 
 // Per-thread state: stream plus staging/scratch buffers.  Freed only at
 // process end (a thread's buffers are reused by its later calls).
@@ -163,13 +171,14 @@ thread_local thread_ctx t_ctx;
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Weight cache: (host pointer, layout, rows, cols) -> packed device copy.
+// Weight cache: (host pointer, layout, rows, cols, host row stride) -> packed device copy.
 struct wkey {
     const void *host;
     int ly, rows, cols;
+    long stride;   // 0: rows are contiguous
     bool operator<(const wkey &o) const
     {
-        return std::tie(host, ly, rows, cols) < std::tie(o.host, o.ly, o.rows, o.cols);
+        return std::tie(host, ly, rows, cols, stride) < std::tie(o.host, o.ly, o.rows, o.cols, o.stride);
     }
 };
 struct wentry {
@@ -213,11 +222,19 @@ std::shared_mutex g_api_mu;
 // Upload + pack a raw host matrix (once).  Returns its packed view and, with
 // scale_flags, the scale scan of the packed copy (mllm_launch_scale_scan, any
 // semantic of the layout: the flags depend on the bytes only).
-int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view, int *scale_flags = nullptr)
+//
+// row_stride (bytes, 0 = contiguous rows): row r of the matrix starts at
+// host + r * row_stride and holds raw_row_bytes(ly, cols) bytes; the rows are
+// gathered on the host before the upload (moe_forward_omp's Q5_0 down rows).
+int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view, int *scale_flags = nullptr,
+               long row_stride = 0)
 {
-    wkey k{host, ly, rows, cols};
-    const long raw = raw_row_bytes(ly, cols) * rows;
-    const uint64_t fpr = fingerprint(host, raw);
+    const long rrb = raw_row_bytes(ly, cols);
+    if (row_stride == rrb) row_stride = 0;
+    wkey k{host, ly, rows, cols, row_stride};
+    const long raw = rrb * rows;
+    const long span = row_stride && rows > 0 ? (long)(rows - 1) * row_stride + rrb : raw;
+    const uint64_t fpr = fingerprint(host, span);
     {
         std::lock_guard<std::mutex> lk(g_cache_mu);
         auto it = g_cache.find(k);
@@ -245,7 +262,15 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view, 
         const int sem_any = ly == LY_MXFP4 ? SEM_MXFP4 : ly == LY_Q6_K ? SEM_Q6_K_GGML : ly == LY_Q4_K ? SEM_Q4_K_GGML
                           : ly == LY_Q5_K_GGML ? SEM_Q5_K_GGML : ly == LY_Q5_K_CE ? SEM_Q5_K_CE : ly == LY_Q8_0 ? SEM_Q8_0
                           : ly == LY_Q4_0 ? SEM_Q4_0 : ly == LY_Q4_1 ? SEM_Q4_1 : ly == LY_Q5_0 ? SEM_Q5_0_F32 : SEM_F32;
-        hipError_t r = hipMemcpyAsync(tmp, host, raw, hipMemcpyHostToDevice, c.st);
+        std::vector<uint8_t> gathered;
+        const void *src = host;
+        if (row_stride) {
+            gathered.resize((size_t)raw);
+            for (int r = 0; r < rows; r++)
+                memcpy(gathered.data() + (size_t)r * rrb, (const uint8_t *)host + (size_t)r * row_stride, (size_t)rrb);
+            src = gathered.data();
+        }
+        hipError_t r = hipMemcpyAsync(tmp, src, raw, hipMemcpyHostToDevice, c.st);
         if (r == hipSuccess) r = mllm_launch_pack(ly, tmp, e.dev, rows, cols, c.st);
         if (r == hipSuccess) r = mllm_launch_fill((float *)fl, 1, 0.0f, c.st);
         if (r == hipSuccess) r = mllm_launch_scale_scan(nullptr, &e.view, 1, sem_any, rows, cols, fl, c.st);
@@ -545,10 +570,12 @@ int host_gemv(int sem, const uint8_t *W, const float *x, float *out, int n_rows,
     }
     memcpy(c.h_in.p, x, xbytes);
     HIP_OK(hipMemcpyAsync(c.d_in.p, c.h_in.p, xbytes, hipMemcpyHostToDevice, c.st));
-    if (run_gemv(sem, view, (const float *)c.d_in.p, (float *)c.d_out.p, n_rows, n_cols, B, c.d_scr.p, c.st, nullptr,
-                 !mllm_scales_need_gemv(sem, scale_flags)))
+    // B <= 8 runs the GEMV kernels, which write each output once: straight into the pinned buffer
+    const bool direct = B <= 8 && obytes <= kDirectOutMax && c.h_out.dp;
+    if (run_gemv(sem, view, (const float *)c.d_in.p, (float *)(direct ? c.h_out.dp : c.d_out.p), n_rows, n_cols, B,
+                 c.d_scr.p, c.st, nullptr, !mllm_scales_need_gemv(sem, scale_flags)))
         return -1;
-    HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
+    if (!direct) HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
     HIP_OK(hipStreamSynchronize(c.st));
     memcpy(out, c.h_out.p, obytes);
     return 0;
@@ -575,6 +602,7 @@ int host_multi_gemv(const int *sems, const uint8_t *const *Ws, float *const *out
     }
     memcpy(c.h_in.p, x, xbytes);
     HIP_OK(hipMemcpyAsync(c.d_in.p, c.h_in.p, xbytes, hipMemcpyHostToDevice, c.st));
+    const bool direct = obytes <= kDirectOutMax && c.h_out.dp;   // B = 1: GEMV kernels write the pinned buffer
     long at = 0;
     for (int i = 0; i < n;) {
         if (sems[i] < 0 || rows[i] <= 0) { i++; continue; }
@@ -586,12 +614,13 @@ int host_multi_gemv(const int *sems, const uint8_t *const *Ws, float *const *out
         if (j - i == 1 ? get_weight(Ws[i], mllm_sem_layout(sems[i]), rows[i], n_cols, view)
                        : get_weight_concat(Ws + i, rows + i, j - i, mllm_sem_layout(sems[i]), n_cols, view))
             return -1;
-        if (run_gemv(sems[i], view, (const float *)c.d_in.p, (float *)c.d_out.p + at, grp_rows, n_cols, 1, nullptr, c.st))
+        if (run_gemv(sems[i], view, (const float *)c.d_in.p, (float *)(direct ? c.h_out.dp : c.d_out.p) + at, grp_rows,
+                     n_cols, 1, nullptr, c.st))
             return -1;
         at += grp_rows;
         i = j;
     }
-    HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
+    if (!direct) HIP_OK(hipMemcpyAsync(c.h_out.p, c.d_out.p, obytes, hipMemcpyDeviceToHost, c.st));
     HIP_OK(hipStreamSynchronize(c.st));
     at = 0;
     for (int i = 0; i < n; i++) {
@@ -778,6 +807,16 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         set_error("moe_forward_omp: MXFP4 down projection needs prealloc_q8 (the reference dereferences NULL); down treated as zero");
         sd = -1;
     }
+    // Q5_0 down rows start row * ((n_embd+31)/32)*22 bytes in (QK:2216, 2230): a
+    // stride from n_embd, not from the n_ff-wide rows.  Followed where every row
+    // stays inside the n_embd x n_ff matrix (n_embd < n_ff); where the reference
+    // reads past the matrix (n_embd > n_ff) the matrix's own rows are used.
+    long q5_stride = 0;
+    if (qt_down == 6 && n_ff_expert > 0) {
+        const long s_ref = (long)((n_embd + 31) / 32) * 22, s_own = (long)((n_ff_expert + 31) / 32) * 22;
+        if (s_ref != s_own && (long)(n_embd - 1) * s_ref + (long)(n_ff_expert / 32) * 22 <= (long)n_embd * s_own)
+            q5_stride = s_ref;
+    }
     // slots with a negative expert id (left empty by a routing) add nothing and are dropped;
     // the remaining slots keep their order, so the k-order combine is unchanged
     std::vector<int> sel;
@@ -792,7 +831,7 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         const int e = sel[k];
         if (sg >= 0 && get_weight(gate_raw[e], mllm_sem_layout(sg), F, N, tab[k])) return;
         if (su >= 0 && get_weight(up_raw[e], mllm_sem_layout(su), F, N, tab[K + k])) return;
-        if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k])) return;
+        if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k], nullptr, q5_stride)) return;
     }
     // device scratch: x | g[K][F] | u[K][F] | h[K][F] | dn[K][N] | w[K]
     size_t o_x = 0, o_g = align256(o_x + N * 4), o_u = align256(o_g + (size_t)K * F * 4),
@@ -812,6 +851,9 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
     memcpy(hin + N * 4 + K * 4, tab.data(), tab.size() * sizeof(mllm_packed));
     mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
     hipStream_t st = c.st;
+    // the combine writes its N outputs straight into the pinned buffer (dx is read by the GEMVs before it)
+    const bool direct = (size_t)N * 4 <= kDirectOutMax && c.h_out.dp;
+    float *cdst = direct ? (float *)c.h_out.dp : dx;
 #define CK(expr) do { if ((expr) != hipSuccess) { set_error("moe_forward_omp: %s failed", #expr); return; } } while (0)
     CK(hipMemcpyAsync(dx, hin, N * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(dw, hin + N * 4, K * 4, hipMemcpyHostToDevice, st));
@@ -832,8 +874,8 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         b.out = ddn; b.out_job_stride = N; b.ldo = N;
         b.n_rows = N; b.n_cols = F; b.B = 1;
         CK(mllm_launch_gemv(sd, b, K, st));
-        CK(mllm_launch_combine(ddn, dw, nullptr, 1, K, N, dx, 0, st));
-        CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
+        CK(mllm_launch_combine(ddn, dw, nullptr, 1, K, N, cdst, 0, st));
+        if (!direct) CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
         CK(hipStreamSynchronize(st));
         memcpy(combined, c.h_out.p, N * 4);
         return;
@@ -861,8 +903,8 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         }
         CK(mllm_launch_gemv(sd, b, K, st));
     }
-    CK(mllm_launch_combine(sd >= 0 ? ddn : nullptr, dw, nullptr, 1, K, N, dx, 0, st));
-    CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
+    CK(mllm_launch_combine(sd >= 0 ? ddn : nullptr, dw, nullptr, 1, K, N, cdst, 0, st));
+    if (!direct) CK(hipMemcpyAsync(c.h_out.p, dx, N * 4, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
 #undef CK
     memcpy(combined, c.h_out.p, N * 4);

@@ -585,6 +585,18 @@ void orc_moe_ffn_token(const float *router_w, const uint8_t *gate, const uint8_t
     free(g); free(u); free(dn);
 }
 
+/* Row stride in bytes of moe_forward_omp's Q5_0 down projection when it
+ * differs from the matrix's own and every row it addresses lies inside the
+ * n_embd x n_ff matrix (QK:2216, 2230: row * ((n_embd+31)/32)*22); else 0. */
+long orc_moe_q5_down_stride(int qt_down, int n_embd, int n_ff)
+{
+    if (qt_down != ORC_QT_Q5_0 || n_embd <= 0 || n_ff <= 0) return 0;
+    const long s_ref = (long)((n_embd + 31) / 32) * 22, s_own = (long)((n_ff + 31) / 32) * 22;
+    if (s_ref == s_own) return 0;
+    const long last = (long)(n_embd - 1) * s_ref + (long)(n_ff / 32) * 22;
+    return last <= (long)n_embd * s_own ? s_ref : 0;
+}
+
 void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
                            const uint8_t *const *down, const float *x, int n_ff, int n_embd,
                            int qt_gate, int qt_up, int qt_down, const int *top_idx,
@@ -598,6 +610,11 @@ void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
     int su = pair_mx ? ORC_MXFP4 : orc_sem_for(3, qt_up);
     int sd = orc_sem_for(4, qt_down);
     if (qt_down == 39 && !has_q8_scratch) sd = -1;   /* reference dereferences NULL here */
+    /* Q5_0 down rows (QK:2216, 2230) start row * ((n_embd+31)/32)*22 bytes in,
+     * a stride taken from n_embd, not from the n_ff-wide rows; followed where
+     * every row stays inside the n_embd x n_ff matrix (n_embd < n_ff), else the
+     * reference reads past it and the matrix's own row stride is used. */
+    const long q5_stride = orc_moe_q5_down_stride(qt_down, n_embd, n_ff);
     for (int i = 0; i < n_embd; i++) out[i] = 0.0f;   /* QK:2192 */
     for (int k = 0; k < top_k; k++) {
         int e = top_idx[k];
@@ -609,7 +626,10 @@ void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
             if (gv > 80.0f) gv = 80.0f;
             g[i] = (gv / (1.0f + expf(-gv))) * u[i];
         }
-        if (sd >= 0) orc_gemv(sd, down[e], g, dn, n_embd, n_ff, 1); else memset(dn, 0, sizeof(float) * n_embd);
+        if (sd >= 0 && q5_stride)
+            for (int r = 0; r < n_embd; r++) orc_gemv(sd, down[e] + (long)r * q5_stride, g, dn + r, 1, n_ff, 1);
+        else if (sd >= 0) orc_gemv(sd, down[e], g, dn, n_embd, n_ff, 1);
+        else memset(dn, 0, sizeof(float) * n_embd);
         for (int i = 0; i < n_embd; i++) out[i] += top_w[k] * dn[i];   /* atomic add, k order here */
     }
     free(g); free(u); free(dn);

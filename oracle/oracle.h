@@ -84,6 +84,10 @@ void orc_moe_ffn_token(const float *router_w, const uint8_t *gate, const uint8_t
                        const uint8_t *down, int qt_gate, int qt_up, int qt_down,
                        int N, int E, int K, int M, const float *x, float *out);
 
+/* moe_forward_omp's Q5_0 down row stride (QK:2216, 2230: taken from n_embd)
+ * where it differs from the matrix's own and stays inside the matrix, else 0. */
+long orc_moe_q5_down_stride(int qt_down, int n_embd, int n_ff);
+
 /* moe_forward_omp QK:2066-2250 for one token, caller-supplied routing.
  * gate/up/down are per-expert pointer arrays.  has_q8_scratch mirrors the
  * prealloc_q8 != NULL condition of QK:2167,2194. combine in k order. */

@@ -3,7 +3,7 @@
 oracle/Makefile) on small seeded inputs.
 
 Usage:  python tests/golden/make_golden.py [group]   (from the repo root;
-        group = gen_requant or gen_nonfinite writes that group only)
+        group = gen_requant, gen_nonfinite or gen_q5_down writes that group only)
 
 Outputs (committed): tests/golden/*.npz.  Each file holds the inputs and the
 reference's outputs, so the tests need neither the reference tree nor
@@ -146,6 +146,26 @@ def gen_nonfinite(ref):
                             n_embd=n_embd, n_ff=n_ff, qts=np.array(qts))
 
 
+def gen_q5_down(ref):
+    """moe_forward_omp with a Q5_0 down projection where n_embd != n_ff: the
+    reference addresses down row r at r * ((n_embd+31)/32)*22 bytes (QK:2216,
+    2230), a stride from n_embd; n_embd < n_ff keeps every row it reads inside
+    the n_embd x n_ff matrix (its rows then overlap)."""
+    rng = np.random.default_rng(74)
+    for tag, qts, n_embd, n_ff in (("q5down", (12, 12, 6), 256, 288), ("q5down_all", (6, 6, 6), 96, 320)):
+        E = 3
+        gates = [W.gen_weights(rng, qts[0], n_ff, n_embd) for _ in range(E)]
+        ups = [W.gen_weights(rng, qts[1], n_ff, n_embd) for _ in range(E)]
+        downs = [W.gen_weights(rng, qts[2], n_embd, n_ff) for _ in range(E)]
+        x = W.gen_x(rng, 1, n_embd)[0]
+        ti = np.array([2, 0, 1], np.int32)
+        tw = np.array([0.5, 0.3, 0.2], np.float32)
+        out = ref.moe_forward(gates, ups, downs, x, n_ff, n_embd, qts, ti, tw)
+        np.savez_compressed(os.path.join(OUT, f"moe_forward_{tag}.npz"), gates=np.stack(gates), ups=np.stack(ups),
+                            downs=np.stack(downs), x=x, top_idx=ti, top_w=tw, out=out,
+                            n_embd=n_embd, n_ff=n_ff, qts=np.array(qts))
+
+
 def main():
     ref = RefLib()
     ref.so.set_num_threads(1)
@@ -267,6 +287,7 @@ def main():
                             crc=crc(router, xs), sel=sel, ffn=ffn)
     gen_requant(ref)
     gen_nonfinite(ref)
+    gen_q5_down(ref)
     print("golden vectors written to", OUT)
 
 

@@ -110,8 +110,10 @@ def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm, T, slices):
     assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
 
 
-@pytest.mark.parametrize("tag", ["qwen", "gptoss"])
+@pytest.mark.parametrize("tag", ["qwen", "gptoss", "q5down", "q5down_all"])
 def test_golden_moe_forward(lib, golden, tag):
+    """q5down*: a Q5_0 down projection with n_embd < n_ff, whose rows the
+    reference addresses with a stride from n_embd (QK:2216, 2230)."""
     g = golden(f"moe_forward_{tag}.npz")
     got = moe_forward(lib, list(g["gates"]), list(g["ups"]), list(g["downs"]), g["x"], int(g["n_ff"]),
                       int(g["n_embd"]), tuple(int(v) for v in g["qts"]), g["top_idx"], g["top_w"])

@@ -107,13 +107,33 @@ def test_golden_moe_forward_nonfinite(orc, golden, tag):
         assert same_nonfinite(got, out, TOL)
 
 
-@pytest.mark.parametrize("tag", ["qwen", "gptoss"])
+@pytest.mark.parametrize("tag", ["qwen", "gptoss", "q5down", "q5down_all"])
 def test_golden_moe_forward(orc, golden, tag):
     g = golden(f"moe_forward_{tag}.npz")
     got = orc.moe_forward_token(list(g["gates"]), list(g["ups"]), list(g["downs"]), g["x"],
                                 int(g["n_ff"]), int(g["n_embd"]), tuple(int(v) for v in g["qts"]),
                                 g["top_idx"], g["top_w"])
     assert O.norm_err(got, g["out"]) < 1e-4
+
+
+@pytest.mark.parametrize("tag", ["q5down", "q5down_all"])
+def test_golden_moe_forward_q5_down_stride_matters(orc, golden, tag):
+    """The Q5_0 down fixtures pin the reference's row stride: the same token
+    through down matrices read with their own (contiguous) row stride misses
+    the reference's output by far more than the tolerance."""
+    g = golden(f"moe_forward_{tag}.npz")
+    N, F = int(g["n_embd"]), int(g["n_ff"])
+    qg, qu, qd = (int(v) for v in g["qts"])
+    assert qd == 6 and N < F
+    x = g["x"]
+    naive = np.zeros(N, np.float32)
+    for e, wk in zip(g["top_idx"], g["top_w"]):
+        gv = orc.gemv(orc.sem_for(3, qg), g["gates"][e], x[None], F, N, 1)[0]
+        uv = orc.gemv(orc.sem_for(3, qu), g["ups"][e], x[None], F, N, 1)[0]
+        gc = np.clip(gv, -80, 80)
+        h = (gc / (1 + np.exp(-gc)) * uv).astype(np.float32)
+        naive += wk * orc.gemv(orc.sem_for(4, qd), g["downs"][e], h[None], N, F, 1)[0]
+    assert O.norm_err(naive, g["out"]) > 0.1
 
 
 @pytest.mark.parametrize("tag", ["q4k", "mxfp4"])

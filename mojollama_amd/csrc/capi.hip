@@ -834,11 +834,13 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
         if (sd >= 0 && get_weight(down_raw[e], mllm_sem_layout(sd), N, F, tab[2 * K + k], nullptr, q5_stride)) return;
     }
     // device scratch: x | g[K][F] | u[K][F] | h[K][F] | dn[K][N] | w[K]
-    size_t o_x = 0, o_g = align256(o_x + N * 4), o_u = align256(o_g + (size_t)K * F * 4),
-           o_h = align256(o_u + (size_t)K * F * 4), o_dn = align256(o_h + (size_t)K * F * 4),
-           o_w = align256(o_dn + (size_t)K * N * 4), total = align256(o_w + K * 4);
-    if (c.d_scr.ensure(total) || c.d_tab.ensure(tab.size() * sizeof(mllm_packed)) ||
-        c.h_in.ensure(N * 4 + K * 4 + tab.size() * sizeof(mllm_packed)) || c.h_out.ensure(N * 4)) {
+    // device scratch: tab | x | w (one upload from the same layout in the pinned buffer) | g[K][F] | u[K][F] |
+    // h[K][F] | dn[K][N]; tables: [0,K) gate, [K,2K) up, [2K,3K) down
+    const size_t tab_b = tab.size() * sizeof(mllm_packed);
+    size_t o_x = align256(tab_b), o_w = o_x + (size_t)N * 4, in_b = o_w + (size_t)K * 4,
+           o_g = align256(in_b), o_u = align256(o_g + (size_t)K * F * 4), o_h = align256(o_u + (size_t)K * F * 4),
+           o_dn = align256(o_h + (size_t)K * F * 4), total = align256(o_dn + (size_t)K * N * 4);
+    if (c.d_scr.ensure(total) || c.h_in.ensure(in_b) || c.h_out.ensure(N * 4)) {
         set_error("moe_forward_omp: scratch allocation failed");
         return;
     }
@@ -846,18 +848,16 @@ MLLM_API void moe_forward_omp(const uint8_t **gate_raw, const uint8_t **up_raw, 
     float *dx = (float *)(S + o_x), *dg = (float *)(S + o_g), *du = (float *)(S + o_u), *dh = (float *)(S + o_h),
           *ddn = (float *)(S + o_dn), *dw = (float *)(S + o_w);
     uint8_t *hin = (uint8_t *)c.h_in.p;
-    memcpy(hin, x_norm, N * 4);
-    memcpy(hin + N * 4, selw.data(), K * 4);
-    memcpy(hin + N * 4 + K * 4, tab.data(), tab.size() * sizeof(mllm_packed));
-    mllm_packed *dtab = (mllm_packed *)c.d_tab.p;
+    memcpy(hin, tab.data(), tab_b);
+    memcpy(hin + o_x, x_norm, N * 4);
+    memcpy(hin + o_w, selw.data(), K * 4);
+    mllm_packed *dtab = (mllm_packed *)S;
     hipStream_t st = c.st;
     // the combine writes its N outputs straight into the pinned buffer (dx is read by the GEMVs before it)
     const bool direct = (size_t)N * 4 <= kDirectOutMax && c.h_out.dp;
     float *cdst = direct ? (float *)c.h_out.dp : dx;
 #define CK(expr) do { if ((expr) != hipSuccess) { set_error("moe_forward_omp: %s failed", #expr); return; } } while (0)
-    CK(hipMemcpyAsync(dx, hin, N * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(dw, hin + N * 4, K * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(dtab, hin + N * 4 + K * 4, tab.size() * sizeof(mllm_packed), hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(S, hin, in_b, hipMemcpyHostToDevice, st));
     // gate and up in one launch when their semantics agree; Q8_0 activations
     // quantised by the GEMV workgroups; silu(g) * u formed by the down
     // projection's staging (fp32 activations) or its quantisation (Q8_0)

@@ -272,6 +272,24 @@ def test_benchmark_shapes_batch_entry(lib, orc, name, R, C, qt, B):
     assert O.norm_err(got, ref) < GEMV_TOL
 
 
+@pytest.mark.parametrize("B,R", [(7, 9000), (8, 9000), (8, 8192)])
+def test_batch_entry_output_paths(lib, orc, B, R):
+    """The host-buffer entry points write results up to 256 KB straight into
+    pinned memory from the kernels and copy larger ones back from HBM: B = 7
+    (252 KB) and B = 8 at 8192 rows (256 KB) take the first path, B = 8 at
+    9000 rows (288 KB) the second; consecutive calls alternate the paths."""
+    rng = np.random.default_rng(1000 * B + R)
+    C = 2048
+    w = W.gen_weights(rng, 12, R, C)
+    x = W.gen_x(rng, B, C)
+    ref = orc.gemv(orc.sem_for(1, 12), w, x, R, C, B)
+    for _ in range(2):
+        got = bmm(lib, "q4_k", w, x, R, C, B)
+        assert O.norm_err(got, ref) < GEMV_TOL
+        small = bmm(lib, "q4_k", w[: 64 * (C // 256) * 144], x[:1], 64, C, 1)
+        assert O.norm_err(small, ref[0, :64]) < GEMV_TOL
+
+
 def test_q4k_q8_path_full_shape(lib, orc):
     """TurboEngine's Q4_K path (quant_matmul_omp -> dot_q4_k_q8_0) at the gate shape."""
     rng = np.random.default_rng(12)

@@ -3,7 +3,9 @@
 // The weights are dequantised once, with the reference's *_dequantize_row
 // arithmetic (QK:762-878: w = fl(s*q) + o), and rounded to fp16; each call
 // rounds its fp32 activations to fp16 under one power-of-two scale chosen
-// from the batch's largest finite element, and the product runs as a plain
+// from the batch's largest finite element (in one pass at scale 1, redone at
+// another scale only when that element falls outside [1/4, 2^15)), and the
+// product runs as a plain
 // GEMM on hipBLASLt (fp16 operands, fp32 accumulation and output, the scale
 // undone through its per-row device alpha).  The copy costs 2 bytes per weight in HBM (3.6x a
 // Q4_K matrix); in exchange the per-tile dequantisation leaves the prefill's
@@ -78,10 +80,18 @@ __device__ __forceinline__ uint2 pack_h4(float4 v, float sc)
                       (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16));
 }
 
-// Largest finite |x| per block over the M x K activations; each thread keeps
-// four 16-byte loads in flight (K is a multiple of 4).
-__global__ __launch_bounds__(256) void k_x16_amax(const float *__restrict__ x, int K, int ldx, long n4,
-                                                  float *__restrict__ part)
+// Largest finite |x| lands in [kScale1Lo, kScale1Hi): fp16(x) at scale 1 rounds
+// every element as fp16(x * 2^E) does at the scale below, except elements
+// under 2^-14 (fp16 subnormals at scale 1), which keep an absolute error under
+// 2^-25, below 2^-23 of the largest element; the one-pass conversion stands.
+constexpr float kScale1Lo = 0.25f, kScale1Hi = 32768.f;
+
+// x16 = fp16(x) (scale 1) and alpha = 1, with the largest finite |x| of each
+// block to part[]; each thread keeps four 16-byte loads in flight (K is a
+// multiple of 4).
+__global__ __launch_bounds__(256) void k_x16_cvt1(const float *__restrict__ x, int K, int ldx, long n4,
+                                                  float *__restrict__ part, uint2 *__restrict__ x16,
+                                                  float *__restrict__ alpha, int n_rows)
 {
     __shared__ float red[4];
     const long G = (long)gridDim.x * 256;
@@ -94,16 +104,26 @@ __global__ __launch_bounds__(256) void k_x16_amax(const float *__restrict__ x, i
 #pragma unroll
         for (int u = 0; u < 4; u++) v[u] = *(const float4 *)(x + x4_off(i + u * G, k4, ldx, flat));
 #pragma unroll
-        for (int u = 0; u < 4; u++) m = amax4(m, v[u]);
+        for (int u = 0; u < 4; u++) {
+            m = amax4(m, v[u]);
+            x16[i + u * G] = pack_h4(v[u], 1.f);
+        }
     }
-    for (; i < n4; i += G) m = amax4(m, *(const float4 *)(x + x4_off(i, k4, ldx, flat)));
+    for (; i < n4; i += G) {
+        const float4 v = *(const float4 *)(x + x4_off(i, k4, ldx, flat));
+        m = amax4(m, v);
+        x16[i] = pack_h4(v, 1.f);
+    }
+    for (long r = (long)blockIdx.x * 256 + threadIdx.x; r < n_rows; r += G) alpha[r] = 1.f;
     m = block_max(m, red);
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-// x16 = fp16(x * 2^E), E such that the largest finite |x| lands in [2^14, 2^15);
-// alpha[r] = 2^-E for the GEMM's n_rows output rows (its per-row device alpha).
-__global__ __launch_bounds__(256) void k_x16_cvt(const float *__restrict__ x, int K, int ldx, long n4,
+// Where the batch's largest finite |x| falls outside [kScale1Lo, kScale1Hi):
+// x16 = fp16(x * 2^E) again, E such that it lands in [2^14, 2^15), and
+// alpha[r] = 2^-E for the GEMM's n_rows output rows (its per-row device
+// alpha); otherwise every workgroup returns at once.
+__global__ __launch_bounds__(256) void k_x16_fix(const float *__restrict__ x, int K, int ldx, long n4,
                                                  const float *__restrict__ part, int n_part, uint2 *__restrict__ x16,
                                                  float *__restrict__ alpha, int n_rows)
 {
@@ -111,27 +131,17 @@ __global__ __launch_bounds__(256) void k_x16_cvt(const float *__restrict__ x, in
     const long G = (long)gridDim.x * 256;
     const int k4 = K / 4;
     const bool flat = ldx == K;
-    // this block's activations load while the partial maxima are reduced
-    long i = (long)blockIdx.x * 256 + threadIdx.x;
-    float4 v[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-        if (i + u * G < n4) v[u] = *(const float4 *)(x + x4_off(i + u * G, k4, ldx, flat));
     float m = 0.f;
     for (int j = threadIdx.x; j < n_part; j += 256) m = fmaxf(m, part[j]);
     m = block_max(m, red);
+    if (m == 0.f || (m >= kScale1Lo && m < kScale1Hi)) return;
     int e = 0;
-    if (m > 0.f) {
-        frexpf(m, &e);   // m < 2^e
-        e = 15 - e;
-    }
-    e = max(-120, min(120, e));
+    frexpf(m, &e);   // m < 2^e
+    e = max(-120, min(120, 15 - e));
     const float sc = ldexpf(1.f, e);
     for (long r = (long)blockIdx.x * 256 + threadIdx.x; r < n_rows; r += G) alpha[r] = ldexpf(1.f, -e);
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-        if (i + u * G < n4) x16[i + u * G] = pack_h4(v[u], sc);
-    for (i += 4 * G; i < n4; i += G) x16[i] = pack_h4(*(const float4 *)(x + x4_off(i, k4, ldx, flat)), sc);
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += G)
+        x16[i] = pack_h4(*(const float4 *)(x + x4_off(i, k4, ldx, flat)), sc);
 }
 
 constexpr int kAlgoCands = 8;   // heuristic candidates timed at plan time
@@ -325,9 +335,9 @@ int mllm_d16_gemm(const void *w16, const float *x, int ldx, int M, float *out, i
     void *bws = (uint8_t *)alpha + align256((size_t)n_rows * 4);
     const long n4 = (long)M * n_cols / 4;
     const int np = (int)std::min<long>(kPartMax, std::max<long>(1, (n4 + 1023) / 1024));
-    hipLaunchKernelGGL(k_x16_amax, dim3(np), dim3(256), 0, st, x, n_cols, ldx, n4, part);
+    hipLaunchKernelGGL(k_x16_cvt1, dim3(np), dim3(256), 0, st, x, n_cols, ldx, n4, part, x16, alpha, n_rows);
     const unsigned gc = (unsigned)std::min<long>((n4 + 1023) / 1024, 16L * device_cus_d16());
-    hipLaunchKernelGGL(k_x16_cvt, dim3(gc), dim3(256), 0, st, x, n_cols, ldx, n4, part, np, x16, alpha, n_rows);
+    hipLaunchKernelGGL(k_x16_fix, dim3(gc), dim3(256), 0, st, x, n_cols, ldx, n4, part, np, x16, alpha, n_rows);
     if (hipGetLastError() != hipSuccess) { err = "activation conversion launch failed"; return -1; }
     const hipblasLtHandle_t h = handle_for_current();
     if (p->chosen.load(std::memory_order_acquire) < 0) {

@@ -173,15 +173,21 @@ def test_gemm16_nonfinite_activations(dev, orc):
     assert O.norm_err(got[fin], ref[fin]) < D16_TOL
 
 
-def test_gemm16_tiny_activation_scale(dev, orc):
-    """Activations ~1e-30 (far below fp16's range unscaled) keep their precision."""
+@pytest.mark.parametrize("scale", [1e-30, 0.02, 0.3, 6000.0, 1e6, 1e30])
+def test_gemm16_activation_scale(dev, orc, scale):
+    """Activations scaled far below and above fp16's range, and either side of
+    the bounds [1/4, 2^15) of the largest element within which the one-pass
+    conversion at scale 1 stands (else it is redone at a power-of-two scale),
+    keep their precision; calls at different scales alternate on one copy."""
     rng = np.random.default_rng(1803)
     R, C, M = 64, 512, 16
     w = W.gen_weights(rng, 8, R, C)
-    x = (W.gen_x(rng, M, C) * np.float32(1e-30)).astype(np.float32)
+    x0 = W.gen_x(rng, M, C)
     w16 = make(dev, K.Q8_0, w, R, C)
-    got = gemm(dev, w16, x, R, C)
-    assert O.norm_err(got, orc.gemv(K.Q8_0, w, x, R, C, M)) < D16_TOL
+    for s in (scale, 1.0, scale):
+        x = (x0 * np.float32(s)).astype(np.float32)
+        got = gemm(dev, w16, x, R, C)
+        assert O.norm_err(got, orc.gemv(K.Q8_0, w, x, R, C, M)) < D16_TOL, s
 
 
 @pytest.mark.parametrize("qt,sem", [(8, K.Q8_0), (39, K.MXFP4)])

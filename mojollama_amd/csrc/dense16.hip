@@ -336,7 +336,8 @@ int mllm_d16_gemm(const void *w16, const float *x, int ldx, int M, float *out, i
     const long n4 = (long)M * n_cols / 4;
     const int np = (int)std::min<long>(kPartMax, std::max<long>(1, (n4 + 1023) / 1024));
     hipLaunchKernelGGL(k_x16_cvt1, dim3(np), dim3(256), 0, st, x, n_cols, ldx, n4, part, x16, alpha, n_rows);
-    const unsigned gc = (unsigned)std::min<long>((n4 + 1023) / 1024, 16L * device_cus_d16());
+    // one workgroup per CU: in the common case each only reads the partials and returns
+    const unsigned gc = (unsigned)std::min<long>((n4 + 1023) / 1024, (long)device_cus_d16());
     hipLaunchKernelGGL(k_x16_fix, dim3(gc), dim3(256), 0, st, x, n_cols, ldx, n4, part, np, x16, alpha, n_rows);
     if (hipGetLastError() != hipSuccess) { err = "activation conversion launch failed"; return -1; }
     const hipblasLtHandle_t h = handle_for_current();

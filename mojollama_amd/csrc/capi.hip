@@ -1391,8 +1391,10 @@ int mllm_moe_ffn_dev_tokens(const float *router, const uint8_t *const bases[3], 
     b.out = ddn; b.out_job_stride = N; b.ldo = N;
     b.n_rows = N; b.n_cols = M; b.B = 1;
     HIP_OK(mllm_launch_gemv(sems[2], b, (int)TK, st));
-    HIP_OK(mllm_launch_combine(ddn, dwt, didx, T, K, N, dout, 1, st));
-    HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
+    // small results: the combine writes them straight into the pinned buffer
+    const bool direct = (size_t)T * N * 4 <= kDirectOutMax && c.h_out.dp;
+    HIP_OK(mllm_launch_combine(ddn, dwt, didx, T, K, N, direct ? (float *)c.h_out.dp : dout, 1, st));
+    if (!direct) HIP_OK(hipMemcpyAsync(c.h_out.p, dout, (size_t)T * N * 4, hipMemcpyDeviceToHost, st));
     HIP_OK(hipStreamSynchronize(st));
     memcpy(out_host, c.h_out.p, (size_t)T * N * 4);
     return 0;

@@ -71,10 +71,10 @@ sys.path.insert(0, ROOT)
 
 from mojollama_amd import kernels as K  # noqa: E402
 from mojollama_amd import workloads as W  # noqa: E402
+from mojollama_amd.decode_chain import EPS, DecodeChain, Matrix, algo_bytes, build_tinyllama  # noqa: E402,F401
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-EPS = 1e-5
 # HBM bytes per launch of a decode-chain GEMV kind, from FETCH_SIZE /
 # WRITE_SIZE counter runs (bench.py --kernel gate_up) calibrated on a copy of
 # known size (bench.py --kernel copy): FETCH 6526.2 KiB x 1.99982 + WRITE
@@ -124,42 +124,6 @@ def cpu_tag(cores, model):
 
 
 # ------------------------------------------------------------------ GPU helpers
-class Matrix:
-    def __init__(self, dev, sem, raw, rows, cols):
-        import torch
-        self.sem, self.rows, self.cols = sem, rows, cols
-        self.raw_bytes = raw.size if isinstance(raw, np.ndarray) else raw.numel()
-        src = torch.from_numpy(raw).cuda() if isinstance(raw, np.ndarray) else raw
-        self.packed = dev.pack(sem, src, rows, cols)
-
-
-def build_tinyllama(dev, rng, n_layers):
-    """Per layer, the device copies as a decode engine runs them: q/k/v rows
-    stacked into one 2560x2048 matrix (one launch, as batch_qkv_omp), o,
-    gate/up rows stacked into one 11264x2048 matrix (batch_gate_up_omp), down;
-    the RMSNorm weights of the attention and FFN norms (1 + 0.1 N(0,1))."""
-    import torch
-    layers = []
-    for _ in range(n_layers):
-        raw = {name: W.gen_weights(rng, qt, rows, cols) for name, rows, cols, qt in W.TINYLLAMA_MATS}
-        qkv = np.concatenate([raw["q"], raw["k"], raw["v"]])
-        gu = np.concatenate([raw["gate"], raw["up"]])
-        layers.append({"qkv": Matrix(dev, K.Q4_K_GGML, qkv, 2560, 2048),
-                       "o": Matrix(dev, K.Q4_K_GGML, raw["o"], 2048, 2048),
-                       "gate_up": Matrix(dev, K.Q4_K_GGML, gu, 11264, 2048),
-                       "down": Matrix(dev, K.Q6_K_SEQ, raw["down"], 2048, 5632),
-                       "attn_norm": torch.from_numpy((1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)).cuda(),
-                       "ffn_norm": torch.from_numpy((1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)).cuda()})
-    name, rows, cols, qt = W.TINYLLAMA_LM_HEAD
-    lm = Matrix(dev, K.Q6_K_SEQ, W.gen_weights(rng, qt, rows, cols), rows, cols)
-    out_norm = torch.from_numpy((1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)).cuda()
-    return layers, lm, out_norm
-
-
-def algo_bytes(m, B):
-    return m.raw_bytes + B * (m.cols + m.rows) * 4
-
-
 def time_region(torch, fn, steps, warmup):
     """ms per call of fn (a sequence of kernel launches), captured once into a
     HIP graph and replayed: host launch overhead stays out of the figure.
@@ -191,48 +155,6 @@ def time_region(torch, fn, steps, warmup):
 def gpu_info(torch):
     p = torch.cuda.get_device_properties(0)
     return f"{p.name} ({getattr(p, 'gcnArchName', '?')}, {p.multi_processor_count} CUs)"
-
-
-class DecodeChain:
-    """The TinyLlama decode pass at batch B through mllm_gemv_fused:
-        qkv  = Wqkv . rmsnorm(x) * g_attn              (simd_ops rms_norm, TE:1516)
-        xb   = x + Wo . q                               (TE:1628-1633; q stands in for attention)
-        h    = silu(Wg . v) * (Wu . v), v = rmsnorm(xb) * g_ffn   (TE:1641, 1660-1710; paired gate/up rows)
-        x'   = xb + Wdown . h
-    for 22 layers, then logits = Wlm . rmsnorm(x) * g_out (TE:1716)."""
-
-    def __init__(self, torch, dev, layers, lm, out_norm, B):
-        self.torch, self.dev, self.layers, self.lm, self.out_norm, self.B = torch, dev, layers, lm, out_norm, B
-        z = lambda *s: torch.zeros(*s, device="cuda")  # noqa: E731
-        self.x0 = torch.randn(B, 2048, device="cuda")
-        self.xa, self.xb = z(B, 2048), z(B, 2048)
-        self.qkv, self.h, self.logits = z(B, 2560), z(B, 5632), z(B, 32000)
-        F = dev.fusion
-        self.f_qkv = [F(rms_w=L["attn_norm"], rms_eps=EPS) for L in layers]
-        self.f_o = F(out_add=self.xa, x_ld=2560)
-        self.f_gu = [F(rms_w=L["ffn_norm"], rms_eps=EPS, silu_pair=True, silu_clamp=False) for L in layers]
-        self.f_down = F(out_add=self.xb)
-        self.f_lm = F(rms_w=out_norm, rms_eps=EPS)
-        wsz = lambda m, f, rows=None: dev.so.mllm_gemv_fused_workspace_size(  # noqa: E731
-            m.sem, rows or m.rows, m.cols, B, ctypes.byref(f))
-        n = max([wsz(layers[0]["qkv"], self.f_qkv[0]), wsz(layers[0]["o"], self.f_o),
-                 wsz(layers[0]["gate_up"], self.f_gu[0], 5632), wsz(layers[0]["down"], self.f_down),
-                 wsz(lm, self.f_lm), 256])
-        self.ws = torch.empty(n, dtype=torch.uint8, device="cuda")
-        self.mats = [m for L in layers for m in (L["qkv"], L["o"], L["gate_up"], L["down"])] + [lm]
-
-    def run(self):
-        d, B, ws = self.dev, self.B, self.ws
-        self.xa.copy_(self.x0)
-        for i, L in enumerate(self.layers):
-            d.gemv_fused(L["qkv"].sem, L["qkv"].packed, self.xa, 2560, 2048, self.f_qkv[i], out=self.qkv, ws=ws)
-            d.gemv_fused(L["o"].sem, L["o"].packed, self.qkv.data_ptr(), 2048, 2048, self.f_o, out=self.xb, ws=ws, B=B)
-            d.gemv_fused(L["gate_up"].sem, L["gate_up"].packed, self.xb, 5632, 2048, self.f_gu[i], out=self.h, ws=ws)
-            d.gemv_fused(L["down"].sem, L["down"].packed, self.h, 2048, 5632, self.f_down, out=self.xa, ws=ws)
-        d.gemv_fused(self.lm.sem, self.lm.packed, self.xa, 32000, 2048, self.f_lm, out=self.logits, ws=ws)
-
-    def bytes(self):
-        return sum(algo_bytes(m, self.B) for m in self.mats)
 
 
 def kernel_only(torch, dev, which):

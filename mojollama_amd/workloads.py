@@ -56,6 +56,28 @@ def gen_weights(rng, qt, n_rows, n_cols):
     return np.ascontiguousarray(blk.ravel())
 
 
+def gen_q4k_centered(rng, n_rows, n_cols):
+    """Q4_K blocks whose weights have mean ~0: sub-block scales sc in [0, 8],
+    mins m = round(7.5 sc) and dmin = d, so w = d sc (q - 7.5) up to the
+    rounding of m.  BASELINE's uniform [0, 63] scales and mins give every row a
+    positive mean, which makes a chain of such matrices saturate (every gate of
+    a SiLU product far below zero after one layer); a parity test of a chain
+    uses these instead.  The scale/min pairs are packed as get_scale_min_k4
+    reads them (QK:62-71)."""
+    nb = n_rows * (n_cols // 256)
+    blk = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    blk[:, 0:2] = _f16_scales(rng, nb)
+    blk[:, 2:4] = blk[:, 0:2]
+    sc = rng.integers(0, 9, size=(nb, 8)).astype(np.uint8)
+    m = np.rint(7.5 * sc).astype(np.uint8)
+    q = np.zeros((nb, 12), np.uint8)
+    q[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+    q[:, 4:8] = m[:, 0:4] | ((m[:, 4:8] >> 4) << 6)
+    q[:, 8:12] = (sc[:, 4:8] & 15) | ((m[:, 4:8] & 15) << 4)
+    blk[:, 4:16] = q
+    return np.ascontiguousarray(blk.ravel())
+
+
 def gen_x(rng, B, n_cols, bf16=False):
     """fp32 activations ~ N(0,1); bf16=True rounds them to bf16 (RNE) and back."""
     x = rng.standard_normal((B, n_cols)).astype(np.float32)

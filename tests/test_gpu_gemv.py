@@ -388,3 +388,40 @@ def test_requantize_lm_head_full_shape(lib, orc):
     q6_logits = orc.gemv(K.Q6_K_GGML, w, x, R, C, 1)[0]   # the ggml order the requantisation decodes
     assert O.norm_err(q8_logits, q6_logits) < 2e-2
     assert lib.requantize_output_q8_0(up(w), R, C, 13, up(out)) == -1
+
+
+# ------------------------------------------------ activations with outliers
+
+@pytest.mark.parametrize("name,qt,C", [("q4_k", 12, 2048), ("q6_k", 14, 2048), ("mxfp4", 39, 2880), ("q8_0", 8, 2048)])
+@pytest.mark.parametrize("B", [1, 8])
+def test_digit_staging_outliers(lib, orc, name, qt, C, B):
+    """fp32 activations with an outlier 10^3-10^4 x its neighbours in every
+    16-element group (real LLM activations have such channels).  The decode
+    GEMVs stage x as three int8 digit planes under one power of two per group
+    of 16 (B = 1) or 32 (the MFMA form at B = 8) elements, exact up to a
+    remainder below 2^-20 of the group's largest element, so the small
+    neighbours of an outlier carry an absolute error of up to 2^-20 x the
+    outlier.  Checked element by element against that bound: for output r,
+    |got - ref| <= 4 * 2^-20 * sum_g max_{i in g}|x_i| * sum_{i in g}|w_ri|
+    + 2^-20 * sum_i |w_ri x_i| (fp32 summation), ref = the dot of the
+    oracle's fp32 weights and x in float64 (groups of 32)."""
+    rng = np.random.default_rng(qt * 31 + B)
+    R = 256
+    w = W.gen_weights(rng, qt, R, C)
+    x = rng.standard_normal((B, C)).astype(np.float32)
+    pos = rng.integers(0, 16, size=(B, C // 16))
+    mag = (10.0 ** rng.uniform(3, 4, size=(B, C // 16)) * rng.choice([-1, 1], size=(B, C // 16))).astype(np.float32)
+    for b in range(B):
+        x[b, np.arange(C // 16) * 16 + pos[b]] *= mag[b]
+    sem = orc.sem_for(1, qt)
+    wf = orc.dequant(sem, w, R, C).astype(np.float64)
+    ref = x.astype(np.float64) @ wf.T                                       # [B][R]
+    gmax = np.abs(x.astype(np.float64)).reshape(B, C // 32, 32).max(axis=2)   # [B][G]
+    wabs = np.abs(wf).reshape(R, C // 32, 32).sum(axis=2)                     # [R][G]
+    bound = 4 * 2.0 ** -20 * (gmax @ wabs.T) + 2.0 ** -20 * (np.abs(x.astype(np.float64)) @ np.abs(wf).T)
+    got = bmm(lib, name, w, x, R, C, B)
+    excess = np.abs(got - ref) / bound
+    print(f"[parity] outliers {name} B={B}: worst |err|/bound {excess.max():.3f}, "
+          f"normalised err {O.norm_err(got, ref):.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert excess.max() <= 1.0, K.last_error(lib)

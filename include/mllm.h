@@ -143,11 +143,62 @@ MLLM_API void gptoss_forward(const int *token, int pos, const float *emb, int V,
 MLLM_API void set_num_threads(int n);
 MLLM_API int get_max_threads(void);
 
-/* Symbols TE binds unconditionally that lie outside this path (TE:263-311,
- * TE:397-408): log once and return without touching any buffer. */
-MLLM_API void ssm_layer_fused(void);
-MLLM_API void qwen36_batch_forward(void);
-MLLM_API void ssm_decode_step(void);
+/* The Qwen3.6 hybrid drivers TE binds (TE:263-311, 397-408).
+ *
+ * ssm_decode_step (CE:736-802): per token, the conv'd input split into gate
+ * and SSM halves, ssm_intermediate[b] = silu(gate) * ssm_in; the per-group
+ * state updated once per token in order (h = exp(A dt) h + [s == 0] (beta.x)
+ * dt, dt = softplus(dt_bias + alpha.x)).  The intermediate does not read the
+ * state (the reference's own arithmetic).  2*inner <= 8192.
+ *
+ * ssm_layer_fused (CE:803-849): ssm_decode_step into `output` (as scratch of
+ * B*inner floats), then per token b: interm *= gate_raw.x_b, output[b*N..] =
+ * residual_b + ssm_out_raw.interm (quant_matmul_omp semantics); output holds
+ * max(B*N, B*inner) floats and its aliasing is reproduced in order.  Gate
+ * gate_nr >= inner rows of N columns (<= 8192), ssm_out N x inner.
+ *
+ * qwen36_batch_forward (CE:859-1231): B tokens through L SSM / attention
+ * layers with MoE FFNs and shared experts, then the output head, every
+ * matmul with quant_matmul_omp semantics; logits [B][out_nr_final].  The
+ * caller's state is read and written as the reference does: the SSM state
+ * (per layer at l * groups * state_size), row kv_lens[l] of each attention
+ * layer's caches ([L][max_ctx][n_kv_h*HD]; kv_lens not incremented), and the
+ * fused-QKV slice of ws (ws + 3*B*S, S from CE:906-913), where V is read at
+ * offset NH*HD + N (CE:1002-1009).  The other workspace slices are not
+ * written.  The device keeps mirrors of the KV caches: rows below kv_lens
+ * that the caller changes between calls must be followed by
+ * mllm_cache_clear() (a changed sample of rows is detected, not every row).
+ * fp32 routers (code 0) are summed in f32_matmul_omp's order, so top-K
+ * selection matches the reference on its own logits.  Refused (error,
+ * outputs untouched): kv_lens[l] outside [0, max_ctx), QKV rows fewer than
+ * NH*HD + n_kv_h*HD, shapes that are not N x inner / inner x N, 2*ssm_inner >
+ * 8192, more than 256 experts or top_k > 16, emb_quant other than 0 / 12, an
+ * MXFP4 down projection with q8_ws == NULL (the reference dereferences it). */
+MLLM_API void ssm_decode_step(const float *x, float *ssm_intermediate, const float *conv1d_w, const float *a_param,
+                              const float *dt_bias, const float *alpha, const float *beta, const float *ssm_norm_w,
+                              float *state, int B, int N, int inner, int groups, int state_size, int conv_kernel,
+                              int dt_rank);
+MLLM_API void ssm_layer_fused(const float *x, float *residual, float *output, const float *conv1d_w,
+                              const float *a_param, const float *dt_bias, const float *alpha, const float *beta,
+                              const float *ssm_norm_w, float *state, const uint8_t *gate_raw, int gate_nr, int gate_nc,
+                              int gate_qt, const uint8_t *ssm_out_raw, int ssm_out_nr, int ssm_out_nc, int ssm_out_qt,
+                              int B, int N, int inner, int groups, int state_size, int conv_kernel, int dt_rank);
+MLLM_API void qwen36_batch_forward(
+    int B, int L, int N, int NH, int n_kv_h, int HD, int FF, int n_experts, int top_k, int n_ff_expert, float eps,
+    int rope_dim, int max_ctx, int ssm_inner, int ssm_groups, int ssm_state_size, int ssm_conv_kernel, int ssm_dt_rank,
+    const float *emb, int emb_quant, const int *layer_types, const int *tokens, float *logits, const float **attn_norm_w,
+    const float **ffn_norm_w, const uint8_t **attn_qkv_raw, const int *qkv_nr, const int *qkv_nc, const int *qkv_qt,
+    const uint8_t **attn_gate_raw, const int *gate_nr, const int *gate_nc, const int *gate_qt,
+    const uint8_t **ssm_out_raw, const int *ssm_out_nr, const int *ssm_out_nc, const int *ssm_out_qt,
+    const uint8_t **attn_out_raw, const int *out_nr, const int *out_nc, const int *out_qt, uint8_t **gate_exp_raw,
+    const int *gate_exp_qt, uint8_t **up_exp_raw, const int *up_exp_qt, uint8_t **down_exp_raw,
+    const int *down_exp_qt, const float **shexp_gate_raw, const float **shexp_up_raw, const float **shexp_down_raw,
+    const float **shexp_router, const int *shexp_int, const uint8_t **moe_router_raw, const int *moe_router_qt,
+    const int *shexp_gate_qt, const int *shexp_up_qt, const int *shexp_down_qt, const float *out_norm_w,
+    const uint8_t *out_w, int out_nr_final, int out_nc_final, int out_qt_final, const float **ssm_conv1d,
+    const float **ssm_a, const float **ssm_dt_bias, const float **ssm_alpha, const float **ssm_beta,
+    const float **ssm_norm, float *ssm_state, float *kv_k, float *kv_v, int *kv_lens, const float *cos_table,
+    const float *sin_table, float *ws, uint8_t *q8_ws);
 
 MLLM_API const char *mllm_last_error(void);
 MLLM_API void mllm_cache_clear(void);

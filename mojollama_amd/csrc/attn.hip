@@ -344,6 +344,15 @@ MLLM_API int mllm_gqa_decode(int mode, const float *q, const mllm_kv_view *kv, c
         mllm_set_error("mllm_gqa_decode: a paged view needs page_size, max_blocks and n_pages > 0");
         return -1;
     }
+    // contiguous rows are read as float4 from b * seq_stride + s * NKH * HD: the
+    // stride keeps that 16-byte aligned and, with several sequences, past the
+    // max_seq rows of the previous one
+    if (!kv->block_tables && (kv->seq_stride < 0 || kv->seq_stride % 4 ||
+                              (B > 1 && kv->seq_stride < (long)max_seq * NKH * HD))) {
+        mllm_set_error("mllm_gqa_decode: seq_stride must be a non-negative multiple of 4 floats and, for B > 1, at "
+                       "least max_seq * NKH * HD");
+        return -1;
+    }
     hipStream_t st = (hipStream_t)stream;
     attn_args a{};
     a.q = q; a.kv = *kv; a.seq_lens = seq_lens; a.max_seq = max_seq > 0 ? max_seq : 1;
@@ -372,6 +381,10 @@ MLLM_API int mllm_kv_append(const mllm_kv_view *kv, const int *pos, const float 
         return -1;
     }
     const int n = NKH * HD;
+    if (!kv->block_tables && (kv->seq_stride < 0 || (B > 1 && kv->seq_stride < n))) {
+        mllm_set_error("mllm_kv_append: seq_stride must be >= 0 and, for B > 1, at least NKH * HD");
+        return -1;
+    }
     hipLaunchKernelGGL(k_kv_append, dim3((n + 255) / 256, B), dim3(256), 0, (hipStream_t)stream, *kv, pos, k_new,
                        v_new, NKH, HD);
     return hipGetLastError() == hipSuccess ? 0 : -1;

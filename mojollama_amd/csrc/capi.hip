@@ -29,6 +29,7 @@
 #include "mllm.h"
 #include "moe.h"
 #include "dense16.h"
+#include "dropin.h"
 
 namespace {
 
@@ -287,6 +288,23 @@ int get_weight(const void *host, int ly, int rows, int cols, mllm_packed &view, 
     if (scale_flags) *scale_flags = ins.first->second.scale_flags;
     return 0;
 }
+
+} // namespace
+
+int mllm_dropin_weight(const void *host, int sem, int rows, int cols, mllm_packed *view, bool *gemv_only)
+{
+    if (sem < 0 || sem >= SEM_COUNT || !host || rows <= 0 || cols <= 0) { set_error("weight: bad matrix"); return -1; }
+    int flags = 0;
+    if (get_weight(host, mllm_sem_layout(sem), rows, cols, *view, &flags)) return -1;
+    if (gemv_only) *gemv_only = mllm_scales_need_gemv(sem, flags);
+    return 0;
+}
+
+int mllm_qmm_sem(int qt) { return sem_for(ENT_QMM, qt); }
+
+std::shared_mutex &mllm_api_mutex() { return g_api_mu; }
+
+namespace {
 
 // Several host matrices of one layout and width stacked row-wise into one
 // packed device matrix (the q/k/v or gate/up matrices of batch_qkv_omp /
@@ -943,10 +961,6 @@ MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_o
     mllm_moe_ffn_host_batched(router, bases, qts, N, E, K, M, x, ffn_out, B);
 }
 
-// Out-of-path symbols the reference caller binds unconditionally (TE:263-311,397-408).
-MLLM_API void ssm_layer_fused(void) { set_error("ssm_layer_fused is outside this library's scope (no-op)"); }
-MLLM_API void qwen36_batch_forward(void) { set_error("qwen36_batch_forward is outside this library's scope (no-op)"); }
-MLLM_API void ssm_decode_step(void) { set_error("ssm_decode_step is outside this library's scope (no-op)"); }
 
 MLLM_API const char *mllm_last_error(void) { return g_last_error.c_str(); }
 
@@ -966,6 +980,7 @@ MLLM_API void mllm_cache_clear(void)
     for (auto &kv : g_router_cache) (void)hipFree(kv.second.first);
     g_router_cache.clear();
     mllm_gptoss_cache_clear();
+    mllm_qwen36_cache_clear();
 }
 
 // ====================================================== device-pointer ABI

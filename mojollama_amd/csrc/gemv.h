@@ -146,6 +146,11 @@ long mllm_route_workspace_floats(int T, int E);
 hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, float *logits_ws, hipStream_t st);
 
+// Softmax and top-K (CE:614-638, renormalised when `renorm`) of logits [T][E]
+// computed elsewhere: k_route_finish on its own.
+hipError_t mllm_launch_route_finish(const float *logits, int T, int E, int K, int renorm, int *top_idx, float *top_w,
+                                    hipStream_t st);
+
 // The fused GEMV activation on its own, T rows of n (one workgroup each):
 // v = (x_up ? silu(x) * x_up : x) + x_res; res_out = v; with rms_w the RMS
 // norm of v (div: (v / rms) * w, else v * (1 / rms) * w).  Any pointer but x

@@ -32,3 +32,21 @@ void mllm_set_error(const char *msg);
 
 // Frees the models and KV mirrors gptoss_forward keeps (part of mllm_cache_clear).
 void mllm_gptoss_cache_clear();
+
+// mllm_moe_forward with the routing supplied (device idx / w [T][K], e.g.
+// computed by a caller's own router): moe_forward_omp's contract (QK:2066).
+int mllm_moe_forward_routed(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
+                            long ws_bytes, const int *idx, const float *w, hipStream_t st);
+
+// A layer for routed forwards over the expert types of moe_forward_omp (GGUF
+// codes, QK:2094-2245) and the device table tab_dev ([E] gate, [E] up, [E]
+// down packed views; the caller's, kept alive while the layer is used).  No
+// router: only mllm_moe_forward_routed serves it.  nullptr for gate/up types
+// the reference's expert path does not compute; synchronous (scans the block
+// scales).  Released with mllm_moe_release.
+mllm_moe_layer *mllm_moe_layer_for_codes(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
+                                         const mllm_packed *tab_dev);
+
+// The semantics a layer gives the codes (gate, up; down: -2 for the
+// reference's Q4_K zeros, -1 unknown).
+void mllm_moe_codes_sems(int qt_gate, int qt_up, int qt_down, int *sem_g, int *sem_u, int *sem_d);

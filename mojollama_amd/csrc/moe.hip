@@ -380,18 +380,28 @@ MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *L, int T)
     return L ? (long)moe_ws_layout(*L, T, nullptr, nullptr) : -1;
 }
 
-// x [T][N] fp32 -> out [T][N]; also returns the routing (idx/w [T][K]) in the workspace.
-MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
-                              long ws_bytes, int *idx_out, float *w_out, void *stream)
+} // extern "C"
+
+// x [T][N] fp32 -> out [T][N].  Routing from the layer's router, or, with
+// idx_in / w_in (device [T][K]), the caller's (moe_forward_omp's own contract,
+// QK:2066-2071).  idx_out / w_out (optional) receive the routing used.
+static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
+                            long ws_bytes, int *idx_out, float *w_out, const int *idx_in, const float *w_in,
+                            hipStream_t st)
 {
     if (!L || T <= 0) return -1;
-    hipStream_t st = (hipStream_t)stream;
     if (ws_bytes < (long)moe_ws_layout(*L, T, nullptr, nullptr)) return -1;
     moe_ws s;
     moe_ws_layout(*L, T, &s, (uint8_t *)workspace);
     const int N = L->N, M = L->M, E = L->E, K = L->K, TK = T * K;
 #define CK(e) do { if ((e) != hipSuccess) return -1; } while (0)
-    CK(mllm_launch_route(L->router_p, x, T, N, E, K, L->renorm, s.idx, s.w, s.logits, st));
+    if (idx_in && w_in) {
+        s.idx = const_cast<int *>(idx_in);
+        s.w = const_cast<float *>(w_in);
+    } else {
+        if (!L->router_p) return -1;
+        CK(mllm_launch_route(L->router_p, x, T, N, E, K, L->renorm, s.idx, s.w, s.logits, st));
+    }
     if (L->sem_g < 0 || L->sem_u < 0) return -1;   // reference-zero gate/up types are not served here
     int8_t *q; float *d, *s4; int *sq;
     const mllm_xq xqx = xq_at(s.xq_x, T, N, &q, &d, &s4, &sq);
@@ -514,6 +524,50 @@ MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, fl
     if (w_out) CK(hipMemcpyAsync(w_out, s.w, (size_t)TK * 4, hipMemcpyDeviceToDevice, st));
 #undef CK
     return 0;
+}
+
+int mllm_moe_forward_routed(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
+                            long ws_bytes, const int *idx, const float *w, hipStream_t st)
+{
+    if (!idx || !w) return -1;
+    return moe_forward_impl(L, x, T, out, workspace, ws_bytes, nullptr, nullptr, idx, w, st);
+}
+
+mllm_moe_layer *mllm_moe_layer_for_codes(int qt_gate, int qt_up, int qt_down, int N, int M, int E, int K,
+                                         const mllm_packed *tab_dev)
+{
+    if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || N <= 0 || M <= 0 || !tab_dev) return nullptr;
+    mllm_moe_layer *L = new mllm_moe_layer;
+    L->N = N; L->M = M; L->E = E; L->K = K; L->renorm = 0;
+    L->clamp = 1;
+    L->owns_router = 0;
+    L->owns_tab = 0;
+    L->sem_g = sem_gu_of(qt_gate, qt_up, 0);
+    L->sem_u = sem_gu_of(qt_gate, qt_up, 1);
+    L->sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);
+    L->router_p = nullptr;
+    L->tab = const_cast<mllm_packed *>(tab_dev);
+    L->gemv_only = mllm_moe_needs_gemv(tab_dev, L->sem_g, L->sem_u, L->sem_d, N, M, E);
+    if (L->sem_g < 0 || L->sem_u < 0 || L->gemv_only < 0) {
+        delete L;
+        return nullptr;
+    }
+    return L;
+}
+
+void mllm_moe_codes_sems(int qt_gate, int qt_up, int qt_down, int *sem_g, int *sem_u, int *sem_d)
+{
+    *sem_g = sem_gu_of(qt_gate, qt_up, 0);
+    *sem_u = sem_gu_of(qt_gate, qt_up, 1);
+    *sem_d = qt_down == 12 ? -2 : sem_down_of(qt_down);
+}
+
+extern "C" {
+
+MLLM_API int mllm_moe_forward(const mllm_moe_layer *L, const float *x, int T, float *out, void *workspace,
+                              long ws_bytes, int *idx_out, float *w_out, void *stream)
+{
+    return moe_forward_impl(L, x, T, out, workspace, ws_bytes, idx_out, w_out, nullptr, nullptr, (hipStream_t)stream);
 }
 
 } // extern "C"

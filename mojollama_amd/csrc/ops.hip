@@ -938,6 +938,14 @@ constexpr int kRouteMinGroups = 128;
 // Decode routing shape: row chunks, and router / x float4 loads per thread and chunk.
 constexpr int kRouteSliceChunks = 2, kRouteSliceSlots = 8, kRouteSliceXSlots = 2;
 
+hipError_t mllm_launch_route_finish(const float *logits, int T, int E, int K, int renorm, int *top_idx, float *top_w,
+                                    hipStream_t st)
+{
+    if (E <= 0 || E > 256 || K <= 0 || K > 16 || K > E || T <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits, T, E, K, renorm, top_idx, top_w);
+    return hipGetLastError();
+}
+
 hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N, int E, int K, int renorm,
                              int *top_idx, float *top_w, float *logits_ws, hipStream_t st)
 {

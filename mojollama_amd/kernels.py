@@ -65,6 +65,38 @@ class GptOssDesc(ctypes.Structure):
         ("sin_t", cf)]
 
 
+# The reference caller's bindings of its whole-layer entry points, kept here
+# so the drop-in and the reference's own C are called identically:
+# ssm_layer_fused (TE:263-271, CE:803-849), qwen36_batch_forward (TE:273-310,
+# CE:859-1231) and ssm_decode_step (TE:401-405, CE:736-802).
+_pf, _pu, _pi = ctypes.POINTER(cf), ctypes.POINTER(cu), ctypes.POINTER(ci)
+SSM_LAYER_FUSED_ARGTYPES = [cf, cf, cf, cf, cf, cf, cf, cf, cf, cf, cu, ci, ci, ci, cu, ci, ci, ci] + [ci] * 7
+SSM_DECODE_STEP_ARGTYPES = [cf] * 9 + [ci] * 7
+QWEN36_ARGTYPES = (
+    [ci] * 7 + [ci, ci, ci, ctypes.c_float] + [ci] * 7        # B, L, N, NH, n_kv_h, HD, FF; E, K, M, eps; rope..dt_rank
+    + [cf, ci]                                                # emb, emb_quant
+    + [_pi, _pi, cf]                                          # layer_types, tokens, logits
+    + [_pf, _pf]                                              # attn_norm_w, ffn_norm_w
+    + [_pu, _pi, _pi, _pi] * 4                                # qkv, attn gate, ssm out, attn out: raw, nr, nc, qt
+    + [_pu, _pi] * 3                                          # gate/up/down experts, quant types
+    + [_pf, _pf, _pf, _pf, _pi]                               # shared expert gate/up/down, router, intermediate
+    + [_pu, _pi, _pi, _pi, _pi]                               # moe router + qt, shared expert quant types
+    + [cf, cu, ci, ci, ci]                                    # out_norm_w, out_w, nr, nc, qt
+    + [_pf] * 6 + [cf]                                        # ssm conv1d, a, dt_bias, alpha, beta, norm; state
+    + [cf, cf, _pi, cf, cf]                                   # kv_k, kv_v, kv_lens, cos_table, sin_table
+    + [cf, cu])                                               # ws, q8_ws
+
+
+def bind_model_entry_points(so):
+    """Bind ssm_layer_fused / qwen36_batch_forward / ssm_decode_step as TE does."""
+    so.ssm_layer_fused.argtypes = SSM_LAYER_FUSED_ARGTYPES
+    so.ssm_layer_fused.restype = None
+    so.qwen36_batch_forward.argtypes = QWEN36_ARGTYPES
+    so.qwen36_batch_forward.restype = None
+    so.ssm_decode_step.argtypes = SSM_DECODE_STEP_ARGTYPES
+    so.ssm_decode_step.restype = None
+
+
 _LIB = None
 
 
@@ -106,6 +138,7 @@ def load_kernels(path=LIB_PATH):
                  "q5_k_batch_matmul", "mxfp4_batch_matmul"):
         getattr(so, name).argtypes = [cu, cf, cf, ci, ci, ci]
         getattr(so, name).restype = None
+    bind_model_entry_points(so)
     so.moe_ffn.argtypes = [cvp, ci, cf, cf, cf, cf, ci]
     so.moe_ffn.restype = None
     so.moe_ffn_batched.argtypes = [cvp, ci, cf, cf, ci]

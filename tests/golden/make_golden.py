@@ -22,6 +22,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 from oracle import RefLib, fp, up  # noqa: E402
+from mojollama_amd import kernels as K  # noqa: E402
 from mojollama_amd import workloads as W  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
@@ -166,6 +167,69 @@ def gen_q5_down(ref):
                             n_embd=n_embd, n_ff=n_ff, qts=np.array(qts))
 
 
+# the ssm_* / qwen36 cases: (tag, seed, B, N, inner, gate_qt, ssm_out_qt); N > inner makes
+# ssm_layer_fused's later tokens read intermediates the earlier ones overwrote (CE:829-846)
+SSM_CASES = [("a", 91, 3, 256, 256, W.QT_Q8_0, W.QT_Q6_K), ("b", 92, 3, 512, 256, W.QT_Q4_K, W.QT_MXFP4),
+             ("c", 93, 2, 256, 384, W.QT_MXFP4, W.QT_Q8_0)]
+
+
+def gen_qwen36(ref):
+    """qwen36_batch_forward (CE:859-1231), ssm_layer_fused and ssm_decode_step
+    as the reference's own C computes them.  The inputs are regenerated in the
+    test from their seeds (workloads.qwen36_case / ssm_case) and checked by
+    CRC; the fixtures hold the outputs: for two consecutive qwen36 calls
+    (kv_lens + 1 between them, as TE:1880 does) the logits, SSM state, the KV
+    rows written and the fused-QKV workspace slice."""
+    K.bind_model_entry_points(ref.so)
+
+    def two_calls(c):
+        call = W.Qwen36Call(c)
+        res = {}
+        for i in range(2):
+            res[f"logits{i}"] = call.call(ref.so, c["tokens"][i])
+            res[f"state{i}"] = call.state.copy()
+            res[f"kv{i}"] = np.stack([call.kv[:, l, call.kv_lens[l]] for l in range(c["L"])])
+            res[f"slice{i}"] = call.qkv_slice()
+            call.kv_lens += 1
+        return res
+    rng = np.random.default_rng(94)
+    for emb_quant in (0, 12):
+        c = W.qwen36_case(0, 2, emb_quant)
+        res = two_calls(c)
+        # the case must not sit on a discrete edge (a top-K near-tie, a clip): a
+        # few ulps of change in any norm weight may move the logits only by
+        # fp32-rounding amounts, else another summation order could flip it
+        worst = 0.0
+        for trial in range(12):
+            c2 = dict(c)
+            which = ("attn_norm", "ffn_norm", "out_norm")[trial % 3]
+            pert = lambda v: np.nextafter(v, v + np.float32(np.inf) * rng.choice([-1, 1], v.shape).astype(np.float32))  # noqa: E731
+            c2[which] = [pert(v) for v in c[which]] if which != "out_norm" else pert(c[which])
+            r2 = two_calls(c2)
+            worst = max(worst, max(float(np.max(np.abs(r2[k] - res[k])) / np.max(np.abs(res[k])))
+                                   for k in ("logits0", "logits1")))
+        assert worst < 1e-4, f"qwen36 case emb{emb_quant} is ulp-sensitive ({worst:.2e})"
+        # the first call again over KV caches whose cached rows all changed: must differ
+        call = W.Qwen36Call(c)
+        nkv = c["n_kv_h"] * c["HD"]
+        for l in range(c["L"]):
+            n = c["kv_lens0"][l]
+            call.kv[:, l, :n] = rng.standard_normal((2, n, nkv)) * 8.0
+        res["kv_mod"] = call.kv.copy()
+        res["logits_mod"] = call.call(ref.so, c["tokens"][0])
+        moved = float(np.max(np.abs(res["logits_mod"] - res["logits0"])) / np.max(np.abs(res["logits0"])))
+        print(f"qwen36 emb{emb_quant}: ulp sensitivity {worst:.2e}, rewritten KV rows move the logits by {moved:.2e}")
+        assert moved > 1e-2
+        np.savez_compressed(os.path.join(OUT, f"qwen36_emb{emb_quant}.npz"), crc=W.qwen36_arrays_crc(c),
+                            ulp_sensitivity=worst, **res)
+    for tag, seed, B, N, inner, gq, sq in SSM_CASES:
+        c = W.ssm_case(seed, B, N, inner, gate_qt=gq, so_qt=sq)
+        out_f, st_f = W.ssm_call(ref.so, c, True)
+        out_d, st_d = W.ssm_call(ref.so, c, False)
+        np.savez_compressed(os.path.join(OUT, f"ssm_{tag}.npz"), crc=crc(c["x"], c["gate"], c["so"], c["state"]),
+                            fused=out_f, fused_state=st_f, step=out_d, step_state=st_d)
+
+
 def main():
     ref = RefLib()
     ref.so.set_num_threads(1)
@@ -288,6 +352,7 @@ def main():
     gen_requant(ref)
     gen_nonfinite(ref)
     gen_q5_down(ref)
+    gen_qwen36(ref)
     print("golden vectors written to", OUT)
 
 

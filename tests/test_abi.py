@@ -89,3 +89,45 @@ def test_page_table_follows_ce(libpath):
     finally:
         so.mllm_page_table_destroy(pt)
     assert so.mllm_page_table_create(0, 64) is None
+
+
+def test_qwen36_and_ssm_refusals_touch_nothing(libpath):
+    """Arguments the drop-ins refuse (the reference would write past its KV
+    cache, or shapes its stack buffers cannot hold) leave every output
+    untouched and record an error -- decided before any device call."""
+    import numpy as np
+    from mojollama_amd import kernels
+    from mojollama_amd import workloads as W
+    so = kernels.load_kernels()
+    c = W.qwen36_case(0, 2, 0)
+    call = W.Qwen36Call(c)
+    call.kv_lens[1] = c["max_ctx"]            # an attention layer at max_ctx
+    call.logits[:] = 7.0
+    st0, ws0 = call.state.copy(), call.ws.copy()
+    call.call(so, c["tokens"][0])
+    assert (call.logits == 7.0).all() and np.array_equal(call.state, st0) and np.array_equal(call.ws, ws0)
+    assert b"kv_lens" in so.mllm_last_error()
+    s = W.ssm_case(91, 2, 256, 256)
+    out, state = W.ssm_call(so, s, True, gate_nc=288)   # gate columns other than N
+    assert np.isnan(out).all() and np.array_equal(state, s["state"])
+    assert b"ssm_layer_fused" in so.mllm_last_error()
+    s = W.ssm_case(92, 2, 256, 4200)           # 2*inner beyond the reference's 8192-float buffer
+    out, state = W.ssm_call(so, s, False)
+    assert np.isnan(out).all() and np.array_equal(state, s["state"])
+    assert b"ssm_decode_step" in so.mllm_last_error()
+
+
+def test_attention_rejects_bad_strides(libpath):
+    """mllm_gqa_decode / mllm_kv_append refuse a contiguous view whose
+    sequence stride is misaligned for the float4 row loads or, with several
+    sequences, shorter than a sequence's rows -- before any launch."""
+    from mojollama_amd import kernels
+    so = kernels.load_kernels()
+    fake = 4096   # never dereferenced: the checks come first
+    for stride, B, ok_msg in ((6, 1, "multiple of 4"), (-4, 1, "multiple of 4"), (64 * 2 * 64 - 4, 2, "max_seq")):
+        kv = kernels.KVView(fake, fake, stride, None, 0, 0, 0)
+        r = so.mllm_gqa_decode(0, fake, ctypes.byref(kv), fake, 64, B, 4, 2, 64, fake, fake, 1 << 30, None)
+        assert r == -1 and b"seq_stride" in so.mllm_last_error()
+    kv = kernels.KVView(fake, fake, 64, None, 0, 0, 0)
+    assert so.mllm_kv_append(ctypes.byref(kv), fake, fake, fake, 2, 2, 64, None) == -1
+    assert b"seq_stride" in so.mllm_last_error()

@@ -25,6 +25,7 @@
 #include <tuple>
 #include <vector>
 #include "gemm.h"
+#include "gemm16.h"
 #include "gemv.h"
 #include "mllm.h"
 #include "moe.h"
@@ -500,9 +501,16 @@ size_t planes_bytes(int sem, long rows, int n_cols)
 // Scratch of run_gemv's GEMM path (B > 8): Q8_0 activation pack, split
 // planes, split-K partials.  The GEMV path needs none (Q8_0 activations are
 // quantised by the GEMV workgroups).
+// The fp16-plane K-quant GEMM (gemm16.hip) serves B > 8 tokens of its
+// semantics over whole super-blocks.
+bool uses_q16(int sem, int n_cols, int B) { return B > 8 && mllm_q16_supported(sem) && n_cols % 256 == 0; }
+
 size_t gemv_required_bytes(int sem, int n_rows, int n_cols, int B)
 {
     if (!(B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem))) return 0;
+    if (uses_q16(sem, n_cols, B))
+        return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + mllm_act16_bytes(sem, B, n_cols) +
+               align256((size_t)mllm_q16_part_floats(sem, n_rows, n_cols, B) * 4);
     return (mllm_sem_uses_q8(sem) ? xq_bytes(B, n_cols) : 0) + (uses_planes(sem, B) ? planes_bytes(sem, B, n_cols) : 0) +
            align256((size_t)mllm_qgemm_part_floats(sem, n_rows, n_cols, B) * 4);
 }
@@ -527,6 +535,30 @@ int run_gemv(int sem, const mllm_packed &W, const float *x, float *out, int n_ro
              void *scratch, hipStream_t st, const float *out_add = nullptr, bool gemm_ok = true)
 {
     const bool q8 = mllm_sem_uses_q8(sem);
+    if (gemm_ok && uses_q16(sem, n_cols, B)) {
+        // prefill / batched K-quants: the fp16-plane MFMA GEMM
+        uint8_t *ws = (uint8_t *)scratch;
+        mllm_xq xq{};
+        if (q8) {
+            const xq_bufs xb = xq_carve(ws, B, n_cols);
+            HIP_OK(mllm_launch_quantize_q8_0(x, B, n_cols, nullptr, xb.q, xb.d, xb.s4, xb.sq, st));
+            xq = {xb.q, xb.d, xb.s4, xb.sq};
+            ws += xq_bytes(B, n_cols);
+        }
+        const act16 ac = mllm_act16_carve(sem, ws, B, n_cols);
+        ws += mllm_act16_bytes(sem, B, n_cols);
+        HIP_OK(mllm_launch_act16(sem, x, n_cols, q8 ? &xq : nullptr, B, n_cols, ac, st));
+        q16_args g{};
+        g.W = W;
+        g.x = ac;
+        g.out = out; g.ldo = n_rows;
+        g.n_rows = n_rows; g.n_cols = n_cols; g.n_entries = B;
+        g.ksplit = mllm_q16_ksplit(sem, n_rows, n_cols, B);
+        if (g.ksplit > 1) g.part = (float *)ws;
+        HIP_OK(mllm_launch_q16(sem, false, g, 0, st));
+        if (out_add) HIP_OK(mllm_launch_add(out, out_add, (long)B * n_rows, st));
+        return 0;
+    }
     if (gemm_ok && B > 8 && mllm_qgemm_supported(sem) && n_cols >= mllm_sem_block_elems(sem)) {
         // prefill / batched: quantised-weight MFMA GEMM over the B tokens
         xq_bufs xb{};

@@ -1,0 +1,709 @@
+// gemm16.hip — the K-quant GEMM on one exact fp16 weight plane (see gemm16.h).
+//
+// Workgroup = 4 wave64s.  A tile is 128 weight rows (DUAL: 128 gate rows and
+// the same 128 up rows) x TM = 32 * EB entries; wave w owns rows 32w .. 32w+31
+// (and their up rows) against all TM entries, so no two waves decode the same
+// weights.  K advances in 64-position steps (a quarter of a super-block; half
+// for Q4_K x Q8_0, whose dot reads 16 of every 32 elements).  Per step a lane
+// (row lane % 32, K half lane / 32) loads its row's bytes for the step (one
+// 16-byte load of nibbles, plus Q6_K's 2-bit planes and scales), turns them
+// into four 8-element fp16 MFMA operands with the 0x6400 exponent trick (a
+// 4-bit code n in the mantissa of 1024 + n) and one v_pk_fma_f16 by the
+// sub-block scale (sc * n - 1024 sc: an integer <= 1024, exact), and
+// multiplies them on v_mfma_f32_32x32x16_f16 against the step's activation
+// tile, which the workgroup double-buffers in LDS.  The activation rows are
+// laid out in exactly the K order each lane's codes arrive in (act16), so the
+// weights never pass through LDS.  Each super-block's products accumulate
+// apart (T) and join the result as acc += d * T, d exchanged per row through
+// a few bytes of LDS into the MFMA output layout (lane l holds entry l % 32,
+// rows 8 g + 4 (l / 32) + r).  Q4_K's min terms run after the loop as a small
+// MFMA product of per-row hi/lo fp16 weights (-dmin m) and fp16 hi/lo sums.
+#include <algorithm>
+#include <type_traits>
+#include "decode.h"
+#include "gemm16.h"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLdb = 72;   // halfs per LDS activation row: 64 + 8 (16-byte pad: conflict-free 16-lane reads)
+
+template <int SEM> struct q16_traits {
+    static constexpr bool A4 = SEM == SEM_Q4_K_Q8;
+    static constexpr bool GGML = SEM == SEM_Q4_K_GGML;
+    static constexpr bool Q6 = SEM == SEM_Q6_K_SEQ || SEM == SEM_Q6_K_LOWNIB;
+    static constexpr int PPS = A4 ? 128 : 256;   // activation positions per super-block
+    static constexpr int SPB = PPS / 64;         // steps per super-block
+    static constexpr int NPL = A4 ? 1 : 2;       // activation planes
+};
+
+// Bits 3 and 4 ... of a step position p: i = p >> 4 (MFMA of the step), kh = (p >> 3) & 1
+// (lane half), j = p & 7 (slot).  sw(j): slot -> byte order of the nibble pairs (j bits 0,1 swapped).
+__host__ __device__ constexpr int sw3(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
+
+// Element (within its super-block) of activation position P (within the super-block's PPS).
+template <int SEM>
+__host__ __device__ constexpr int q16_elem(int P)
+{
+    const int st = P >> 6, p = P & 63, i = p >> 4, kh = (p >> 3) & 1, j = p & 7;
+    if (SEM == SEM_Q4_K_GGML) return 64 * st + 32 * (i >> 1) + 16 * kh + 8 * (i & 1) + sw3(j);
+    if (SEM == SEM_Q4_K_Q8) return 32 * (2 * (2 * st + kh) + (i >> 1)) + 8 * (i & 1) + sw3(j);
+    if (SEM == SEM_Q6_K_SEQ) return 64 * st + 32 * kh + 8 * i + 4 * (j & 1) + (j >> 1);
+    // SEM_Q6_K_LOWNIB: step = (half h, l-half lh); quad q = kh + 2 (i >> 1)
+    return 128 * (st >> 1) + 32 * (kh + 2 * (i >> 1)) + 16 * (st & 1) + 8 * (i & 1) + sw3(j);
+}
+
+MLLM_DEV uint32_t mk(uint32_t x, int sh) { return ((x >> sh) & 0x000F000Fu) | 0x64006400u; }
+
+MLLM_DEV uint32_t scl(uint32_t w, h2 s, h2 c)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, w), s, c));
+}
+
+MLLM_DEV h2 hh(float v) { return h2{(_Float16)v, (_Float16)v}; }
+
+// Raw bytes of one row for one step.
+struct q16_raw {
+    u32x4 a;       // nibble bytes
+    u32x4 b;       // Q6_K: qh bytes (SEQ: .x, .y)
+    uint4 m;       // Q4_K: super-block metadata (kq_pairs layout); Q6_K: .x = scales (2 bytes), .y = d
+};
+
+// The step's four MFMA operands (8 fp16 each, as 4 words) and the super-block's d.
+template <int SEM>
+MLLM_DEV void q16_decode(const q16_raw &r, int st, int kh, u32x4 (&o)[4], float &d)
+{
+    if constexpr (SEM == SEM_Q4_K_GGML || SEM == SEM_Q4_K_Q8) {
+        // group g's sub-blocks 2g (low nibbles) and 2g+1 (high nibbles), QK:62-71 pairs
+        const int g = SEM == SEM_Q4_K_GGML ? st : 2 * st + kh;
+        int s1, m1, s2, m2;
+        kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
+        d = h2f(r.m.x & 0xFFFF);
+        const h2 sa = hh((float)s1), ca = hh(-1024.0f * (float)s1);
+        const h2 sb = hh((float)s2), cb = hh(-1024.0f * (float)s2);
+        const u32x4 A = r.a;
+        o[0] = u32x4{scl(mk(A.x, 0), sa, ca), scl(mk(A.x, 8), sa, ca), scl(mk(A.y, 0), sa, ca), scl(mk(A.y, 8), sa, ca)};
+        o[1] = u32x4{scl(mk(A.z, 0), sa, ca), scl(mk(A.z, 8), sa, ca), scl(mk(A.w, 0), sa, ca), scl(mk(A.w, 8), sa, ca)};
+        o[2] = u32x4{scl(mk(A.x, 4), sb, cb), scl(mk(A.x, 12), sb, cb), scl(mk(A.y, 4), sb, cb), scl(mk(A.y, 12), sb, cb)};
+        o[3] = u32x4{scl(mk(A.z, 4), sb, cb), scl(mk(A.z, 12), sb, cb), scl(mk(A.w, 4), sb, cb), scl(mk(A.w, 12), sb, cb)};
+    } else if constexpr (SEM == SEM_Q6_K_SEQ) {
+        // CE:315-378: element e = nibble (e&1) of ql[e/2] | 2 bits (e&3) of qh[e/4], minus 32, scale sc[e/16]
+        d = h2f(r.m.y);
+        const float s0 = (float)(int8_t)(r.m.x & 0xFF), s1 = (float)(int8_t)(r.m.x >> 8);
+        const h2 sa = hh(s0), ca = hh(-1056.0f * s0), sb = hh(s1), cb = hh(-1056.0f * s1);
+        const uint32_t L[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t hv = ((i < 2 ? r.b.x : r.b.y) >> (16 * (i & 1))) & 0xFFFFu;
+            const uint32_t hs = (hv & 0xFFu) | ((hv & 0xFF00u) << 8);
+            const h2 s = i < 2 ? sa : sb, c = i < 2 ? ca : cb;
+            o[i] = u32x4{scl(mk(L[i], 0) | ((hs << 4) & 0x00300030u), s, c),
+                         scl(mk(L[i], 4) | ((hs << 2) & 0x00300030u), s, c),
+                         scl(mk(L[i], 8) | (hs & 0x00300030u), s, c),
+                         scl(mk(L[i], 12) | ((hs >> 2) & 0x00300030u), s, c)};
+        }
+    } else {
+        // QK:1778-1812 (low nibble in all four quadrants): quad q = kh + 2 (i >> 1) takes qh bits 2q
+        d = h2f(r.m.y);
+        const float s0 = (float)(int8_t)(r.m.x & 0xFF), s1 = (float)(int8_t)(r.m.x >> 8);
+        const h2 sa = hh(s0), ca = hh(-1056.0f * s0), sb = hh(s1), cb = hh(-1056.0f * s1);
+        const uint32_t L[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, Q[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = kh + 2 * (i >> 1), w0 = 2 * (i & 1);
+            const uint32_t t0 = Q[w0] >> (2 * q), t1 = Q[w0 + 1] >> (2 * q);
+            const h2 s = i < 2 ? sa : sb, c = i < 2 ? ca : cb;
+            o[i] = u32x4{scl(mk(L[w0], 0) | ((t0 << 4) & 0x00300030u), s, c),
+                         scl(mk(L[w0], 8) | ((t0 >> 4) & 0x00300030u), s, c),
+                         scl(mk(L[w0 + 1], 0) | ((t1 << 4) & 0x00300030u), s, c),
+                         scl(mk(L[w0 + 1], 8) | ((t1 >> 4) & 0x00300030u), s, c)};
+        }
+    }
+}
+
+// v and its fp16 remainder: v = hi + lo (lo the fp16 rounding of v - hi).
+MLLM_DEV void split16(float v, _Float16 &hi, _Float16 &lo)
+{
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+// Q4_K min-term weights of one row for one k16 slice of the min product: 8 values at once.
+// GGML: -dmin_b * m_j for the 8 sub-blocks of super-block b (hi/lo fp16); A4: -dmin_b for
+// super-blocks b0 .. b0+7 (exact in fp16).
+template <int SEM>
+MLLM_DEV void q16_min_w(const mllm_packed &W, int nb, int row, int u0, f16x8 &hi, f16x8 &lo)
+{
+    if constexpr (SEM == SEM_Q4_K_GGML) {
+        const int b = u0 / 8;   // the 8 sub-blocks of super-block b
+        float v[8];
+        if (b < nb) {
+            const uint4 m = gld<uint4>(W.p[1] + ((long)row * nb + b) * 16);
+            const float dmin = h2f(m.x >> 16);
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                int s1, m1, s2, m2;
+                kq_pairs(m, j, s1, m1, s2, m2);
+                v[j] = -(dmin * (float)m1);
+                v[j + 1] = -(dmin * (float)m2);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 a, c;
+            split16(v[j], a, c);
+            hi[j] = a;
+            lo[j] = c;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int b = u0 + j;
+            float v = 0.0f;
+            if (b < nb) v = -h2f(gld<uint32_t>(W.p[1] + ((long)row * nb + b) * 16) >> 16);
+            hi[j] = (_Float16)v;
+            lo[j] = (_Float16)0.0f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- the GEMM
+// Byte offset loads from a wave-uniform base: the address is base (SGPRs) +
+// a 32-bit per-lane offset, so the loop issues no 64-bit address arithmetic.
+template <class T> MLLM_DEV T gldo(const void *base, uint32_t off) { return gld<T>((const uint8_t *)base + off); }
+
+template <int SEM, bool DUAL, int EB>
+__global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
+{
+    using Q = q16_traits<SEM>;
+    constexpr int RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 128, SPB = Q::SPB, NPL = Q::NPL;
+    static_assert(SPB % 2 == 0, "the LDS buffer parity follows the step parity within a super-block");
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][NPL][TM * kLdb];
+    __shared__ __attribute__((aligned(16))) float sD[4][RB * 32];
+    __shared__ int s_row[TM];
+
+    // ---- work tile (XCD-contiguous ranges of the live tiles, entry tile fastest)
+    int bx, by;
+    {
+        const int nx = gridDim.x, ny = a.tile_expert ? *a.n_tiles : (int)gridDim.y, total = nx * ny;
+        const int L = blockIdx.x + nx * blockIdx.y;
+        if (L >= total) return;
+        const int xcd = L & 7;
+        const int w = xcd * (total >> 3) + min(xcd, total & 7) + (L >> 3);
+        by = w % ny;
+        bx = w / ny;
+    }
+    int p0, p1;
+    mllm_packed W, W2;
+    if (a.tile_expert) {
+        const int e = a.tile_expert[by];
+        p0 = a.tile_begin[by];
+        p1 = a.tile_end[by];
+        W = a.table[e];
+        if constexpr (DUAL) W2 = a.table2[e];
+    } else {
+        p0 = by * TM;
+        p1 = min(p0 + TM, a.n_entries);
+        W = a.W;
+        if constexpr (DUAL) W2 = a.W2;
+    }
+    const int n_ent = __builtin_amdgcn_readfirstlane(p1 - p0);
+    if (n_ent <= 0) return;
+    const int n0 = bx * TN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 31, kh = lane >> 5;
+    int lo_any = 0;
+    if (tid < TM) {
+        const int row = tid < n_ent ? (a.row_of ? a.row_of[p0 + tid] : p0 + tid) : (a.row_of ? a.row_of[p0] : p0);
+        s_row[tid] = row;
+        if (NPL > 1) lo_any = tid < n_ent && a.x.lo_nz[row] != 0;
+    }
+    lo_any = __syncthreads_or(lo_any);
+    const int npl = __builtin_amdgcn_readfirstlane(NPL > 1 && lo_any ? 2 : 1);
+    const int neb = __builtin_amdgcn_readfirstlane(min(EB, (n_ent + 31) / 32));   // entry blocks holding entries
+
+    const int nb = a.n_cols / 256;
+    // super-blocks of this workgroup: all, or split z of a.ksplit (whole super-blocks: d joins per block)
+    int b_beg = 0, b_end = nb;
+    if (a.ksplit > 1) {
+        const int bpp = (nb + a.ksplit - 1) / a.ksplit;
+        b_beg = min(nb, (int)blockIdx.z * bpp);
+        b_end = min(nb, b_beg + bpp);
+    }
+    const int wrow = min(n0 + 32 * wave + lr, a.n_rows - 1);   // the row this lane decodes
+
+    // per-lane byte offsets (the step's part is added to the wave-uniform base)
+    constexpr int NCH = TM * 8 / 256;   // activation chunks per thread and plane
+    uint32_t boff[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int ch = tid + 256 * c;
+        boff[c] = (uint32_t)s_row[ch >> 3] * (uint32_t)(a.x.ldh * 2) + 16u * (ch & 7);
+    }
+    // weight rows: bulk plane bytes per super-block (Q4_K / Q6_K ql: 128) and per-row offsets
+    const uint32_t rq = (uint32_t)wrow * (uint32_t)nb;   // row's first super-block index
+    auto fetch_w = [&](const mllm_packed &M, int s, q16_raw &r) __attribute__((always_inline)) {
+        const int b = s / SPB, st = s % SPB;
+        const uint32_t bi = rq + (uint32_t)b;
+        if constexpr (SEM == SEM_Q4_K_GGML) {
+            r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
+            r.m = gldo<uint4>(M.p[1], bi * 16u);
+        } else if constexpr (SEM == SEM_Q4_K_Q8) {
+            r.a = gldo<u32x4>(M.p[0] + 64 * st, bi * 128u + 32u * kh);
+            r.m = gldo<uint4>(M.p[1], bi * 16u);
+        } else if constexpr (SEM == SEM_Q6_K_SEQ) {
+            r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
+            const uint2 q = gldo<uint2>(M.p[1] + 16 * st, bi * 64u + 8u * kh);
+            r.b.x = q.x; r.b.y = q.y;
+            r.m.x = gldo<uint16_t>(M.p[2] + 4 * st, bi * 16u + 2u * kh);
+            r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+        } else {   // SEM_Q6_K_LOWNIB
+            const int h = st >> 1, lh = st & 1;
+            r.a = gldo<u32x4>(M.p[0] + 64 * h + 16 * lh, bi * 128u + 32u * kh);
+            r.b = gldo<u32x4>(M.p[1] + 32 * h + 16 * lh, bi * 64u);
+            const uint32_t so = bi * 16u + 2u * kh;
+            r.m.x = gldo<uint8_t>(M.p[2] + 8 * h + lh, so) | ((uint32_t)gldo<uint8_t>(M.p[2] + 8 * h + lh + 4, so) << 8);
+            r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+        }
+    };
+
+    f32x16 acc[RB][EB], T[RB][EB];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int e = 0; e < EB; e++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) { acc[r][e][v] = 0.0f; T[r][e][v] = 0.0f; }
+
+    auto fetch_b = [&](int s, uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+        const _Float16 *base = a.x.h + 64 * (long)s;
+#pragma unroll
+        for (int p = 0; p < NPL; p++)
+#pragma unroll
+            for (int c = 0; c < NCH; c++)
+                if (p < npl) bx_[p][c] = gldo<uint4>(base + p * a.x.hplane, boff[c]);
+    };
+    auto store_b = [&](int buf, const uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < NPL; p++)
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const int ch = tid + 256 * c, e = ch >> 3, pc = ch & 7;
+                if (p < npl) *reinterpret_cast<uint4 *>(&sB[buf][p][e * kLdb + 8 * pc]) = bx_[p][c];
+            }
+    };
+    // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0)
+    auto mfmas = [&](auto st_c, const q16_raw (&r)[RB]) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value, buf = st & 1;
+        u32x4 A[RB][4];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            float d;
+            q16_decode<SEM>(r[rb], st, kh, A[rb], d);
+            if (st == 0 && kh == 0) sD[wave][rb * 32 + lr] = d;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < EB; e++) {
+                if (e >= neb) continue;
+#pragma unroll
+                for (int p = 0; p < NPL; p++) {
+                    if (p >= npl) continue;
+                    const f16x8 bv = *reinterpret_cast<const f16x8 *>(&sB[buf][p][(32 * e + lr) * kLdb + 16 * i + 8 * kh]);
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) {
+                        const f32x16 c = (st == 0 && i == 0 && p == 0) ? f32x16{} : T[rb][e];
+                        T[rb][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A[rb][i]), bv, c,
+                                                                          0, 0, 0);
+                    }
+                }
+            }
+    };
+    auto d_apply = [&]() __attribute__((always_inline)) {
+        // the super-block's d, per output row (rows 8 g + 4 kh + r of the lane's 16)
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            float dv[16];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 q = *reinterpret_cast<const float4 *>(&sD[wave][rb * 32 + 8 * g + 4 * kh]);
+                dv[4 * g] = q.x; dv[4 * g + 1] = q.y; dv[4 * g + 2] = q.z; dv[4 * g + 3] = q.w;
+            }
+#pragma unroll
+            for (int e = 0; e < EB; e++) {
+                if (e >= neb) continue;
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(dv[v], T[rb][e][v], acc[rb][e][v]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    if (b_beg < b_end) {
+        const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
+        uint4 bx[NPL][NCH];
+        q16_raw rw[2][RB];
+        auto fw = [&](int s, q16_raw (&r)[RB]) __attribute__((always_inline)) {
+            const int sc = min(s, s_last);
+            fetch_w(W, sc, r[0]);
+            if constexpr (DUAL) fetch_w(W2, sc, r[1]);
+        };
+        fw(s_beg, rw[0]);
+        fetch_b(s_beg, bx);
+        store_b(0, bx);
+        fetch_b(min(s_beg + 1, s_last), bx);
+        __syncthreads();
+        for (int b = b_beg; b < b_end; b++) {
+            const int s0 = b * SPB;
+            // step st: prefetch the next step's weights, run this step, stage the next
+            // step's activations into the other buffer and fetch the one after
+            auto one = [&](auto st_c) __attribute__((always_inline)) {
+                constexpr int st = decltype(st_c)::value;
+                const int s = s0 + st;
+                fw(s + 1, rw[(st + 1) & 1]);
+                mfmas(st_c, rw[st & 1]);
+                if (s < s_last) {
+                    store_b((st + 1) & 1, bx);
+                    fetch_b(min(s + 2, s_last), bx);
+                }
+                __syncthreads();
+            };
+            one(std::integral_constant<int, 0>{});
+            one(std::integral_constant<int, 1>{});
+            if constexpr (SPB == 4) {
+                one(std::integral_constant<int, 2>{});
+                one(std::integral_constant<int, 3>{});
+            }
+            d_apply();
+        }
+    }
+
+    // ---- Q4_K min terms (split 0 only): acc += sum over units of (-dmin m) (x) sums
+    if constexpr (Q::GGML || Q::A4) {
+        if (blockIdx.z == 0) {
+            const int nu = Q::GGML ? nb * 8 : nb;                 // sub-blocks / super-blocks
+            for (int u0 = 0; u0 < nu; u0 += 16) {
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    f16x8 whi, wlo;
+                    q16_min_w<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, whi, wlo);
+#pragma unroll
+                    for (int e = 0; e < EB; e++) {
+                        if (e >= neb) continue;
+                        const long er = s_row[32 * e + lr];
+                        const _Float16 *mp = a.x.m + er * a.x.ldm + u0 + 8 * kh;
+                        const f16x8 s0 = __builtin_bit_cast(f16x8, gld<u32x4>(mp));
+                        const f16x8 s1 = __builtin_bit_cast(f16x8, gld<u32x4>(mp + a.x.mplane));
+                        f32x16 t = u0 == 0 ? f32x16{} : T[rb][e];
+                        t = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi, s0, t, 0, 0, 0);
+                        t = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi, s1, t, 0, 0, 0);
+                        if constexpr (Q::GGML) t = __builtin_amdgcn_mfma_f32_32x32x16_f16(wlo, s0, t, 0, 0, 0);
+                        T[rb][e] = t;
+                    }
+                }
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int e = 0; e < EB; e++) {
+                    if (e >= neb) continue;
+                    const float im = Q::A4 ? a.x.inv_m[s_row[32 * e + lr]] : 1.0f;
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(im, T[rb][e][v], acc[rb][e][v]);
+                }
+        }
+    }
+
+    // ---- epilogue
+    float *out = a.out;
+    long ldo = a.ldo;
+    if (a.ksplit > 1) { out = a.part + (long)blockIdx.z * a.n_entries * a.n_rows; ldo = a.n_rows; }
+#pragma unroll
+    for (int e = 0; e < EB; e++) {
+        const int ent = 32 * e + lr;
+        if (ent >= n_ent) continue;
+        const float is = a.x.inv_s[s_row[ent]];
+        const long orow = a.out_row ? a.out_row[p0 + ent] : (long)(p0 + ent);
+        float *o = out + orow * ldo;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int n = n0 + 32 * wave + 8 * g + 4 * kh;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float x0 = acc[0][e][4 * g + r] * is;
+                if constexpr (DUAL) {
+                    // moe_forward_omp SiLU (QK:2157-2164): clamp to +-80, then silu(g) * u
+                    if (a.clamp_silu) x0 = fminf(fmaxf(x0, -80.0f), 80.0f);
+                    x0 = (x0 / (1.0f + expf(-x0))) * (acc[DUAL ? 1 : 0][e][4 * g + r] * is);
+                }
+                v[r] = x0;
+            }
+            if (n + 3 < a.n_rows && (ldo & 3) == 0) {
+                *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (n + r < a.n_rows) o[n + r] = v[r];
+            }
+        }
+    }
+}
+
+// out[e][n] = sum over z < ks of part[z][e][n], in order.
+__global__ void k_q16_ksum(const float *__restrict__ part, int ks, long plane, int n_rows, float *__restrict__ out,
+                           int ldo)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= plane) return;
+    float v = part[i];
+    for (int z = 1; z < ks; z++) v += part[z * plane + i];
+    const long e = i / n_rows, n = i - e * n_rows;
+    out[e * ldo + n] = v;
+}
+
+// ---------------------------------------------------------------- activations
+// fp32 row -> scaled fp16 planes in the semantic's K order, the row's inverse
+// scale, lo_nz, and (Q4_K ggml) the fp16 hi/lo sums of each 32-element
+// sub-block.  One workgroup per row.
+template <int SEM>
+__global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int ldx, int K, act16 a)
+{
+    using Q = q16_traits<SEM>;
+    __shared__ float red[4];
+    __shared__ int nzs[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (long)row * ldx;
+    const int nb = K / 256, kused = nb * 256;
+    // largest finite |x| (a NaN fails the comparison and is skipped)
+    float m = 0.0f;
+    for (int k = tid; k < kused; k += 256) {
+        const float v = fabsf(xr[k]);
+        if (v < INFINITY) m = fmaxf(m, v);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // s = 2^(9 - e) puts the largest element in [2^8, 2^9) (m = f 2^e, f in [0.5, 1))
+    int e = 0;
+    if (m > 0.0f) (void)frexpf(m, &e);
+    e = max(e, -117);
+    const float s = m > 0.0f ? ldexpf(1.0f, 9 - e) : 1.0f;
+    const float inv = m > 0.0f ? ldexpf(1.0f, e - 9) : 1.0f;
+    int nz = 0;
+    _Float16 *h0 = a.h + (long)row * a.ldh, *h1 = h0 + a.hplane;
+    for (int P = 8 * tid; P < a.ldh; P += 2048) {
+        f16x8 v0, v1;
+        const int sb = P / Q::PPS, pw = P % Q::PPS;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = sb < nb ? xr[sb * 256 + q16_elem<SEM>(pw + j)] * s : 0.0f;
+            _Float16 hi, lo;
+            split16(v, hi, lo);
+            v0[j] = hi;
+            v1[j] = lo;
+            nz |= (float)lo != 0.0f;
+        }
+        *reinterpret_cast<f16x8 *>(h0 + P) = v0;
+        *reinterpret_cast<f16x8 *>(h1 + P) = v1;
+    }
+    if constexpr (Q::GGML) {
+        _Float16 *m0 = a.m + (long)row * a.ldm, *m1 = m0 + a.mplane;
+        for (int j = tid; j < a.ldm; j += 256) {
+            float sum = 0.0f;
+            if (j < nb * 8)
+                for (int k = 0; k < 32; k++) sum += xr[32 * j + k] * s;
+            _Float16 hi, lo;
+            split16(sum, hi, lo);
+            m0[j] = hi;
+            m1[j] = lo;
+        }
+    }
+    nz = __syncthreads_or(nz);
+    if (tid == 0) {
+        a.lo_nz[row] = nz;
+        a.inv_s[row] = inv;
+    }
+    (void)nzs;
+}
+
+// Q4_K x Q8_0 (dot_q4_k_q8_0): the Q8_0 quants of elements 32 j + k, k < 16,
+// as fp16 in the K order; u_b = sum over the 8 sub-blocks of super-block b of
+// the Q8_0 min-term sums (QK:1714-1732) as scaled fp16 hi/lo.
+__global__ __launch_bounds__(256) void k_act16_q8(mllm_xq xq, int K, act16 a)
+{
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int nb = K / 256, nbk = K / 32;
+    const int8_t *q = xq.q + (long)row * nbk * 32;
+    _Float16 *h0 = a.h + (long)row * a.ldh;
+    for (int P = 8 * tid; P < a.ldh; P += 2048) {
+        f16x8 v0;
+        const int sb = P / 128, pw = P % 128;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            v0[j] = sb < nb ? (_Float16)(float)q[sb * 256 + q16_elem<SEM_Q4_K_Q8>(pw + j)] : (_Float16)0.0f;
+        *reinterpret_cast<f16x8 *>(h0 + P) = v0;
+    }
+    // super-block sums and their scale: largest |u| into [2^10, 2^11)
+    float u = 0.0f;
+    if (tid < nb) {
+        const float *s4 = xq.s4 + (long)row * nbk + 8 * tid;
+#pragma unroll
+        for (int j = 0; j < 8; j++) u += s4[j];
+    }
+    float m = tid < nb && fabsf(u) < INFINITY ? fabsf(u) : 0.0f;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (m > 0.0f) (void)frexpf(m, &e);
+    e = max(e, -115);
+    const float s = m > 0.0f ? ldexpf(1.0f, 11 - e) : 1.0f;
+    _Float16 *m0 = a.m + (long)row * a.ldm, *m1 = m0 + a.mplane;
+    for (int j = tid; j < a.ldm; j += 256) {
+        _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
+        if (j < nb) split16((j == tid ? u : 0.0f) * s, hi, lo);
+        m0[j] = hi;
+        m1[j] = lo;
+    }
+    if (tid == 0) {
+        a.lo_nz[row] = 0;
+        a.inv_s[row] = 1.0f;
+        a.inv_m[row] = m > 0.0f ? ldexpf(1.0f, e - 11) : 1.0f;
+    }
+}
+
+size_t al256(size_t n) { return (n + 255) / 256 * 256; }
+
+template <int SEM, bool DUAL, int EB>
+hipError_t launch16(const q16_args &a, int max_tiles, hipStream_t st)
+{
+    constexpr int TM = 32 * EB;
+    const int ks = (a.ksplit > 1 && !DUAL && !a.tile_expert && !a.out_row) ? a.ksplit : 1;
+    dim3 grid((a.n_rows + 127) / 128, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
+    if (grid.y == 0) return hipSuccess;
+    q16_args b = a;
+    b.ksplit = ks;
+    hipLaunchKernelGGL((k_q16<SEM, DUAL, EB>), grid, dim3(256), 0, st, b);
+    if (ks > 1) {
+        const long plane = (long)a.n_entries * a.n_rows;
+        hipLaunchKernelGGL(k_q16_ksum, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part, ks, plane,
+                           a.n_rows, a.out, a.ldo);
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+bool mllm_q16_supported(int sem)
+{
+    return sem == SEM_Q4_K_GGML || sem == SEM_Q4_K_Q8 || sem == SEM_Q6_K_SEQ || sem == SEM_Q6_K_LOWNIB;
+}
+
+// Activation layout: h [planes][rows][ldh] | m [2][rows][ldm] | inv_s | inv_m | lo_nz.
+static void act16_dims(int sem, int K, int &nplanes, int &ldh, int &ldm)
+{
+    const int nb = K / 256;
+    const bool a4 = sem == SEM_Q4_K_Q8;
+    nplanes = a4 ? 1 : 2;
+    ldh = nb * (a4 ? 128 : 256);
+    ldm = sem == SEM_Q4_K_GGML ? (nb * 8 + 15) / 16 * 16 : a4 ? (nb + 15) / 16 * 16 : 0;
+    if (ldh == 0) ldh = 64;
+}
+
+size_t mllm_act16_bytes(int sem, long rows, int K)
+{
+    int np, ldh, ldm;
+    act16_dims(sem, K, np, ldh, ldm);
+    return al256((size_t)np * rows * ldh * 2) + al256((size_t)2 * rows * ldm * 2) + 3 * al256((size_t)rows * 4);
+}
+
+act16 mllm_act16_carve(int sem, void *ws, long rows, int K)
+{
+    int np, ldh, ldm;
+    act16_dims(sem, K, np, ldh, ldm);
+    uint8_t *p = (uint8_t *)ws;
+    act16 a{};
+    a.h = (_Float16 *)p;
+    a.hplane = (long)rows * ldh;
+    a.ldh = ldh;
+    p += al256((size_t)np * rows * ldh * 2);
+    a.m = ldm ? (_Float16 *)p : nullptr;
+    a.mplane = (long)rows * ldm;
+    a.ldm = ldm;
+    p += al256((size_t)2 * rows * ldm * 2);
+    a.inv_s = (float *)p;
+    p += al256((size_t)rows * 4);
+    a.inv_m = (float *)p;
+    p += al256((size_t)rows * 4);
+    a.lo_nz = (int *)p;
+    return a;
+}
+
+hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq, int rows, int K, const act16 &act,
+                             hipStream_t st)
+{
+    if (rows <= 0) return hipSuccess;
+    if (K < 256 || K % 256 || ((uintptr_t)act.h & 15)) return hipErrorInvalidValue;
+    switch (sem) {
+    case SEM_Q4_K_GGML: hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q6_K_SEQ: hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q6_K_LOWNIB: hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q4_K_Q8:
+        if (!xq || K / 256 > 256) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_act16_q8, dim3(rows), dim3(256), 0, st, *xq, K, act);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Dense launches take 128-entry tiles once there are 256 entries, else 64;
+// grouped launches the bucketing's 64-entry tiles.
+int mllm_q16_tile_entries(bool grouped, int n_entries) { return !grouped && n_entries >= 256 ? 128 : 64; }
+
+// Split along K (whole super-blocks) while a dense launch has fewer than two
+// tiles per CU (512), each split keeping at least 4 super-blocks.
+int mllm_q16_ksplit(int sem, int n_rows, int n_cols, int n_entries)
+{
+    if (!mllm_q16_supported(sem) || n_entries <= 0) return 1;
+    const int tm = mllm_q16_tile_entries(false, n_entries);
+    const long tiles = (long)((n_rows + 127) / 128) * ((n_entries + tm - 1) / tm);
+    if (tiles >= 384) return 1;
+    const int nb = n_cols / 256;
+    int ks = (int)(512 / tiles);
+    ks = std::min(ks, std::max(1, nb / 4));
+    return std::max(1, std::min(ks, 8));
+}
+
+hipError_t mllm_launch_q16(int sem, bool dual, const q16_args &a, int max_tiles, hipStream_t st)
+{
+    if (a.n_cols < 256 || a.n_cols % 256) return hipErrorInvalidValue;
+    const bool grouped = a.tile_expert != nullptr;
+    const int tm = mllm_q16_tile_entries(grouped, a.n_entries);
+#define Q16(S)                                                                         \
+    if (sem == S) {                                                                    \
+        if (dual) return launch16<S, true, 2>(a, max_tiles, st);                       \
+        return tm == 128 ? launch16<S, false, 4>(a, max_tiles, st) : launch16<S, false, 2>(a, max_tiles, st); \
+    }
+    Q16(SEM_Q4_K_GGML)
+    Q16(SEM_Q4_K_Q8)
+    Q16(SEM_Q6_K_SEQ)
+    Q16(SEM_Q6_K_LOWNIB)
+#undef Q16
+    return hipErrorInvalidValue;
+}

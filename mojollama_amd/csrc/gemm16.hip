@@ -59,6 +59,17 @@ __host__ __device__ constexpr int q16_elem(int P)
 
 MLLM_DEV uint32_t mk(uint32_t x, int sh) { return ((x >> sh) & 0x000F000Fu) | 0x64006400u; }
 
+// 0x6400 in both halves: fp16 1024, whose ulp is 1 (a code in mantissa bits 0..9 adds to it).
+constexpr uint32_t kMagic = 0x64006400u;
+
+// (x & m) | c in one VOP3 instruction (m from an SGPR, c from a VGPR: gfx9 VOP3 takes no literal).
+MLLM_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+    return r;
+}
+
 MLLM_DEV uint32_t scl(uint32_t w, h2 s, h2 c)
 {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, w), s, c));
@@ -83,13 +94,24 @@ MLLM_DEV void q16_decode(const q16_raw &r, int st, int kh, u32x4 (&o)[4], float 
         int s1, m1, s2, m2;
         kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
         d = h2f(r.m.x & 0xFFFF);
+        // low nibbles (bits 0-3 of each half) give 1024 + n: sa n = (1024 + n) sa - 1024 sa;
+        // high nibbles stay in bits 4-7 and give 1024 + 16 n: sb n = (1024 + 16 n) (sb / 16) - 64 sb
         const h2 sa = hh((float)s1), ca = hh(-1024.0f * (float)s1);
-        const h2 sb = hh((float)s2), cb = hh(-1024.0f * (float)s2);
-        const u32x4 A = r.a;
-        o[0] = u32x4{scl(mk(A.x, 0), sa, ca), scl(mk(A.x, 8), sa, ca), scl(mk(A.y, 0), sa, ca), scl(mk(A.y, 8), sa, ca)};
-        o[1] = u32x4{scl(mk(A.z, 0), sa, ca), scl(mk(A.z, 8), sa, ca), scl(mk(A.w, 0), sa, ca), scl(mk(A.w, 8), sa, ca)};
-        o[2] = u32x4{scl(mk(A.x, 4), sb, cb), scl(mk(A.x, 12), sb, cb), scl(mk(A.y, 4), sb, cb), scl(mk(A.y, 12), sb, cb)};
-        o[3] = u32x4{scl(mk(A.z, 4), sb, cb), scl(mk(A.z, 12), sb, cb), scl(mk(A.w, 4), sb, cb), scl(mk(A.w, 12), sb, cb)};
+        const h2 sb = hh((float)s2 * 0.0625f), cb = hh(-64.0f * (float)s2);
+        const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t y = w[q] >> 8;
+            lo[2 * q] = scl(and_or(w[q], 0x000F000Fu, kMagic), sa, ca);
+            lo[2 * q + 1] = scl(and_or(y, 0x000F000Fu, kMagic), sa, ca);
+            hi[2 * q] = scl(and_or(w[q], 0x00F000F0u, kMagic), sb, cb);
+            hi[2 * q + 1] = scl(and_or(y, 0x00F000F0u, kMagic), sb, cb);
+        }
+        o[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        o[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+        o[2] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        o[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
     } else if constexpr (SEM == SEM_Q6_K_SEQ) {
         // CE:315-378: element e = nibble (e&1) of ql[e/2] | 2 bits (e&3) of qh[e/4], minus 32, scale sc[e/16]
         d = h2f(r.m.y);
@@ -227,7 +249,6 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     }
     lo_any = __syncthreads_or(lo_any);
     const int npl = __builtin_amdgcn_readfirstlane(NPL > 1 && lo_any ? 2 : 1);
-    const int neb = __builtin_amdgcn_readfirstlane(min(EB, (n_ent + 31) / 32));   // entry blocks holding entries
 
     const int nb = a.n_cols / 256;
     // super-blocks of this workgroup: all, or split z of a.ksplit (whole super-blocks: d joins per block)
@@ -282,25 +303,29 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
             for (int v = 0; v < 16; v++) { acc[r][e][v] = 0.0f; T[r][e][v] = 0.0f; }
 
-    auto fetch_b = [&](int s, uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+    // NP: the activation planes this tile multiplies (1 when no row of the tile has a second)
+    auto fetch_b = [&](auto np_c, int s, uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value;
         const _Float16 *base = a.x.h + 64 * (long)s;
 #pragma unroll
-        for (int p = 0; p < NPL; p++)
+        for (int p = 0; p < NP; p++)
 #pragma unroll
-            for (int c = 0; c < NCH; c++)
-                if (p < npl) bx_[p][c] = gldo<uint4>(base + p * a.x.hplane, boff[c]);
+            for (int c = 0; c < NCH; c++) bx_[p][c] = gldo<uint4>(base + p * a.x.hplane, boff[c]);
     };
-    auto store_b = [&](int buf, const uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+    auto store_b = [&](auto np_c, int buf, const uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value;
 #pragma unroll
-        for (int p = 0; p < NPL; p++)
+        for (int p = 0; p < NP; p++)
 #pragma unroll
             for (int c = 0; c < NCH; c++) {
                 const int ch = tid + 256 * c, e = ch >> 3, pc = ch & 7;
-                if (p < npl) *reinterpret_cast<uint4 *>(&sB[buf][p][e * kLdb + 8 * pc]) = bx_[p][c];
+                *reinterpret_cast<uint4 *>(&sB[buf][p][e * kLdb + 8 * pc]) = bx_[p][c];
             }
     };
-    // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0)
-    auto mfmas = [&](auto st_c, const q16_raw (&r)[RB]) __attribute__((always_inline)) {
+    // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0).  Entry
+    // blocks past the tile's entries run on copies of its first row; the epilogue drops them.
+    auto mfmas = [&](auto np_c, auto st_c, const q16_raw (&r)[RB]) __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value;
         constexpr int st = decltype(st_c)::value, buf = st & 1;
         u32x4 A[RB][4];
 #pragma unroll
@@ -313,10 +338,8 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int e = 0; e < EB; e++) {
-                if (e >= neb) continue;
 #pragma unroll
-                for (int p = 0; p < NPL; p++) {
-                    if (p >= npl) continue;
+                for (int p = 0; p < NP; p++) {
                     const f16x8 bv = *reinterpret_cast<const f16x8 *>(&sB[buf][p][(32 * e + lr) * kLdb + 16 * i + 8 * kh]);
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++) {
@@ -339,16 +362,14 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                 dv[4 * g] = q.x; dv[4 * g + 1] = q.y; dv[4 * g + 2] = q.z; dv[4 * g + 3] = q.w;
             }
 #pragma unroll
-            for (int e = 0; e < EB; e++) {
-                if (e >= neb) continue;
+            for (int e = 0; e < EB; e++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(dv[v], T[rb][e][v], acc[rb][e][v]);
-            }
         }
         __builtin_amdgcn_wave_barrier();
     };
 
-    if (b_beg < b_end) {
+    auto main_loop = [&](auto np_c) __attribute__((always_inline)) {
         const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
         uint4 bx[NPL][NCH];
         q16_raw rw[2][RB];
@@ -358,23 +379,22 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             if constexpr (DUAL) fetch_w(W2, sc, r[1]);
         };
         fw(s_beg, rw[0]);
-        fetch_b(s_beg, bx);
-        store_b(0, bx);
-        fetch_b(min(s_beg + 1, s_last), bx);
+        fetch_b(np_c, s_beg, bx);
+        store_b(np_c, 0, bx);
+        fetch_b(np_c, min(s_beg + 1, s_last), bx);
         __syncthreads();
         for (int b = b_beg; b < b_end; b++) {
             const int s0 = b * SPB;
             // step st: prefetch the next step's weights, run this step, stage the next
-            // step's activations into the other buffer and fetch the one after
+            // step's activations into the other buffer (after the last step: a copy
+            // nobody reads) and fetch the one after
             auto one = [&](auto st_c) __attribute__((always_inline)) {
                 constexpr int st = decltype(st_c)::value;
                 const int s = s0 + st;
                 fw(s + 1, rw[(st + 1) & 1]);
-                mfmas(st_c, rw[st & 1]);
-                if (s < s_last) {
-                    store_b((st + 1) & 1, bx);
-                    fetch_b(min(s + 2, s_last), bx);
-                }
+                mfmas(np_c, st_c, rw[st & 1]);
+                store_b(np_c, (st + 1) & 1, bx);
+                fetch_b(np_c, min(s + 2, s_last), bx);
                 __syncthreads();
             };
             one(std::integral_constant<int, 0>{});
@@ -385,6 +405,10 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             }
             d_apply();
         }
+    };
+    if (b_beg < b_end) {
+        if (NPL > 1 && npl > 1) main_loop(std::integral_constant<int, NPL>{});
+        else main_loop(std::integral_constant<int, 1>{});
     }
 
     // ---- Q4_K min terms (split 0 only): acc += sum over units of (-dmin m) (x) sums
@@ -398,7 +422,6 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                     q16_min_w<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, whi, wlo);
 #pragma unroll
                     for (int e = 0; e < EB; e++) {
-                        if (e >= neb) continue;
                         const long er = s_row[32 * e + lr];
                         const _Float16 *mp = a.x.m + er * a.x.ldm + u0 + 8 * kh;
                         const f16x8 s0 = __builtin_bit_cast(f16x8, gld<u32x4>(mp));
@@ -415,7 +438,6 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             for (int rb = 0; rb < RB; rb++)
 #pragma unroll
                 for (int e = 0; e < EB; e++) {
-                    if (e >= neb) continue;
                     const float im = Q::A4 ? a.x.inv_m[s_row[32 * e + lr]] : 1.0f;
 #pragma unroll
                     for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(im, T[rb][e][v], acc[rb][e][v]);
@@ -480,16 +502,46 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
 {
     using Q = q16_traits<SEM>;
     __shared__ float red[4];
-    __shared__ int nzs[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *xr = x + (long)row * ldx;
+    const bool vec = ((uintptr_t)xr & 15) == 0;
     const int nb = K / 256, kused = nb * 256;
+    // eight consecutive elements from k (a multiple of 8)
+    auto ld8 = [&](int k, float (&v)[8]) __attribute__((always_inline)) {
+        if (vec) {
+            const float4 p = *reinterpret_cast<const float4 *>(xr + k), q = *reinterpret_cast<const float4 *>(xr + k + 4);
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = xr[k + j];
+        }
+    };
+    // thread t takes positions P = 8 t + 2048 it (it < nit): eight positions hold one
+    // aligned group of 8 elements, in the order q16_elem gives (base + q16_elem(j)).
+    // The first kHeld groups stay in registers between the two passes.
+    constexpr int kHeld = 4;
+    const int nit = (a.ldh - 8 * tid + 2047) / 2048;
+    auto gbase = [&](int P) __attribute__((always_inline)) { return (P / Q::PPS) * 256 + q16_elem<SEM>(P % Q::PPS); };
+    float g[kHeld][8];
     // largest finite |x| (a NaN fails the comparison and is skipped)
     float m = 0.0f;
-    for (int k = tid; k < kused; k += 256) {
-        const float v = fabsf(xr[k]);
-        if (v < INFINITY) m = fmaxf(m, v);
+    auto mx = [&](const float (&v)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (fabsf(v[j]) < INFINITY) m = fmaxf(m, fabsf(v[j]));
+    };
+#pragma unroll
+    for (int it = 0; it < kHeld; it++)
+        if (it < nit) {
+            ld8(gbase(8 * tid + 2048 * it), g[it]);
+            mx(g[it]);
+        }
+    for (int it = kHeld; it < nit; it++) {
+        float v[8];
+        ld8(gbase(8 * tid + 2048 * it), v);
+        mx(v);
     }
+    (void)kused;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -503,31 +555,47 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     const float inv = m > 0.0f ? ldexpf(1.0f, e - 9) : 1.0f;
     int nz = 0;
     _Float16 *h0 = a.h + (long)row * a.ldh, *h1 = h0 + a.hplane;
-    for (int P = 8 * tid; P < a.ldh; P += 2048) {
-        f16x8 v0, v1;
+    auto emit = [&](int P, const float (&gv)[8]) __attribute__((always_inline)) {
         const int sb = P / Q::PPS, pw = P % Q::PPS;
+        f16x8 v0, v1;
+        float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float v = sb < nb ? xr[sb * 256 + q16_elem<SEM>(pw + j)] * s : 0.0f;
+            const float v = gv[q16_elem<SEM>(j)] * s;
             _Float16 hi, lo;
             split16(v, hi, lo);
             v0[j] = hi;
             v1[j] = lo;
             nz |= (float)lo != 0.0f;
+            part += gv[j] * s;
         }
         *reinterpret_cast<f16x8 *>(h0 + P) = v0;
         *reinterpret_cast<f16x8 *>(h1 + P) = v1;
+        if constexpr (Q::GGML) {
+            // sub-block 8 sb + 2 (pw / 64) + (pw / 32) % 2: the four groups of threads 4q .. 4q+3
+            part += __shfl_xor(part, 1, 64);
+            part += __shfl_xor(part, 2, 64);
+            if ((tid & 3) == 0) {
+                const int j = 8 * sb + pw / 32;
+                _Float16 hi, lo;
+                split16(part, hi, lo);
+                a.m[(long)row * a.ldm + j] = hi;
+                a.m[a.mplane + (long)row * a.ldm + j] = lo;
+            }
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < kHeld; it++)
+        if (it < nit) emit(8 * tid + 2048 * it, g[it]);
+    for (int it = kHeld; it < nit; it++) {
+        float v[8];
+        ld8(gbase(8 * tid + 2048 * it), v);
+        emit(8 * tid + 2048 * it, v);
     }
     if constexpr (Q::GGML) {
-        _Float16 *m0 = a.m + (long)row * a.ldm, *m1 = m0 + a.mplane;
-        for (int j = tid; j < a.ldm; j += 256) {
-            float sum = 0.0f;
-            if (j < nb * 8)
-                for (int k = 0; k < 32; k++) sum += xr[32 * j + k] * s;
-            _Float16 hi, lo;
-            split16(sum, hi, lo);
-            m0[j] = hi;
-            m1[j] = lo;
+        for (int j = nb * 8 + tid; j < a.ldm; j += 256) {
+            a.m[(long)row * a.ldm + j] = (_Float16)0.0f;
+            a.m[a.mplane + (long)row * a.ldm + j] = (_Float16)0.0f;
         }
     }
     nz = __syncthreads_or(nz);
@@ -535,7 +603,6 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
         a.lo_nz[row] = nz;
         a.inv_s[row] = inv;
     }
-    (void)nzs;
 }
 
 // Q4_K x Q8_0 (dot_q4_k_q8_0): the Q8_0 quants of elements 32 j + k, k < 16,
@@ -551,9 +618,12 @@ __global__ __launch_bounds__(256) void k_act16_q8(mllm_xq xq, int K, act16 a)
     for (int P = 8 * tid; P < a.ldh; P += 2048) {
         f16x8 v0;
         const int sb = P / 128, pw = P % 128;
+        const uint2 w = *reinterpret_cast<const uint2 *>(q + sb * 256 + q16_elem<SEM_Q4_K_Q8>(pw));
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            v0[j] = sb < nb ? (_Float16)(float)q[sb * 256 + q16_elem<SEM_Q4_K_Q8>(pw + j)] : (_Float16)0.0f;
+        for (int j = 0; j < 8; j++) {
+            const int t = q16_elem<SEM_Q4_K_Q8>(j);
+            v0[j] = (_Float16)(float)(int8_t)(((t < 4 ? w.x : w.y) >> (8 * (t & 3))) & 0xFF);
+        }
         *reinterpret_cast<f16x8 *>(h0 + P) = v0;
     }
     // super-block sums and their scale: largest |u| into [2^10, 2^11)

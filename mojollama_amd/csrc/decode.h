@@ -45,6 +45,14 @@ template <> struct gld_impl<uint4> {
         return make_uint4(v.x, v.y, v.z, v.w);
     }
 };
+typedef unsigned int mllm_u32x3 __attribute__((ext_vector_type(3)));
+template <> struct gld_impl<uint3> {
+    static MLLM_DEV uint3 load(const void *p)
+    {
+        const mllm_u32x3 v = *(const MLLM_GLOBAL mllm_u32x3 *)p;
+        return make_uint3(v.x, v.y, v.z);
+    }
+};
 template <> struct gld_impl<uint2> {
     static MLLM_DEV uint2 load(const void *p)
     {

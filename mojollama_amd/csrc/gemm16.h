@@ -38,6 +38,7 @@ struct act16 {
     float *inv_s;      // [rows]: 1 / the row's power-of-two scale (Q4_K x Q8_0: 1)
     float *inv_m;      // [rows]: 1 / the min-term planes' scale (Q4_K x Q8_0)
     int *lo_nz;        // [rows]: the second plane holds a non-zero element
+    _Float16 *zero;    // [ldh] zeros: the second-plane row of rows whose lo_nz is 0 (whose row may be unwritten)
 };
 size_t mllm_act16_bytes(int sem, long rows, int K);
 act16 mllm_act16_carve(int sem, void *ws, long rows, int K);

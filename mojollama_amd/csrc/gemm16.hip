@@ -30,8 +30,6 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLdb = 72;   // halfs per LDS activation row: 64 + 8 (16-byte pad: conflict-free 16-lane reads)
-
 template <int SEM> struct q16_traits {
     static constexpr bool A4 = SEM == SEM_Q4_K_Q8;
     static constexpr bool GGML = SEM == SEM_Q4_K_GGML;
@@ -81,19 +79,19 @@ MLLM_DEV h2 hh(float v) { return h2{(_Float16)v, (_Float16)v}; }
 struct q16_raw {
     u32x4 a;       // nibble bytes
     u32x4 b;       // Q6_K: qh bytes (SEQ: .x, .y)
-    uint4 m;       // Q4_K: super-block metadata (kq_pairs layout); Q6_K: .x = scales (2 bytes), .y = d
+    uint4 m;       // Q6_K: .x = scales (2 bytes), .y = d
 };
 
 // The step's four MFMA operands (8 fp16 each, as 4 words) and the super-block's d.
 template <int SEM>
-MLLM_DEV void q16_decode(const q16_raw &r, int st, int kh, u32x4 (&o)[4], float &d)
+MLLM_DEV void q16_decode(const q16_raw &r, const uint4 &meta, int st, int kh, u32x4 (&o)[4], float &d)
 {
     if constexpr (SEM == SEM_Q4_K_GGML || SEM == SEM_Q4_K_Q8) {
         // group g's sub-blocks 2g (low nibbles) and 2g+1 (high nibbles), QK:62-71 pairs
         const int g = SEM == SEM_Q4_K_GGML ? st : 2 * st + kh;
         int s1, m1, s2, m2;
-        kq_pairs(r.m, 2 * g, s1, m1, s2, m2);
-        d = h2f(r.m.x & 0xFFFF);
+        kq_pairs(meta, 2 * g, s1, m1, s2, m2);
+        d = h2f(meta.x & 0xFFFF);
         // low nibbles (bits 0-3 of each half) give 1024 + n: sa n = (1024 + n) sa - 1024 sa;
         // high nibbles stay in bits 4-7 and give 1024 + 16 n: sb n = (1024 + 16 n) (sb / 16) - 64 sb
         const h2 sa = hh((float)s1), ca = hh(-1024.0f * (float)s1);
@@ -206,8 +204,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 {
     using Q = q16_traits<SEM>;
     constexpr int RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 128, SPB = Q::SPB, NPL = Q::NPL;
-    static_assert(SPB % 2 == 0, "the LDS buffer parity follows the step parity within a super-block");
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][NPL][TM * kLdb];
+    static_assert(SPB == 2 || SPB == 4, "steps run in units of four");
     __shared__ __attribute__((aligned(16))) float sD[4][RB * 32];
     __shared__ int s_row[TM];
 
@@ -260,25 +257,72 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     }
     const int wrow = min(n0 + 32 * wave + lr, a.n_rows - 1);   // the row this lane decodes
 
-    // per-lane byte offsets (the step's part is added to the wave-uniform base)
-    constexpr int NCH = TM * 8 / 256;   // activation chunks per thread and plane
-    uint32_t boff[NCH];
+    // ---- activation tiles: direct global -> LDS loads (global_load_lds_dwordx4, 16 bytes a
+    // lane).  One load instruction of a wave fills 1 KB of a buffer = 8 entry rows of 128
+    // bytes (the step's 64 positions); lane i writes row i / 8, slot i % 8, and fetches
+    // chunk slot ^ f(row) of its entry row, f(r) = (r ^ r >> 3) & 7 over r mod 32, so the
+    // MFMA reads of 16 lanes (rows r .. r+15, one chunk each) fall in distinct banks.
+    // Four buffers, each its own LDS object: the compiler then tracks which outstanding
+    // loads write which buffer.  One plane: buffer = step % 4, loads run three steps
+    // ahead; two planes: buffer = 2 (step % 2) + plane, one step ahead.
+    constexpr int NCH = TM * 8 / 256;   // load instructions per wave, plane and step (= EB)
+    __shared__ __attribute__((aligned(16))) _Float16 sB0[TM * 64], sB1[TM * 64], sB2[TM * 64], sB3[TM * 64];
+    auto sbuf = [&](auto i_c) __attribute__((always_inline)) -> _Float16 * {
+        constexpr int i = decltype(i_c)::value;
+        if constexpr (i == 0) return sB0;
+        else if constexpr (i == 1) return sB1;
+        else if constexpr (i == 2) return sB2;
+        else return sB3;
+    };
+    auto fsw = [](int r) { return (r ^ (r >> 3)) & 7; };
+    // boff: a lane's byte offsets in the first plane; boff1 in the second (from its base,
+    // set by the two-plane path): rows whose second plane is zero read the zero row after it
+    uint32_t boff[NCH], boff1[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int ch = tid + 256 * c;
-        boff[c] = (uint32_t)s_row[ch >> 3] * (uint32_t)(a.x.ldh * 2) + 16u * (ch & 7);
+        const int ch = 256 * c + 64 * wave + lane, r = ch >> 3;
+        boff[c] = (uint32_t)s_row[r] * (uint32_t)(a.x.ldh * 2) + 16u * (uint32_t)((ch & 7) ^ fsw(r & 31));
+        boff1[c] = boff[c];
     }
+    auto set_boff1 = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int ch = 256 * c + 64 * wave + lane, r = ch >> 3;
+            if (!a.x.lo_nz[s_row[r]])
+                boff1[c] = (uint32_t)(a.x.zero - (a.x.h + a.x.hplane)) * 2u + 16u * (uint32_t)((ch & 7) ^ fsw(r & 31));
+        }
+    };
+    uint32_t raddr[4];   // byte offset of the lane's MFMA operand i in a 32-row block
+    {
+        const int fl = fsw(lr);
+#pragma unroll
+        for (int i = 0; i < 4; i++) raddr[i] = 128u * lr + 16u * (uint32_t)((2 * i + kh) ^ fl);
+    }
+    auto dma = [&](int s, int p, _Float16 *dst) __attribute__((always_inline)) {
+        const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+            __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
+                                             (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
+    };
+    // this wave's loads older than the newest n are done, then the workgroup meets: every
+    // wave's older loads have landed and every wave has finished the previous step
+    // (the builtins, not asm: the compiler's own wait tracking then knows of the wait)
+    auto sync_loads = [&](auto n_c) __attribute__((always_inline)) {
+        constexpr int n = decltype(n_c)::value;
+        static_assert(n < 64, "vmcnt is six bits");
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x0F70);   // vmcnt(n), expcnt/lgkmcnt: no wait
+        __builtin_amdgcn_s_barrier();
+    };
+
     // weight rows: bulk plane bytes per super-block (Q4_K / Q6_K ql: 128) and per-row offsets
     const uint32_t rq = (uint32_t)wrow * (uint32_t)nb;   // row's first super-block index
-    auto fetch_w = [&](const mllm_packed &M, int s, q16_raw &r) __attribute__((always_inline)) {
-        const int b = s / SPB, st = s % SPB;
+    auto fetch_w = [&](const mllm_packed &M, int b, int st, q16_raw &r) __attribute__((always_inline)) {
         const uint32_t bi = rq + (uint32_t)b;
         if constexpr (SEM == SEM_Q4_K_GGML) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
-            r.m = gldo<uint4>(M.p[1], bi * 16u);
         } else if constexpr (SEM == SEM_Q4_K_Q8) {
             r.a = gldo<u32x4>(M.p[0] + 64 * st, bi * 128u + 32u * kh);
-            r.m = gldo<uint4>(M.p[1], bi * 16u);
         } else if constexpr (SEM == SEM_Q6_K_SEQ) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
             const uint2 q = gldo<uint2>(M.p[1] + 16 * st, bi * 64u + 8u * kh);
@@ -303,44 +347,29 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
             for (int v = 0; v < 16; v++) { acc[r][e][v] = 0.0f; T[r][e][v] = 0.0f; }
 
-    // NP: the activation planes this tile multiplies (1 when no row of the tile has a second)
-    auto fetch_b = [&](auto np_c, int s, uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value;
-        const _Float16 *base = a.x.h + 64 * (long)s;
-#pragma unroll
-        for (int p = 0; p < NP; p++)
-#pragma unroll
-            for (int c = 0; c < NCH; c++) bx_[p][c] = gldo<uint4>(base + p * a.x.hplane, boff[c]);
-    };
-    auto store_b = [&](auto np_c, int buf, const uint4 (&bx_)[NPL][NCH]) __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value;
-#pragma unroll
-        for (int p = 0; p < NP; p++)
-#pragma unroll
-            for (int c = 0; c < NCH; c++) {
-                const int ch = tid + 256 * c, e = ch >> 3, pc = ch & 7;
-                *reinterpret_cast<uint4 *>(&sB[buf][p][e * kLdb + 8 * pc]) = bx_[p][c];
-            }
-    };
-    // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0).  Entry
-    // blocks past the tile's entries run on copies of its first row; the epilogue drops them.
-    auto mfmas = [&](auto np_c, auto st_c, const q16_raw (&r)[RB]) __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value;
-        constexpr int st = decltype(st_c)::value, buf = st & 1;
+    // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0) against
+    // the step's buffers.  Entry blocks past the tile's entries run on copies of its first
+    // row; the epilogue drops them.
+    auto mfmas = [&](auto np_c, auto st_c, auto u_c, const q16_raw (&r)[RB], const uint4 (&meta)[RB])
+                     __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value, st = decltype(st_c)::value, u = decltype(u_c)::value;
         u32x4 A[RB][4];
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
             float d;
-            q16_decode<SEM>(r[rb], st, kh, A[rb], d);
+            q16_decode<SEM>(r[rb], meta[rb], st, kh, A[rb], d);
             if (st == 0 && kh == 0) sD[wave][rb * 32 + lr] = d;
         }
+        const uint8_t *bp[NP];
+        bp[0] = (const uint8_t *)sbuf(std::integral_constant<int, NP == 1 ? u : 2 * (u & 1)>{});
+        if constexpr (NP > 1) bp[1] = (const uint8_t *)sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{});
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int e = 0; e < EB; e++) {
 #pragma unroll
                 for (int p = 0; p < NP; p++) {
-                    const f16x8 bv = *reinterpret_cast<const f16x8 *>(&sB[buf][p][(32 * e + lr) * kLdb + 16 * i + 8 * kh]);
+                    const f16x8 bv = *reinterpret_cast<const f16x8 *>(bp[p] + 4096 * e + raddr[i]);
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++) {
                         const f32x16 c = (st == 0 && i == 0 && p == 0) ? f32x16{} : T[rb][e];
@@ -369,46 +398,89 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         __builtin_amdgcn_wave_barrier();
     };
 
+    // Steps run in units of four (one super-block, or two for Q4_K x Q8_0's two-step
+    // super-blocks); weights are fetched three steps ahead into a ring of four.
     auto main_loop = [&](auto np_c) __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value, D = NP == 1 ? 3 : 1;
         const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
-        uint4 bx[NPL][NCH];
-        q16_raw rw[2][RB];
+        q16_raw rw[4][RB];
+        // Q4_K super-block metadata (kq_pairs layout): mA for the unit's first super-block,
+        // mB for its second (SPB == 2) or the next unit's (SPB == 4), one unit half ahead
+        uint4 mA[RB], mB[RB];
         auto fw = [&](int s, q16_raw (&r)[RB]) __attribute__((always_inline)) {
             const int sc = min(s, s_last);
-            fetch_w(W, sc, r[0]);
-            if constexpr (DUAL) fetch_w(W2, sc, r[1]);
+            fetch_w(W, sc / SPB, sc % SPB, r[0]);
+            if constexpr (DUAL) fetch_w(W2, sc / SPB, sc % SPB, r[1]);
         };
+        auto fm = [&](int b, uint4 (&m)[RB]) __attribute__((always_inline)) {
+            if constexpr (Q::GGML || Q::A4) {
+                // d, dmin and the six-bit scales (the mins enter through the min-term product)
+                const uint32_t bi = rq + (uint32_t)min(b, b_end - 1);
+                const uint3 q0 = gldo<uint3>(W.p[1], bi * 16u);
+                m[0] = make_uint4(q0.x, q0.y, q0.z, 0u);
+                if constexpr (DUAL) {
+                    const uint3 q1 = gldo<uint3>(W2.p[1], bi * 16u);
+                    m[1] = make_uint4(q1.x, q1.y, q1.z, 0u);
+                }
+            }
+        };
+        // the loads of step s (unit position u = (s - s_beg) % 4)
+        auto load_b = [&](int s, auto u_c) __attribute__((always_inline)) {
+            constexpr int u = decltype(u_c)::value;
+            const int sc = min(s, s_last);
+            if constexpr (NP == 1) {
+                dma(sc, 0, sbuf(std::integral_constant<int, u>{}));
+            } else {
+                dma(sc, 0, sbuf(std::integral_constant<int, 2 * (u & 1)>{}));
+                dma(sc, 1, sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{}));
+            }
+        };
+        load_b(s_beg, std::integral_constant<int, 0>{});
+        if constexpr (D >= 2) load_b(s_beg + 1, std::integral_constant<int, 1>{});
+        if constexpr (D >= 3) load_b(s_beg + 2, std::integral_constant<int, 2>{});
+        fm(b_beg, mA);
         fw(s_beg, rw[0]);
-        fetch_b(np_c, s_beg, bx);
-        store_b(np_c, 0, bx);
-        fetch_b(np_c, min(s_beg + 1, s_last), bx);
-        __syncthreads();
-        for (int b = b_beg; b < b_end; b++) {
-            const int s0 = b * SPB;
-            // step st: prefetch the next step's weights, run this step, stage the next
-            // step's activations into the other buffer (after the last step: a copy
-            // nobody reads) and fetch the one after
-            auto one = [&](auto st_c) __attribute__((always_inline)) {
-                constexpr int st = decltype(st_c)::value;
-                const int s = s0 + st;
-                fw(s + 1, rw[(st + 1) & 1]);
-                mfmas(np_c, st_c, rw[st & 1]);
-                store_b(np_c, (st + 1) & 1, bx);
-                fetch_b(np_c, min(s + 2, s_last), bx);
-                __syncthreads();
+        fw(s_beg + 1, rw[1]);
+        fw(s_beg + 2, rw[2]);
+        for (int s0 = s_beg; s0 <= s_last; s0 += 4) {
+            const int b0 = s0 / SPB;
+            // unit step u (= step s0 + u): wait for its activation loads, start those of
+            // step + D into the buffer the previous step read, and the weights of step + 3
+            auto one = [&](auto u_c) __attribute__((always_inline)) {
+                constexpr int u = decltype(u_c)::value;
+                const int s = s0 + u;
+                sync_loads(std::integral_constant<int, (D - 1) * NCH * NP>{});
+                load_b(s + D, std::integral_constant<int, (u + D) & 3>{});
+                fw(s + 3, rw[(u + 3) & 3]);
+                if constexpr (u == 0) fm(b0 + 1, mB);
+                if constexpr (SPB == 2 && u == 2) fm(b0 + 2, mA);
+                mfmas(np_c, std::integral_constant<int, u % SPB>{}, u_c, rw[u], (SPB == 2 && u >= 2) ? mB : mA);
+                if constexpr (u % SPB == SPB - 1) d_apply();
             };
             one(std::integral_constant<int, 0>{});
             one(std::integral_constant<int, 1>{});
             if constexpr (SPB == 4) {
                 one(std::integral_constant<int, 2>{});
                 one(std::integral_constant<int, 3>{});
+            } else if (s0 + 2 <= s_last) {
+                one(std::integral_constant<int, 2>{});
+                one(std::integral_constant<int, 3>{});
             }
-            d_apply();
+            if constexpr (SPB == 4) {
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) mA[rb] = mB[rb];
+            }
         }
+        // no load may still be writing the buffers when the workgroup's LDS is released
+        __builtin_amdgcn_s_waitcnt(0x0F70);
     };
     if (b_beg < b_end) {
-        if (NPL > 1 && npl > 1) main_loop(std::integral_constant<int, NPL>{});
-        else main_loop(std::integral_constant<int, 1>{});
+        if (NPL > 1 && npl > 1) {
+            set_boff1();
+            main_loop(std::integral_constant<int, NPL>{});
+        } else {
+            main_loop(std::integral_constant<int, 1>{});
+        }
     }
 
     // ---- Q4_K min terms (split 0 only): acc += sum over units of (-dmin m) (x) sums
@@ -503,6 +575,10 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     using Q = q16_traits<SEM>;
     __shared__ float red[4];
     const int row = blockIdx.x, tid = threadIdx.x;
+    if (row == (int)gridDim.x - 1) {   // the last workgroup: the zero row
+        for (int P = 8 * tid; P < a.ldh; P += 2048) *reinterpret_cast<f16x8 *>(a.zero + P) = f16x8{};
+        return;
+    }
     const float *xr = x + (long)row * ldx;
     const bool vec = ((uintptr_t)xr & 15) == 0;
     const int nb = K / 256, kused = nb * 256;
@@ -555,9 +631,13 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     const float inv = m > 0.0f ? ldexpf(1.0f, e - 9) : 1.0f;
     int nz = 0;
     _Float16 *h0 = a.h + (long)row * a.ldh, *h1 = h0 + a.hplane;
-    auto emit = [&](int P, const float (&gv)[8]) __attribute__((always_inline)) {
+    // rows that fit the held groups store their second plane only when it holds a
+    // non-zero element (the GEMM reads the zero row for the others); longer rows store it
+    const bool whole = a.ldh <= kHeld * 2048;
+    f16x8 held1[kHeld];
+    auto emit = [&](int P, const float (&gv)[8], f16x8 &v1) __attribute__((always_inline)) {
         const int sb = P / Q::PPS, pw = P % Q::PPS;
-        f16x8 v0, v1;
+        f16x8 v0;
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -570,7 +650,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
             part += gv[j] * s;
         }
         *reinterpret_cast<f16x8 *>(h0 + P) = v0;
-        *reinterpret_cast<f16x8 *>(h1 + P) = v1;
+        if (!whole) *reinterpret_cast<f16x8 *>(h1 + P) = v1;
         if constexpr (Q::GGML) {
             // sub-block 8 sb + 2 (pw / 64) + (pw / 32) % 2: the four groups of threads 4q .. 4q+3
             part += __shfl_xor(part, 1, 64);
@@ -586,11 +666,12 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     };
 #pragma unroll
     for (int it = 0; it < kHeld; it++)
-        if (it < nit) emit(8 * tid + 2048 * it, g[it]);
+        if (it < nit) emit(8 * tid + 2048 * it, g[it], held1[it]);
     for (int it = kHeld; it < nit; it++) {
         float v[8];
+        f16x8 v1;
         ld8(gbase(8 * tid + 2048 * it), v);
-        emit(8 * tid + 2048 * it, v);
+        emit(8 * tid + 2048 * it, v, v1);
     }
     if constexpr (Q::GGML) {
         for (int j = nb * 8 + tid; j < a.ldm; j += 256) {
@@ -599,6 +680,11 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
         }
     }
     nz = __syncthreads_or(nz);
+    if (whole && nz) {
+#pragma unroll
+        for (int it = 0; it < kHeld; it++)
+            if (it < nit) *reinterpret_cast<f16x8 *>(h1 + 8 * tid + 2048 * it) = held1[it];
+    }
     if (tid == 0) {
         a.lo_nz[row] = nz;
         a.inv_s[row] = inv;
@@ -699,7 +785,7 @@ size_t mllm_act16_bytes(int sem, long rows, int K)
 {
     int np, ldh, ldm;
     act16_dims(sem, K, np, ldh, ldm);
-    return al256((size_t)np * rows * ldh * 2) + al256((size_t)2 * rows * ldm * 2) + 3 * al256((size_t)rows * 4);
+    return al256((size_t)(np * rows + 1) * ldh * 2) + al256((size_t)2 * rows * ldm * 2) + 3 * al256((size_t)rows * 4);
 }
 
 act16 mllm_act16_carve(int sem, void *ws, long rows, int K)
@@ -711,7 +797,8 @@ act16 mllm_act16_carve(int sem, void *ws, long rows, int K)
     a.h = (_Float16 *)p;
     a.hplane = (long)rows * ldh;
     a.ldh = ldh;
-    p += al256((size_t)np * rows * ldh * 2);
+    a.zero = a.h + (long)np * rows * ldh;
+    p += al256((size_t)(np * rows + 1) * ldh * 2);
     a.m = ldm ? (_Float16 *)p : nullptr;
     a.mplane = (long)rows * ldm;
     a.ldm = ldm;
@@ -730,9 +817,11 @@ hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq
     if (rows <= 0) return hipSuccess;
     if (K < 256 || K % 256 || ((uintptr_t)act.h & 15)) return hipErrorInvalidValue;
     switch (sem) {
-    case SEM_Q4_K_GGML: hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
-    case SEM_Q6_K_SEQ: hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
-    case SEM_Q6_K_LOWNIB: hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q4_K_GGML: hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q6_K_SEQ: hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q6_K_LOWNIB:
+        hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act);
+        break;
     case SEM_Q4_K_Q8:
         if (!xq || K / 256 > 256) return hipErrorInvalidValue;
         hipLaunchKernelGGL(k_act16_q8, dim3(rows), dim3(256), 0, st, *xq, K, act);

@@ -23,6 +23,7 @@
 #include "gemv.h"
 #include "mllm.h"
 #include "moe.h"
+#include "gemm16.h"
 
 namespace {
 
@@ -234,7 +235,19 @@ struct moe_ws {
     __bf16 *xp_x, *xp_h;      // split planes of x [T][N] and h [T*K][M] (batched path)
     int *lo_x, *lo_h;
     float *logits;            // routing logits [T][E] (decode path, expert slices)
+    uint8_t *a16_x, *a16_h;   // fp16-plane GEMM activations of x and h (batched path), or null
 };
+
+// Whether the batched path runs gate/up and down on the fp16-plane GEMM (gemm16.h):
+// K-quant semantics over whole super-blocks, on the packed experts (not the dense copies).
+static bool moe_q16_gu(const mllm_moe_layer &L)
+{
+    return L.sem_g == L.sem_u && mllm_q16_supported(L.sem_g) && !L.dense_gu && L.N % 256 == 0;
+}
+static bool moe_q16_d(const mllm_moe_layer &L)
+{
+    return L.sem_d >= 0 && mllm_q16_supported(L.sem_d) && !L.dense_d && L.M % 256 == 0;
+}
 
 // Tokens up to which the layer runs the decode GEMVs (one job per (token,
 // slot); an expert picked by several tokens is streamed once per token) rather
@@ -272,6 +285,8 @@ static size_t moe_ws_layout(const mllm_moe_layer &L, int T, moe_ws *w, uint8_t *
     s.lo_x = (int *)take((size_t)T * 4);
     s.lo_h = (int *)take(TK * 4);
     s.logits = (float *)take((size_t)mllm_route_workspace_floats(T, L.E) * 4);
+    s.a16_x = moe_q16_gu(L) ? take(mllm_act16_bytes(L.sem_g, T, L.N)) : nullptr;
+    s.a16_h = moe_q16_d(L) ? take(mllm_act16_bytes(L.sem_d, (long)TK, L.M)) : nullptr;
     if (w) *w = s;
     return o;
 }
@@ -420,6 +435,22 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
         CK(launch_bucket(s.idx, TK, E, K, s.bscr, s.bscr + (TK / kBucketThreads + 1) * E, s.off, s.perm, s.pos_of,
                          s.tok, s.tile_expert, s.tile_begin, s.tile_end, s.n_tiles, st));
         const int max_tiles = TK / kTileEntries + E + 1;
+        static_assert(kTileEntries == 64, "the bucketing's tiles are the grouped GEMMs' 64-entry tiles");
+        if (moe_q16_gu(*L)) {
+            // gate + up + SiLU in bucket order on the fp16-plane GEMM
+            const act16 ax = mllm_act16_carve(L->sem_g, s.a16_x, T, N);
+            CK(mllm_launch_act16(L->sem_g, x, N, &xqx, T, N, ax, st));
+            q16_args a{};
+            a.table = L->tab; a.table2 = L->tab + E;
+            a.x = ax;
+            a.row_of = s.tok;
+            a.out = s.h; a.ldo = M;
+            a.n_rows = M; a.n_cols = N; a.n_entries = TK;
+            a.tile_expert = s.tile_expert; a.tile_begin = s.tile_begin; a.tile_end = s.tile_end; a.n_tiles = s.n_tiles;
+            a.clamp_silu = L->clamp;
+            a.ksplit = 1;
+            CK(mllm_launch_q16(L->sem_g, true, a, max_tiles, st));
+        } else {
         // gate + up (+ SiLU) in bucket order
         qgemm_args a{};
         a.table = L->tab; a.table2 = L->tab + E;
@@ -446,8 +477,21 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
             CK(mllm_launch_qgemm(L->sem_u, xmode_of(L->sem_u), false, a, max_tiles, st));
             CK(mllm_launch_silu_mul(s.g, s.u, s.h, (long)TK * M, L->clamp, st));
         }
+        }
         // down, rows of h already in bucket order
-        if (L->sem_d >= 0) {
+        if (moe_q16_d(*L)) {
+            const act16 ah = mllm_act16_carve(L->sem_d, s.a16_h, TK, M);
+            if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
+            CK(mllm_launch_act16(L->sem_d, s.h, M, &xqh, TK, M, ah, st));
+            q16_args b{};
+            b.table = L->tab + 2 * E;
+            b.x = ah;
+            b.out = s.dn; b.ldo = N;
+            b.n_rows = N; b.n_cols = M; b.n_entries = TK;
+            b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;
+            b.ksplit = 1;
+            CK(mllm_launch_q16(L->sem_d, false, b, max_tiles, st));
+        } else if (L->sem_d >= 0) {
             if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
             qgemm_args b{};
             b.table = L->tab + 2 * E;

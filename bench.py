@@ -92,7 +92,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
     ap.add_argument("--kernel", choices=("gate_up", "down", "gate_up_b8", "down_b8", "copy", "gemm_gate",
-                                         "gemm_down", "gemm16_gate", "gemm16_down", "moe_gptoss", "moe_qwen3",
+                                         "gemm_down", "moe_gptoss", "moe_qwen3",
                                          "moe_gptoss_dense"),
                     help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
                          "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
@@ -166,26 +166,17 @@ def kernel_only(torch, dev, which):
         torch.cuda.synchronize()
         for _ in range(50):
             b.copy_(a)
-    elif which in ("gemm_gate", "gemm_down", "gemm16_gate", "gemm16_down"):
+    elif which in ("gemm_gate", "gemm_down"):
         # configs[2] prefill at M = 1280: the Q4_K gate (5632x2048) or the Q6_K down (2048x5632), 10 launches
-        # (gemm16_*: over the load-time fp16 copy, mllm_gemm16)
         gen = torch.Generator(device="cuda").manual_seed(3)
         sem, qt, R, C = (K.Q4_K_GGML, W.QT_Q4_K, 5632, 2048) if which.endswith("gate") else \
             (K.Q6_K_SEQ, W.QT_Q6_K, 2048, 5632)
         packed = dev.pack(sem, W.gen_weights_torch(gen, qt, R, C), R, C)
         x = torch.randn(1280, C, device="cuda", generator=gen).bfloat16().float()
         o = torch.empty(1280, R, device="cuda")
-        if which.startswith("gemm16"):
-            w16 = dev.dense16(sem, packed, R, C)
-            ws = dev.gemm16_workspace(R, C, 1280, x.device)
-            dev.gemm16(w16, x, R, C, out=o, ws=ws)   # the plan (and its timed choice) outside the counted launches
-            torch.cuda.synchronize()
-            for _ in range(10):
-                dev.gemm16(w16, x, R, C, out=o, ws=ws)
-        else:
-            ws = dev.workspace(sem, C, 1280, x.device, R)
-            for _ in range(10):
-                dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
+        ws = dev.workspace(sem, C, 1280, x.device, R)
+        for _ in range(10):
+            dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
     elif which in ("moe_gptoss", "moe_qwen3", "moe_gptoss_dense"):
         # the MoE layer at T = 1280, 5 forwards (_dense: over bf16 expert copies)
         wl = W.moe_workload(which.split("_")[1], 1280)
@@ -338,10 +329,11 @@ def bench_q8(torch, dev, args):
 
 
 def bench_prefill(torch, dev, args):
-    """configs[2]: Q4_K gate/up 5632x2048 and Q6_K down 2048x5632 at M in {128, 512, 1280}
-    bf16-valued activations, *_batch_matmul semantics: through the quantised-weight
-    MFMA GEMM (mllm_gemv), and through the load-time fp16 copy (mllm_gemm16,
-    hipBLASLt; the activation conversion launches inside the timed region)."""
+    """Q4_K gate/up 5632x2048 and Q6_K down 2048x5632 at M in {128, 512, 1280},
+    *_batch_matmul semantics, through mllm_gemv (the fp16-plane GEMM: weights decoded
+    from the packed bytes in registers, activations staged inside the timed region).
+    Activations bf16-valued (one fp16 plane after scaling) and, at M=1280, general
+    fp32 (two planes, twice the MFMA work)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(3)
     out = {}
@@ -349,24 +341,20 @@ def bench_prefill(torch, dev, args):
     for name, (sem, qt, R, C) in mats.items():
         raw = W.gen_weights_torch(gen, qt, R, C)
         packed = dev.pack(sem, raw, R, C)
-        w16 = dev.dense16(sem, packed, R, C)
-        for M in (128, 512, 1280):
-            x = torch.randn(M, C, device="cuda", generator=gen).bfloat16().float()
+        for M, act in ((128, "bf16"), (512, "bf16"), (1280, "bf16"), (1280, "fp32")):
+            x = torch.randn(M, C, device="cuda", generator=gen)
+            if act == "bf16":
+                x = x.bfloat16().float()
             o = torch.empty(M, R, device="cuda")
             ws = dev.workspace(sem, C, M, x.device, R)
             ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o, ws=ws), max(5, args.steps),
                              args.warmup)
-            ws16 = dev.gemm16_workspace(R, C, M, x.device)
-            ms16 = time_region(torch, lambda: dev.gemm16(w16, x, R, C, out=o, ws=ws16), max(5, args.steps),
-                               args.warmup)
             flops = 2.0 * R * C * M
-            tf = lambda t: round(flops / (t * 1e-3) / 1e12, 1)  # noqa: E731
-            out[f"{name}_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": tf(ms),
-                                   "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                                   "fp16_copy": {"us": round(ms16 * 1e3, 2), "TFLOP/s": tf(ms16),
-                                                 "mfma_frac": round(tf(ms16) / MFMA_BF16_PEAK_TFLOPS, 4)}}
-            log(f"prefill {name} M={M}: {ms * 1e3:.1f} us, {tf(ms)} TFLOP/s; fp16 copy (hipBLASLt) "
-                f"{ms16 * 1e3:.1f} us, {tf(ms16)} TFLOP/s")
+            tf = round(flops / (ms * 1e-3) / 1e12, 1)
+            key = f"{name}_M{M}" + ("" if act == "bf16" else "_fp32_act")
+            out[key] = {"us": round(ms * 1e3, 2), "TFLOP/s": tf,
+                        "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4), "activations": act}
+            log(f"prefill {name} M={M} ({act} activations): {ms * 1e3:.1f} us, {tf} TFLOP/s")
     return out
 
 

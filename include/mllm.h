@@ -294,24 +294,6 @@ MLLM_API int mllm_route(const float *router_p_dev, const float *x_dev, int T, in
 /* fp32 weights of a packed matrix (fp32-weight semantics only). */
 MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_cols, float *out_dev, void *stream);
 
-/* Prefill over a load-time fp16 copy of a packed matrix: the batched product
- * of q4_k / q6_k / q8_0 / q4_0 / q5_k / mxfp4_batch_matmul (CE:68-534) and
- * quant_matmul_omp's fp32-activation forms at batch M, traded for 2 bytes per
- * weight of HBM.  mllm_dense16_make dequantises as the *_dequantize_row
- * functions do (QK:762-878) and rounds to fp16 (fp32-weight semantics only;
- * fails, leaving the caller on mllm_gemv, when a weight is not finite in
- * fp16); it synchronises `stream`.  mllm_gemm16: out[t][r] (stride ldo, 0:
- * n_rows) = row r . x[t] (stride ldx, 0: n_cols) for t < M, the activations
- * rounded to fp16 under one power-of-two scale and the product accumulated in
- * fp32 (hipBLASLt), ~3e-4 of the output scale from the reference.  The first
- * call per shape builds the GEMM plan (not capturable), later calls only
- * launch. */
-MLLM_API long mllm_dense16_size(int n_rows, int n_cols);
-MLLM_API int mllm_dense16_make(int sem, const void *packed_dev, int n_rows, int n_cols, void *w16_dev, void *stream);
-MLLM_API long mllm_gemm16_workspace_size(int n_rows, int n_cols, int M);
-MLLM_API int mllm_gemm16(const void *w16_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols, int M,
-                         int ldx, int ldo, void *workspace, long workspace_bytes, void *stream);
-
 /* ------------------------------------------------------- MoE layer, T tokens */
 
 /* A prepared MoE layer: per-expert packed weights (device pointers, arrays of E

@@ -29,7 +29,6 @@
 #include "gemv.h"
 #include "mllm.h"
 #include "moe.h"
-#include "dense16.h"
 #include "dropin.h"
 
 namespace {
@@ -1332,40 +1331,6 @@ MLLM_API int mllm_dequant(int sem, const void *packed_dev, int n_rows, int n_col
 {
     mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
     return mllm_launch_dequant(sem, view, n_rows, n_cols, out_dev, (hipStream_t)stream);
-}
-
-MLLM_API long mllm_dense16_size(int n_rows, int n_cols) { return mllm_d16_bytes(n_rows, n_cols); }
-
-MLLM_API int mllm_dense16_make(int sem, const void *packed_dev, int n_rows, int n_cols, void *w16_dev, void *stream)
-{
-    if (sem < 0 || sem >= SEM_COUNT || n_rows <= 0 || n_cols <= 0 || !packed_dev || !w16_dev) {
-        set_error("mllm_dense16_make: bad arguments");
-        return -1;
-    }
-    std::string err;
-    mllm_packed view = mllm_packed_view(mllm_sem_layout(sem), (const uint8_t *)packed_dev, n_rows, n_cols);
-    if (mllm_d16_make(sem, view, n_rows, n_cols, w16_dev, (hipStream_t)stream, err) != 0) {
-        set_error("mllm_dense16_make: %s", err.c_str());
-        return -1;
-    }
-    return 0;
-}
-
-MLLM_API long mllm_gemm16_workspace_size(int n_rows, int n_cols, int M)
-{
-    return mllm_d16_workspace_bytes(n_rows, n_cols, M);
-}
-
-MLLM_API int mllm_gemm16(const void *w16_dev, const float *x_dev, float *out_dev, int n_rows, int n_cols, int M,
-                         int ldx, int ldo, void *workspace, long workspace_bytes, void *stream)
-{
-    std::string err;
-    if (mllm_d16_gemm(w16_dev, x_dev, ldx ? ldx : n_cols, M, out_dev, ldo ? ldo : n_rows, n_rows, n_cols, workspace,
-                      workspace_bytes, (hipStream_t)stream, err) != 0) {
-        set_error("mllm_gemm16: %s", err.c_str());
-        return -1;
-    }
-    return 0;
 }
 
 } // extern "C"

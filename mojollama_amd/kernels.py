@@ -190,14 +190,6 @@ def load_kernels(path=LIB_PATH):
     so.mllm_dequant.restype = ci
     so.mllm_moe_dense_experts.argtypes = [cvp, cvp]
     so.mllm_moe_dense_experts.restype = ctypes.c_long
-    so.mllm_dense16_size.argtypes = [ci, ci]
-    so.mllm_dense16_size.restype = ctypes.c_long
-    so.mllm_dense16_make.argtypes = [ci, cvp, ci, ci, cvp, cvp]
-    so.mllm_dense16_make.restype = ci
-    so.mllm_gemm16_workspace_size.argtypes = [ci, ci, ci]
-    so.mllm_gemm16_workspace_size.restype = ctypes.c_long
-    so.mllm_gemm16.argtypes = [cvp, cvp, cvp, ci, ci, ci, ci, ci, cvp, ctypes.c_long, cvp]
-    so.mllm_gemm16.restype = ci
     so.mllm_moe_prepare.argtypes = [ci, ci, ci, ci, ci, ci, ci, ctypes.POINTER(cvp), ctypes.POINTER(cvp),
                                     ctypes.POINTER(cvp), cvp, ci]
     so.mllm_moe_prepare.restype = cvp
@@ -363,30 +355,6 @@ class DeviceOps:
         out = torch.empty((n_rows, n_cols), dtype=torch.float32, device=packed.device)
         self._check(self.so.mllm_dequant(sem, packed.data_ptr(), n_rows, n_cols, out.data_ptr(), self._stream()),
                     "mllm_dequant")
-        return out
-
-    def dense16(self, sem, packed, n_rows, n_cols):
-        """Load-time fp16 copy of a packed matrix (mllm_dense16_make)."""
-        torch = self.torch
-        out = torch.empty((n_rows, n_cols), dtype=torch.float16, device=packed.device)
-        self._check(self.so.mllm_dense16_make(sem, packed.data_ptr(), n_rows, n_cols, out.data_ptr(), self._stream()),
-                    "mllm_dense16_make")
-        return out
-
-    def gemm16_workspace(self, n_rows, n_cols, M, device):
-        n = self.so.mllm_gemm16_workspace_size(n_rows, n_cols, M)
-        return self.torch.empty(n, dtype=self.torch.uint8, device=device)
-
-    def gemm16(self, w16, x, n_rows, n_cols, out=None, ws=None, M=None, ldx=0, ldo=0):
-        """out[t] = W . x[t] over the fp16 copy (mllm_gemm16)."""
-        torch = self.torch
-        M = M if M is not None else x.numel() // n_cols
-        if out is None:
-            out = torch.empty((M, n_rows), dtype=torch.float32, device=x.device)
-        if ws is None:
-            ws = self.gemm16_workspace(n_rows, n_cols, M, x.device)
-        self._check(self.so.mllm_gemm16(w16.data_ptr(), x.data_ptr(), out.data_ptr(), n_rows, n_cols, M, ldx, ldo,
-                                        ws.data_ptr(), ws.numel(), self._stream()), "mllm_gemm16")
         return out
 
     # ------------------------------------------------------------ MoE layer

@@ -298,10 +298,11 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
         for (int i = 0; i < 4; i++) raddr[i] = 128u * lr + 16u * (uint32_t)((2 * i + kh) ^ fl);
     }
-    auto dma = [&](int s, int p, _Float16 *dst) __attribute__((always_inline)) {
+    auto dma = [&](auto nb_c, int s, int p, _Float16 *dst) __attribute__((always_inline)) {
+        constexpr int NEB = decltype(nb_c)::value;   // chunk c holds entry block c
         const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
 #pragma unroll
-        for (int c = 0; c < NCH; c++)
+        for (int c = 0; c < NEB; c++)
             __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
                                              (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
     };
@@ -350,9 +351,10 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0) against
     // the step's buffers.  Entry blocks past the tile's entries run on copies of its first
     // row; the epilogue drops them.
-    auto mfmas = [&](auto np_c, auto st_c, auto u_c, const q16_raw (&r)[RB], const uint4 (&meta)[RB])
+    auto mfmas = [&](auto np_c, auto nb_c, auto st_c, auto u_c, const q16_raw (&r)[RB], const uint4 (&meta)[RB])
                      __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value, st = decltype(st_c)::value, u = decltype(u_c)::value;
+        constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value;
+        constexpr int st = decltype(st_c)::value, u = decltype(u_c)::value;
         u32x4 A[RB][4];
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int e = 0; e < EB; e++) {
+            for (int e = 0; e < NEB; e++) {
 #pragma unroll
                 for (int p = 0; p < NP; p++) {
                     const f16x8 bv = *reinterpret_cast<const f16x8 *>(bp[p] + 4096 * e + raddr[i]);
@@ -379,7 +381,8 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                 }
             }
     };
-    auto d_apply = [&]() __attribute__((always_inline)) {
+    auto d_apply = [&](auto nb_c) __attribute__((always_inline)) {
+        constexpr int NEB = decltype(nb_c)::value;
         // the super-block's d, per output row (rows 8 g + 4 kh + r of the lane's 16)
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -391,7 +394,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                 dv[4 * g] = q.x; dv[4 * g + 1] = q.y; dv[4 * g + 2] = q.z; dv[4 * g + 3] = q.w;
             }
 #pragma unroll
-            for (int e = 0; e < EB; e++)
+            for (int e = 0; e < NEB; e++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(dv[v], T[rb][e][v], acc[rb][e][v]);
         }
@@ -400,8 +403,10 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 
     // Steps run in units of four (one super-block, or two for Q4_K x Q8_0's two-step
     // super-blocks); weights are fetched three steps ahead into a ring of four.
-    auto main_loop = [&](auto np_c) __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value, D = NP == 1 ? 3 : 1;
+    // NEB: the entry blocks the tile's entries occupy (a bucketing tile of at most 32
+    // entries runs one: half the MFMAs and activation loads)
+    auto main_loop = [&](auto np_c, auto nb_c) __attribute__((always_inline)) {
+        constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value, D = NP == 1 ? 3 : 1;
         const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
         q16_raw rw[4][RB];
         // Q4_K super-block metadata (kq_pairs layout): mA for the unit's first super-block,
@@ -429,10 +434,10 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             constexpr int u = decltype(u_c)::value;
             const int sc = min(s, s_last);
             if constexpr (NP == 1) {
-                dma(sc, 0, sbuf(std::integral_constant<int, u>{}));
+                dma(nb_c, sc, 0, sbuf(std::integral_constant<int, u>{}));
             } else {
-                dma(sc, 0, sbuf(std::integral_constant<int, 2 * (u & 1)>{}));
-                dma(sc, 1, sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{}));
+                dma(nb_c, sc, 0, sbuf(std::integral_constant<int, 2 * (u & 1)>{}));
+                dma(nb_c, sc, 1, sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{}));
             }
         };
         load_b(s_beg, std::integral_constant<int, 0>{});
@@ -449,13 +454,13 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             auto one = [&](auto u_c) __attribute__((always_inline)) {
                 constexpr int u = decltype(u_c)::value;
                 const int s = s0 + u;
-                sync_loads(std::integral_constant<int, (D - 1) * NCH * NP>{});
+                sync_loads(std::integral_constant<int, (D - 1) * NEB * NP>{});
                 load_b(s + D, std::integral_constant<int, (u + D) & 3>{});
                 fw(s + 3, rw[(u + 3) & 3]);
                 if constexpr (u == 0) fm(b0 + 1, mB);
                 if constexpr (SPB == 2 && u == 2) fm(b0 + 2, mA);
-                mfmas(np_c, std::integral_constant<int, u % SPB>{}, u_c, rw[u], (SPB == 2 && u >= 2) ? mB : mA);
-                if constexpr (u % SPB == SPB - 1) d_apply();
+                mfmas(np_c, nb_c, std::integral_constant<int, u % SPB>{}, u_c, rw[u], (SPB == 2 && u >= 2) ? mB : mA);
+                if constexpr (u % SPB == SPB - 1) d_apply(nb_c);
             };
             one(std::integral_constant<int, 0>{});
             one(std::integral_constant<int, 1>{});
@@ -474,12 +479,21 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         // no load may still be writing the buffers when the workgroup's LDS is released
         __builtin_amdgcn_s_waitcnt(0x0F70);
     };
+    const int neb = __builtin_amdgcn_readfirstlane(min(EB, (n_ent + 31) / 32));
+    auto by_blocks = [&](auto np_c) __attribute__((always_inline)) {
+        if constexpr (EB == 2) {
+            if (neb == 1) main_loop(np_c, std::integral_constant<int, 1>{});
+            else main_loop(np_c, std::integral_constant<int, 2>{});
+        } else {
+            main_loop(np_c, std::integral_constant<int, EB>{});
+        }
+    };
     if (b_beg < b_end) {
         if (NPL > 1 && npl > 1) {
             set_boff1();
-            main_loop(std::integral_constant<int, NPL>{});
+            by_blocks(std::integral_constant<int, NPL>{});
         } else {
-            main_loop(std::integral_constant<int, 1>{});
+            by_blocks(std::integral_constant<int, 1>{});
         }
     }
 
@@ -494,6 +508,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                     q16_min_w<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, whi, wlo);
 #pragma unroll
                     for (int e = 0; e < EB; e++) {
+                        if (e >= neb) continue;
                         const long er = s_row[32 * e + lr];
                         const _Float16 *mp = a.x.m + er * a.x.ldm + u0 + 8 * kh;
                         const f16x8 s0 = __builtin_bit_cast(f16x8, gld<u32x4>(mp));

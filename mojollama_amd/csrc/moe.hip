@@ -157,6 +157,25 @@ size_t bucket_scratch_ints(int TK, int E) { return (size_t)(TK / kBucketThreads 
 __global__ void k_combine_pos(const float *__restrict__ dn, const float *__restrict__ w,
                               const int *__restrict__ pos_of, int K, int N, float *__restrict__ out)
 {
+    // four consecutive n per thread (N % 4 == 0: 16-byte loads), the same
+    // per-element arithmetic as one n per thread
+    const int t = blockIdx.y;
+    const int n = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (n >= N) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < K; k++) {
+        const int pos = pos_of[t * K + k];
+        if (pos < 0) continue;
+        const float wk = w[t * K + k];
+        const float4 v = dn ? *reinterpret_cast<const float4 *>(dn + (long)pos * N + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        acc.x += wk * v.x; acc.y += wk * v.y; acc.z += wk * v.z; acc.w += wk * v.w;
+    }
+    *reinterpret_cast<float4 *>(out + (long)t * N + n) = acc;
+}
+
+__global__ void k_combine_pos1(const float *__restrict__ dn, const float *__restrict__ w,
+                               const int *__restrict__ pos_of, int K, int N, float *__restrict__ out)
+{
     const int t = blockIdx.y;
     const int n = blockIdx.x * blockDim.x + threadIdx.x;
     if (n >= N) return;
@@ -507,8 +526,12 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
             b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;
             CK(mllm_launch_qgemm(L->sem_d, xmode_of(L->sem_d), false, b, max_tiles, st));
         }
-        hipLaunchKernelGGL(k_combine_pos, dim3((N + 255) / 256, T), dim3(256), 0, st, L->sem_d >= 0 ? s.dn : nullptr,
-                           s.w, s.pos_of, K, N, out);
+        if (N % 4 == 0 && ((uintptr_t)out & 15) == 0)
+            hipLaunchKernelGGL(k_combine_pos, dim3((N / 4 + 255) / 256, T), dim3(256), 0, st,
+                               L->sem_d >= 0 ? s.dn : nullptr, s.w, s.pos_of, K, N, out);
+        else
+            hipLaunchKernelGGL(k_combine_pos1, dim3((N + 255) / 256, T), dim3(256), 0, st,
+                               L->sem_d >= 0 ? s.dn : nullptr, s.w, s.pos_of, K, N, out);
         CK(hipGetLastError());
     } else {
         // decode: one GEMV launch per projection over all T*K (token, slot)

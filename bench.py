@@ -27,28 +27,38 @@ import os
 
 
 def host_cpu():
-    """(threads to use, CPU model): the physical cores this process may run on,
-    at most 16 (one GPU's share of the box's cores)."""
+    """(threads to use, CPU description): the physical cores this process may
+    run on, at most 16 (one GPU's share of the box's cores), and the host's
+    model name with its family / model / stepping numbers and physical core
+    count (sockets x cores) from /proc/cpuinfo."""
     aff = os.sched_getaffinity(0)
-    model, cores, cur = "unknown", set(), {}
+    model, cores, all_cores, cur, ids = "unknown", set(), set(), {}, {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f.read().split("\n") + [""]:
                 if not line.strip():
-                    if cur.get("processor") is not None and int(cur["processor"]) in aff:
-                        cores.add((cur.get("physical id", "0"), cur.get("core id", cur["processor"])))
+                    if cur.get("processor") is not None:
+                        key = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+                        all_cores.add(key)
+                        if int(cur["processor"]) in aff:
+                            cores.add(key)
                     cur = {}
                     continue
                 k, _, v = line.partition(":")
-                cur[k.strip()] = v.strip()
-                if k.strip() == "model name":
+                k = k.strip()
+                cur[k] = v.strip()
+                if k == "model name":
                     model = v.strip()
+                if k in ("cpu family", "model", "stepping") and k not in ids:
+                    ids[k] = v.strip()
     except OSError:
         pass
     n = len(cores)
     if n < max(1, len(aff) // 4):   # a virtualised cpuinfo that does not list the cores this process may use
         n = len(aff)
-    return max(1, min(n, 16)), model
+    desc = {"model_name": model, "family": ids.get("cpu family"), "model": ids.get("model"),
+            "stepping": ids.get("stepping"), "physical_cores": len(all_cores), "logical_cpus_visible": len(aff)}
+    return max(1, min(n, 16)), desc
 
 
 # The host reference runs in a child process (bench.py --cpu-leg NAME) that
@@ -119,6 +129,11 @@ def median_time(fn, reps, warm=3):
 
 
 def cpu_tag(cores, model):
+    """cores: the threads the reference ran on; model: host_cpu()'s description."""
+    if isinstance(model, dict):
+        model = (f"{model['model_name']} (family {model['family']} model {model['model']} stepping "
+                 f"{model['stepping']}; {model['physical_cores']} physical cores, {model['logical_cpus_visible']} "
+                 "logical CPUs visible to this process)")
     return {"cores": cores, "cpu_model": model, "kind": "reference", "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
             "omp_places": os.environ.get("OMP_PLACES")}
 

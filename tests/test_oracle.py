@@ -9,6 +9,8 @@ Three independent pins:
 """
 import zlib
 
+import math
+
 import numpy as np
 import pytest
 
@@ -546,6 +548,64 @@ def test_attention_gqa_c_equal_scores_closed_form(orc, S):
     want = np.repeat(num / den, nh // nkh, axis=0).ravel()
     assert O.norm_err(got, want) < 1e-5
     assert orc.exp_ps_simd(0.0) == np.float32(0.0013333558146428)
+
+
+def _exp_ps_simd_exact(x):
+    """exp_ps_simd (gqa_attention.c:32-48) for one float32 x, evaluated with
+    exact rational arithmetic and one rounding to float32 per operation: the
+    fp32 multiply by log2e, t + 0.5 rounded to an integer with ties to even
+    (cvtps_epi32 under the default MXCSR), f = t - n, five fused multiply-adds
+    starting from p = 1, the clamped biased exponent.  The five coefficients
+    are not copied from any source: they are (ln 2)^k / k! for k = 1..5 (the
+    Taylor coefficients of 2^f the source's literals spell to 16 digits),
+    rounded to float32 as a float literal is."""
+    from fractions import Fraction as F
+
+    def r32(q):
+        # round the exact rational q to the nearest float32 (ties to even)
+        v = np.float32(float(q))             # within an ulp; then fix up exactly
+        lo, hi = np.nextafter(v, np.float32(-np.inf)), np.nextafter(v, np.float32(np.inf))
+        best = min((lo, v, hi), key=lambda c: (abs(F(float(c)) - q), int(np.float32(c).view(np.uint32)) & 1))
+        return np.float32(best)
+
+    coef = [r32(F(math.log(2) ** k) / math.factorial(k)) for k in range(1, 6)]
+    log2e = np.float32(1.4426950408889634)
+    t = r32(F(float(np.float32(x))) * F(float(log2e)))
+    h = r32(F(float(t)) + F(1, 2))
+    n = int(np.rint(np.float64(h)))          # ties to even
+    f = r32(F(float(t)) - n)
+    p = np.float32(1.0)
+    for c in coef:
+        p = r32(F(float(p)) * F(float(f)) + F(float(c)))
+    b = min(max(n + 127, 0), 255)
+    two_n = np.array([b << 23], np.uint32).view(np.float32)[0]
+    return r32(F(float(p)) * F(float(two_n)))
+
+
+def test_exp_ps_simd_pinned_over_its_range(orc):
+    """The oracle's exp_ps_simd bit for bit against an exact-arithmetic
+    evaluation of the source's steps with coefficients derived from the
+    Taylor series of 2^f (not typed from the source) over many arguments:
+    scores of a softmax (<= 0) down to the underflow of 2^n, small positive
+    ones, every half-integer t (where the rounding of t + 0.5 decides n) and
+    signed zeros.  A wrong coefficient, a different Horner order or a
+    different rounding of n changes thousands of these."""
+    rng = np.random.default_rng(33)
+    xs = list(rng.uniform(-110.0, 0.0, 3000).astype(np.float32))
+    xs += list(rng.uniform(-2.0, 2.0, 1500).astype(np.float32))
+    xs += list(rng.uniform(0.0, 60.0, 500).astype(np.float32))
+    ln2 = np.float32(math.log(2))
+    xs += [np.float32(k * 0.5 * ln2) for k in range(-60, 61)]   # t near k / 2
+    xs += [np.float32(0.0), np.float32(-0.0), np.float32(-87.3), np.float32(-1e-30)]
+    bad = []
+    for x in xs:
+        want = _exp_ps_simd_exact(x)
+        got = np.float32(orc.exp_ps_simd(float(x)))
+        if not (got == want or (np.isnan(got) and np.isnan(want))):
+            bad.append((float(x), float(got), float(want)))
+    assert not bad, f"{len(bad)} mismatches, e.g. {bad[:4]}"
+    # and the closed form where f = 0: exp_ps_simd(0) is the last coefficient, (ln 2)^5 / 120
+    assert np.float32(orc.exp_ps_simd(0.0)) == np.float32(math.log(2) ** 5 / 120)
 
 
 def test_attention_modes_differ_from_eight_positions(orc):

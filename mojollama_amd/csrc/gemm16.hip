@@ -154,26 +154,39 @@ MLLM_DEV void split16(float v, _Float16 &hi, _Float16 &lo)
 
 // Q4_K min-term weights of one row for one k16 slice of the min product: 8 values at once.
 // GGML: -dmin_b * m_j for the 8 sub-blocks of super-block b (hi/lo fp16); A4: -dmin_b for
-// super-blocks b0 .. b0+7 (exact in fp16).
+// super-blocks b0 .. b0+7 (exact in fp16).  Loaded (q16_min_ld) one slice ahead of their
+// use (q16_min_mk), so the min product's loads overlap the previous slice's MFMAs.
+struct q16_min_raw {
+    uint4 m;          // GGML: super-block b's metadata; A4: .x .. .w and m2 hold dmin words
+    uint4 m2;
+};
 template <int SEM>
-MLLM_DEV void q16_min_w(const mllm_packed &W, int nb, int row, int u0, f16x8 &hi, f16x8 &lo)
+MLLM_DEV void q16_min_ld(const mllm_packed &W, int nb, int row, int u0, q16_min_raw &r)
 {
     if constexpr (SEM == SEM_Q4_K_GGML) {
-        const int b = u0 / 8;   // the 8 sub-blocks of super-block b
+        const int b = min(u0 / 8, nb - 1);   // the 8 sub-blocks of super-block u0 / 8 (past nb: zeros, below)
+        r.m = gld<uint4>(W.p[1] + ((long)row * nb + b) * 16);
+    } else {
+        uint32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = gld<uint32_t>(W.p[1] + ((long)row * nb + min(u0 + j, nb - 1)) * 16);
+        r.m = make_uint4(v[0], v[1], v[2], v[3]);
+        r.m2 = make_uint4(v[4], v[5], v[6], v[7]);
+    }
+}
+template <int SEM>
+MLLM_DEV void q16_min_mk(const q16_min_raw &r, int nb, int u0, f16x8 &hi, f16x8 &lo)
+{
+    if constexpr (SEM == SEM_Q4_K_GGML) {
+        const bool live = u0 / 8 < nb;
+        const float dmin = h2f(r.m.x >> 16);
         float v[8];
-        if (b < nb) {
-            const uint4 m = gld<uint4>(W.p[1] + ((long)row * nb + b) * 16);
-            const float dmin = h2f(m.x >> 16);
 #pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                int s1, m1, s2, m2;
-                kq_pairs(m, j, s1, m1, s2, m2);
-                v[j] = -(dmin * (float)m1);
-                v[j + 1] = -(dmin * (float)m2);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        for (int j = 0; j < 8; j += 2) {
+            int s1, m1, s2, m2;
+            kq_pairs(r.m, j, s1, m1, s2, m2);
+            v[j] = live ? -(dmin * (float)m1) : 0.0f;
+            v[j + 1] = live ? -(dmin * (float)m2) : 0.0f;
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -183,12 +196,10 @@ MLLM_DEV void q16_min_w(const mllm_packed &W, int nb, int row, int u0, f16x8 &hi
             lo[j] = c;
         }
     } else {
+        const uint32_t w[8] = {r.m.x, r.m.y, r.m.z, r.m.w, r.m2.x, r.m2.y, r.m2.z, r.m2.w};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int b = u0 + j;
-            float v = 0.0f;
-            if (b < nb) v = -h2f(gld<uint32_t>(W.p[1] + ((long)row * nb + b) * 16) >> 16);
-            hi[j] = (_Float16)v;
+            hi[j] = (_Float16)(u0 + j < nb ? -h2f(w[j] >> 16) : 0.0f);
             lo[j] = (_Float16)0.0f;
         }
     }
@@ -480,6 +491,16 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         __builtin_amdgcn_s_waitcnt(0x0F70);
     };
     const int neb = __builtin_amdgcn_readfirstlane(min(EB, (n_ent + 31) / 32));
+    // the epilogue's per-entry values, loaded now (their latency hides under the main loop)
+    float inv_s[EB], inv_m[EB];
+    long orow_e[EB];
+#pragma unroll
+    for (int e = 0; e < EB; e++) {
+        const int ent = 32 * e + lr, row = s_row[ent];
+        inv_s[e] = a.x.inv_s[row];
+        inv_m[e] = Q::A4 ? a.x.inv_m[row] : 1.0f;
+        orow_e[e] = a.out_row ? (long)a.out_row[p0 + min(ent, n_ent - 1)] : (long)(p0 + ent);
+    }
     auto by_blocks = [&](auto np_c) __attribute__((always_inline)) {
         if constexpr (EB == 2) {
             if (neb == 1) main_loop(np_c, std::integral_constant<int, 1>{});
@@ -497,22 +518,38 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         }
     }
 
-    // ---- Q4_K min terms (split 0 only): acc += sum over units of (-dmin m) (x) sums
+    // ---- Q4_K min terms (split 0 only): acc += sum over units of (-dmin m) (x) sums, in
+    // slices of 16 units, each slice's loads issued while the previous slice multiplies
     if constexpr (Q::GGML || Q::A4) {
         if (blockIdx.z == 0) {
             const int nu = Q::GGML ? nb * 8 : nb;                 // sub-blocks / super-blocks
+            struct slice_ld {
+                q16_min_raw w[RB];
+                u32x4 s0[EB], s1[EB];
+            };
+            auto ld = [&](int u0, slice_ld &L) __attribute__((always_inline)) {
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) q16_min_ld<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, L.w[rb]);
+#pragma unroll
+                for (int e = 0; e < EB; e++) {
+                    const _Float16 *mp = a.x.m + (long)s_row[32 * e + lr] * a.x.ldm + u0 + 8 * kh;
+                    L.s0[e] = gld<u32x4>(mp);
+                    L.s1[e] = gld<u32x4>(mp + a.x.mplane);
+                }
+            };
+            slice_ld cur, nxt;
+            ld(0, cur);
             for (int u0 = 0; u0 < nu; u0 += 16) {
+                if (u0 + 16 < nu) ld(u0 + 16, nxt);
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) {
                     f16x8 whi, wlo;
-                    q16_min_w<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, whi, wlo);
+                    q16_min_mk<SEM>(cur.w[rb], nb, u0 + 8 * kh, whi, wlo);
 #pragma unroll
                     for (int e = 0; e < EB; e++) {
                         if (e >= neb) continue;
-                        const long er = s_row[32 * e + lr];
-                        const _Float16 *mp = a.x.m + er * a.x.ldm + u0 + 8 * kh;
-                        const f16x8 s0 = __builtin_bit_cast(f16x8, gld<u32x4>(mp));
-                        const f16x8 s1 = __builtin_bit_cast(f16x8, gld<u32x4>(mp + a.x.mplane));
+                        const f16x8 s0 = __builtin_bit_cast(f16x8, cur.s0[e]);
+                        const f16x8 s1 = __builtin_bit_cast(f16x8, cur.s1[e]);
                         f32x16 t = u0 == 0 ? f32x16{} : T[rb][e];
                         t = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi, s0, t, 0, 0, 0);
                         t = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi, s1, t, 0, 0, 0);
@@ -520,12 +557,13 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                         T[rb][e] = t;
                     }
                 }
+                cur = nxt;
             }
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
 #pragma unroll
                 for (int e = 0; e < EB; e++) {
-                    const float im = Q::A4 ? a.x.inv_m[s_row[32 * e + lr]] : 1.0f;
+                    const float im = Q::A4 ? inv_m[e] : 1.0f;
 #pragma unroll
                     for (int v = 0; v < 16; v++) acc[rb][e][v] = fmaf(im, T[rb][e][v], acc[rb][e][v]);
                 }
@@ -540,8 +578,8 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     for (int e = 0; e < EB; e++) {
         const int ent = 32 * e + lr;
         if (ent >= n_ent) continue;
-        const float is = a.x.inv_s[s_row[ent]];
-        const long orow = a.out_row ? a.out_row[p0 + ent] : (long)(p0 + ent);
+        const float is = inv_s[e];
+        const long orow = orow_e[e];
         float *o = out + orow * ldo;
 #pragma unroll
         for (int g = 0; g < 4; g++) {

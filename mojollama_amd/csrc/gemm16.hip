@@ -649,7 +649,8 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     // aligned group of 8 elements, in the order q16_elem gives (base + q16_elem(j)).
     // The first kHeld groups stay in registers between the two passes.
     constexpr int kHeld = 4;
-    const int nit = (a.ldh - 8 * tid + 2047) / 2048;
+    const int npos = nb * Q::PPS;   // positions in use (the row stride ldh is padded past them)
+    const int nit = (npos - 8 * tid + 2047) / 2048;
     auto gbase = [&](int P) __attribute__((always_inline)) { return (P / Q::PPS) * 256 + q16_elem<SEM>(P % Q::PPS); };
     float g[kHeld][8];
     // largest finite |x| (a NaN fails the comparison and is skipped)
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     _Float16 *h0 = a.h + (long)row * a.ldh, *h1 = h0 + a.hplane;
     // rows that fit the held groups store their second plane only when it holds a
     // non-zero element (the GEMM reads the zero row for the others); longer rows store it
-    const bool whole = a.ldh <= kHeld * 2048;
+    const bool whole = npos <= kHeld * 2048;
     f16x8 held1[kHeld];
     auto emit = [&](int P, const float (&gv)[8], f16x8 &v1) __attribute__((always_inline)) {
         const int sb = P / Q::PPS, pw = P % Q::PPS;
@@ -754,7 +755,7 @@ __global__ __launch_bounds__(256) void k_act16_q8(mllm_xq xq, int K, act16 a)
     const int nb = K / 256, nbk = K / 32;
     const int8_t *q = xq.q + (long)row * nbk * 32;
     _Float16 *h0 = a.h + (long)row * a.ldh;
-    for (int P = 8 * tid; P < a.ldh; P += 2048) {
+    for (int P = 8 * tid; P < nb * 128; P += 2048) {
         f16x8 v0;
         const int sb = P / 128, pw = P % 128;
         const uint2 w = *reinterpret_cast<const uint2 *>(q + sb * 256 + q16_elem<SEM_Q4_K_Q8>(pw));
@@ -829,9 +830,10 @@ static void act16_dims(int sem, int K, int &nplanes, int &ldh, int &ldm)
     const int nb = K / 256;
     const bool a4 = sem == SEM_Q4_K_Q8;
     nplanes = a4 ? 1 : 2;
-    ldh = nb * (a4 ? 128 : 256);
+    // the row stride is padded by 256 bytes: a power-of-two stride would put the same
+    // 128-byte column of every row on one L2 channel
+    ldh = nb * (a4 ? 128 : 256) + 128;
     ldm = sem == SEM_Q4_K_GGML ? (nb * 8 + 15) / 16 * 16 : a4 ? (nb + 15) / 16 * 16 : 0;
-    if (ldh == 0) ldh = 64;
 }
 
 size_t mllm_act16_bytes(int sem, long rows, int K)

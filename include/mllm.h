@@ -319,6 +319,12 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *layer);
  * speed trade of moe_forward_omp's experts (QK:2066-2250) on 288 GB HBM. */
 MLLM_API long mllm_moe_dense_experts(mllm_moe_layer *layer, void *stream);
 MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *layer, int T);
+/* Which GEMMs the layer's batched path runs, as bits: 1 gate/up and 2 down on
+ * the fp16-plane GEMM (K-quant super-blocks; MXFP4 when the matrices' E8M0
+ * exponents span at most 25 binades), 4 the whole layer on the per-token
+ * GEMVs (scales the GEMMs would not reproduce).  -1 for a null layer.  No
+ * reference counterpart: a query for callers and tests. */
+MLLM_API int mllm_moe_layer_info(const mllm_moe_layer *layer);
 /* out[T][N]; idx_out/w_out (optional, device [T][K]) receive the routing. */
 MLLM_API int mllm_moe_forward(const mllm_moe_layer *layer, const float *x, int T, float *out, void *workspace,
                               long ws_bytes, int *idx_out, float *w_out, void *stream);

@@ -14,6 +14,9 @@
 // the activation is exact in one fp16 plane (bf16 or Q8_0 inputs), two
 // otherwise -- against two bf16 planes on each side before.
 //
+// MXFP4 (one 32-element block per lane and step, its E8M0 scale folded into
+// the fp16 weights) runs on the same loop without per-super-block scales.
+//
 // Activations (mllm_launch_act16) are rows of fp16 in the MFMA's K order for
 // the semantic (each 64-position step of a row holds the elements a lane's
 // decoded weights meet, so weights decode straight into MFMA registers), the
@@ -26,6 +29,20 @@
 
 // Whether the fp16-plane GEMM serves a semantic.
 bool mllm_q16_supported(int sem);
+
+// MXFP4 on the fp16 plane (grouped expert GEMMs): a weight v 2^(E-127)
+// (QK:683-720, 629-678) decodes as the fp16 v 2^(E + eoff), exact when every
+// non-zero exponent E of the launch's matrices lies in [emax - 25, emax] with
+// eoff = 5 - emax; the result is scaled by wscale = 2^(-127 - eoff).
+// mllm_q16_mx: the MXFP4 semantics the GEMM serves (SEM_MXFP4 against fp32
+// activations, SEM_MXFP4_Q8 against the dequantised Q8_0 pack).
+bool mllm_q16_mx(int sem);
+// ORs the exponent range of n_mats MXFP4 matrices (device table) into
+// range[0] (smallest non-zero E, start at 255) and range[1] (largest, start at 0).
+hipError_t mllm_launch_mx_erange(const mllm_packed *tab_dev, int n_mats, int n_rows, int n_cols, int *range,
+                                 hipStream_t st);
+// eoff / wscale for an exponent range; false when the range does not fit.
+bool mllm_q16_mx_shift(int emin, int emax, int *eoff, float *wscale);
 
 // The activation rows of the fp16-plane GEMM (a workspace carve).
 struct act16 {
@@ -43,7 +60,8 @@ struct act16 {
 size_t mllm_act16_bytes(int sem, long rows, int K);
 act16 mllm_act16_carve(int sem, void *ws, long rows, int K);
 // fp32 rows x[r * ldx + k] (fp32-activation semantics), or the Q8_0 pack xq
-// (Q4_K x Q8_0: mllm_launch_quantize_q8_0's quants and min-term sums) -> act.
+// (Q4_K x Q8_0: mllm_launch_quantize_q8_0's quants and min-term sums; MXFP4 x
+// Q8_0: its quants times their block scales, exact in fp32) -> act.
 hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq, int rows, int K, const act16 &act,
                              hipStream_t st);
 
@@ -67,6 +85,9 @@ struct q16_args {
     int clamp_silu;
     int ksplit;
     float *part;
+    int eoff;        // MXFP4: weights decode as v 2^(E + eoff) (mllm_q16_mx_shift)
+    float wscale;    // MXFP4: 2^(-127 - eoff), applied to the result
+    int rows_fast;   // set by the launch: work tiles ordered row block fastest
 };
 // Entries per work tile of a launch (grouped launches: the bucketing's tile).
 int mllm_q16_tile_entries(bool grouped, int n_entries);

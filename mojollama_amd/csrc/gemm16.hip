@@ -19,6 +19,7 @@
 // rows 8 g + 4 (l / 32) + r).  Q4_K's min terms run after the loop as a small
 // MFMA product of per-row hi/lo fp16 weights (-dmin m) and fp16 hi/lo sums.
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 #include "decode.h"
 #include "gemm16.h"
@@ -34,14 +35,21 @@ template <int SEM> struct q16_traits {
     static constexpr bool A4 = SEM == SEM_Q4_K_Q8;
     static constexpr bool GGML = SEM == SEM_Q4_K_GGML;
     static constexpr bool Q6 = SEM == SEM_Q6_K_SEQ || SEM == SEM_Q6_K_LOWNIB;
-    static constexpr int PPS = A4 ? 128 : 256;   // activation positions per super-block
-    static constexpr int SPB = PPS / 64;         // steps per super-block
-    static constexpr int NPL = A4 ? 1 : 2;       // activation planes
+    // MXFP4: the scale rides in the weights, so a "super-block" is one step (two 32-blocks)
+    static constexpr bool MX = SEM == SEM_MXFP4 || SEM == SEM_MXFP4_Q8;
+    static constexpr bool Q8IN = SEM == SEM_MXFP4_Q8;   // activations from the Q8_0 pack
+    static constexpr int PPS = MX ? 64 : A4 ? 128 : 256;   // activation positions per super-block
+    static constexpr int EPS = MX ? 64 : 256;              // elements per super-block
+    static constexpr int SPB = PPS / 64;                   // steps per super-block
+    static constexpr int NPL = A4 ? 1 : 2;                 // activation planes
 };
 
 // Bits 3 and 4 ... of a step position p: i = p >> 4 (MFMA of the step), kh = (p >> 3) & 1
 // (lane half), j = p & 7 (slot).  sw(j): slot -> byte order of the nibble pairs (j bits 0,1 swapped).
 __host__ __device__ constexpr int sw3(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
+// MXFP4 slot order: slots 0,1 / 2,3 come from the low nibbles of bytes 0,2 / 1,3 of a word,
+// slots 4,5 / 6,7 from their high nibbles, i.e. elements 0,4,2,6,1,5,3,7 (bits reversed).
+__host__ __device__ constexpr int rev3(int j) { return ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1); }
 
 // Element (within its super-block) of activation position P (within the super-block's PPS).
 template <int SEM>
@@ -51,6 +59,8 @@ __host__ __device__ constexpr int q16_elem(int P)
     if (SEM == SEM_Q4_K_GGML) return 64 * st + 32 * (i >> 1) + 16 * kh + 8 * (i & 1) + sw3(j);
     if (SEM == SEM_Q4_K_Q8) return 32 * (2 * (2 * st + kh) + (i >> 1)) + 8 * (i & 1) + sw3(j);
     if (SEM == SEM_Q6_K_SEQ) return 64 * st + 32 * kh + 8 * i + 4 * (j & 1) + (j >> 1);
+    // MXFP4 (one step = two 32-blocks): lane half kh takes block kh, MFMA i its word i
+    if (SEM == SEM_MXFP4 || SEM == SEM_MXFP4_Q8) return 32 * kh + 8 * i + rev3(j);
     // SEM_Q6_K_LOWNIB: step = (half h, l-half lh); quad q = kh + 2 (i >> 1)
     return 128 * (st >> 1) + 32 * (kh + 2 * (i >> 1)) + 16 * (st & 1) + 8 * (i & 1) + sw3(j);
 }
@@ -145,6 +155,28 @@ MLLM_DEV void q16_decode(const q16_raw &r, const uint4 &meta, int st, int kh, u3
     }
 }
 
+// MXFP4 (QK:683-720, 629-678): element e of a 32-block is v = sext4(nibble e & 1 of byte
+// e / 2) times 2^(E - 127).  With the nibbles flipped by 8 (n ^ 8 = v + 8) the low nibble
+// of a byte gives the fp16 1032 + v and the high nibble, left in place, 1152 + 16 v; with
+// s = 2^(E + eoff) (E + eoff in [-20, 5]: every value below exact in fp16)
+//     v s = (1032 + v) s - 1032 s = (1152 + 16 v) (s / 16) - 72 s,
+// one v_pk_fma_f16 per pair.  E = 0 gives s = 0 (the reference's zero scale).
+MLLM_DEV void q16_decode_mx(const q16_raw &r, int kh, int eoff, u32x4 (&o)[4])
+{
+    // E of the lane's block (byte kh of the pair); min(E, 1) 2^(E + eoff): no compare,
+    // whose flag the compiler would form (and wait for) where E is loaded, not used
+    const uint32_t E = __builtin_amdgcn_ubfe(r.m.x, 8 * kh, 8);
+    const float s = __builtin_ldexpf(fminf((float)E, 1.0f), (int)E + eoff);
+    const h2 sa = hh(s), ca = hh(-1032.0f * s), sb = hh(0.0625f * s), cb = hh(-72.0f * s);
+    const uint32_t w[4] = {r.a.x ^ 0x88888888u, r.a.y ^ 0x88888888u, r.a.z ^ 0x88888888u, r.a.w ^ 0x88888888u};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t y = w[q] >> 8;
+        o[q] = u32x4{scl(and_or(w[q], 0x000F000Fu, kMagic), sa, ca), scl(and_or(y, 0x000F000Fu, kMagic), sa, ca),
+                     scl(and_or(w[q], 0x00F000F0u, kMagic), sb, cb), scl(and_or(y, 0x00F000F0u, kMagic), sb, cb)};
+    }
+}
+
 // v and its fp16 remainder: v = hi + lo (lo the fp16 rounding of v - hi).
 MLLM_DEV void split16(float v, _Float16 &hi, _Float16 &lo)
 {
@@ -206,6 +238,27 @@ MLLM_DEV void q16_min_mk(const q16_min_raw &r, int nb, int u0, f16x8 &hi, f16x8 
 }
 
 // ---------------------------------------------------------------- the GEMM
+// Raw buffer resource over p: byte offsets from p, no range limit below 2^32 - 1.
+MLLM_DEV __amdgpu_buffer_rsrc_t mk_rsrc(const void *p)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, -1, 0x00020000);
+}
+
+// silu(g) = g / (1 + e^-g) with e^-g = 2^t (1 + r ln 2), t = -g log2(e) rounded and r its
+// rounding error (an fma), on v_exp_f32 and v_rcp_f32 (each within 1 ulp): a few ulp from
+// the correctly rounded quotient, in a third of the instructions of expf and the IEEE
+// division.  Where the correction is not a number (2^t = inf, or g = +-inf and r NaN) 2^t
+// stands: inf (silu = -0), 0 (g = +inf: silu = inf), inf (g = -inf: NaN), as the quotient.
+MLLM_DEV float silu16(float g)
+{
+    constexpr float L = 1.44269502f, Llo = 1.92596299e-8f;   // log2(e) = L + Llo
+    const float t = -g * L;
+    const float r = fmaf(-g, L, -t) - g * Llo;
+    const float e0 = __builtin_amdgcn_exp2f(t);
+    const float e1 = fmaf(e0 * r, 0.693147181f, e0);
+    const float e = e1 == e1 ? e1 : e0;
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
 // Byte offset loads from a wave-uniform base: the address is base (SGPRs) +
 // a 32-bit per-lane offset, so the loop issues no 64-bit address arithmetic.
 template <class T> MLLM_DEV T gldo(const void *base, uint32_t off) { return gld<T>((const uint8_t *)base + off); }
@@ -215,11 +268,14 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 {
     using Q = q16_traits<SEM>;
     constexpr int RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 128, SPB = Q::SPB, NPL = Q::NPL;
-    static_assert(SPB == 2 || SPB == 4, "steps run in units of four");
+    constexpr bool MX = Q::MX;
+    static_assert(SPB == 2 || SPB == 4 || MX, "steps run in units of four");
     __shared__ __attribute__((aligned(16))) float sD[4][RB * 32];
     __shared__ int s_row[TM];
 
-    // ---- work tile (XCD-contiguous ranges of the live tiles, entry tile fastest)
+    // ---- work tile (XCD-contiguous ranges of the live tiles; entry tile fastest, so
+    // the workgroups an XCD runs at once share weight rows, or with rows_fast row block
+    // fastest, so they share activation tiles)
     int bx, by;
     {
         const int nx = gridDim.x, ny = a.tile_expert ? *a.n_tiles : (int)gridDim.y, total = nx * ny;
@@ -227,8 +283,13 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         if (L >= total) return;
         const int xcd = L & 7;
         const int w = xcd * (total >> 3) + min(xcd, total & 7) + (L >> 3);
-        by = w % ny;
-        bx = w / ny;
+        if (a.rows_fast) {
+            bx = w % nx;
+            by = w / nx;
+        } else {
+            by = w % ny;
+            bx = w / ny;
+        }
     }
     int p0, p1;
     mllm_packed W, W2;
@@ -258,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     lo_any = __syncthreads_or(lo_any);
     const int npl = __builtin_amdgcn_readfirstlane(NPL > 1 && lo_any ? 2 : 1);
 
-    const int nb = a.n_cols / 256;
+    const int nb = a.n_cols / Q::EPS;
     // super-blocks of this workgroup: all, or split z of a.ksplit (whole super-blocks: d joins per block)
     int b_beg = 0, b_end = nb;
     if (a.ksplit > 1) {
@@ -273,18 +334,29 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // bytes (the step's 64 positions); lane i writes row i / 8, slot i % 8, and fetches
     // chunk slot ^ f(row) of its entry row, f(r) = (r ^ r >> 3) & 7 over r mod 32, so the
     // MFMA reads of 16 lanes (rows r .. r+15, one chunk each) fall in distinct banks.
-    // Four buffers, each its own LDS object: the compiler then tracks which outstanding
-    // loads write which buffer.  One plane: buffer = step % 4, loads run three steps
-    // ahead; two planes: buffer = 2 (step % 2) + plane, one step ahead.
+    // Buffers, each its own LDS object: the compiler then tracks which outstanding loads
+    // write which buffer.  One plane: buffer = step % 4, loads run three steps ahead; two
+    // planes, MXFP4: buffer = 2 (step % 4) + plane, three steps ahead (eight buffers); two
+    // planes, K-quants: buffer = 2 (step % 2) + plane, one step ahead.
     constexpr int NCH = TM * 8 / 256;   // load instructions per wave, plane and step (= EB)
+    constexpr bool B8 = MX;   // K-quant tiles keep four buffers (their LDS then admits a third workgroup per CU)
+    constexpr int D2 = B8 ? 3 : 1;      // two-plane prefetch distance (steps)
     __shared__ __attribute__((aligned(16))) _Float16 sB0[TM * 64], sB1[TM * 64], sB2[TM * 64], sB3[TM * 64];
+    __shared__ __attribute__((aligned(16))) _Float16 sB4[B8 ? TM * 64 : 8], sB5[B8 ? TM * 64 : 8],
+        sB6[B8 ? TM * 64 : 8], sB7[B8 ? TM * 64 : 8];
     auto sbuf = [&](auto i_c) __attribute__((always_inline)) -> _Float16 * {
         constexpr int i = decltype(i_c)::value;
         if constexpr (i == 0) return sB0;
         else if constexpr (i == 1) return sB1;
         else if constexpr (i == 2) return sB2;
-        else return sB3;
+        else if constexpr (i == 3) return sB3;
+        else if constexpr (i == 4) return sB4;
+        else if constexpr (i == 5) return sB5;
+        else if constexpr (i == 6) return sB6;
+        else return sB7;
     };
+    // buffer of unit step u (0..3), plane p of a two-plane tile
+    auto bidx2 = [](int u, int p) constexpr { return D2 == 3 ? 2 * u + p : 2 * (u & 1) + p; };
     auto fsw = [](int r) { return (r ^ (r >> 3)) & 7; };
     // boff: a lane's byte offsets in the first plane; boff1 in the second (from its base,
     // set by the two-plane path): rows whose second plane is zero read the zero row after it
@@ -309,13 +381,25 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
         for (int i = 0; i < 4; i++) raddr[i] = 128u * lr + 16u * (uint32_t)((2 * i + kh) ^ fl);
     }
+    // MXFP4 reads through buffer resources (base in SGPRs, a 32-bit lane offset, the step's
+    // offset in an SGPR): no per-load 64-bit address arithmetic in the loop
+    const __amdgpu_buffer_rsrc_t xrs = mk_rsrc(a.x.h);
     auto dma = [&](auto nb_c, int s, int p, _Float16 *dst) __attribute__((always_inline)) {
         constexpr int NEB = decltype(nb_c)::value;   // chunk c holds entry block c
-        const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
+        if constexpr (MX) {
+            const int so = 2 * (p * (int)a.x.hplane + 64 * s);
 #pragma unroll
-        for (int c = 0; c < NEB; c++)
-            __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
-                                             (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
+            for (int c = 0; c < NEB; c++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xrs, (__attribute__((address_space(3))) void *)(dst + (256 * c + 64 * wave) * 8), 16,
+                    (int)(p ? boff1[c] : boff[c]), so, 0, 0);
+        } else {
+            const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
+#pragma unroll
+            for (int c = 0; c < NEB; c++)
+                __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
+                                                 (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
+        }
     };
     // this wave's loads older than the newest n are done, then the workgroup meets: every
     // wave's older loads have landed and every wave has finished the previous step
@@ -328,13 +412,17 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     };
 
     // weight rows: bulk plane bytes per super-block (Q4_K / Q6_K ql: 128) and per-row offsets
-    const uint32_t rq = (uint32_t)wrow * (uint32_t)nb;   // row's first super-block index
+    const uint32_t rq = (uint32_t)wrow * (uint32_t)(MX ? 2 * nb : nb);   // row's first super-block (MX: 32-block)
     auto fetch_w = [&](const mllm_packed &M, int b, int st, q16_raw &r) __attribute__((always_inline)) {
         const uint32_t bi = rq + (uint32_t)b;
         if constexpr (SEM == SEM_Q4_K_GGML) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
         } else if constexpr (SEM == SEM_Q4_K_Q8) {
             r.a = gldo<u32x4>(M.p[0] + 64 * st, bi * 128u + 32u * kh);
+        } else if constexpr (MX) {
+            // step b: blocks 2b (lane half 0) and 2b + 1 (half 1), 16 nibble bytes and E each
+            r.a = __builtin_amdgcn_raw_buffer_load_b128(mk_rsrc(M.p[0]), (int)(rq * 16u + 16u * kh), 32 * b, 0);
+            r.m.x = __builtin_amdgcn_raw_buffer_load_b16(mk_rsrc(M.p[1]), (int)rq, 2 * b, 0);   // both blocks' E (rq is even)
         } else if constexpr (SEM == SEM_Q6_K_SEQ) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
             const uint2 q = gldo<uint2>(M.p[1] + 16 * st, bi * 64u + 8u * kh);
@@ -369,13 +457,17 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         u32x4 A[RB][4];
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
-            float d;
-            q16_decode<SEM>(r[rb], meta[rb], st, kh, A[rb], d);
-            if (st == 0 && kh == 0) sD[wave][rb * 32 + lr] = d;
+            if constexpr (MX) {
+                q16_decode_mx(r[rb], kh, a.eoff, A[rb]);
+            } else {
+                float d;
+                q16_decode<SEM>(r[rb], meta[rb], st, kh, A[rb], d);
+                if (st == 0 && kh == 0) sD[wave][rb * 32 + lr] = d;
+            }
         }
         const uint8_t *bp[NP];
-        bp[0] = (const uint8_t *)sbuf(std::integral_constant<int, NP == 1 ? u : 2 * (u & 1)>{});
-        if constexpr (NP > 1) bp[1] = (const uint8_t *)sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{});
+        bp[0] = (const uint8_t *)sbuf(std::integral_constant<int, NP == 1 ? u : bidx2(u, 0)>{});
+        if constexpr (NP > 1) bp[1] = (const uint8_t *)sbuf(std::integral_constant<int, bidx2(u, 1)>{});
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -385,9 +477,13 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                     const f16x8 bv = *reinterpret_cast<const f16x8 *>(bp[p] + 4096 * e + raddr[i]);
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++) {
-                        const f32x16 c = (st == 0 && i == 0 && p == 0) ? f32x16{} : T[rb][e];
-                        T[rb][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A[rb][i]), bv, c,
-                                                                          0, 0, 0);
+                        const f16x8 av = __builtin_bit_cast(f16x8, A[rb][i]);
+                        if constexpr (MX) {   // scaled weights: straight into the result
+                            acc[rb][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[rb][e], 0, 0, 0);
+                        } else {
+                            const f32x16 c = (st == 0 && i == 0 && p == 0) ? f32x16{} : T[rb][e];
+                            T[rb][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, c, 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -417,7 +513,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // NEB: the entry blocks the tile's entries occupy (a bucketing tile of at most 32
     // entries runs one: half the MFMAs and activation loads)
     auto main_loop = [&](auto np_c, auto nb_c) __attribute__((always_inline)) {
-        constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value, D = NP == 1 ? 3 : 1;
+        constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value, D = NP == 1 ? 3 : D2;
         const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
         q16_raw rw[4][RB];
         // Q4_K super-block metadata (kq_pairs layout): mA for the unit's first super-block,
@@ -447,45 +543,86 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             if constexpr (NP == 1) {
                 dma(nb_c, sc, 0, sbuf(std::integral_constant<int, u>{}));
             } else {
-                dma(nb_c, sc, 0, sbuf(std::integral_constant<int, 2 * (u & 1)>{}));
-                dma(nb_c, sc, 1, sbuf(std::integral_constant<int, 2 * (u & 1) + 1>{}));
+                dma(nb_c, sc, 0, sbuf(std::integral_constant<int, bidx2(u, 0)>{}));
+                dma(nb_c, sc, 1, sbuf(std::integral_constant<int, bidx2(u, 1)>{}));
             }
         };
-        load_b(s_beg, std::integral_constant<int, 0>{});
-        if constexpr (D >= 2) load_b(s_beg + 1, std::integral_constant<int, 1>{});
-        if constexpr (D >= 3) load_b(s_beg + 2, std::integral_constant<int, 2>{});
-        fm(b_beg, mA);
-        fw(s_beg, rw[0]);
-        fw(s_beg + 1, rw[1]);
-        fw(s_beg + 2, rw[2]);
-        for (int s0 = s_beg; s0 <= s_last; s0 += 4) {
+        if constexpr (MX && D == 3) {
+            // in the loop's order (a step's activations, then its weights), so the loads in
+            // flight at the loop head are counted alike on entry and on the back edge
+            load_b(s_beg, std::integral_constant<int, 0>{});
+            fw(s_beg, rw[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(s_beg + 1, std::integral_constant<int, 1>{});
+            fw(s_beg + 1, rw[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(s_beg + 2, std::integral_constant<int, 2>{});
+            fw(s_beg + 2, rw[2]);
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            load_b(s_beg, std::integral_constant<int, 0>{});
+            if constexpr (D >= 2) load_b(s_beg + 1, std::integral_constant<int, 1>{});
+            if constexpr (D >= 3) load_b(s_beg + 2, std::integral_constant<int, 2>{});
+            fm(b_beg, mA);
+            fw(s_beg, rw[0]);
+            fw(s_beg + 1, rw[1]);
+            fw(s_beg + 2, rw[2]);
+        }
+        // unit of four steps from s0.  MXFP4: a short unit (the last, when the step count is
+        // not a multiple of four) runs its first s_last - s0 + 1 steps, after the loop: inside
+        // it, the skipped steps would hide the count of loads in flight at the loop head from
+        // the compiler, which then waits for all of them
+        auto unit = [&](int s0, auto full_c) __attribute__((always_inline)) {
+            constexpr bool full = decltype(full_c)::value;
             const int b0 = s0 / SPB;
             // unit step u (= step s0 + u): wait for its activation loads, start those of
             // step + D into the buffer the previous step read, and the weights of step + 3
             auto one = [&](auto u_c) __attribute__((always_inline)) {
                 constexpr int u = decltype(u_c)::value;
                 const int s = s0 + u;
-                sync_loads(std::integral_constant<int, (D - 1) * NEB * NP>{});
+                if constexpr (MX) {
+                    // loads that surely follow step s's activation loads: those of steps s + 1
+                    // .. s + D - 1 (activations, and the two weight loads per matrix, which
+                    // the compiler may order before or after a step's activation loads)
+                    sync_loads(std::integral_constant<int, (D - 1) * (NEB * NP + 2 * RB)>{});
+                    // keep each step's decode in its step: hoisted into an earlier one, it
+                    // would wait there for weight loads just issued
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    sync_loads(std::integral_constant<int, (D - 1) * NEB * NP>{});
+                }
                 load_b(s + D, std::integral_constant<int, (u + D) & 3>{});
                 fw(s + 3, rw[(u + 3) & 3]);
                 if constexpr (u == 0) fm(b0 + 1, mB);
                 if constexpr (SPB == 2 && u == 2) fm(b0 + 2, mA);
                 mfmas(np_c, nb_c, std::integral_constant<int, u % SPB>{}, u_c, rw[u], (SPB == 2 && u >= 2) ? mB : mA);
-                if constexpr (u % SPB == SPB - 1) d_apply(nb_c);
+                if constexpr (!MX && u % SPB == SPB - 1) d_apply(nb_c);
             };
             one(std::integral_constant<int, 0>{});
-            one(std::integral_constant<int, 1>{});
-            if constexpr (SPB == 4) {
+            if constexpr (MX) {
+                if (full || s0 + 1 <= s_last) one(std::integral_constant<int, 1>{});
+                if (full || s0 + 2 <= s_last) one(std::integral_constant<int, 2>{});
+                if (full || s0 + 3 <= s_last) one(std::integral_constant<int, 3>{});
+            } else if constexpr (SPB == 4) {
+                one(std::integral_constant<int, 1>{});
                 one(std::integral_constant<int, 2>{});
                 one(std::integral_constant<int, 3>{});
-            } else if (s0 + 2 <= s_last) {
-                one(std::integral_constant<int, 2>{});
-                one(std::integral_constant<int, 3>{});
-            }
-            if constexpr (SPB == 4) {
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) mA[rb] = mB[rb];
+            } else {   // two-step super-blocks: a unit holds one or two
+                one(std::integral_constant<int, 1>{});
+                if (s0 + 2 <= s_last) {
+                    one(std::integral_constant<int, 2>{});
+                    one(std::integral_constant<int, 3>{});
+                }
             }
+        };
+        if constexpr (MX) {
+            int s0 = s_beg;
+            for (; s0 + 3 <= s_last; s0 += 4) unit(s0, std::true_type{});
+            if (s0 <= s_last) unit(s0, std::false_type{});
+        } else {
+            for (int s0 = s_beg; s0 <= s_last; s0 += 4) unit(s0, std::true_type{});
         }
         // no load may still be writing the buffers when the workgroup's LDS is released
         __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -579,6 +716,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         const int ent = 32 * e + lr;
         if (ent >= n_ent) continue;
         const float is = inv_s[e];
+        const float ws = MX ? a.wscale : 1.0f;   // the weights' scale, after the row's (exact powers of two)
         const long orow = orow_e[e];
         float *o = out + orow * ldo;
 #pragma unroll
@@ -588,10 +726,13 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 float x0 = acc[0][e][4 * g + r] * is;
+                if constexpr (MX) x0 *= ws;
                 if constexpr (DUAL) {
                     // moe_forward_omp SiLU (QK:2157-2164): clamp to +-80, then silu(g) * u
                     if (a.clamp_silu) x0 = fminf(fmaxf(x0, -80.0f), 80.0f);
-                    x0 = (x0 / (1.0f + expf(-x0))) * (acc[DUAL ? 1 : 0][e][4 * g + r] * is);
+                    float x1 = acc[DUAL ? 1 : 0][e][4 * g + r] * is;
+                    if constexpr (MX) x1 *= ws;
+                    x0 = silu16(x0) * x1;
                 }
                 v[r] = x0;
             }
@@ -621,9 +762,11 @@ __global__ void k_q16_ksum(const float *__restrict__ part, int ks, long plane, i
 // ---------------------------------------------------------------- activations
 // fp32 row -> scaled fp16 planes in the semantic's K order, the row's inverse
 // scale, lo_nz, and (Q4_K ggml) the fp16 hi/lo sums of each 32-element
-// sub-block.  One workgroup per row.
+// sub-block.  One workgroup per row.  MXFP4 x Q8_0 reads the row from the
+// Q8_0 pack instead: quant times block scale (int8 times an fp16 value: exact
+// in fp32), the activation mxfp4_row_dot_q8 (QK:629-678) multiplies.
 template <int SEM>
-__global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int ldx, int K, act16 a)
+__global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int ldx, mllm_xq xq, int K, act16 a)
 {
     using Q = q16_traits<SEM>;
     __shared__ float red[4];
@@ -632,12 +775,18 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
         for (int P = 8 * tid; P < a.ldh; P += 2048) *reinterpret_cast<f16x8 *>(a.zero + P) = f16x8{};
         return;
     }
-    const float *xr = x + (long)row * ldx;
+    const float *xr = Q::Q8IN ? nullptr : x + (long)row * ldx;
     const bool vec = ((uintptr_t)xr & 15) == 0;
-    const int nb = K / 256, kused = nb * 256;
+    const int nb = K / Q::EPS;
     // eight consecutive elements from k (a multiple of 8)
     auto ld8 = [&](int k, float (&v)[8]) __attribute__((always_inline)) {
-        if (vec) {
+        if constexpr (Q::Q8IN) {
+            const long nbk = K / 32;
+            const uint2 w = *reinterpret_cast<const uint2 *>(xq.q + (long)row * nbk * 32 + k);
+            const float d = xq.d[(long)row * nbk + (k >> 5)];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = (float)(int8_t)(((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xFF) * d;
+        } else if (vec) {
             const float4 p = *reinterpret_cast<const float4 *>(xr + k), q = *reinterpret_cast<const float4 *>(xr + k + 4);
             v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
         } else {
@@ -651,7 +800,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     constexpr int kHeld = 4;
     const int npos = nb * Q::PPS;   // positions in use (the row stride ldh is padded past them)
     const int nit = (npos - 8 * tid + 2047) / 2048;
-    auto gbase = [&](int P) __attribute__((always_inline)) { return (P / Q::PPS) * 256 + q16_elem<SEM>(P % Q::PPS); };
+    auto gbase = [&](int P) __attribute__((always_inline)) { return (P / Q::PPS) * Q::EPS + q16_elem<SEM>(P % Q::PPS); };
     float g[kHeld][8];
     // largest finite |x| (a NaN fails the comparison and is skipped)
     float m = 0.0f;
@@ -671,7 +820,6 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
         ld8(gbase(8 * tid + 2048 * it), v);
         mx(v);
     }
-    (void)kused;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -701,7 +849,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
             v0[j] = hi;
             v1[j] = lo;
             nz |= (float)lo != 0.0f;
-            part += gv[j] * s;
+            if constexpr (Q::GGML) part += gv[j] * s;
         }
         *reinterpret_cast<f16x8 *>(h0 + P) = v0;
         if (!whole) *reinterpret_cast<f16x8 *>(h1 + P) = v1;
@@ -799,6 +947,35 @@ __global__ __launch_bounds__(256) void k_act16_q8(mllm_xq xq, int K, act16 a)
 
 size_t al256(size_t n) { return (n + 255) / 256 * 256; }
 
+// range[0] = min over non-zero E, range[1] = max E of the matrices' E8M0 bytes.
+__global__ void k_mx_erange(const mllm_packed *__restrict__ tab, long nblk, int *__restrict__ range)
+{
+    const uint8_t *e = tab[blockIdx.y].p[1];
+    int lo = 255, hi = 0;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nblk; i += (long)gridDim.x * blockDim.x) {
+        const int v = e[i];
+        if (v) lo = min(lo, v);
+        hi = max(hi, v);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        lo = min(lo, __shfl_xor(lo, o, 64));
+        hi = max(hi, __shfl_xor(hi, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        if (lo < 255) atomicMin(range, lo);
+        if (hi > 0) atomicMax(range + 1, hi);
+    }
+}
+
+// Grouped launches whose activation planes hold at least this many bytes are walked row
+// block fastest: an XCD's L2 (4 MB) then keeps the few activation tiles its workgroups
+// read at once, where entry tile fastest would read every tile once per row block.
+// Measured on the MoE down projections: GPT-OSS T = 1280 (62 MB) 256 -> 234 us, Qwen3
+// T = 1280 (37 MB) 158 -> 146 us; GPT-OSS T = 256 (12 MB) 93 -> 104 us, so smaller
+// planes keep entry tile fastest.
+constexpr long kRowsFastBytes = 24l << 20;
+
 template <int SEM, bool DUAL, int EB>
 hipError_t launch16(const q16_args &a, int max_tiles, hipStream_t st)
 {
@@ -808,6 +985,7 @@ hipError_t launch16(const q16_args &a, int max_tiles, hipStream_t st)
     if (grid.y == 0) return hipSuccess;
     q16_args b = a;
     b.ksplit = ks;
+    b.rows_fast = a.tile_expert && (long)a.n_entries * a.x.ldh * 2 * q16_traits<SEM>::NPL >= kRowsFastBytes;
     hipLaunchKernelGGL((k_q16<SEM, DUAL, EB>), grid, dim3(256), 0, st, b);
     if (ks > 1) {
         const long plane = (long)a.n_entries * a.n_rows;
@@ -824,6 +1002,31 @@ bool mllm_q16_supported(int sem)
     return sem == SEM_Q4_K_GGML || sem == SEM_Q4_K_Q8 || sem == SEM_Q6_K_SEQ || sem == SEM_Q6_K_LOWNIB;
 }
 
+bool mllm_q16_mx(int sem) { return sem == SEM_MXFP4 || sem == SEM_MXFP4_Q8; }
+
+hipError_t mllm_launch_mx_erange(const mllm_packed *tab_dev, int n_mats, int n_rows, int n_cols, int *range,
+                                 hipStream_t st)
+{
+    const long nblk = (long)n_rows * (n_cols / 32);
+    if (n_mats <= 0 || nblk <= 0) return hipSuccess;
+    const unsigned gx = (unsigned)std::min<long>((nblk + 255) / 256, 64);
+    hipLaunchKernelGGL(k_mx_erange, dim3(gx, (unsigned)n_mats), dim3(256), 0, st, tab_dev, nblk, range);
+    return hipGetLastError();
+}
+
+// Largest exponent to E' = 5 (then 1032 s <= 33024 and 8 s <= 256 fit fp16), smallest
+// non-zero to E' >= -20 (then s / 16 >= 2^-24, the least fp16 subnormal); emax <= 177
+// (2^50 scales: the Q8_0 form's scale clamp never binds, as in the scale scan) and
+// emax >= 6 (wscale a normal float).  No non-zero exponent: all weights zero.
+bool mllm_q16_mx_shift(int emin, int emax, int *eoff, float *wscale)
+{
+    if (emax <= 0) { *eoff = 0; *wscale = 1.0f; return true; }
+    if (emax - emin > 25 || emax < 6 || emax > 177) return false;
+    *eoff = 5 - emax;
+    *wscale = std::ldexp(1.0f, -127 - *eoff);
+    return true;
+}
+
 // Activation layout: h [planes][rows][ldh] | m [2][rows][ldm] | inv_s | inv_m | lo_nz.
 static void act16_dims(int sem, int K, int &nplanes, int &ldh, int &ldm)
 {
@@ -832,7 +1035,7 @@ static void act16_dims(int sem, int K, int &nplanes, int &ldh, int &ldm)
     nplanes = a4 ? 1 : 2;
     // the row stride is padded by 256 bytes: a power-of-two stride would put the same
     // 128-byte column of every row on one L2 channel
-    ldh = nb * (a4 ? 128 : 256) + 128;
+    ldh = (mllm_q16_mx(sem) ? K : nb * (a4 ? 128 : 256)) + 128;
     ldm = sem == SEM_Q4_K_GGML ? (nb * 8 + 15) / 16 * 16 : a4 ? (nb + 15) / 16 * 16 : 0;
 }
 
@@ -870,12 +1073,25 @@ hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq
                              hipStream_t st)
 {
     if (rows <= 0) return hipSuccess;
-    if (K < 256 || K % 256 || ((uintptr_t)act.h & 15)) return hipErrorInvalidValue;
+    const int unit = mllm_q16_mx(sem) ? 64 : 256;
+    if (K < unit || K % unit || ((uintptr_t)act.h & 15)) return hipErrorInvalidValue;
+    const mllm_xq nq{};
     switch (sem) {
-    case SEM_Q4_K_GGML: hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
-    case SEM_Q6_K_SEQ: hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q4_K_GGML:
+        hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
+        break;
+    case SEM_Q6_K_SEQ:
+        hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
+        break;
     case SEM_Q6_K_LOWNIB:
-        hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act);
+        hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
+        break;
+    case SEM_MXFP4:
+        hipLaunchKernelGGL(k_act16<SEM_MXFP4>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
+        break;
+    case SEM_MXFP4_Q8:
+        if (!xq) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_act16<SEM_MXFP4_Q8>, dim3(rows + 1), dim3(256), 0, st, nullptr, 0, *xq, K, act);
         break;
     case SEM_Q4_K_Q8:
         if (!xq || K / 256 > 256) return hipErrorInvalidValue;
@@ -894,7 +1110,7 @@ int mllm_q16_tile_entries(bool grouped, int n_entries) { return !grouped && n_en
 // tiles per CU (512), each split keeping at least 4 super-blocks.
 int mllm_q16_ksplit(int sem, int n_rows, int n_cols, int n_entries)
 {
-    if (!mllm_q16_supported(sem) || n_entries <= 0) return 1;
+    if (!mllm_q16_supported(sem) || n_entries <= 0) return 1;   // MXFP4: grouped launches, no split
     const int tm = mllm_q16_tile_entries(false, n_entries);
     const long tiles = (long)((n_rows + 127) / 128) * ((n_entries + tm - 1) / tm);
     if (tiles >= 384) return 1;
@@ -906,7 +1122,9 @@ int mllm_q16_ksplit(int sem, int n_rows, int n_cols, int n_entries)
 
 hipError_t mllm_launch_q16(int sem, bool dual, const q16_args &a, int max_tiles, hipStream_t st)
 {
-    if (a.n_cols < 256 || a.n_cols % 256) return hipErrorInvalidValue;
+    const int unit = mllm_q16_mx(sem) ? 64 : 256;
+    if (a.n_cols < unit || a.n_cols % unit) return hipErrorInvalidValue;
+    if (mllm_q16_mx(sem) && a.ksplit > 1) return hipErrorInvalidValue;
     const bool grouped = a.tile_expert != nullptr;
     const int tm = mllm_q16_tile_entries(grouped, a.n_entries);
 #define Q16(S)                                                                         \
@@ -919,5 +1137,8 @@ hipError_t mllm_launch_q16(int sem, bool dual, const q16_args &a, int max_tiles,
     Q16(SEM_Q6_K_SEQ)
     Q16(SEM_Q6_K_LOWNIB)
 #undef Q16
+    // MXFP4: the grouped expert GEMMs (gate + up fused against fp32 x, down against Q8_0 h)
+    if (sem == SEM_MXFP4 && dual && grouped) return launch16<SEM_MXFP4, true, 2>(a, max_tiles, st);
+    if (sem == SEM_MXFP4_Q8 && !dual && grouped) return launch16<SEM_MXFP4_Q8, false, 2>(a, max_tiles, st);
     return hipErrorInvalidValue;
 }

@@ -245,6 +245,10 @@ struct mllm_moe_layer {
     mllm_packed *dtab = nullptr;
     void *dmem = nullptr;
     int dense_gu = 0, dense_d = 0, ld_gu = 0, ld_d = 0;
+    // MXFP4 on the fp16-plane GEMM (mllm_q16_mx_shift of the matrices' exponent range):
+    // gate/up (both MXFP4) and down, with their exponent offsets and result scales
+    int mx_gu = 0, mx_d = 0, eoff_gu = 0, eoff_d = 0;
+    float ws_gu = 1.0f, ws_d = 1.0f;
 };
 
 struct moe_ws {
@@ -258,14 +262,36 @@ struct moe_ws {
 };
 
 // Whether the batched path runs gate/up and down on the fp16-plane GEMM (gemm16.h):
-// K-quant semantics over whole super-blocks, on the packed experts (not the dense copies).
+// K-quant semantics over whole super-blocks, on the packed experts (not the dense copies);
+// MXFP4 over whole 64-element steps when the exponent ranges fit (moe_mx_setup).
 static bool moe_q16_gu(const mllm_moe_layer &L)
 {
-    return L.sem_g == L.sem_u && mllm_q16_supported(L.sem_g) && !L.dense_gu && L.N % 256 == 0;
+    return (L.sem_g == L.sem_u && mllm_q16_supported(L.sem_g) && !L.dense_gu && L.N % 256 == 0) ||
+           (L.mx_gu && L.N % 64 == 0);
 }
 static bool moe_q16_d(const mllm_moe_layer &L)
 {
-    return L.sem_d >= 0 && mllm_q16_supported(L.sem_d) && !L.dense_d && L.M % 256 == 0;
+    return (L.sem_d >= 0 && mllm_q16_supported(L.sem_d) && !L.dense_d && L.M % 256 == 0) || (L.mx_d && L.M % 64 == 0);
+}
+
+// The exponent ranges of the MXFP4 gate/up pair and down matrices; sets mx_gu / mx_d
+// where they fit the fp16 plane.  Returns 0, or -1 on a HIP error.
+static int moe_mx_setup(mllm_moe_layer *L)
+{
+    const bool gu = L->sem_g == SEM_MXFP4 && L->sem_u == SEM_MXFP4, dn = L->sem_d == SEM_MXFP4_Q8;
+    if (L->gemv_only || (!gu && !dn)) return 0;
+    int h[4] = {255, 0, 255, 0};
+    int *f = nullptr;
+    if (hipMalloc(&f, sizeof h) != hipSuccess) return -1;
+    hipError_t r = hipMemcpy(f, h, sizeof h, hipMemcpyHostToDevice);
+    if (r == hipSuccess && gu) r = mllm_launch_mx_erange(L->tab, 2 * L->E, L->M, L->N, f, nullptr);
+    if (r == hipSuccess && dn) r = mllm_launch_mx_erange(L->tab + 2 * L->E, L->E, L->N, L->M, f + 2, nullptr);
+    if (r == hipSuccess) r = hipMemcpy(h, f, sizeof h, hipMemcpyDeviceToHost);
+    (void)hipFree(f);
+    if (r != hipSuccess) return -1;
+    if (gu) L->mx_gu = mllm_q16_mx_shift(h[0], h[1], &L->eoff_gu, &L->ws_gu);
+    if (dn) L->mx_d = mllm_q16_mx_shift(h[2], h[3], &L->eoff_d, &L->ws_d);
+    return 0;
 }
 
 // Tokens up to which the layer runs the decode GEMVs (one job per (token,
@@ -340,7 +366,8 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
         hipMalloc(&L->router_p, rbytes) != hipSuccess ||
         mllm_launch_router_pack(router_dev, N, E, L->router_p, nullptr) != hipSuccess ||
         hipStreamSynchronize(nullptr) != hipSuccess ||
-        (L->gemv_only = mllm_moe_needs_gemv(L->tab, L->sem_g, L->sem_u, L->sem_d, N, M, E)) < 0) {
+        (L->gemv_only = mllm_moe_needs_gemv(L->tab, L->sem_g, L->sem_u, L->sem_d, N, M, E)) < 0 ||
+        moe_mx_setup(L) != 0) {
         mllm_moe_release(L);
         return nullptr;
     }
@@ -414,6 +441,12 @@ MLLM_API long mllm_moe_workspace_size(const mllm_moe_layer *L, int T)
     return L ? (long)moe_ws_layout(*L, T, nullptr, nullptr) : -1;
 }
 
+MLLM_API int mllm_moe_layer_info(const mllm_moe_layer *L)
+{
+    if (!L) return -1;
+    return (moe_q16_gu(*L) ? 1 : 0) | (moe_q16_d(*L) ? 2 : 0) | (L->gemv_only ? 4 : 0);
+}
+
 } // extern "C"
 
 // x [T][N] fp32 -> out [T][N].  Routing from the layer's router, or, with
@@ -468,6 +501,7 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
             a.tile_expert = s.tile_expert; a.tile_begin = s.tile_begin; a.tile_end = s.tile_end; a.n_tiles = s.n_tiles;
             a.clamp_silu = L->clamp;
             a.ksplit = 1;
+            a.eoff = L->eoff_gu; a.wscale = L->ws_gu;
             CK(mllm_launch_q16(L->sem_g, true, a, max_tiles, st));
         } else {
         // gate + up (+ SiLU) in bucket order
@@ -509,6 +543,7 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
             b.n_rows = N; b.n_cols = M; b.n_entries = TK;
             b.tile_expert = s.tile_expert; b.tile_begin = s.tile_begin; b.tile_end = s.tile_end; b.n_tiles = s.n_tiles;
             b.ksplit = 1;
+            b.eoff = L->eoff_d; b.wscale = L->ws_d;
             CK(mllm_launch_q16(L->sem_d, false, b, max_tiles, st));
         } else if (L->sem_d >= 0) {
             if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
@@ -615,7 +650,7 @@ mllm_moe_layer *mllm_moe_layer_for_codes(int qt_gate, int qt_up, int qt_down, in
     L->router_p = nullptr;
     L->tab = const_cast<mllm_packed *>(tab_dev);
     L->gemv_only = mllm_moe_needs_gemv(tab_dev, L->sem_g, L->sem_u, L->sem_d, N, M, E);
-    if (L->sem_g < 0 || L->sem_u < 0 || L->gemv_only < 0) {
+    if (L->sem_g < 0 || L->sem_u < 0 || L->gemv_only < 0 || moe_mx_setup(L) != 0) {
         delete L;
         return nullptr;
     }

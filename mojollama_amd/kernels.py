@@ -197,6 +197,8 @@ def load_kernels(path=LIB_PATH):
     so.mllm_moe_release.restype = None
     so.mllm_moe_workspace_size.argtypes = [cvp, ci]
     so.mllm_moe_workspace_size.restype = ctypes.c_long
+    so.mllm_moe_layer_info.argtypes = [cvp]
+    so.mllm_moe_layer_info.restype = ci
     so.mllm_moe_forward.argtypes = [cvp, cvp, ci, cvp, cvp, ctypes.c_long, cvp, cvp, cvp]
     so.mllm_moe_forward.restype = ci
     so.mllm_moe_forward_noalloc.argtypes = [cvp, cvp, ci, cvp, cvp, cvp, cvp]
@@ -440,6 +442,11 @@ class MoELayer:
         if n < 0:
             raise RuntimeError("mllm_moe_dense_experts failed: " + last_error(self.ops.so))
         return n
+
+    def info(self):
+        """mllm_moe_layer_info: bit 1 gate/up and bit 2 down on the fp16-plane GEMM,
+        bit 4 the whole layer on the per-token GEMVs."""
+        return self.ops.so.mllm_moe_layer_info(self.h)
 
     def workspace(self, T):
         n = self.ops.so.mllm_moe_workspace_size(self.h, T)

@@ -214,7 +214,7 @@ def test_bucketing_stable_and_exact(dev):
     assert np.all(cover == 1)
 
 
-def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False, plant=None):
+def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False, plant=None, info=None):
     import torch
     rng = np.random.default_rng(seed)
     gates = [W.gen_weights(rng, qts[0], M, N) for _ in range(E)]
@@ -237,7 +237,39 @@ def _moe_case(dev, orc, qts, N, M, E, Kk, T, renorm, seed, skew=False, plant=Non
     assert np.array_equal(idx.cpu().numpy(), ri), "routing differs"
     assert np.max(np.abs(w.cpu().numpy() - rw) / np.abs(rw)) < 1e-6
     ref = np.stack([orc.moe_forward_token(gates, ups, downs, x[t], M, N, qts, ri[t], rw[t]) for t in range(T)])
+    if info is not None:
+        info.append(layer.info())
     return got, ref
+
+
+def _plant_mxfp4_span(span, zero_blocks, big=147):
+    """Every MXFP4 block of every expert matrix at E = big - span, except blocks 3, 40
+    and 77 of each: E = big with all-zero codes (they set the largest exponent and add
+    nothing), and with zero_blocks blocks 5 and 6 at E = 0 (a zero scale)."""
+    def plant(gates, ups, downs):
+        for a in gates + ups + downs:
+            b = a.reshape(-1, 17)
+            b[:, 16] = big - span
+            b[[3, 40, 77], :16] = 0
+            b[[3, 40, 77], 16] = big
+            if zero_blocks:
+                b[[5, 6], 16] = 0
+    return plant
+
+
+@pytest.mark.parametrize("span,zero_blocks,fits", [(22, True, True), (25, False, True), (26, True, False)])
+def test_moe_layer_mxfp4_exponent_span(dev, orc, span, zero_blocks, fits):
+    """T = 40 MXFP4 layers whose weights sit 22, 25 and 26 binades below the largest
+    exponent.  Up to 25 the grouped GEMMs run on the fp16 plane (the weights fp16
+    subnormals, down to 2^-24 at 25; E = 0 blocks zero); at 26 they keep the bf16
+    tiles.  Either way the outputs match the oracle."""
+    qts = (39, 39, 39)
+    info = []
+    got, ref = _moe_case(dev, orc, qts, N=512, M=2880, E=8, Kk=2, T=40, renorm=0, seed=span,
+                         plant=_plant_mxfp4_span(span, zero_blocks), info=info)
+    assert info[0] == (3 if fits else 0), info
+    assert np.all(np.isfinite(ref)) and np.mean(np.abs(ref)) > 1.0
+    assert O.norm_err(got, ref) < moe_tol(qts)
 
 
 def _plant_mxfp4_exponents(tensor, e_byte):
@@ -322,7 +354,9 @@ def test_moe_layer_repeated_decode_calls(dev, orc):
 
 def test_moe_layer_gptoss_shape(dev, orc):
     """GPT-OSS-20B expert shapes (N = M = 2880, MXFP4, top-4), batched path."""
-    got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=32, renorm=1, seed=4)
+    info = []
+    got, ref = _moe_case(dev, orc, (39, 39, 39), N=2880, M=2880, E=8, Kk=4, T=32, renorm=1, seed=4, info=info)
+    assert info[0] == 3, info   # gate/up and down on the fp16-plane GEMM
     assert O.norm_err(got, ref) < moe_tol((39, 39, 39))
 
 

@@ -43,6 +43,16 @@ hipError_t mllm_launch_mx_erange(const mllm_packed *tab_dev, int n_mats, int n_r
                                  hipStream_t st);
 // eoff / wscale for an exponent range; false when the range does not fit.
 bool mllm_q16_mx_shift(int emin, int emax, int *eoff, float *wscale);
+// Step-major metadata: a matrix's per-block metadata transposed so the rows of one
+// super-block are contiguous (a wave's 32 rows read one short run instead of 32 scattered
+// lines).  Records (b, row) at (b * n_rows + row) * R: Q4_K its 16-byte d / dmin / scales
+// record (R = 16); Q6_K its 16 sub-block scales (R = 16), then at sm_doff its d (R = 2);
+// MXFP4 per 64-element step b the E bytes of blocks 2b, 2b+1 (R = 2).  Bytes per matrix
+// (256-aligned) and the d offset; 0 for semantics without a form.
+long mllm_q16_smeta_bytes(int sem, int n_rows, int n_cols, long *doff);
+// The copies of n_mats matrices (device table), matrix m at dst + m * stride.
+hipError_t mllm_launch_q16_smeta(int sem, const mllm_packed *tab_dev, int n_mats, int n_rows, int n_cols, uint8_t *dst,
+                                 long stride, hipStream_t st);
 
 // The activation rows of the fp16-plane GEMM (a workspace carve).
 struct act16 {
@@ -59,9 +69,9 @@ struct act16 {
 };
 size_t mllm_act16_bytes(int sem, long rows, int K);
 act16 mllm_act16_carve(int sem, void *ws, long rows, int K);
-// fp32 rows x[r * ldx + k] (fp32-activation semantics), or the Q8_0 pack xq
-// (Q4_K x Q8_0: mllm_launch_quantize_q8_0's quants and min-term sums; MXFP4 x
-// Q8_0: its quants times their block scales, exact in fp32) -> act.
+// fp32 rows x[r * ldx + k] (fp32-activation semantics; MXFP4 x Q8_0: their Q8_0
+// quantisation, quants times block scales), or the Q8_0 pack xq (Q4_K x Q8_0:
+// mllm_launch_quantize_q8_0's quants and min-term sums) -> act.
 hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq, int rows, int K, const act16 &act,
                              hipStream_t st);
 
@@ -88,6 +98,11 @@ struct q16_args {
     int eoff;        // MXFP4: weights decode as v 2^(E + eoff) (mllm_q16_mx_shift)
     float wscale;    // MXFP4: 2^(-127 - eoff), applied to the result
     int rows_fast;   // set by the launch: work tiles ordered row block fastest
+    // step-major metadata (mllm_launch_q16_smeta) of W / table[e] at sm + e * sm_stride and of
+    // W2 / table2[e] at sm2 + e * sm_stride, or null (K-quants then read the packed planes;
+    // MXFP4 needs it)
+    const uint8_t *sm, *sm2;
+    long sm_stride, sm_doff;
 };
 // Entries per work tile of a launch (grouped launches: the bucketing's tile).
 int mllm_q16_tile_entries(bool grouped, int n_entries);

@@ -23,6 +23,7 @@
 #include <type_traits>
 #include "decode.h"
 #include "gemm16.h"
+#include "gemv.h"
 
 namespace {
 
@@ -30,6 +31,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 template <int SEM> struct q16_traits {
     static constexpr bool A4 = SEM == SEM_Q4_K_Q8;
@@ -43,6 +45,11 @@ template <int SEM> struct q16_traits {
     static constexpr int SPB = PPS / 64;                   // steps per super-block
     static constexpr int NPL = A4 ? 1 : 2;                 // activation planes
 };
+
+// Waves per workgroup (each owns 32 weight rows).  MXFP4 down projections take 256 rows,
+// so each activation tile staged in LDS serves twice the rows (the activation loads bound
+// these GEMMs); gate + up, whose two matrices already share each tile, keep 128.
+template <int SEM, bool DUAL> constexpr int q16_wpg() { return q16_traits<SEM>::MX && !DUAL ? 8 : 4; }
 
 // Bits 3 and 4 ... of a step position p: i = p >> 4 (MFMA of the step), kh = (p >> 3) & 1
 // (lane half), j = p & 7 (slot).  sw(j): slot -> byte order of the nibble pairs (j bits 0,1 swapped).
@@ -92,10 +99,23 @@ struct q16_raw {
     uint4 m;       // Q6_K: .x = scales (2 bytes), .y = d
 };
 
+// A super-block's metadata as the loop holds it: Q4_K the 16-byte record (kq_pairs layout);
+// Q6_K from the step-major copy, its 16 sub-block scales and d.
+struct q16_meta {
+    uint4 m;
+    uint32_t d;
+};
+
+// Component i (compile-time) of a uint4.
+template <int I> MLLM_DEV uint32_t u4at(const uint4 &v) { return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w; }
+
 // The step's four MFMA operands (8 fp16 each, as 4 words) and the super-block's d.
-template <int SEM>
-MLLM_DEV void q16_decode(const q16_raw &r, const uint4 &meta, int st, int kh, u32x4 (&o)[4], float &d)
+// SM: Q6_K's scales and d come from the step-major metadata (meta), not the step's loads.
+template <int SEM, bool SM, int ST>
+MLLM_DEV void q16_decode(const q16_raw &r, const q16_meta &mt, int kh, u32x4 (&o)[4], float &d)
 {
+    constexpr int st = ST;
+    const uint4 &meta = mt.m;
     if constexpr (SEM == SEM_Q4_K_GGML || SEM == SEM_Q4_K_Q8) {
         // group g's sub-blocks 2g (low nibbles) and 2g+1 (high nibbles), QK:62-71 pairs
         const int g = SEM == SEM_Q4_K_GGML ? st : 2 * st + kh;
@@ -122,8 +142,10 @@ MLLM_DEV void q16_decode(const q16_raw &r, const uint4 &meta, int st, int kh, u3
         o[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
     } else if constexpr (SEM == SEM_Q6_K_SEQ) {
         // CE:315-378: element e = nibble (e&1) of ql[e/2] | 2 bits (e&3) of qh[e/4], minus 32, scale sc[e/16]
-        d = h2f(r.m.y);
-        const float s0 = (float)(int8_t)(r.m.x & 0xFF), s1 = (float)(int8_t)(r.m.x >> 8);
+        // (scales 4 st + 2 kh and + 1)
+        const uint32_t sp = SM ? __builtin_amdgcn_ubfe(u4at<ST>(meta), 16 * kh, 16) : r.m.x;
+        d = h2f(SM ? mt.d : r.m.y);
+        const float s0 = (float)(int8_t)(sp & 0xFF), s1 = (float)(int8_t)(sp >> 8);
         const h2 sa = hh(s0), ca = hh(-1056.0f * s0), sb = hh(s1), cb = hh(-1056.0f * s1);
         const uint32_t L[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
@@ -138,8 +160,16 @@ MLLM_DEV void q16_decode(const q16_raw &r, const uint4 &meta, int st, int kh, u3
         }
     } else {
         // QK:1778-1812 (low nibble in all four quadrants): quad q = kh + 2 (i >> 1) takes qh bits 2q
-        d = h2f(r.m.y);
-        const float s0 = (float)(int8_t)(r.m.x & 0xFF), s1 = (float)(int8_t)(r.m.x >> 8);
+        // (scales 8 h + lh + 2 kh and + 4 of half h = st / 2, l-half lh = st % 2)
+        d = h2f(SM ? mt.d : r.m.y);
+        float s0, s1;
+        if constexpr (SM) {
+            s0 = (float)(int8_t)__builtin_amdgcn_ubfe(u4at<2 * (ST >> 1)>(meta), 8 * ((ST & 1) + 2 * kh), 8);
+            s1 = (float)(int8_t)__builtin_amdgcn_ubfe(u4at<2 * (ST >> 1) + 1>(meta), 8 * ((ST & 1) + 2 * kh), 8);
+        } else {
+            s0 = (float)(int8_t)(r.m.x & 0xFF);
+            s1 = (float)(int8_t)(r.m.x >> 8);
+        }
         const h2 sa = hh(s0), ca = hh(-1056.0f * s0), sb = hh(s1), cb = hh(-1056.0f * s1);
         const uint32_t L[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, Q[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
@@ -193,8 +223,24 @@ struct q16_min_raw {
     uint4 m2;
 };
 template <int SEM>
-MLLM_DEV void q16_min_ld(const mllm_packed &W, int nb, int row, int u0, q16_min_raw &r)
+MLLM_DEV void q16_min_ld(const mllm_packed &W, int nb, int row, int u0, q16_min_raw &r, const uint8_t *sm, int n_rows)
 {
+    if (sm) {   // step-major metadata: record (b, row) at (b * n_rows + row) * 16
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(sm), (short)0, -1,
+                                                                            0x00020000);
+        if constexpr (SEM == SEM_Q4_K_GGML) {
+            const int b = min(u0 / 8, nb - 1);
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * row, 16 * b * n_rows, 0);
+            r.m = make_uint4(v.x, v.y, v.z, v.w);
+        } else {
+            uint32_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, 16 * row, 16 * min(u0 + j, nb - 1) * n_rows, 0);
+            r.m = make_uint4(v[0], v[1], v[2], v[3]);
+            r.m2 = make_uint4(v[4], v[5], v[6], v[7]);
+        }
+        return;
+    }
     if constexpr (SEM == SEM_Q4_K_GGML) {
         const int b = min(u0 / 8, nb - 1);   // the 8 sub-blocks of super-block u0 / 8 (past nb: zeros, below)
         r.m = gld<uint4>(W.p[1] + ((long)row * nb + b) * 16);
@@ -263,14 +309,17 @@ MLLM_DEV float silu16(float g)
 // a 32-bit per-lane offset, so the loop issues no 64-bit address arithmetic.
 template <class T> MLLM_DEV T gldo(const void *base, uint32_t off) { return gld<T>((const uint8_t *)base + off); }
 
-template <int SEM, bool DUAL, int EB>
-__global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
+// SM: the matrices' super-block metadata (MXFP4: exponents) read from the step-major copy
+// (a.sm, mllm_launch_q16_smeta) instead of the packed planes.
+template <int SEM, bool DUAL, int EB, bool SM>
+__global__ __launch_bounds__((64 * q16_wpg<SEM, DUAL>()), (8 / q16_wpg<SEM, DUAL>())) void k_q16(q16_args a)
 {
     using Q = q16_traits<SEM>;
-    constexpr int RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 128, SPB = Q::SPB, NPL = Q::NPL;
+    constexpr int WPG = q16_wpg<SEM, DUAL>(), RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 32 * WPG, SPB = Q::SPB, NPL = Q::NPL;
     constexpr bool MX = Q::MX;
     static_assert(SPB == 2 || SPB == 4 || MX, "steps run in units of four");
-    __shared__ __attribute__((aligned(16))) float sD[4][RB * 32];
+    static_assert(SM || !MX, "MXFP4 reads its exponents step-major");
+    __shared__ __attribute__((aligned(16))) float sD[WPG][RB * 32];
     __shared__ int s_row[TM];
 
     // ---- work tile (XCD-contiguous ranges of the live tiles; entry tile fastest, so
@@ -293,17 +342,23 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     }
     int p0, p1;
     mllm_packed W, W2;
+    const uint8_t *sm0 = nullptr, *sm1 = nullptr;   // this tile's matrices' step-major metadata
     if (a.tile_expert) {
         const int e = a.tile_expert[by];
         p0 = a.tile_begin[by];
         p1 = a.tile_end[by];
         W = a.table[e];
         if constexpr (DUAL) W2 = a.table2[e];
+        if constexpr (SM) {
+            sm0 = a.sm + (long)e * a.sm_stride;
+            if constexpr (DUAL) sm1 = a.sm2 + (long)e * a.sm_stride;
+        }
     } else {
         p0 = by * TM;
         p1 = min(p0 + TM, a.n_entries);
         W = a.W;
         if constexpr (DUAL) W2 = a.W2;
+        if constexpr (SM) { sm0 = a.sm; sm1 = a.sm2; }
     }
     const int n_ent = __builtin_amdgcn_readfirstlane(p1 - p0);
     if (n_ent <= 0) return;
@@ -338,7 +393,9 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // write which buffer.  One plane: buffer = step % 4, loads run three steps ahead; two
     // planes, MXFP4: buffer = 2 (step % 4) + plane, three steps ahead (eight buffers); two
     // planes, K-quants: buffer = 2 (step % 2) + plane, one step ahead.
-    constexpr int NCH = TM * 8 / 256;   // load instructions per wave, plane and step (= EB)
+    // load instructions per wave, plane and step (four waves: EB; MXFP4's eight: one, for
+    // waves whose rows the tile's entry blocks reach)
+    constexpr int NCH = TM * 8 / (64 * WPG);
     constexpr bool B8 = MX;   // K-quant tiles keep four buffers (their LDS then admits a third workgroup per CU)
     constexpr int D2 = B8 ? 3 : 1;      // two-plane prefetch distance (steps)
     __shared__ __attribute__((aligned(16))) _Float16 sB0[TM * 64], sB1[TM * 64], sB2[TM * 64], sB3[TM * 64];
@@ -363,14 +420,14 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     uint32_t boff[NCH], boff1[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int ch = 256 * c + 64 * wave + lane, r = ch >> 3;
+        const int ch = 64 * WPG * c + 64 * wave + lane, r = ch >> 3;
         boff[c] = (uint32_t)s_row[r] * (uint32_t)(a.x.ldh * 2) + 16u * (uint32_t)((ch & 7) ^ fsw(r & 31));
         boff1[c] = boff[c];
     }
     auto set_boff1 = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
-            const int ch = 256 * c + 64 * wave + lane, r = ch >> 3;
+            const int ch = 64 * WPG * c + 64 * wave + lane, r = ch >> 3;
             if (!a.x.lo_nz[s_row[r]])
                 boff1[c] = (uint32_t)(a.x.zero - (a.x.h + a.x.hplane)) * 2u + 16u * (uint32_t)((ch & 7) ^ fsw(r & 31));
         }
@@ -388,11 +445,20 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         constexpr int NEB = decltype(nb_c)::value;   // chunk c holds entry block c
         if constexpr (MX) {
             const int so = 2 * (p * (int)a.x.hplane + 64 * s);
+            if constexpr (WPG == 8) {
+                // one instruction of each of the eight waves covers two entry blocks (64 rows);
+                // a one-block tile is loaded by waves 0..3
+                static_assert(NCH == 1 && NEB <= 2, "eight-wave MXFP4 tiles: 64 entries");
+                if (NEB == 2 || wave < 4)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *)(dst + 512 * wave),
+                                                             16, (int)(p ? boff1[0] : boff[0]), so, 0, 0);
+            } else {
 #pragma unroll
-            for (int c = 0; c < NEB; c++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    xrs, (__attribute__((address_space(3))) void *)(dst + (256 * c + 64 * wave) * 8), 16,
-                    (int)(p ? boff1[c] : boff[c]), so, 0, 0);
+                for (int c = 0; c < NEB; c++)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        xrs, (__attribute__((address_space(3))) void *)(dst + (256 * c + 64 * wave) * 8), 16,
+                        (int)(p ? boff1[c] : boff[c]), so, 0, 0);
+            }
         } else {
             const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
 #pragma unroll
@@ -413,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
 
     // weight rows: bulk plane bytes per super-block (Q4_K / Q6_K ql: 128) and per-row offsets
     const uint32_t rq = (uint32_t)wrow * (uint32_t)(MX ? 2 * nb : nb);   // row's first super-block (MX: 32-block)
-    auto fetch_w = [&](const mllm_packed &M, int b, int st, q16_raw &r) __attribute__((always_inline)) {
+    auto fetch_w = [&](const mllm_packed &M, const uint8_t *smp, int b, int st, q16_raw &r) __attribute__((always_inline)) {
         const uint32_t bi = rq + (uint32_t)b;
         if constexpr (SEM == SEM_Q4_K_GGML) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
@@ -422,20 +488,26 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
         } else if constexpr (MX) {
             // step b: blocks 2b (lane half 0) and 2b + 1 (half 1), 16 nibble bytes and E each
             r.a = __builtin_amdgcn_raw_buffer_load_b128(mk_rsrc(M.p[0]), (int)(rq * 16u + 16u * kh), 32 * b, 0);
-            r.m.x = __builtin_amdgcn_raw_buffer_load_b16(mk_rsrc(M.p[1]), (int)rq, 2 * b, 0);   // both blocks' E (rq is even)
+            // both blocks' E from the step-major copy: the wave's 32 rows read 64 contiguous
+            // bytes, where the row-major plane spreads them over ~23 lines
+            r.m.x = __builtin_amdgcn_raw_buffer_load_b16(mk_rsrc(smp), (int)(2u * (uint32_t)wrow), 2 * b * a.n_rows, 0);
         } else if constexpr (SEM == SEM_Q6_K_SEQ) {
             r.a = gldo<u32x4>(M.p[0] + 32 * st, bi * 128u + 16u * kh);
             const uint2 q = gldo<uint2>(M.p[1] + 16 * st, bi * 64u + 8u * kh);
             r.b.x = q.x; r.b.y = q.y;
-            r.m.x = gldo<uint16_t>(M.p[2] + 4 * st, bi * 16u + 2u * kh);
-            r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+            if constexpr (!SM) {
+                r.m.x = gldo<uint16_t>(M.p[2] + 4 * st, bi * 16u + 2u * kh);
+                r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+            }
         } else {   // SEM_Q6_K_LOWNIB
             const int h = st >> 1, lh = st & 1;
             r.a = gldo<u32x4>(M.p[0] + 64 * h + 16 * lh, bi * 128u + 32u * kh);
             r.b = gldo<u32x4>(M.p[1] + 32 * h + 16 * lh, bi * 64u);
-            const uint32_t so = bi * 16u + 2u * kh;
-            r.m.x = gldo<uint8_t>(M.p[2] + 8 * h + lh, so) | ((uint32_t)gldo<uint8_t>(M.p[2] + 8 * h + lh + 4, so) << 8);
-            r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+            if constexpr (!SM) {
+                const uint32_t so = bi * 16u + 2u * kh;
+                r.m.x = gldo<uint8_t>(M.p[2] + 8 * h + lh, so) | ((uint32_t)gldo<uint8_t>(M.p[2] + 8 * h + lh + 4, so) << 8);
+                r.m.y = gldo<uint16_t>(M.p[3], bi * 2u);
+            }
         }
     };
 
@@ -450,7 +522,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // step st of a super-block: decode, then the MFMAs into T (fresh at st == 0) against
     // the step's buffers.  Entry blocks past the tile's entries run on copies of its first
     // row; the epilogue drops them.
-    auto mfmas = [&](auto np_c, auto nb_c, auto st_c, auto u_c, const q16_raw (&r)[RB], const uint4 (&meta)[RB])
+    auto mfmas = [&](auto np_c, auto nb_c, auto st_c, auto u_c, const q16_raw (&r)[RB], const q16_meta (&meta)[RB])
                      __attribute__((always_inline)) {
         constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value;
         constexpr int st = decltype(st_c)::value, u = decltype(u_c)::value;
@@ -461,7 +533,7 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                 q16_decode_mx(r[rb], kh, a.eoff, A[rb]);
             } else {
                 float d;
-                q16_decode<SEM>(r[rb], meta[rb], st, kh, A[rb], d);
+                q16_decode<SEM, SM, st>(r[rb], meta[rb], kh, A[rb], d);
                 if (st == 0 && kh == 0) sD[wave][rb * 32 + lr] = d;
             }
         }
@@ -514,25 +586,55 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
     // entries runs one: half the MFMAs and activation loads)
     auto main_loop = [&](auto np_c, auto nb_c) __attribute__((always_inline)) {
         constexpr int NP = decltype(np_c)::value, NEB = decltype(nb_c)::value, D = NP == 1 ? 3 : D2;
+        // weight load instructions every step issues at least (16-byte loads, and MXFP4's
+        // exponent pair: none the compiler could merge)
+        constexpr int NW = RB * (MX || Q::Q6 ? 2 : 1);
+        // ORD: loads issued in order (a step's activations, then its weights), so the wait
+        // below counts the weights issued after them (measured: MXFP4; Q6_K down 134 -> 132
+        // us at Qwen3 T = 1280).  Not Q4_K (its fused gate + up there: 92 -> 99 us, the
+        // fence costs more than the wait) nor gate and up in Q6_K (their registers would
+        // spill): those wait for every older load instead
+        constexpr bool ORD = MX || (Q::Q6 && !DUAL);
+        // activation load instructions per wave and step (eight waves: a wave whose rows the
+        // tile reaches issues one per plane; the others none, and for them the count only
+        // overstates what may stay in flight, which their own loads never need)
+        constexpr int NDMA = WPG == 8 ? NP : NEB * NP;
         const int s_beg = b_beg * SPB, s_last = b_end * SPB - 1;
         q16_raw rw[4][RB];
-        // Q4_K super-block metadata (kq_pairs layout): mA for the unit's first super-block,
-        // mB for its second (SPB == 2) or the next unit's (SPB == 4), one unit half ahead
-        uint4 mA[RB], mB[RB];
+        // super-block metadata (Q4_K: kq_pairs layout; Q6_K step-major: scales and d): mA
+        // for the unit's first super-block, mB for its second (SPB == 2) or the next unit's
+        // (SPB == 4), one unit half ahead
+        q16_meta mA[RB], mB[RB];
         auto fw = [&](int s, q16_raw (&r)[RB]) __attribute__((always_inline)) {
             const int sc = min(s, s_last);
-            fetch_w(W, sc / SPB, sc % SPB, r[0]);
-            if constexpr (DUAL) fetch_w(W2, sc / SPB, sc % SPB, r[1]);
+            fetch_w(W, sm0, sc / SPB, sc % SPB, r[0]);
+            if constexpr (DUAL) fetch_w(W2, sm1, sc / SPB, sc % SPB, r[1]);
         };
-        auto fm = [&](int b, uint4 (&m)[RB]) __attribute__((always_inline)) {
-            if constexpr (Q::GGML || Q::A4) {
+        auto fm = [&](int b, q16_meta (&m)[RB]) __attribute__((always_inline)) {
+            const int bc = min(b, b_end - 1);
+            if constexpr (SM && (Q::GGML || Q::A4 || Q::Q6)) {
+                // the step-major record (bc, wrow): the wave's 32 rows are contiguous
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    const __amdgpu_buffer_rsrc_t rs = mk_rsrc(rb == 0 ? sm0 : sm1);
+                    const int so = 16 * bc * a.n_rows;
+                    if constexpr (Q::Q6) {
+                        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * wrow, so, 0);
+                        m[rb].m = make_uint4(v.x, v.y, v.z, v.w);
+                        m[rb].d = __builtin_amdgcn_raw_buffer_load_b16(rs, 2 * wrow, (int)a.sm_doff + 2 * bc * a.n_rows, 0);
+                    } else {
+                        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, 16 * wrow, so, 0);
+                        m[rb].m = make_uint4(v.x, v.y, v.z, 0u);
+                    }
+                }
+            } else if constexpr (Q::GGML || Q::A4) {
                 // d, dmin and the six-bit scales (the mins enter through the min-term product)
-                const uint32_t bi = rq + (uint32_t)min(b, b_end - 1);
+                const uint32_t bi = rq + (uint32_t)bc;
                 const uint3 q0 = gldo<uint3>(W.p[1], bi * 16u);
-                m[0] = make_uint4(q0.x, q0.y, q0.z, 0u);
+                m[0].m = make_uint4(q0.x, q0.y, q0.z, 0u);
                 if constexpr (DUAL) {
                     const uint3 q1 = gldo<uint3>(W2.p[1], bi * 16u);
-                    m[1] = make_uint4(q1.x, q1.y, q1.z, 0u);
+                    m[1].m = make_uint4(q1.x, q1.y, q1.z, 0u);
                 }
             }
         };
@@ -547,9 +649,20 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
                 dma(nb_c, sc, 1, sbuf(std::integral_constant<int, bidx2(u, 1)>{}));
             }
         };
-        if constexpr (MX && D == 3) {
-            // in the loop's order (a step's activations, then its weights), so the loads in
-            // flight at the loop head are counted alike on entry and on the back edge
+        // the prologue issues its loads in the loop's order (per step its activations, then
+        // its weights), so the loads in flight at the loop head are counted alike on entry and
+        // on the back edge (else the compiler waits for all of them there)
+        fm(b_beg, mA);
+        if constexpr (!ORD) {
+            load_b(s_beg, std::integral_constant<int, 0>{});
+            if constexpr (D >= 3) {
+                load_b(s_beg + 1, std::integral_constant<int, 1>{});
+                load_b(s_beg + 2, std::integral_constant<int, 2>{});
+            }
+            fw(s_beg, rw[0]);
+            fw(s_beg + 1, rw[1]);
+            fw(s_beg + 2, rw[2]);
+        } else if constexpr (D == 3) {
             load_b(s_beg, std::integral_constant<int, 0>{});
             fw(s_beg, rw[0]);
             __builtin_amdgcn_sched_barrier(0);
@@ -559,14 +672,15 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             load_b(s_beg + 2, std::integral_constant<int, 2>{});
             fw(s_beg + 2, rw[2]);
             __builtin_amdgcn_sched_barrier(0);
-        } else {
-            load_b(s_beg, std::integral_constant<int, 0>{});
-            if constexpr (D >= 2) load_b(s_beg + 1, std::integral_constant<int, 1>{});
-            if constexpr (D >= 3) load_b(s_beg + 2, std::integral_constant<int, 2>{});
-            fm(b_beg, mA);
+        } else {   // D == 1: step s issues the activations of s + 1 and the weights of s + 3
             fw(s_beg, rw[0]);
+            __builtin_amdgcn_sched_barrier(0);
             fw(s_beg + 1, rw[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(s_beg, std::integral_constant<int, 0>{});
+            __builtin_amdgcn_sched_barrier(0);
             fw(s_beg + 2, rw[2]);
+            __builtin_amdgcn_sched_barrier(0);
         }
         // unit of four steps from s0.  MXFP4: a short unit (the last, when the step count is
         // not a multiple of four) runs its first s_last - s0 + 1 steps, after the loop: inside
@@ -580,18 +694,15 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             auto one = [&](auto u_c) __attribute__((always_inline)) {
                 constexpr int u = decltype(u_c)::value;
                 const int s = s0 + u;
-                if constexpr (MX) {
-                    // loads that surely follow step s's activation loads: those of steps s + 1
-                    // .. s + D - 1 (activations, and the two weight loads per matrix, which
-                    // the compiler may order before or after a step's activation loads)
-                    sync_loads(std::integral_constant<int, (D - 1) * (NEB * NP + 2 * RB)>{});
-                    // keep each step's decode in its step: hoisted into an earlier one, it
-                    // would wait there for weight loads just issued
-                    __builtin_amdgcn_sched_barrier(0);
-                } else {
-                    sync_loads(std::integral_constant<int, (D - 1) * NEB * NP>{});
-                }
+                // the loads that surely follow step s's activation loads: each step issues its
+                // activation loads, then (after a scheduling fence) at least NW weight loads,
+                // so the weights issued with them and those of steps s + 1 .. s + D - 1
+                sync_loads(std::integral_constant<int, ORD ? NW + (D - 1) * (NDMA + NW) : (D - 1) * NDMA>{});
+                // MXFP4: keep each step's decode in its step (hoisted into an earlier one, it
+                // would wait there for weight loads just issued)
+                if constexpr (MX) __builtin_amdgcn_sched_barrier(0);
                 load_b(s + D, std::integral_constant<int, (u + D) & 3>{});
+                if constexpr (ORD) __builtin_amdgcn_sched_barrier(0);
                 fw(s + 3, rw[(u + 3) & 3]);
                 if constexpr (u == 0) fm(b0 + 1, mB);
                 if constexpr (SPB == 2 && u == 2) fm(b0 + 2, mA);
@@ -666,7 +777,8 @@ __global__ __launch_bounds__(256, 2) void k_q16(q16_args a)
             };
             auto ld = [&](int u0, slice_ld &L) __attribute__((always_inline)) {
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) q16_min_ld<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, L.w[rb]);
+                for (int rb = 0; rb < RB; rb++)
+                    q16_min_ld<SEM>(rb == 0 ? W : W2, nb, wrow, u0 + 8 * kh, L.w[rb], rb == 0 ? sm0 : sm1, a.n_rows);
 #pragma unroll
                 for (int e = 0; e < EB; e++) {
                     const _Float16 *mp = a.x.m + (long)s_row[32 * e + lr] * a.x.ldm + u0 + 8 * kh;
@@ -762,11 +874,11 @@ __global__ void k_q16_ksum(const float *__restrict__ part, int ks, long plane, i
 // ---------------------------------------------------------------- activations
 // fp32 row -> scaled fp16 planes in the semantic's K order, the row's inverse
 // scale, lo_nz, and (Q4_K ggml) the fp16 hi/lo sums of each 32-element
-// sub-block.  One workgroup per row.  MXFP4 x Q8_0 reads the row from the
-// Q8_0 pack instead: quant times block scale (int8 times an fp16 value: exact
-// in fp32), the activation mxfp4_row_dot_q8 (QK:629-678) multiplies.
+// sub-block.  One workgroup per row.  MXFP4 x Q8_0 first quantises the row to
+// Q8_0 and takes quant times block scale (int8 times an fp16 value: exact in
+// fp32), the activation mxfp4_row_dot_q8 (QK:629-678) multiplies.
 template <int SEM>
-__global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int ldx, mllm_xq xq, int K, act16 a)
+__global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int ldx, int K, act16 a)
 {
     using Q = q16_traits<SEM>;
     __shared__ float red[4];
@@ -775,23 +887,47 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
         for (int P = 8 * tid; P < a.ldh; P += 2048) *reinterpret_cast<f16x8 *>(a.zero + P) = f16x8{};
         return;
     }
-    const float *xr = Q::Q8IN ? nullptr : x + (long)row * ldx;
+    const float *xr = x + (long)row * ldx;
     const bool vec = ((uintptr_t)xr & 15) == 0;
     const int nb = K / Q::EPS;
     // eight consecutive elements from k (a multiple of 8)
     auto ld8 = [&](int k, float (&v)[8]) __attribute__((always_inline)) {
-        if constexpr (Q::Q8IN) {
-            const long nbk = K / 32;
-            const uint2 w = *reinterpret_cast<const uint2 *>(xq.q + (long)row * nbk * 32 + k);
-            const float d = xq.d[(long)row * nbk + (k >> 5)];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = (float)(int8_t)(((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xFF) * d;
-        } else if (vec) {
+        if (vec) {
             const float4 p = *reinterpret_cast<const float4 *>(xr + k), q = *reinterpret_cast<const float4 *>(xr + k + 4);
             v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
         } else {
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = xr[k + j];
+        }
+        if constexpr (Q::Q8IN) {
+            // the row's Q8_0 quantisation (k_quantize_q8_0, QK:1406-1455), block k / 32 held by
+            // the four threads whose tid differs in bits 1 and 2 (quarters 8 i .. 8 i + 7):
+            // amax (without a NaN the plain maximum; with one the reference's vector order,
+            // from the block's 32 values), d = amax / 127 (1 if 0), q = rint(clamp(v / d)),
+            // and the value the dot multiplies, q * fp16(d) (exact in fp32)
+            float m = 0.0f;
+            bool nan = false;
+#pragma unroll
+            for (int j = 0; j < 8; j++) { m = fmaxf(m, fabsf(v[j])); nan |= v[j] != v[j]; }
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            nan |= __shfl_xor((int)nan, 2, 64) != 0;
+            nan |= __shfl_xor((int)nan, 4, 64) != 0;
+            if (nan) {
+                const float *bp = xr + (k & ~31);
+                m = mllm_q8_amax_ref([&](int i) { return fabsf(bp[i]); });
+            }
+            float d = m / 127.0f;
+            if (d == 0.0f) d = 1.0f;
+            const float id = 1.0f / d;
+            const float d8 = (float)(_Float16)d;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                float p = v[j] * id;
+                p = (p > -127.0f) ? p : -127.0f;
+                p = (p < 127.0f) ? p : 127.0f;
+                v[j] = (float)(int)rintf(p) * d8;
+            }
         }
     };
     // thread t takes positions P = 8 t + 2048 it (it < nit): eight positions hold one
@@ -947,6 +1083,22 @@ __global__ __launch_bounds__(256) void k_act16_q8(mllm_xq xq, int K, act16 a)
 
 size_t al256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Step-major copy of one metadata plane: for matrix m = blockIdx.y, the record of R bytes
+// at src = tab[m].p[plane] + (row * nb + b) * R goes to dst + m * stride + off + (b * n_rows + row) * R.
+template <int R>
+__global__ void k_smeta(const mllm_packed *__restrict__ tab, int plane, int n_rows, int nb, uint8_t *__restrict__ dst,
+                        long stride, long off)
+{
+    const uint8_t *src = tab[blockIdx.y].p[plane];
+    uint8_t *d = dst + (long)blockIdx.y * stride + off;
+    const long n = (long)n_rows * nb;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+        const long b = i / n_rows, row = i - b * n_rows;
+        if constexpr (R == 16) *reinterpret_cast<uint4 *>(d + i * 16) = *reinterpret_cast<const uint4 *>(src + (row * nb + b) * 16);
+        else *reinterpret_cast<uint16_t *>(d + i * 2) = *reinterpret_cast<const uint16_t *>(src + (row * nb + b) * 2);
+    }
+}
+
 // range[0] = min over non-zero E, range[1] = max E of the matrices' E8M0 bytes.
 __global__ void k_mx_erange(const mllm_packed *__restrict__ tab, long nblk, int *__restrict__ range)
 {
@@ -976,17 +1128,18 @@ __global__ void k_mx_erange(const mllm_packed *__restrict__ tab, long nblk, int 
 // planes keep entry tile fastest.
 constexpr long kRowsFastBytes = 24l << 20;
 
-template <int SEM, bool DUAL, int EB>
+template <int SEM, bool DUAL, int EB, bool SM>
 hipError_t launch16(const q16_args &a, int max_tiles, hipStream_t st)
 {
     constexpr int TM = 32 * EB;
     const int ks = (a.ksplit > 1 && !DUAL && !a.tile_expert && !a.out_row) ? a.ksplit : 1;
-    dim3 grid((a.n_rows + 127) / 128, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
+    constexpr int TN = 32 * q16_wpg<SEM, DUAL>();
+    dim3 grid((a.n_rows + TN - 1) / TN, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
     if (grid.y == 0) return hipSuccess;
     q16_args b = a;
     b.ksplit = ks;
     b.rows_fast = a.tile_expert && (long)a.n_entries * a.x.ldh * 2 * q16_traits<SEM>::NPL >= kRowsFastBytes;
-    hipLaunchKernelGGL((k_q16<SEM, DUAL, EB>), grid, dim3(256), 0, st, b);
+    hipLaunchKernelGGL((k_q16<SEM, DUAL, EB, SM>), grid, dim3(2 * TN), 0, st, b);
     if (ks > 1) {
         const long plane = (long)a.n_entries * a.n_rows;
         hipLaunchKernelGGL(k_q16_ksum, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part, ks, plane,
@@ -1011,6 +1164,40 @@ hipError_t mllm_launch_mx_erange(const mllm_packed *tab_dev, int n_mats, int n_r
     if (n_mats <= 0 || nblk <= 0) return hipSuccess;
     const unsigned gx = (unsigned)std::min<long>((nblk + 255) / 256, 64);
     hipLaunchKernelGGL(k_mx_erange, dim3(gx, (unsigned)n_mats), dim3(256), 0, st, tab_dev, nblk, range);
+    return hipGetLastError();
+}
+
+long mllm_q16_smeta_bytes(int sem, int n_rows, int n_cols, long *doff)
+{
+    long a = 0, d = 0;
+    if (mllm_q16_mx(sem)) {
+        a = (long)n_rows * (n_cols / 64) * 2;
+    } else if (mllm_q16_supported(sem)) {
+        a = (long)n_rows * (n_cols / 256) * 16;
+        if (sem == SEM_Q6_K_SEQ || sem == SEM_Q6_K_LOWNIB) d = (long)n_rows * (n_cols / 256) * 2;
+    }
+    const long ao = (long)al256((size_t)a);
+    if (doff) *doff = ao;
+    return ao + (long)al256((size_t)d);
+}
+
+hipError_t mllm_launch_q16_smeta(int sem, const mllm_packed *tab_dev, int n_mats, int n_rows, int n_cols, uint8_t *dst,
+                                 long stride, hipStream_t st)
+{
+    long doff = 0;
+    if (n_mats <= 0 || mllm_q16_smeta_bytes(sem, n_rows, n_cols, &doff) <= 0) return hipErrorInvalidValue;
+    const bool mx = mllm_q16_mx(sem);
+    const int nb = mx ? n_cols / 64 : n_cols / 256;
+    const unsigned gx = (unsigned)std::min<long>(((long)n_rows * nb + 255) / 256, 256);
+    const dim3 g(gx, (unsigned)n_mats);
+    if (mx) {
+        hipLaunchKernelGGL(k_smeta<2>, g, dim3(256), 0, st, tab_dev, 1, n_rows, nb, dst, stride, 0l);
+    } else if (sem == SEM_Q6_K_SEQ || sem == SEM_Q6_K_LOWNIB) {
+        hipLaunchKernelGGL(k_smeta<16>, g, dim3(256), 0, st, tab_dev, 2, n_rows, nb, dst, stride, 0l);
+        hipLaunchKernelGGL(k_smeta<2>, g, dim3(256), 0, st, tab_dev, 3, n_rows, nb, dst, stride, doff);
+    } else {
+        hipLaunchKernelGGL(k_smeta<16>, g, dim3(256), 0, st, tab_dev, 1, n_rows, nb, dst, stride, 0l);
+    }
     return hipGetLastError();
 }
 
@@ -1075,24 +1262,14 @@ hipError_t mllm_launch_act16(int sem, const float *x, int ldx, const mllm_xq *xq
     if (rows <= 0) return hipSuccess;
     const int unit = mllm_q16_mx(sem) ? 64 : 256;
     if (K < unit || K % unit || ((uintptr_t)act.h & 15)) return hipErrorInvalidValue;
-    const mllm_xq nq{};
     switch (sem) {
-    case SEM_Q4_K_GGML:
-        hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
-        break;
-    case SEM_Q6_K_SEQ:
-        hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
-        break;
+    case SEM_Q4_K_GGML: hipLaunchKernelGGL(k_act16<SEM_Q4_K_GGML>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_Q6_K_SEQ: hipLaunchKernelGGL(k_act16<SEM_Q6_K_SEQ>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
     case SEM_Q6_K_LOWNIB:
-        hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
+        hipLaunchKernelGGL(k_act16<SEM_Q6_K_LOWNIB>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act);
         break;
-    case SEM_MXFP4:
-        hipLaunchKernelGGL(k_act16<SEM_MXFP4>, dim3(rows + 1), dim3(256), 0, st, x, ldx, nq, K, act);
-        break;
-    case SEM_MXFP4_Q8:
-        if (!xq) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(k_act16<SEM_MXFP4_Q8>, dim3(rows + 1), dim3(256), 0, st, nullptr, 0, *xq, K, act);
-        break;
+    case SEM_MXFP4: hipLaunchKernelGGL(k_act16<SEM_MXFP4>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
+    case SEM_MXFP4_Q8: hipLaunchKernelGGL(k_act16<SEM_MXFP4_Q8>, dim3(rows + 1), dim3(256), 0, st, x, ldx, K, act); break;
     case SEM_Q4_K_Q8:
         if (!xq || K / 256 > 256) return hipErrorInvalidValue;
         hipLaunchKernelGGL(k_act16_q8, dim3(rows), dim3(256), 0, st, *xq, K, act);
@@ -1127,10 +1304,15 @@ hipError_t mllm_launch_q16(int sem, bool dual, const q16_args &a, int max_tiles,
     if (mllm_q16_mx(sem) && a.ksplit > 1) return hipErrorInvalidValue;
     const bool grouped = a.tile_expert != nullptr;
     const int tm = mllm_q16_tile_entries(grouped, a.n_entries);
-#define Q16(S)                                                                         \
-    if (sem == S) {                                                                    \
-        if (dual) return launch16<S, true, 2>(a, max_tiles, st);                       \
-        return tm == 128 ? launch16<S, false, 4>(a, max_tiles, st) : launch16<S, false, 2>(a, max_tiles, st); \
+    // grouped launches with step-major metadata take the SM forms (not gate and up in Q6_K,
+    // whose registers the SM form would spill)
+#define Q16(S)                                                                                   \
+    if (sem == S) {                                                                              \
+        constexpr bool q6 = S == SEM_Q6_K_SEQ || S == SEM_Q6_K_LOWNIB;                           \
+        if (grouped && a.sm && !dual) return launch16<S, false, 2, true>(a, max_tiles, st);      \
+        if constexpr (!q6) if (grouped && a.sm) return launch16<S, true, 2, true>(a, max_tiles, st); \
+        if (dual) return launch16<S, true, 2, false>(a, max_tiles, st);                          \
+        return tm == 128 ? launch16<S, false, 4, false>(a, max_tiles, st) : launch16<S, false, 2, false>(a, max_tiles, st); \
     }
     Q16(SEM_Q4_K_GGML)
     Q16(SEM_Q4_K_Q8)
@@ -1138,7 +1320,7 @@ hipError_t mllm_launch_q16(int sem, bool dual, const q16_args &a, int max_tiles,
     Q16(SEM_Q6_K_LOWNIB)
 #undef Q16
     // MXFP4: the grouped expert GEMMs (gate + up fused against fp32 x, down against Q8_0 h)
-    if (sem == SEM_MXFP4 && dual && grouped) return launch16<SEM_MXFP4, true, 2>(a, max_tiles, st);
-    if (sem == SEM_MXFP4_Q8 && !dual && grouped) return launch16<SEM_MXFP4_Q8, false, 2>(a, max_tiles, st);
+    if (sem == SEM_MXFP4 && dual && grouped && a.sm) return launch16<SEM_MXFP4, true, 2, true>(a, max_tiles, st);
+    if (sem == SEM_MXFP4_Q8 && !dual && grouped && a.sm) return launch16<SEM_MXFP4_Q8, false, 2, true>(a, max_tiles, st);
     return hipErrorInvalidValue;
 }

@@ -249,6 +249,10 @@ struct mllm_moe_layer {
     // gate/up (both MXFP4) and down, with their exponent offsets and result scales
     int mx_gu = 0, mx_d = 0, eoff_gu = 0, eoff_d = 0;
     float ws_gu = 1.0f, ws_d = 1.0f;
+    // step-major metadata (mllm_launch_q16_smeta) of the matrices the fp16-plane GEMM
+    // multiplies: gate / up / down of expert e at sm_g / sm_u / sm_d + e * stride
+    uint8_t *smem = nullptr, *sm_g = nullptr, *sm_u = nullptr, *sm_d = nullptr;
+    long sms_gu = 0, sms_d = 0, smd_gu = 0, smd_d = 0;
 };
 
 struct moe_ws {
@@ -263,7 +267,7 @@ struct moe_ws {
 
 // Whether the batched path runs gate/up and down on the fp16-plane GEMM (gemm16.h):
 // K-quant semantics over whole super-blocks, on the packed experts (not the dense copies);
-// MXFP4 over whole 64-element steps when the exponent ranges fit (moe_mx_setup).
+// MXFP4 over whole 64-element steps when the exponent ranges fit (moe_q16_setup).
 static bool moe_q16_gu(const mllm_moe_layer &L)
 {
     return (L.sem_g == L.sem_u && mllm_q16_supported(L.sem_g) && !L.dense_gu && L.N % 256 == 0) ||
@@ -274,23 +278,45 @@ static bool moe_q16_d(const mllm_moe_layer &L)
     return (L.sem_d >= 0 && mllm_q16_supported(L.sem_d) && !L.dense_d && L.M % 256 == 0) || (L.mx_d && L.M % 64 == 0);
 }
 
-// The exponent ranges of the MXFP4 gate/up pair and down matrices; sets mx_gu / mx_d
-// where they fit the fp16 plane.  Returns 0, or -1 on a HIP error.
-static int moe_mx_setup(mllm_moe_layer *L)
+// The fp16-plane GEMM's per-layer state: the MXFP4 exponent ranges (mx_gu / mx_d where
+// they fit) and the step-major metadata of the matrices it multiplies.  Returns 0, or -1
+// on a HIP error.
+static int moe_q16_setup(mllm_moe_layer *L)
 {
-    const bool gu = L->sem_g == SEM_MXFP4 && L->sem_u == SEM_MXFP4, dn = L->sem_d == SEM_MXFP4_Q8;
-    if (L->gemv_only || (!gu && !dn)) return 0;
-    int h[4] = {255, 0, 255, 0};
-    int *f = nullptr;
-    if (hipMalloc(&f, sizeof h) != hipSuccess) return -1;
-    hipError_t r = hipMemcpy(f, h, sizeof h, hipMemcpyHostToDevice);
-    if (r == hipSuccess && gu) r = mllm_launch_mx_erange(L->tab, 2 * L->E, L->M, L->N, f, nullptr);
-    if (r == hipSuccess && dn) r = mllm_launch_mx_erange(L->tab + 2 * L->E, L->E, L->N, L->M, f + 2, nullptr);
-    if (r == hipSuccess) r = hipMemcpy(h, f, sizeof h, hipMemcpyDeviceToHost);
-    (void)hipFree(f);
-    if (r != hipSuccess) return -1;
-    if (gu) L->mx_gu = mllm_q16_mx_shift(h[0], h[1], &L->eoff_gu, &L->ws_gu);
-    if (dn) L->mx_d = mllm_q16_mx_shift(h[2], h[3], &L->eoff_d, &L->ws_d);
+    if (L->gemv_only) return 0;
+    const int E = L->E, N = L->N, M = L->M;
+    const bool gmx = L->sem_g == SEM_MXFP4 && L->sem_u == SEM_MXFP4, dmx = L->sem_d == SEM_MXFP4_Q8;
+    if (gmx || dmx) {
+        int h[4] = {255, 0, 255, 0};
+        int *f = nullptr;
+        if (hipMalloc(&f, sizeof h) != hipSuccess) return -1;
+        hipError_t r = hipMemcpy(f, h, sizeof h, hipMemcpyHostToDevice);
+        if (r == hipSuccess && gmx) r = mllm_launch_mx_erange(L->tab, 2 * E, M, N, f, nullptr);
+        if (r == hipSuccess && dmx) r = mllm_launch_mx_erange(L->tab + 2 * E, E, N, M, f + 2, nullptr);
+        if (r == hipSuccess) r = hipMemcpy(h, f, sizeof h, hipMemcpyDeviceToHost);
+        (void)hipFree(f);
+        if (r != hipSuccess) return -1;
+        if (gmx) L->mx_gu = mllm_q16_mx_shift(h[0], h[1], &L->eoff_gu, &L->ws_gu);
+        if (dmx) L->mx_d = mllm_q16_mx_shift(h[2], h[3], &L->eoff_d, &L->ws_d);
+    }
+    // gate and up in Q6_K run without it (mllm_launch_q16)
+    const bool gu = moe_q16_gu(*L) && L->sem_g != SEM_Q6_K_SEQ && L->sem_g != SEM_Q6_K_LOWNIB, dn = moe_q16_d(*L);
+    if (!gu && !dn) return 0;
+    const long sg = gu ? mllm_q16_smeta_bytes(L->sem_g, M, N, &L->smd_gu) : 0;
+    const long sd = dn ? mllm_q16_smeta_bytes(L->sem_d, N, M, &L->smd_d) : 0;
+    uint8_t *m = nullptr;
+    if (hipMalloc(&m, (size_t)(2 * E * sg + E * sd)) != hipSuccess) return -1;
+    if ((gu && (mllm_launch_q16_smeta(L->sem_g, L->tab, E, M, N, m, sg, nullptr) != hipSuccess ||
+                mllm_launch_q16_smeta(L->sem_u, L->tab + E, E, M, N, m + E * sg, sg, nullptr) != hipSuccess)) ||
+        (dn && mllm_launch_q16_smeta(L->sem_d, L->tab + 2 * E, E, N, M, m + 2 * E * sg, sd, nullptr) != hipSuccess) ||
+        hipStreamSynchronize(nullptr) != hipSuccess) {
+        (void)hipFree(m);
+        return -1;
+    }
+    L->smem = m;
+    if (gu) { L->sm_g = m; L->sm_u = m + E * sg; }
+    if (dn) L->sm_d = m + 2 * E * sg;
+    L->sms_gu = sg; L->sms_d = sd;
     return 0;
 }
 
@@ -367,7 +393,7 @@ MLLM_API mllm_moe_layer *mllm_moe_prepare(int qt_gate, int qt_up, int qt_down, i
         mllm_launch_router_pack(router_dev, N, E, L->router_p, nullptr) != hipSuccess ||
         hipStreamSynchronize(nullptr) != hipSuccess ||
         (L->gemv_only = mllm_moe_needs_gemv(L->tab, L->sem_g, L->sem_u, L->sem_d, N, M, E)) < 0 ||
-        moe_mx_setup(L) != 0) {
+        moe_q16_setup(L) != 0) {
         mllm_moe_release(L);
         return nullptr;
     }
@@ -380,6 +406,7 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *L)
     if (L->tab && L->owns_tab) (void)hipFree(L->tab);
     if (L->dtab) (void)hipFree(L->dtab);
     if (L->dmem) (void)hipFree(L->dmem);
+    if (L->smem) (void)hipFree(L->smem);
     if (L->router_p && L->owns_router) (void)hipFree(L->router_p);
     delete L;
 }
@@ -494,6 +521,7 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
             CK(mllm_launch_act16(L->sem_g, x, N, &xqx, T, N, ax, st));
             q16_args a{};
             a.table = L->tab; a.table2 = L->tab + E;
+            a.sm = L->sm_g; a.sm2 = L->sm_u; a.sm_stride = L->sms_gu; a.sm_doff = L->smd_gu;
             a.x = ax;
             a.row_of = s.tok;
             a.out = s.h; a.ldo = M;
@@ -534,10 +562,11 @@ static int moe_forward_impl(const mllm_moe_layer *L, const float *x, int T, floa
         // down, rows of h already in bucket order
         if (moe_q16_d(*L)) {
             const act16 ah = mllm_act16_carve(L->sem_d, s.a16_h, TK, M);
-            if (mllm_sem_uses_q8(L->sem_d)) CK(mllm_launch_quantize_q8_0(s.h, TK, M, nullptr, hq, hd, hs4, hsq, st));
+            // (MXFP4 x Q8_0: the activation kernel quantises h to Q8_0 itself)
             CK(mllm_launch_act16(L->sem_d, s.h, M, &xqh, TK, M, ah, st));
             q16_args b{};
             b.table = L->tab + 2 * E;
+            b.sm = L->sm_d; b.sm_stride = L->sms_d; b.sm_doff = L->smd_d;
             b.x = ah;
             b.out = s.dn; b.ldo = N;
             b.n_rows = N; b.n_cols = M; b.n_entries = TK;
@@ -650,7 +679,7 @@ mllm_moe_layer *mllm_moe_layer_for_codes(int qt_gate, int qt_up, int qt_down, in
     L->router_p = nullptr;
     L->tab = const_cast<mllm_packed *>(tab_dev);
     L->gemv_only = mllm_moe_needs_gemv(tab_dev, L->sem_g, L->sem_u, L->sem_d, N, M, E);
-    if (L->sem_g < 0 || L->sem_u < 0 || L->gemv_only < 0 || moe_mx_setup(L) != 0) {
+    if (L->sem_g < 0 || L->sem_u < 0 || L->gemv_only < 0 || moe_q16_setup(L) != 0) {
         delete L;
         return nullptr;
     }

@@ -966,14 +966,28 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
 
     // Every prefetch is issued unconditionally (clamped to the last row group):
     // with the same loads outstanding on every path, the compiler waits only
-    // for the older buffer instead of draining all loads.
-    raw_chunk bufA[R], bufB[R];
+    // for the oldest slot instead of draining all loads.  A ring of NR steps:
+    // slot u holds the chunks of step s + u, so NR - 1 steps of weight loads
+    // stay in flight while a step computes (one in flight, 32 bytes a lane,
+    // leaves a long matrix bound by memory latency, not bandwidth)
+    // (the ring on long rows only -- 64 lanes per row, batch 1, no fusion: on the short
+    // matrices of a decode chain its prologue and tail cost more than it hides)
+    constexpr int NR = (R == 1 && BM == 1 && LPR == 64 && FUSE == 0) ? 4 : 2;
+    raw_chunk ring[NR][R];
     int rg = rg0, it = 0;
+    int rgf = rg0, itf = 0;   // the fetch cursor, NR - 1 steps ahead once the prologue has run
+    auto prefetch = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NR - 1; j++) {
+            fetch_step(min(rgf, nrg - 1), itf, ring[j]);
+            advance(rgf, itf);
+        }
+    };
     // prologue: sum(v^2) of each staged 8-element piece, past the staged activation
     float *part = xl + a.pro_lds / 4;
     if constexpr (Q8) {
         if (a.xq.q) {
-            fetch_step(min(rg, nrg - 1), it, bufA);
+            prefetch();
             stage_q8(xl, a.xq, jv.xj * a.x_job_stride, jv.xj * (a.x_job_stride / 32), a.ldx, B, KT, tstride, qstride,
                      0, kused);
         } else {
@@ -983,7 +997,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             q8f_stage qs;
             q8f_load(qs, xf, xuf, a.ldx, B, 0, kused, 0);
             if constexpr (PRO) q8f_pro_load(qs, a, B, kused, 0);
-            fetch_step(min(rg, nrg - 1), it, bufA);
+            prefetch();
             for (int pass = 0;;) {
                 q8f_store(qs, xuf != nullptr, xl, B, KT, tstride, qstride, kused, pass, !a.silu_noclamp,
                           PRO ? &a : nullptr, part);
@@ -1001,7 +1015,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
         if constexpr (PRO) {
             pro_regs pr;
             pro_load(pr, a, B, kused, 0);
-            fetch_step(min(rg, nrg - 1), it, bufA);
+            prefetch();
             // pass 0 out of the pass loop (see stage_digits)
             const int passes = (B * (kused >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
             bool bad = stage_store<SEM, false, true>(xst, reinterpret_cast<uint8_t *>(xl), dg, B, kused, 0, true, &pr,
@@ -1018,7 +1032,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
             if (!a.rms_w && __any(bad))
                 stage_fix<SEM>(reinterpret_cast<uint8_t *>(xl), dg, xj, nullptr, a.x_res, a.ldx, B, 0, kused, true);
         } else {
-            fetch_step(min(rg, nrg - 1), it, bufA);
+            prefetch();
             stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
                                     !a.silu_noclamp);
         }
@@ -1060,18 +1074,42 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
         }
     }
     if (rg >= nrg) return;
-    for (;;) {
-        int rg1 = rg, it1 = it;
-        advance(rg1, it1);
-        fetch_step(min(rg1, nrg - 1), it1, bufB);
-        run_step(rg, it, bufA);
-        if (rg1 >= nrg) break;
-        int rg2 = rg1, it2 = it1;
-        advance(rg2, it2);
-        fetch_step(min(rg2, nrg - 1), it2, bufA);
-        run_step(rg1, it1, bufB);
-        if (rg2 >= nrg) break;
-        rg = rg2; it = it2;
+    if constexpr (NR == 2) {
+        // two buffers, alternating
+        for (;;) {
+            int rg1 = rg, it1 = it;
+            advance(rg1, it1);
+            fetch_step(min(rg1, nrg - 1), it1, ring[1]);
+            run_step(rg, it, ring[0]);
+            if (rg1 >= nrg) break;
+            int rg2 = rg1, it2 = it1;
+            advance(rg2, it2);
+            fetch_step(min(rg2, nrg - 1), it2, ring[0]);
+            run_step(rg1, it1, ring[1]);
+            if (rg2 >= nrg) break;
+            rg = rg2; it = it2;
+        }
+        return;
+    }
+    // the wave's steps: its row groups rg0, rg0 + wstride, ... times iters; whole units of NR
+    // steps in the loop (one exit, so the ring stays in its registers), the rest after it,
+    // already in the ring
+    const int nsteps = ((nrg - 1 - rg0) / wstride + 1) * iters;
+    int s = 0;
+    for (; s + NR <= nsteps; s += NR) {
+#pragma unroll
+        for (int u = 0; u < NR; u++) {
+            fetch_step(min(rgf, nrg - 1), itf, ring[(u + NR - 1) % NR]);
+            advance(rgf, itf);
+            run_step(rg, it, ring[u]);
+            advance(rg, it);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NR - 1; u++) {
+        if (s + u >= nsteps) break;
+        run_step(rg, it, ring[u]);
+        advance(rg, it);
     }
 }
 

@@ -102,10 +102,11 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the configs[1] decode set")
     ap.add_argument("--cpu-leg", choices=CPU_LEGS, help="(internal) run one host-CPU reference leg and print it")
     ap.add_argument("--kernel", choices=("gate_up", "down", "gate_up_b8", "down_b8", "copy", "gemm_gate",
-                                         "gemm_down", "moe_gptoss", "moe_qwen3",
-                                         "moe_gptoss_dense"),
-                    help="run only 50 launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
-                         "decode chain's fused gate+up or down GEMV, or a 256 MiB device copy to calibrate bytes")
+                                         "gemm_down", "moe_gptoss", "moe_qwen3", "long_q4k", "long_mxfp4"),
+                    help="run only a few launches of one kernel and exit, for counter runs (rocprofv3 --pmc): the "
+                         "decode chain's fused gate+up or down GEMV (50), a 256 MiB device copy to calibrate bytes "
+                         "(50), the configs[2] GEMMs (10), the MoE layers at T = 1280 (5 forwards), or the "
+                         "16384 x 16384 batch-1 GEMV (20)")
     return ap.parse_args()
 
 
@@ -173,7 +174,7 @@ def gpu_info(torch):
 
 
 def kernel_only(torch, dev, which):
-    """50 launches of one kernel, nothing else on the GPU besides set-up."""
+    """A few launches of one kernel, nothing else on the GPU besides set-up."""
     if which == "copy":
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         b = torch.empty_like(a)
@@ -192,14 +193,22 @@ def kernel_only(torch, dev, which):
         ws = dev.workspace(sem, C, 1280, x.device, R)
         for _ in range(10):
             dev.gemv(sem, packed, x, R, C, out=o, ws=ws)
-    elif which in ("moe_gptoss", "moe_qwen3", "moe_gptoss_dense"):
-        # the MoE layer at T = 1280, 5 forwards (_dense: over bf16 expert copies)
+    elif which in ("long_q4k", "long_mxfp4"):
+        # the batch-1 decode GEMV on a 16384 x 16384 matrix (bench_long_gemv), 20 launches
+        # rotating over copies that together exceed the Infinity Cache
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        sem, qt = (K.Q4_K_GGML, W.QT_Q4_K) if which.endswith("q4k") else (K.MXFP4, W.QT_MXFP4)
+        copies, _ = long_gemv_copies(torch, dev, gen, sem, qt)
+        x = torch.randn(1, LONG_GEMV, device="cuda", generator=gen)
+        o = torch.empty(1, LONG_GEMV, device="cuda")
+        for i in range(20):
+            dev.gemv(sem, copies[i % len(copies)], x, LONG_GEMV, LONG_GEMV, out=o)
+    elif which in ("moe_gptoss", "moe_qwen3"):
+        # the MoE layer at T = 1280, 5 forwards
         wl = W.moe_workload(which.split("_")[1], 1280)
         c = wl["cfg"]
         layer = dev.moe_prepare(wl["qts"], c["N"], c["M"], c["E"], c["K"], wl["gates"], wl["ups"], wl["downs"],
                                 torch.from_numpy(wl["router"]).cuda(), 1)
-        if which.endswith("_dense"):
-            layer.dense_experts()
         x = torch.from_numpy(wl["x"]).cuda()
         o = torch.empty(1280, c["N"], device="cuda")
         for _ in range(5):
@@ -219,7 +228,7 @@ def kernel_only(torch, dev, which):
             else:
                 dev.gemv_fused(L["down"].sem, L["down"].packed, ch.h, 2048, 5632, ch.f_down, out=ch.xa, ws=ch.ws)
     torch.cuda.synchronize()
-    print(f"[bench] {which}: 50 launches done", file=sys.stderr, flush=True)
+    print(f"[bench] {which}: launches done", file=sys.stderr, flush=True)
 
 
 def log(msg):
@@ -276,34 +285,54 @@ def bench_kinds(torch, dev, layers, lm, out_norm, args):
     return res
 
 
+LONG_GEMV = 16384   # rows = columns of the long-matrix GEMV
+
+
+def long_gemv_copies(torch, dev, gen, sem, qt):
+    """Packed copies of one 16384 x 16384 matrix, two or more so that together
+    they exceed the 256 MB Infinity Cache (launches rotate over them)."""
+    R = C = LONG_GEMV
+    raw = W.gen_weights_torch(gen, qt, R, C)
+    nbytes = raw.numel()
+    copies = [dev.pack(sem, raw, R, C) for _ in range(max(2, -(-320_000_000 // nbytes)))]
+    del raw
+    return copies, nbytes
+
+
 def bench_long_gemv(torch, dev, args):
     """The batch-1 decode GEMV on one long matrix per format (16384 x 16384,
     143-285 MB: a launch long enough for its steady rate to show), against a
-    plain read of the same bytes."""
+    plain read of the same bytes; each timed replay runs 8 launches rotating
+    over copies that together exceed the Infinity Cache."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
     sink = torch.empty(64, dtype=torch.uint8, device="cuda")
     res = {}
-    R = C = 16384
+    R = C = LONG_GEMV
+    reps = 8
     for name, sem, qt in (("Q4_K", K.Q4_K_GGML, W.QT_Q4_K), ("Q6_K", K.Q6_K_SEQ, W.QT_Q6_K),
                           ("Q8_0", K.Q8_0, W.QT_Q8_0), ("MXFP4", K.MXFP4, W.QT_MXFP4)):
-        raw = W.gen_weights_torch(gen, qt, R, C)
-        nbytes = raw.numel()
-        packed = dev.pack(sem, raw, R, C)
-        del raw
+        copies, nbytes = long_gemv_copies(torch, dev, gen, sem, qt)
         x = torch.randn(1, C, device="cuda")
         o = torch.empty(1, R, device="cuda")
-        ms = time_region(torch, lambda: dev.gemv(sem, packed, x, R, C, out=o), max(5, args.steps), args.warmup)
-        rd = time_region(torch, lambda: dev.so.mllm_read_probe(packed.data_ptr(), packed.numel() // 16 * 16,
-                                                                sink.data_ptr(), dev._stream()),
-                         max(5, args.steps), args.warmup)
+
+        def run():
+            for i in range(reps):
+                dev.gemv(sem, copies[i % len(copies)], x, R, C, out=o)
+
+        def read():
+            for i in range(reps):
+                p = copies[i % len(copies)]
+                dev.so.mllm_read_probe(p.data_ptr(), p.numel() // 16 * 16, sink.data_ptr(), dev._stream())
+        ms = time_region(torch, run, max(5, args.steps), args.warmup) / reps
+        rd = time_region(torch, read, max(5, args.steps), args.warmup) / reps
         gbs = (nbytes + 4 * (R + C)) / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                      "plain_read_us": round(rd * 1e3, 1), "frac_of_plain_read": round(rd / ms, 3),
-                     "MB": round(nbytes / 1e6, 1)}
+                     "MB": round(nbytes / 1e6, 1), "copies": len(copies)}
         log(f"long GEMV {name} {R}x{C} B=1: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); "
-            f"plain read {rd * 1e3:.1f} us")
-        del packed
+            f"plain read {rd * 1e3:.1f} us ({len(copies)} copies)")
+        del copies
         torch.cuda.empty_cache()
     return res
 
@@ -414,7 +443,8 @@ def bench_moe(torch, dev, args, tag, sizes=(1, 1280)):
         res[f"T{Tn}"] = r
         log(f"MoE {tag} T={Tn}: {ms * 1e3:.1f} us, {r['tokens/s']} tokens/s")
     # the batched path over load-time bf16 expert copies (mllm_moe_dense_experts:
-    # the MXFP4 forms, bit-identical results), where the layer's formats allow it
+    # MXFP4 matrices left on the bf16-tile GEMM, bit-identical results), where the
+    # layer has any (none at configs[3] / configs[4]: the fp16-plane GEMM takes them)
     big = max(sizes)
     if big > 24:
         dl = dev.moe_prepare(qts, N, M, E, Kk, gates, ups, downs, router, 1)

@@ -313,7 +313,9 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *layer);
 /* Load-time bf16 copies of the layer's expert matrices whose weights are exact
  * in bf16 (the MXFP4 forms: gate/up of one semantic, down), which the batched
  * path (T > 24) then copies into its tiles instead of decoding; results are
- * bit-identical.  2 bytes per weight (3.8x MXFP4), freed with the layer.
+ * bit-identical.  Matrices the batched path runs on the fp16-plane GEMM
+ * (mllm_moe_layer_info bits 1 / 2) are not copied: that GEMM reads the packed
+ * weights and is faster.  2 bytes per weight (3.8x MXFP4), freed with the layer.
  * Returns the bytes allocated (0: nothing qualifies, or already made), -1 on
  * error; synchronises `stream`.  No reference counterpart: the memory-for-
  * speed trade of moe_forward_omp's experts (QK:2066-2250) on 288 GB HBM. */

@@ -413,15 +413,17 @@ MLLM_API void mllm_moe_release(mllm_moe_layer *L)
 
 // Load-time bf16 plane copies of the expert matrices (mllm_launch_dense_planes:
 // the values put_w would write into the tiles, so results are bit-identical);
-// gate and up take them when they share a semantic.
+// gate and up take them when they share a semantic.  Only matrices the batched
+// path runs on the bf16-tile GEMM are copied: those on the fp16-plane GEMM
+// (moe_q16_gu / moe_q16_d) never read a copy.
 MLLM_API long mllm_moe_dense_experts(mllm_moe_layer *L, void *stream)
 {
     if (!L) return -1;
     if (L->dmem) return 0;
     const int pg = L->sem_g >= 0 ? mllm_dense_planes(L->sem_g) : 0;
     const int pd = L->sem_d >= 0 ? mllm_dense_planes(L->sem_d) : 0;
-    const bool gu = !L->gemv_only && pg > 0 && L->sem_g == L->sem_u;
-    const bool dn = !L->gemv_only && pd > 0;
+    const bool gu = !L->gemv_only && pg > 0 && L->sem_g == L->sem_u && !moe_q16_gu(*L);
+    const bool dn = !L->gemv_only && pd > 0 && !moe_q16_d(*L);
     if (!gu && !dn) return 0;
     hipStream_t st = (hipStream_t)stream;
     const int E = L->E, N = L->N, M = L->M;

@@ -632,68 +632,120 @@ __global__ __launch_bounds__(256) void k_route_slice(const float *__restrict__ r
     if (wave == 0 && lane < ES) logits[(long)t * E + e0 + lane] = dot;
 }
 
-// Routing logits for many tokens: a workgroup takes RT_T tokens x RT_E
-// experts and every lane runs one (token, expert) chain, so all 256 lanes of
-// every workgroup are busy.  Router rows and x rows are staged in LDS in
-// chunks of KC steps (each row contiguous, stride RS float4 with RS % 16 == 1
-// so the 16 token rows a wave reads fall on distinct banks), two buffers:
-// chunk c+1 is loaded into registers while chunk c's chains run, and stored
-// to the other buffer afterwards.  The chains use chain72 (the hand-scheduled
-// loop of k_route_slice).  Steps from N up to the padded length are zero in
-// both operands.  Raw logits go to `logits` for k_route_finish.
-constexpr int RT_T = 16, RT_E = 16;     // tokens and experts per workgroup
-constexpr int RT_KC = 432;              // steps per chunk (6 chain72 iterations)
-constexpr int RT_RS = 129;              // row stride in float4: >= 108 + 12 of slack, 1 mod 16
-constexpr int RT_ROWS = RT_T + RT_E;
-constexpr int RT_SLOTS = (RT_ROWS * (RT_KC / 4) + 255) / 256;   // float4 loads per thread and chunk
+// Routing logits for many tokens with each token's x broadcast across a DPP
+// row.  A workgroup takes RB_E = 16 experts and 16 tokens: lane column
+// c = lane & 15 is expert e0 + c and each 16-lane row (4 per wave) one token,
+// so every lane runs one chain.  Per 16-step group a lane holds x[t][k + c]
+// of its row's token in a register, and step i of the group takes x[t][k + i]
+// from lane i of the row as the DPP source of its FMA (row_newbcast:i): x
+// costs no LDS traffic, only the lane's router values do (a float4 per four
+// steps).  Router chunks of 16 * G steps are staged in LDS ([quad][expert],
+// two buffers), loaded into registers one chunk ahead like the x values of
+// the next chunk; steps from N up to the padded length are zero in both
+// operands (x through the range check of its buffer loads), and
+// fma(0, 0, d) == d as in chain72.  The chunk count is even so the loop
+// alternates two register sets for x, which only buffer loads write (a DPP
+// source written by a VALU instruction needs two wait states; every group's
+// FMAs start with them anyway).  Measured against two or four chains per
+// lane (more router reuse per LDS read, fewer waves): one chain is fastest
+// at both benchmark shapes, whose time is the chains' FMA latency.
+constexpr int RB_E = 16;
+#define RB1(i, r) "v_fmac_f32_dpp %0, %1, %" #r " row_newbcast:" #i " row_mask:0xf bank_mask:0xf\n"
 
-__global__ __launch_bounds__(256) void k_route_tile(const float *__restrict__ router_p, const float *__restrict__ x,
-                                                    int T, int N, int E, int nch, float *__restrict__ logits)
+// acc = fma(x[k + i], r[i], acc) for i = 0..15 in order, x[k + i] from lane i
+// of the row of xv.
+__device__ __forceinline__ float rb_group(float acc, float xv, const float4 (&r)[4])
 {
-    extern __shared__ float4 lds4[];
-    const int tid = threadIdx.x;
-    const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
-    // lane (token tt, expert te): a wave holds 16 tokens x 4 experts
-    const int tt = tid & 15, te = tid >> 4;
-    const int N4 = N >> 2, KQ = RT_KC / 4;
+    asm("s_nop 1\n" RB1(0, 2) RB1(1, 3) RB1(2, 4) RB1(3, 5) RB1(4, 6) RB1(5, 7) RB1(6, 8) RB1(7, 9) RB1(8, 10)
+            RB1(9, 11) RB1(10, 12) RB1(11, 13) RB1(12, 14) RB1(13, 15) RB1(14, 16) RB1(15, 17)
+        : "+v"(acc)
+        : "v"(xv), "v"(r[0].x), "v"(r[0].y), "v"(r[0].z), "v"(r[0].w), "v"(r[1].x), "v"(r[1].y), "v"(r[1].z),
+          "v"(r[1].w), "v"(r[2].x), "v"(r[2].y), "v"(r[2].z), "v"(r[2].w), "v"(r[3].x), "v"(r[3].y), "v"(r[3].z),
+          "v"(r[3].w));
+    return acc;
+}
+#undef RB1
+
+template <int G>
+__global__ __launch_bounds__(256) void k_route_bc(const float *__restrict__ router_p, const float *__restrict__ x,
+                                                  int T, int N, int E, int nch, float *__restrict__ logits)
+{
+    constexpr int KQ = 4 * G, KC = 16 * G;       // quads and steps per chunk
+    constexpr int SL = KQ * RB_E / 256;          // staged router float4 per thread and chunk
+    static_assert(SL * 256 == KQ * RB_E, "whole staging slots");
+    __shared__ float4 rl[2][KQ * RB_E];
+    const int tid = threadIdx.x, c = tid & 15;
+    const int e0 = blockIdx.y * RB_E, t = blockIdx.x * 16 + (tid >> 4);
+    const int N4 = N >> 2;
     const float4 *r4 = reinterpret_cast<const float4 *>(router_p);
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float4 st[RT_SLOTS];
-    // slot j of a chunk: row j / KQ (experts first, then tokens), quad j % KQ
-    auto load = [&](int c) __attribute__((always_inline)) {
+    // x through buffer loads: lanes past the tokens or past N read zeros (offset
+    // 2^31 >= the buffer's T*N*4 bytes)
+    const __amdgpu_buffer_rsrc_t xs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x), (short)0, T * N * 4, 0x00020000);
+    constexpr uint32_t kOut = 0x80000000u;
+    const uint32_t xo = t < T ? (uint32_t)(t * N + c) * 4u : kOut;
+    float4 st[SL];
+    auto stage_load = [&](int ch) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < RT_SLOTS; s++) {
-            const int j = tid + 256 * s, row = j / KQ, q = c * KQ + (j - row * KQ);
+        for (int s = 0; s < SL; s++) {
+            const int i = tid + 256 * s, q = ch * KQ + (i >> 4), e = e0 + (i & 15);
             st[s] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (row < RT_E) {
-                if (e0 + row < E && q < N4) st[s] = gld<float4>(r4 + (long)q * E + e0 + row);
-            } else if (row < RT_ROWS) {
-                const int t = t0 + row - RT_E;
-                if (t < T && q < N4) st[s] = gld<float4>(x4 + (long)t * N4 + q);
+            if (q < N4 && e < E) st[s] = gld<float4>(r4 + (long)q * E + e);
+        }
+    };
+    auto stage_store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < SL; s++) rl[buf][tid + 256 * s] = st[s];
+    };
+    auto load_x = [&](int ch, float (&xv)[G]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const int k = ch * KC + 16 * g;
+            // sign bit set where c >= N - k (past the row's end): arithmetic, not a
+            // select, which the compiler would turn into branches around the loads
+            const uint32_t oob = (uint32_t)(N - 1 - k - c) & kOut;
+            xv[g] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xs, xo | oob, 4 * k, 0));
+        }
+    };
+    float acc = 0.0f;
+    auto chains = [&](int buf, const float (&xv)[G]) __attribute__((always_inline)) {
+        const float4 *b = rl[buf] + c;
+        float4 rc[4], rn[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) rc[u] = b[u * RB_E];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (g + 1 < G) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) rn[u] = b[(4 * (g + 1) + u) * RB_E];
+            }
+            acc = rb_group(acc, xv[g], rc);
+            if (g + 1 < G) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) rc[u] = rn[u];
             }
         }
     };
-    auto store = [&](int buf) __attribute__((always_inline)) {
-        float4 *b = lds4 + buf * RT_ROWS * RT_RS;
-#pragma unroll
-        for (int s = 0; s < RT_SLOTS; s++) {
-            const int j = tid + 256 * s, row = j / KQ;
-            if (row < RT_ROWS) b[row * RT_RS + (j - row * KQ)] = st[s];
-        }
-    };
-    float dot = 0.0f;
-    load(0);
-    store(0);
-    for (int c = 0; c < nch; c++) {
-        if (c + 1 < nch) load(c + 1);
-        __syncthreads();                              // chunk c stored by every thread
-        const float4 *b = lds4 + (c & 1) * RT_ROWS * RT_RS;
-        dot = chain72(dot, (unsigned)(uintptr_t)(b + te * RT_RS), (unsigned)(uintptr_t)(b + (RT_E + tt) * RT_RS),
-                      RT_KC / kChainIter);
-        // buffer (c+1)&1 was last read by chunk c-1's chains, before this iteration's barrier
-        if (c + 1 < nch) store((c + 1) & 1);
+    float xa[G], xb[G];
+    stage_load(0);
+    stage_store(0);
+    load_x(0, xa);
+    // chunk ch: load chunk ch + 1 (the last one again at the end: harmless),
+    // barrier (chunk ch stored), chains over chunk ch, store chunk ch + 1 into
+    // the buffer chunk ch - 1's chains finished reading before the barrier
+    for (int ch = 0; ch < nch; ch += 2) {
+        stage_load(min(ch + 1, nch - 1));
+        load_x(min(ch + 1, nch - 1), xb);
+        __syncthreads();
+        chains(0, xa);
+        stage_store(1);
+        stage_load(min(ch + 2, nch - 1));
+        load_x(min(ch + 2, nch - 1), xa);
+        __syncthreads();
+        chains(1, xb);
+        stage_store(0);
     }
-    if (t0 + tt < T && e0 + te < E) logits[(long)(t0 + tt) * E + e0 + te] = dot;
+    if (t < T && e0 + c < E) logits[(long)t * E + e0 + c] = acc;
 }
 
 // Softmax and top-K of logits[t][0..E) written by the expert slices of k_route.
@@ -974,12 +1026,19 @@ hipError_t mllm_launch_route(const float *router_p, const float *x, int T, int N
             return hipGetLastError();
         }
     }
-    // More tokens with a logits workspace: k_route_tile, then k_route_finish.
-    if (T > 8 && logits_ws && N % 4 == 0) {
-        const int nch = (N + RT_KC - 1) / RT_KC;
-        const size_t lds = 2 * (size_t)RT_ROWS * RT_RS * sizeof(float4);
-        hipLaunchKernelGGL(k_route_tile, dim3((T + RT_T - 1) / RT_T, (E + RT_E - 1) / RT_E), dim3(256), lds, st,
-                           router_p, x, T, N, E, nch, logits_ws);
+    // More tokens with a logits workspace: k_route_bc, then k_route_finish,
+    // over token ranges that keep each launch's x below 2^31 bytes (the range
+    // check of its buffer loads).
+    if (T > 8 && logits_ws) {
+        constexpr int G = 16, KC = 16 * G;
+        const int nch = ((N + KC - 1) / KC + 1) & ~1;   // even: the loop runs chunk pairs
+        const long lim = ((1l << 31) - 1) / ((long)N * 4) / 16 * 16;
+        if (lim < 16) return hipErrorInvalidValue;
+        for (int t0 = 0; t0 < T; t0 += (int)lim) {
+            const int Tc = (int)(T - t0 < lim ? T - t0 : lim);
+            hipLaunchKernelGGL((k_route_bc<G>), dim3((Tc + 15) / 16, (E + RB_E - 1) / RB_E), dim3(256), 0, st,
+                               router_p, x + (long)t0 * N, Tc, N, E, nch, logits_ws + (long)t0 * E);
+        }
         hipLaunchKernelGGL(k_route_finish, dim3(T), dim3(256), 0, st, logits_ws, T, E, K, renorm, top_idx, top_w);
         return hipGetLastError();
     }

@@ -110,6 +110,22 @@ def test_device_route_vs_oracle(dev, orc, E, N, Kk, renorm, T, slices):
     assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
 
 
+@pytest.mark.parametrize("E,N,Kk,renorm", [(128, 2048, 8, 1), (144, 1000, 6, 0), (130, 2884, 8, 1)])
+def test_device_route_many_tokens_vs_oracle(dev, orc, E, N, Kk, renorm):
+    """T = 1100 (a ragged last token group) through the many-token routing
+    kernel, with N % 16 != 0 (a 16-step group that straddles the end of the
+    rows) and E not a multiple of 16."""
+    import torch
+    T = 1100
+    rng = np.random.default_rng(E + N)
+    rw = W.gen_router(rng, E, N)
+    x = W.gen_x(rng, T, N)
+    ri, rwt = orc.route(rw, x, Kk, renorm)
+    idx, wt = dev.route(torch.from_numpy(rw).cuda(), torch.from_numpy(x).cuda(), Kk, renorm)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    assert np.max(np.abs(wt.cpu().numpy() - rwt) / rwt) < 1e-6
+
+
 @pytest.mark.parametrize("tag", ["qwen", "gptoss", "q5down", "q5down_all"])
 def test_golden_moe_forward(lib, golden, tag):
     """q5down*: a Q5_0 down projection with n_embd < n_ff, whose rows the

@@ -46,10 +46,15 @@ template <int SEM> struct q16_traits {
     static constexpr int NPL = A4 ? 1 : 2;                 // activation planes
 };
 
-// Waves per workgroup (each owns 32 weight rows).  MXFP4 down projections take 256 rows,
-// so each activation tile staged in LDS serves twice the rows (the activation loads bound
-// these GEMMs); gate + up, whose two matrices already share each tile, keep 128.
-template <int SEM, bool DUAL> constexpr int q16_wpg() { return q16_traits<SEM>::MX && !DUAL ? 8 : 4; }
+// Waves per workgroup (each owns 32 weight rows).  Single-matrix launches over the MoE
+// layer's 64-entry expert tiles (the MXFP4 and Q6_K down projections) take 256 rows, so
+// each activation tile staged in LDS serves twice the rows (the activation loads bound
+// these GEMMs; Qwen3's short-K Q6_K down gained 4%, bit-identical); gate + up, whose
+// two matrices already share each tile, and the 128-entry dense tiles keep 128.
+template <int SEM, bool DUAL, int EB> constexpr int q16_wpg()
+{
+    return (q16_traits<SEM>::MX || (q16_traits<SEM>::Q6 && EB == 2)) && !DUAL ? 8 : 4;
+}
 
 // Bits 3 and 4 ... of a step position p: i = p >> 4 (MFMA of the step), kh = (p >> 3) & 1
 // (lane half), j = p & 7 (slot).  sw(j): slot -> byte order of the nibble pairs (j bits 0,1 swapped).
@@ -312,10 +317,10 @@ template <class T> MLLM_DEV T gldo(const void *base, uint32_t off) { return gld<
 // SM: the matrices' super-block metadata (MXFP4: exponents) read from the step-major copy
 // (a.sm, mllm_launch_q16_smeta) instead of the packed planes.
 template <int SEM, bool DUAL, int EB, bool SM>
-__global__ __launch_bounds__((64 * q16_wpg<SEM, DUAL>()), (8 / q16_wpg<SEM, DUAL>())) void k_q16(q16_args a)
+__global__ __launch_bounds__((64 * q16_wpg<SEM, DUAL, EB>()), (8 / q16_wpg<SEM, DUAL, EB>())) void k_q16(q16_args a)
 {
     using Q = q16_traits<SEM>;
-    constexpr int WPG = q16_wpg<SEM, DUAL>(), RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 32 * WPG, SPB = Q::SPB, NPL = Q::NPL;
+    constexpr int WPG = q16_wpg<SEM, DUAL, EB>(), RB = DUAL ? 2 : 1, TM = 32 * EB, TN = 32 * WPG, SPB = Q::SPB, NPL = Q::NPL;
     constexpr bool MX = Q::MX;
     static_assert(SPB == 2 || SPB == 4 || MX, "steps run in units of four");
     static_assert(SM || !MX, "MXFP4 reads its exponents step-major");
@@ -461,10 +466,17 @@ __global__ __launch_bounds__((64 * q16_wpg<SEM, DUAL>()), (8 / q16_wpg<SEM, DUAL
             }
         } else {
             const uint8_t *src = (const uint8_t *)(a.x.h + p * a.x.hplane + 64 * (long)s);
+            if constexpr (WPG == 8) {
+                static_assert(NCH == 1 && NEB <= 2, "eight-wave tiles: 64 entries");
+                if (NEB == 2 || wave < 4)
+                    __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[0] : boff[0])),
+                                                     (void *)(dst + 512 * wave), 16, 0, 0);
+            } else {
 #pragma unroll
-            for (int c = 0; c < NEB; c++)
-                __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
-                                                 (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
+                for (int c = 0; c < NEB; c++)
+                    __builtin_amdgcn_global_load_lds((const void *)(src + (p ? boff1[c] : boff[c])),
+                                                     (void *)(dst + (256 * c + 64 * wave) * 8), 16, 0, 0);
+            }
         }
     };
     // this wave's loads older than the newest n are done, then the workgroup meets: every
@@ -1133,7 +1145,7 @@ hipError_t launch16(const q16_args &a, int max_tiles, hipStream_t st)
 {
     constexpr int TM = 32 * EB;
     const int ks = (a.ksplit > 1 && !DUAL && !a.tile_expert && !a.out_row) ? a.ksplit : 1;
-    constexpr int TN = 32 * q16_wpg<SEM, DUAL>();
+    constexpr int TN = 32 * q16_wpg<SEM, DUAL, EB>();
     dim3 grid((a.n_rows + TN - 1) / TN, a.tile_expert ? max_tiles : (a.n_entries + TM - 1) / TM, ks);
     if (grid.y == 0) return hipSuccess;
     q16_args b = a;

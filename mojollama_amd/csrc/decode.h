@@ -20,6 +20,7 @@
 // are in flight together.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include "mllm_common.h"
 
 #define MLLM_DEV __device__ __forceinline__
@@ -188,6 +189,66 @@ MLLM_DEV void fetch(const mllm_packed &P, int nb, int row, int c, raw_chunk &r)
         r.b.x = q.x; r.b.y = q.y;
         r.m.x = gld<uint16_t>(P.p[2] + bi * 16 + 2 * cc);
         r.d = gld<uint16_t>(P.p[3] + bi * 2);
+    }
+}
+
+// fetch<SEM> for the chunks c = 64 it + l of one row whose 64 lanes l take a step together:
+// the step's first block is uniform (ublk = row * nb + it * 64 / CPB), so each plane is
+// read through a buffer resource with the step's offset in an SGPR and a lane-constant
+// offset in a VGPR, without per-step 64-bit address arithmetic.  Lanes past the row's last
+// chunk read the next row's bytes, or zeros past the plane's end (the resource's range
+// check): their values are discarded, like the clamped chunk of fetch.  Each plane of the
+// matrix must be below 4 GiB (the launcher keeps larger matrices off this path).
+template <int SEM>
+constexpr bool kFetchLin = SEM == SEM_Q4_K_GGML || SEM == SEM_MXFP4 || SEM == SEM_Q8_0 || SEM == SEM_Q6_K_SEQ;
+
+struct lin_planes {
+    __amdgpu_buffer_rsrc_t r[4];
+};
+
+template <int SEM>
+MLLM_DEV lin_planes lin_make(const mllm_packed &P, uint32_t nblk)   // nblk: the matrix's blocks
+{
+    lin_planes L{};
+    auto mk = [&](int i, uint32_t per) {
+        L.r[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(P.p[i]), (short)0, (int)(nblk * per),
+                                                   0x00020000);
+    };
+    if constexpr (SEM == SEM_Q4_K_GGML) { mk(0, 128); mk(1, 16); }
+    else if constexpr (SEM == SEM_MXFP4) { mk(0, 16); mk(1, 1); }
+    else if constexpr (SEM == SEM_Q8_0) { mk(0, 32); mk(1, 2); }
+    else { mk(0, 128); mk(1, 64); mk(2, 16); mk(3, 2); }
+    return L;
+}
+
+template <int SEM>
+MLLM_DEV void fetch_lin(const lin_planes &L, uint32_t ublk, int l, raw_chunk &r)
+{
+    static_assert(kFetchLin<SEM>, "formats with a linear chunk layout");
+    // codes: cache policy non-temporal (they stream once, as ld16); metadata: default
+    auto b128 = [&](int i, int vo, uint32_t so, auto nt_c) {
+        const mllm_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(L.r[i], vo, (int)so, decltype(nt_c)::value ? 2 : 0);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    using NT = std::true_type;
+    using TC = std::false_type;
+    if constexpr (SEM == SEM_Q4_K_GGML) {
+        r.a = b128(0, 16 * l, ublk * 128u, NT{});
+        r.m = b128(1, 16 * (l >> 3), ublk * 16u, TC{});
+    } else if constexpr (SEM == SEM_MXFP4) {
+        r.a = b128(0, 16 * l, ublk * 16u, NT{});
+        r.d = __builtin_amdgcn_raw_buffer_load_b8(L.r[1], l, (int)ublk, 0);
+    } else if constexpr (SEM == SEM_Q8_0) {
+        r.a = b128(0, 32 * l, ublk * 32u, NT{});
+        r.b = b128(0, 32 * l + 16, ublk * 32u, NT{});
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(L.r[1], 2 * l, (int)(ublk * 2u), 0);
+    } else {   // SEM_Q6_K_SEQ
+        r.a = b128(0, 16 * l, ublk * 128u, NT{});
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(L.r[1], 8 * l, (int)(ublk * 64u), 0);
+        r.b.x = q[0];
+        r.b.y = q[1];
+        r.m.x = __builtin_amdgcn_raw_buffer_load_b16(L.r[2], 2 * l, (int)(ublk * 16u), 0);
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(L.r[3], 2 * (l >> 3), (int)(ublk * 2u), 0);
     }
 }
 

@@ -898,7 +898,16 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     auto out_row = [&](int rg, int r) __attribute__((always_inline)) {
         return PAIR ? rg * OPW + (grp >> 1) : rg * OPW + grp * R + r;
     };
+    // the ring path's formats with a linear chunk layout: buffer-resource loads (fetch_lin)
+    constexpr bool LIN = R == 1 && BM == 1 && LPR == 64 && FUSE == 0 && !Q8 && kFetchLin<SEM>;
+    lin_planes lp{};
+    if constexpr (LIN) lp = lin_make<SEM>(W, (uint32_t)n_out * (uint32_t)nb);
     auto fetch_step = [&](int rg, int it, raw_chunk (&buf)[R]) __attribute__((always_inline)) {
+        if constexpr (LIN) {
+            const uint32_t ublk = (uint32_t)min(out_row(rg, 0), n_out - 1) * (uint32_t)nb + (uint32_t)(it * (64 / CPB));
+            fetch_lin<SEM>(lp, ublk, sl, buf[0]);
+            return;
+        }
         const int c = min(it * LPR + sl, nch - 1);
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -1237,6 +1246,9 @@ int pick_lpr(const mllm_gemv_args &a, int n_jobs, int HR)
         // short matrices: wider lane groups (fewer rows per workgroup) until
         // the launch has about two workgroups per CU
         while (lpr < 64 && wgs_at(lpr) < 2L * device_cus()) lpr *= 2;
+        // 64 lanes per row read through 32-bit buffer offsets (fetch_lin): matrices
+        // of 4 GiB and more take 32
+        if (lpr == 64 && (long)a.n_rows * row_bytes >= (1l << 32)) lpr = 32;
     } else {
         // lanes per row: enough chunks per lane to keep every lane busy on short
         // rows; 32 where that still leaves two workgroups per CU (fewer lane-group

@@ -88,15 +88,18 @@ MLLM_API void moe_ffn(const void *c, int l, float *x, float *gate_buf, float *up
  * un-renormalised top-K routing, k-order combine. */
 MLLM_API void moe_ffn_batched(const void *c, int l, const float *x, float *ffn_out, int B);
 
-/* TE:515-518, 620-666 (_requantize_output): the caller's load-time conversion
- * of a Q4_K / Q6_K lm_head to Q8_0, done in numpy there and on the GPU here:
- * each row dequantised as q4_k/q6_k_dequantize_row (QK:762-828), then per 32
- * elements amax = max(max|x|, 1e-10), d = amax/127, q = rint(x/d) clamped to
- * +-127, d stored as fp16 -- bit-exact with TE's result.  Host pointers: W
- * is the raw GGUF matrix, out receives n_rows * (n_cols/32) * 34 bytes.
- * Returns 0, or -1 for another type (TE's F16 branch converts the raw bit
- * patterns, TE:643-645, and is not reproduced).  No counterpart symbol in
- * the reference's C library: the routine TE would call in place of its loop. */
+/* TE:515-522, 620-666 (_requantize_output): the caller's load-time conversion
+ * of a Q4_K / Q6_K / F16 lm_head to Q8_0, done in numpy there and on the GPU
+ * here: each row dequantised as q4_k/q6_k_dequantize_row (QK:762-828), or for
+ * F16 (quant_type 1) converted as TE:643-645 does, which takes each 16-bit
+ * pattern's integer value (0x3C00 -> 15360.0f) rather than its fp16 value;
+ * then per 32 elements amax = max(max|x|, 1e-10), d = amax/127, q = rint(x/d)
+ * clamped to +-127, d stored as fp16 -- bit-exact with TE's result.  Host
+ * pointers: W is the raw GGUF matrix, out receives n_rows * (n_cols/32) * 34
+ * bytes.  Returns 0, or -1 for another type (TE's Q5_K branch raises) or an
+ * F16 row length that is not a multiple of 32 (TE's reshape raises).  No
+ * counterpart symbol in the reference's C library: the routine TE would call
+ * in place of its loop. */
 MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, int quant_type, uint8_t *out);
 
 /* gqa_attention.c:93 gqa_attention_decode: decode attention of one token.
@@ -262,8 +265,9 @@ MLLM_API long mllm_gemv_fused_workspace_size(int sem, int n_rows, int n_cols, in
 MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev, float *out_dev, int n_rows,
                              int n_cols, int B, const mllm_gemv_fusion *f, void *workspace, void *stream);
 
-/* requantize_output_q8_0 on device data: raw_dev (raw GGUF Q4_K / Q6_K) ->
- * q8_dev (raw Q8_0 blocks); workspace of mllm_requantize_workspace_size bytes. */
+/* requantize_output_q8_0 on device data: raw_dev (raw GGUF Q4_K / Q6_K, or
+ * F16 patterns) -> q8_dev (raw Q8_0 blocks); workspace of
+ * mllm_requantize_workspace_size bytes. */
 MLLM_API long mllm_requantize_workspace_size(int quant_type, int n_rows, int n_cols);
 MLLM_API int mllm_requantize_q8_0(int quant_type, const void *raw_dev, int n_rows, int n_cols, void *q8_dev,
                                   void *workspace, void *stream);

@@ -1191,11 +1191,14 @@ MLLM_API int mllm_gemv_fused(int sem, const void *packed_dev, const float *x_dev
 
 // ------------------------------------------------ lm_head requantisation (f2)
 static int requant_sem(int qt) { return qt == 12 ? SEM_Q4_K_GGML : qt == 14 ? SEM_Q6_K_GGML : -1; }
+constexpr int kQtF16 = 1;   // TE:519-522: F16 output matrices are requantised too
 
 MLLM_API long mllm_requantize_workspace_size(int quant_type, int n_rows, int n_cols)
 {
+    if (n_rows <= 0 || n_cols <= 0) return -1;
+    if (quant_type == kQtF16) return (long)align256((size_t)n_rows * n_cols * 4);
     const int sem = requant_sem(quant_type);
-    if (sem < 0 || n_rows <= 0 || n_cols <= 0) return -1;
+    if (sem < 0) return -1;
     return (long)(align256(mllm_packed_bytes(mllm_sem_layout(sem), n_rows, n_cols, nullptr)) +
                   align256((size_t)n_rows * n_cols * 4));
 }
@@ -1204,10 +1207,24 @@ MLLM_API int mllm_requantize_q8_0(int quant_type, const void *raw_dev, int n_row
                                   void *workspace, void *stream)
 {
     const int sem = requant_sem(quant_type);
-    if (sem < 0) { set_error("mllm_requantize_q8_0: type %d is not requantised (Q4_K and Q6_K only, TE:515-518)", quant_type); return -1; }
+    if (sem < 0 && quant_type != kQtF16) {
+        set_error("mllm_requantize_q8_0: type %d is not requantised (Q4_K, Q6_K and F16 only, TE:515-522)", quant_type);
+        return -1;
+    }
+    if (quant_type == kQtF16 && n_cols % 32) {
+        set_error("mllm_requantize_q8_0: F16 rows of whole 32-element blocks only (TE:650-651 reshapes by 32)");
+        return -1;
+    }
     if (n_rows <= 0 || n_cols < 32) return 0;
     if (!workspace) { set_error("mllm_requantize_q8_0: needs a workspace"); return -1; }
     hipStream_t st = (hipStream_t)stream;
+    if (quant_type == kQtF16) {
+        // TE:643-645: the patterns' integer values, then TE's Q8_0 statements
+        float *f32 = (float *)workspace;
+        HIP_OK(mllm_launch_u16_value_f32((const uint16_t *)raw_dev, (long)n_rows * n_cols, f32, st));
+        HIP_OK(mllm_launch_requant_q8_0(f32, n_rows, n_cols, (uint8_t *)q8_dev, st));
+        return 0;
+    }
     const int ly = mllm_sem_layout(sem);
     uint8_t *packed = (uint8_t *)workspace;
     float *f32 = (float *)(packed + align256(mllm_packed_bytes(ly, n_rows, n_cols, nullptr)));
@@ -1227,11 +1244,19 @@ MLLM_API int requantize_output_q8_0(const uint8_t *W, int n_rows, int n_cols, in
 {
     API_GUARD;
     const int sem = requant_sem(quant_type);
-    if (sem < 0) { set_error("requantize_output_q8_0: type %d is not requantised (Q4_K and Q6_K only)", quant_type); return -1; }
+    if (sem < 0 && quant_type != kQtF16) {
+        set_error("requantize_output_q8_0: type %d is not requantised (Q4_K, Q6_K and F16 only)", quant_type);
+        return -1;
+    }
+    if (quant_type == kQtF16 && n_cols % 32) {
+        set_error("requantize_output_q8_0: F16 rows of whole 32-element blocks only (TE:650-651 reshapes by 32)");
+        return -1;
+    }
     if (n_rows <= 0 || n_cols < 32) return 0;
     thread_ctx &c = t_ctx;
     if (c.init()) return -1;
-    const size_t raw = (size_t)raw_row_bytes(mllm_sem_layout(sem), n_cols) * n_rows;
+    const size_t raw = quant_type == kQtF16 ? (size_t)n_rows * n_cols * 2
+                                            : (size_t)raw_row_bytes(mllm_sem_layout(sem), n_cols) * n_rows;
     const size_t q8 = (size_t)n_rows * (n_cols / 32) * 34;
     const long ws = mllm_requantize_workspace_size(quant_type, n_rows, n_cols);
     // a load-time conversion: its buffers are allocated for the call and freed after it

@@ -164,6 +164,8 @@ hipError_t mllm_launch_read_probe(const void *p, long bytes, void *sink, hipStre
 hipError_t mllm_launch_requant_q8_0(const float *w, int n_rows, int n_cols, uint8_t *out, hipStream_t st);
 // p[i] = v, i < n (a fill kernel: nothing here records a memset node).
 hipError_t mllm_launch_fill(float *p, long n, float v, hipStream_t st);
+// out[i] = (float)u[i]: TE:643-645's F16 conversion (the patterns' integer values)
+hipError_t mllm_launch_u16_value_f32(const uint16_t *u, long n, float *out, hipStream_t st);
 // ORs into *flags (device int): 1 = some block scale of the n_mats matrices in
 // tab_dev (device array; or the single host-side view `one` when tab_dev is
 // null) is inf/NaN, 2 = some E8M0 exponent is >= 178 (see k_scale_scan).

@@ -866,6 +866,14 @@ __global__ void k_requant_q8_0(const float *__restrict__ w, int n_rows, int n_co
     }
 }
 
+// TE:643-645's F16 conversion, raw_u16.astype(np.float32).view(np.float32): each
+// 16-bit pattern becomes its integer value (exact in fp32), not its fp16 value.
+__global__ void k_u16_value_f32(const uint16_t *__restrict__ u, long n, float *__restrict__ out)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = (float)u[i];
+}
+
 __global__ void k_fill_f32(float *__restrict__ p, long n, float v)
 {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1137,6 +1145,13 @@ hipError_t mllm_launch_requant_q8_0(const float *w, int n_rows, int n_cols, uint
     const long n = (long)n_rows * (n_cols / 32);
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_requant_q8_0, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, n_rows, n_cols, out);
+    return hipGetLastError();
+}
+
+hipError_t mllm_launch_u16_value_f32(const uint16_t *u, long n, float *out, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_u16_value_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, u, n, out);
     return hipGetLastError();
 }
 

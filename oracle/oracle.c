@@ -640,22 +640,33 @@ void orc_moe_forward_token(const uint8_t *const *gate, const uint8_t *const *up,
 /* The reference caller's lm_head requantisation (TE:620-666,
  * _requantize_output): each row of a Q4_K / Q6_K matrix dequantised as
  * q4_k_dequantize_row / q6_k_dequantize_row do (QK:762-828; columns past the
- * last whole super-block stay 0, as TE's np.zeros buffer leaves them), then
- * per 32 elements in float32 as TE's numpy code computes it:
+ * last whole super-block stay 0, as TE's np.zeros buffer leaves them), or of
+ * an F16 matrix (type 1) as TE:643-645 converts it,
+ * raw_u16.astype(np.float32).view(np.float32): the integer value of each
+ * 16-bit pattern, not its fp16 value (0x3C00 -> 15360.0f); then per 32
+ * elements in float32 as TE's numpy code computes it:
  * amax = max(max|x|, 1e-10f), d = amax / 127, q = round-half-even(x / d)
  * clamped to +-127, d stored as fp16 (RNE) before the 32 quants.
- * Returns 0, or -1 for a type TE does not requantise this way. */
+ * Returns 0, or -1 for a type TE does not requantise this way (and for an F16
+ * row length TE's reshape into 32-element blocks rejects). */
 int orc_requant_q8_0(int qt, const uint8_t *W, int n_rows, int n_cols, uint8_t *out)
 {
+    const int f16 = qt == ORC_QT_F16;
     const int sem = qt == ORC_QT_Q4_K ? ORC_Q4_K_GGML : qt == ORC_QT_Q6_K ? ORC_Q6_K_GGML : -1;
-    if (sem < 0) return -1;
-    const long rb = orc_row_bytes(sem, n_cols);
+    if (sem < 0 && !f16) return -1;
+    if (f16 && n_cols % 32) return -1;
+    const long rb = f16 ? 2L * n_cols : orc_row_bytes(sem, n_cols);
     const int nb = n_cols / 32;
     float *w = (float *)malloc((size_t)(n_cols > 0 ? n_cols : 1) * sizeof(float));
     if (!w) return -1;
     for (int r = 0; r < n_rows; r++) {
         memset(w, 0, (size_t)n_cols * sizeof(float));
-        orc_dequant_row(sem, W + (long)r * rb, w, n_cols / 256 * 256);
+        if (f16) {
+            const uint8_t *src = W + (long)r * rb;
+            for (int i = 0; i < n_cols; i++) w[i] = (float)(uint16_t)(src[2 * i] | (src[2 * i + 1] << 8));
+        } else {
+            orc_dequant_row(sem, W + (long)r * rb, w, n_cols / 256 * 256);
+        }
         for (int b = 0; b < nb; b++) {
             const float *x = w + 32 * b;
             uint8_t *dst = out + ((long)r * nb + b) * 34;

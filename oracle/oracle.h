@@ -43,7 +43,7 @@ enum orc_sem {
 };
 
 /* GGUF type codes used by the reference (QK:6-14, TE:19-25). */
-enum { ORC_QT_F32 = 0, ORC_QT_Q4_0 = 2, ORC_QT_Q4_1 = 3, ORC_QT_Q5_0 = 6, ORC_QT_Q8_0 = 8,
+enum { ORC_QT_F32 = 0, ORC_QT_F16 = 1, ORC_QT_Q4_0 = 2, ORC_QT_Q4_1 = 3, ORC_QT_Q5_0 = 6, ORC_QT_Q8_0 = 8,
        ORC_QT_Q4_K = 12, ORC_QT_Q5_K = 13, ORC_QT_Q6_K = 14, ORC_QT_MXFP4 = 39 };
 
 float    orc_f16_to_f32(uint16_t h);

@@ -153,7 +153,8 @@ class Oracle:
         return idx, w
 
     def requant_q8_0(self, qt, W, n_rows, n_cols):
-        """TE:620-666: a Q4_K / Q6_K matrix requantised to raw Q8_0 blocks."""
+        """TE:620-666: a Q4_K / Q6_K matrix, or F16 bit patterns taken as
+        integers (TE:643-645), requantised to raw Q8_0 blocks."""
         out = np.zeros(n_rows * (n_cols // 32) * 34, dtype=np.uint8)
         rc = self.lib.orc_requant_q8_0(qt, up(np.ascontiguousarray(W, dtype=np.uint8)), n_rows, n_cols, up(out))
         if rc != 0:

@@ -85,11 +85,16 @@ def te_requantize(ref, W, qt, n_rows, n_cols):
     row through the reference's own C dequantize_row, then TE's numpy Q8_0
     quantisation, statement for statement."""
     f32 = np.zeros((n_rows, n_cols), dtype=np.float32)
-    rb = n_cols // 256 * (144 if qt == 12 else 210)
-    fn = ref.so.q4_k_dequantize_row if qt == 12 else ref.so.q6_k_dequantize_row
-    for r in range(n_rows):
-        row = np.ascontiguousarray(W[r * rb:(r + 1) * rb])
-        fn(up(row), fp(f32[r]), n_cols)
+    if qt == 1:
+        # TE:643-645 statement for statement (the integer value of each 16-bit pattern)
+        raw_u16 = np.frombuffer(W[:n_rows * n_cols * 2], dtype=np.uint16).copy().reshape(n_rows, n_cols)
+        f32 = raw_u16.astype(np.float32).view(np.float32)
+    else:
+        rb = n_cols // 256 * (144 if qt == 12 else 210)
+        fn = ref.so.q4_k_dequantize_row if qt == 12 else ref.so.q6_k_dequantize_row
+        for r in range(n_rows):
+            row = np.ascontiguousarray(W[r * rb:(r + 1) * rb])
+            fn(up(row), fp(f32[r]), n_cols)
     n_blocks = n_cols // 32
     blocks = f32.reshape(n_rows, n_blocks, 32)
     amax = np.max(np.abs(blocks), axis=2, keepdims=True)
@@ -106,12 +111,17 @@ def te_requantize(ref, W, qt, n_rows, n_cols):
 
 def gen_requant(ref):
     """lm_head requantisation fixtures: Q4_K and Q6_K matrices (one row's
-    super-blocks zeroed to exercise the amax floor) -> Q8_0."""
-    for qt, R, C, seed in ((12, 24, 768, 71), (14, 24, 768, 72)):
+    super-blocks zeroed to exercise the amax floor) and an F16 matrix (random
+    16-bit patterns, one row zero) -> Q8_0."""
+    for qt, R, C, seed in ((12, 24, 768, 71), (14, 24, 768, 72), (1, 24, 800, 74)):
         rng = np.random.default_rng(seed)
-        w = W.gen_weights(rng, qt, R, C)
-        rb = C // 256 * (144 if qt == 12 else 210)
-        w[3 * rb:4 * rb] = 0          # row 3: d = dmin = 0 -> all-zero blocks
+        if qt == 1:
+            w = rng.integers(0, 256, size=R * C * 2, dtype=np.uint8)
+            rb = 2 * C
+        else:
+            w = W.gen_weights(rng, qt, R, C)
+            rb = C // 256 * (144 if qt == 12 else 210)
+        w[3 * rb:4 * rb] = 0          # row 3: all-zero blocks (the amax floor)
         out = te_requantize(ref, w, qt, R, C)
         np.savez_compressed(os.path.join(OUT, f"requant_q8_{qt}.npz"), W=w, out=out, qt=qt, n_rows=R, n_cols=C)
 

@@ -363,10 +363,11 @@ def test_batch_qkv_unknown_type_leaves_output(lib, orc):
     assert O.norm_err(ov, orc.gemv(orc.sem_for(2, 12), Wv, x, 16, C, 1)[0]) < GEMV_TOL
 
 
-@pytest.mark.parametrize("qt", [12, 14])
+@pytest.mark.parametrize("qt", [12, 14, 1])
 def test_golden_requantize_output_q8_0(lib, golden, qt):
     """TE's lm_head requantisation (TE:620-666) through the C ABI: bit-exact
-    with the fixture (the reference's dequantize_row + TE's numpy statements)."""
+    with the fixture (the reference's dequantize_row, or for F16 TE:643-645's
+    conversion of the patterns, + TE's numpy statements)."""
     g = golden(f"requant_q8_{qt}.npz")
     R, C = int(g["n_rows"]), int(g["n_cols"])
     out = np.full(R * (C // 32) * 34, 0xAB, np.uint8)
@@ -388,6 +389,7 @@ def test_requantize_lm_head_full_shape(lib, orc):
     q6_logits = orc.gemv(K.Q6_K_GGML, w, x, R, C, 1)[0]   # the ggml order the requantisation decodes
     assert O.norm_err(q8_logits, q6_logits) < 2e-2
     assert lib.requantize_output_q8_0(up(w), R, C, 13, up(out)) == -1
+    assert lib.requantize_output_q8_0(up(w), 2, 80, 1, up(out)) == -1   # F16: whole 32-element blocks only
 
 
 # ------------------------------------------------ activations with outliers

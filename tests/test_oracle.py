@@ -166,13 +166,39 @@ def test_golden_route_selection_bitexact(orc, golden, tag):
     assert np.all(np.abs(ratio / ratio[:, :1] - 1.0) < 1e-5)
 
 
-@pytest.mark.parametrize("qt", [12, 14])
+@pytest.mark.parametrize("qt", [12, 14, 1])
 def test_golden_requant_q8_0(orc, golden, qt):
     """TE's lm_head requantisation (TE:620-666) as the fixture generator ran it:
-    the reference's own dequantize_row per row, then TE's numpy statements."""
+    the reference's own dequantize_row per row (F16: TE:643-645's conversion),
+    then TE's numpy statements."""
     g = golden(f"requant_q8_{qt}.npz")
     got = orc.requant_q8_0(qt, g["W"], int(g["n_rows"]), int(g["n_cols"]))
     assert np.array_equal(got, g["out"])
+
+
+def test_requant_f16_takes_bit_patterns_as_integers():
+    """TE:643-645 turns each fp16 pattern into its integer value, not its fp16
+    value: a block of the pattern 0x3C00 (fp16 1.0) is 32 values 15360, so
+    d = fp16(15360 / 127) and every quant is 127; a block whose patterns are
+    0..31 has amax 31, d = fp16(31 / 127) and quants rint(k * 127 / 31)
+    (half to even); a row of fp16 -0.0 patterns (0x8000 = 32768) is not zero.
+    Reading the patterns as fp16 fails all three."""
+    orc = O.Oracle()
+    C = 96
+    u = np.zeros((2, C), np.uint16)
+    u[0, :32] = 0x3C00
+    u[0, 32:64] = np.arange(32)
+    u[0, 64:] = 0x8000
+    got = orc.requant_q8_0(1, u.view(np.uint8).ravel(), 1, C).reshape(-1, 34)
+    d = got[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    q = got[:, 2:].view(np.int8)
+    assert d[0] == np.float16(np.float32(15360.0) / np.float32(127.0)) and np.all(q[0] == 127)
+    d1 = np.float32(31.0) / np.float32(127.0)
+    assert d[1] == np.float16(d1)
+    assert np.array_equal(q[1], np.clip(np.round(np.arange(32, dtype=np.float32) / d1), -127, 127).astype(np.int8))
+    assert d[2] == np.float16(np.float32(32768.0) / np.float32(127.0)) and np.all(q[2] == 127)
+    with pytest.raises(ValueError):
+        orc.requant_q8_0(1, u.view(np.uint8).ravel(), 1, 80)   # not whole 32-element blocks
 
 
 def test_requant_q8_0_differs_from_quantize_row():

@@ -118,7 +118,7 @@ template <> struct x_stage<true> {
     float4 u[kStageSlots][2];
 };
 
-template <bool SILU>
+template <bool SILU, int NT = 256>
 MLLM_DEV void stage_load(x_stage<SILU> &st, const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B,
                          int k0, int kn, int pass)
 {
@@ -130,7 +130,7 @@ MLLM_DEV void stage_load(x_stage<SILU> &st, const float *__restrict__ x, const f
     const bool vec = (ldx & 3) == 0;
 #pragma unroll
     for (int q = 0; q < kStageSlots; q++) {
-        const int base = 256 * (q + pass * kStageSlots);
+        const int base = NT * (q + pass * kStageSlots);
         if (base >= n) break;
         const int idx = min(base + (int)threadIdx.x, n - 1);
         const int b = idx / nh, h = idx - b * nh;
@@ -238,7 +238,7 @@ MLLM_DEV uint32_t pack_b0(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
     return lo | hi;
 }
 
-template <int SEM, bool SILU, bool PRO = false>
+template <int SEM, bool SILU, bool PRO = false, int NT = 256>
 MLLM_DEV bool stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geom &dg, int B, int kn, int pass,
                           bool clamp, const pro_regs *pr = nullptr, const mllm_gemv_args *pa = nullptr,
                           float *part = nullptr)
@@ -248,7 +248,7 @@ MLLM_DEV bool stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
     bool any_bad = false;
 #pragma unroll
     for (int q = 0; q < kStageSlots; q++) {
-        const int idx = threadIdx.x + 256 * (q + pass * kStageSlots);
+        const int idx = threadIdx.x + NT * (q + pass * kStageSlots);
         if (idx >= B * nh) continue;       // B * nh is even: both halves of a group take the same path
         const int b = idx / nh, h = idx - b * nh, g = h >> 1, half = h & 1;
         float v[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
@@ -309,13 +309,13 @@ MLLM_DEV bool stage_store(const x_stage<SILU> &st, uint8_t *lds, const digit_geo
 // under P = +inf, which sends every chunk reading it to chunk_value's
 // per-element path; a NaN keeps P = NaN; an all-finite group whose sum
 // overflowed is staged as usual.  v = silu(x, xu) with xu, + x_res with x_res.
-template <int SEM>
+template <int SEM, int NT = 256>
 MLLM_DEV void stage_fix(uint8_t *lds, const digit_geom &dg, const float *__restrict__ x, const float *__restrict__ xu,
                         const float *__restrict__ x_res, int ldx, int B, int k0, int kn, bool clamp)
 {
     constexpr float M = 12582912.0f;
     const int nh = kn >> 3, n = B * nh;
-    for (int base = 0; base < n; base += 256) {      // n even: both halves of a group stay in step
+    for (int base = 0; base < n; base += NT) {       // n even: both halves of a group stay in step
         const int idx = base + (int)threadIdx.x;
         if (idx >= n) break;
         const int b = idx / nh, h = idx - b * nh, g = h >> 1, half = h & 1;
@@ -366,7 +366,7 @@ MLLM_DEV void stage_fix(uint8_t *lds, const digit_geom &dg, const float *__restr
 
 // Stage tokens b < B, elements [k0, k0+kn), as digits; load_first = a pass-0
 // load already issued by the caller.
-template <int SEM, bool SILU>
+template <int SEM, bool SILU, int NT = 256>
 MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, const digit_geom &dg,
                            const float *__restrict__ x, const float *__restrict__ xu, int ldx, int B, int k0, int kn,
                            bool clamp = true)
@@ -374,14 +374,14 @@ MLLM_DEV void stage_digits(x_stage<SILU> &st, bool load_first, uint8_t *lds, con
     // pass 0 stays out of the pass loop: there the wait before the digits
     // covers the activation loads only, not weight loads the caller issued
     // behind them (at a loop head the wait would cover every load in flight)
-    const int passes = (B * (kn >> 3) + 256 * kStageSlots - 1) / (256 * kStageSlots);
-    if (!load_first) stage_load<SILU>(st, x, xu, ldx, B, k0, kn, 0);
-    bool bad = stage_store<SEM, SILU>(st, lds, dg, B, kn, 0, clamp);
+    const int passes = (B * (kn >> 3) + NT * kStageSlots - 1) / (NT * kStageSlots);
+    if (!load_first) stage_load<SILU, NT>(st, x, xu, ldx, B, k0, kn, 0);
+    bool bad = stage_store<SEM, SILU, false, NT>(st, lds, dg, B, kn, 0, clamp);
     for (int pass = 1; pass < passes; pass++) {
-        stage_load<SILU>(st, x, xu, ldx, B, k0, kn, pass);
-        bad |= stage_store<SEM, SILU>(st, lds, dg, B, kn, pass, clamp);
+        stage_load<SILU, NT>(st, x, xu, ldx, B, k0, kn, pass);
+        bad |= stage_store<SEM, SILU, false, NT>(st, lds, dg, B, kn, pass, clamp);
     }
-    if (__any(bad)) stage_fix<SEM>(lds, dg, x, SILU ? xu : nullptr, nullptr, ldx, B, k0, kn, clamp);
+    if (__any(bad)) stage_fix<SEM, NT>(lds, dg, x, SILU ? xu : nullptr, nullptr, ldx, B, k0, kn, clamp);
 }
 
 // The digit words of the run starting at tile-relative element e.
@@ -849,8 +849,19 @@ template <int SEM, bool Q8> struct gemv_geom {
 // the even group writes silu(gate) * up after one cross-lane exchange.
 constexpr int kFusePro = 1, kFusePair = 2;
 
+// Waves per workgroup of the persistent kernel: eight on the ring path (64
+// lanes per row, batch 1, no fusion), four elsewhere.  The ring path serves
+// long rows, whose whole-K staging holds a workgroup to up to ~60 KB of LDS
+// (two workgroups per CU): eight waves per workgroup keep four waves per SIMD
+// in flight instead of two, sharing one staged copy of the activation.
+template <int SEM, bool Q8, int BM, int R, int LPR, int FUSE>
+constexpr int gemv_p_waves()
+{
+    return (R == 1 && BM == 1 && LPR == 64 && FUSE == 0 && !Q8 && kFetchLin<SEM>) ? 8 : 4;
+}
+
 template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU, int FUSE>
-__global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
+__global__ __launch_bounds__((64 * gemv_p_waves<SEM, Q8, BM, R, LPR, FUSE>())) void k_gemv_p(mllm_gemv_args a)
 {
     static_assert(!(Q8 && SILU), "the SiLU product of Q8_0 activations is formed by the quantiser");
     static_assert(!(SILU && FUSE), "the SiLU staging and the fusions are exclusive");
@@ -860,6 +871,8 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     constexpr int BE = gemv_geom<SEM, Q8>::BE, CPB = gemv_geom<SEM, Q8>::CPB;
     constexpr int GPW = 64 / LPR;                       // lane groups per wave
     constexpr int OPW = PAIR ? GPW / 2 : GPW * R;       // output rows per wave and step
+    constexpr int NW = gemv_p_waves<SEM, Q8, BM, R, LPR, FUSE>(), NT = 64 * NW;
+    static_assert(NT == 256 || (!PRO && !Q8), "the prologue and Q8_0 staging take 256 threads");
     const job_view jv = view_job(a, blockIdx.y);
     const mllm_packed W = jv.W;
     // the "up" rows of a pair: table2's matrix of the job's expert, else the same matrix n_rows further
@@ -885,8 +898,8 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
     if (iters == 0) return;   // no whole block per row: the launcher writes zeros instead of launching this
     const int n_out = a.n_rows;
     const int nrg = (n_out + OPW - 1) / OPW;
-    const int wstride = gridDim.x * 4;
-    const int rg0 = blockIdx.x * 4 + wave;
+    const int wstride = gridDim.x * NW;
+    const int rg0 = blockIdx.x * NW + wave;
     const int B = a.B;
     // LDS geometry (whole K staged): activation digits, or the Q8_0 pack
     const int KT = (kused + 255) / 256 * 256;
@@ -1020,7 +1033,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
         x_stage<SILU> xst;
         const float *xj = a.x + jv.xj * a.x_job_stride;
         const float *xuj = SILU ? a.x_up + jv.xj * a.x_job_stride : nullptr;
-        stage_load<SILU>(xst, xj, xuj, a.ldx, B, 0, kused, 0);
+        stage_load<SILU, NT>(xst, xj, xuj, a.ldx, B, 0, kused, 0);
         if constexpr (PRO) {
             pro_regs pr;
             pro_load(pr, a, B, kused, 0);
@@ -1042,7 +1055,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(mllm_gemv_args a)
                 stage_fix<SEM>(reinterpret_cast<uint8_t *>(xl), dg, xj, nullptr, a.x_res, a.ldx, B, 0, kused, true);
         } else {
             prefetch();
-            stage_digits<SEM, SILU>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
+            stage_digits<SEM, SILU, NT>(xst, true, reinterpret_cast<uint8_t *>(xl), dg, xj, xuj, a.ldx, B, 0, kused,
                                     !a.silu_noclamp);
         }
     }
@@ -1203,7 +1216,9 @@ constexpr size_t kPersistentLds = 72 * 1024;
 template <int SEM, bool Q8, int BM, int R, int LPR, bool SILU>
 void launch_lpr(bool persistent, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
 {
-    if (persistent) hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, LPR, SILU, 0>), grid, dim3(256), lds, st, a);
+    if (persistent)
+        hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, LPR, SILU, 0>), grid, dim3(64 * gemv_p_waves<SEM, Q8, BM, R, LPR, 0>()),
+                           lds, st, a);
     else if constexpr (Q8) hipLaunchKernelGGL((k_gemv_q8<SEM, BM, R, LPR>), grid, dim3(256), lds, st, a);
     else hipLaunchKernelGGL((k_gemv<SEM, BM, R, LPR, SILU>), grid, dim3(256), lds, st, a);
 }
@@ -1276,8 +1291,10 @@ void launch_sem(mllm_gemv_args a, int n_jobs, hipStream_t st)
     const int ktp = (kused + 255) / 256 * 256;
     const size_t lds_p = Q8 ? (size_t)BM * (ktp + ktp / 16 + 8 * (ktp / 32)) : (size_t)BM * digit_geom_for(ktp).tstride;
     if (lds_p <= kPersistentLds) {
-        const int per_cu = lds_p <= 40 * 1024 ? 3 : 2;
-        const int wgs = std::max(1, std::min(wg_needed, device_cus() * per_cu / std::max(1, n_jobs)));
+        const int nw = lpr == 64 ? gemv_p_waves<SEM, Q8, BM, R, 64, 0>() : 4;
+        const int rows_p = nw * (64 / lpr) * R;
+        const int per_cu = nw == 8 ? 2 : lds_p <= 40 * 1024 ? 3 : 2;
+        const int wgs = std::max(1, std::min((a.n_rows + rows_p - 1) / rows_p, device_cus() * per_cu / std::max(1, n_jobs)));
         launch_shape<SEM, Q8, BM, R>(true, lpr, dim3(wgs, n_jobs), lds_p, a, st);
         return;
     }
@@ -1309,6 +1326,7 @@ template <int SEM, bool Q8, int BM, int R, int FUSE>
 void launch_fused_lpr(int lpr, dim3 grid, size_t lds, const mllm_gemv_args &a, hipStream_t st)
 {
     constexpr bool PAIR = (FUSE & kFusePair) != 0;
+    static_assert(FUSE != 0, "fused launches run four-wave workgroups");
     if constexpr (!PAIR) {
         if (lpr == 64) { hipLaunchKernelGGL((k_gemv_p<SEM, Q8, BM, R, 64, false, FUSE>), grid, dim3(256), lds, st, a); return; }
     }

@@ -262,11 +262,10 @@ MLLM_DEV uint32_t ilv_bit4(uint32_t bits, int e0)
 
 // SIGNED_Q8: Q8_0 codes are left as the signed quant bytes (bias 0) instead of
 // q + 128, for the integer-dot GEMV.
+// Chunk cc of block blk of a row (chunk index c = blk * CPB + cc).
 template <int SEM, bool SIGNED_Q8 = false>
-MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
+MLLM_DEV void codes_at(const raw_chunk &r, int blk, int cc, chunk_codes &k)
 {
-    constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
-    const int blk = (int)((unsigned)c / CPB), cc = (int)((unsigned)c % CPB);   // c >= 0
     const uint32_t A[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
     const uint32_t L4 = 0x0F0F0F0Fu;
     k.o0 = k.o1 = 0.0f;
@@ -379,6 +378,13 @@ MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
         k.s1 = d * (float)(int8_t)(r.m.x >> 8);
         k.x0 = 256 * blk + 32 * cc; k.x1 = k.x0 + 16;
     }
+}
+
+template <int SEM, bool SIGNED_Q8 = false>
+MLLM_DEV void codes(const raw_chunk &r, int c, chunk_codes &k)
+{
+    constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
+    codes_at<SEM, SIGNED_Q8>(r, (int)((unsigned)c / CPB), (int)((unsigned)c % CPB), k);   // c >= 0
 }
 
 // Byte t of w as a float: one v_cvt_f32_ubyte{t} (the compiler's own

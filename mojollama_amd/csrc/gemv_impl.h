@@ -451,7 +451,9 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
     constexpr float bias = (float)ibias;
     constexpr bool need_sum = ibias != 0 || sem_traits<SEM>::kOffset;
     float t = fmaf(k.s0 * x0.P, run_idot<SEM>(k.U, x0), (k.s1 * x1.P) * run_idot<SEM>(k.U + 4, x1));
-    if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), x0.sum, fmaf(fmaf(-k.s1, bias, k.o1), x1.sum, t));
+    // (with no bias the offset term is o * sum x: an infinite s already makes the first term non-finite)
+    if constexpr (need_sum && ibias == 0) t = fmaf(k.o0, x0.sum, fmaf(k.o1, x1.sum, t));
+    else if constexpr (need_sum) t = fmaf(fmaf(-k.s0, bias, k.o0), x0.sum, fmaf(fmaf(-k.s1, bias, k.o1), x1.sum, t));
     if (!isfinite(t)) {
         // inf/NaN somewhere (scale, activation or an overflowing partial): weigh each
         // element as the reference does (w = s*q first, then w*x), x rebuilt from its digits.
@@ -501,6 +503,52 @@ MLLM_DEV float chunk_value(const chunk_codes &k, const run_digits &x0, const run
     return t;
 }
 
+// The run at digit offset dp (dpad of its first element) with its record at rec.
+MLLM_DEV void load_run_at(const uint8_t *tb, const digit_geom &dg, int dp, int rec, run_digits &r)
+{
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(tb + p * dg.PL + dp);
+        r.w[p][0] = q.x; r.w[p][1] = q.y; r.w[p][2] = q.z; r.w[p][3] = q.w;
+    }
+    const float2 v = *reinterpret_cast<const float2 *>(tb + 3 * dg.PL + rec);
+    r.P = v.x;
+    r.sum = v.y;
+}
+
+// Batch 1: chunk cc of block blk of R rows (already fetched into raw), activation
+// digits from LDS (tile starting at element k0); SET: acc = the value, else +=.
+// WHOLE: the tile is the whole row (k0 = 0); a chunk's two runs then lie in one
+// 256-element segment of it, so their padded offsets follow from the segment
+// and the chunk's place in it without the general dpad.
+template <int SEM, int R, bool SET = false, bool WHOLE = false>
+MLLM_DEV void accumulate_at(const raw_chunk (&raw)[R], int blk, int cc, const uint8_t *xl, const digit_geom &dg,
+                            int k0, float (&acc)[R][1])
+{
+    // activation digits once per chunk, reused by the R rows
+    chunk_codes k;
+    codes_at<SEM, true>(raw[0], blk, cc, k);
+    run_digits x0, x1;
+    if constexpr (WHOLE) {
+        constexpr int EPB = sem_traits<SEM>::kBlockElems;
+        static_assert(EPB == 256 || EPB == 32, "blocks of 32 or 256 elements");
+        const int seg = EPB == 256 ? blk : blk >> 3;
+        const int f0 = k.x0 - 256 * seg, d1 = k.x1 - k.x0;    // f0 + d1 + 16 <= 256 in every format
+        const int dp = 272 * seg + f0, rec = 128 * seg + 8 * (f0 >> 4);
+        load_run_at(xl, dg, dp, rec, x0);
+        load_run_at(xl, dg, dp + d1, rec + d1 / 2, x1);
+    } else {
+        load_run(xl, dg, k.x0 - k0, x0);
+        load_run(xl, dg, k.x1 - k0, x1);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (r) codes_at<SEM, true>(raw[r], blk, cc, k);
+        const float v = chunk_value<SEM>(k, x0, x1);
+        acc[r][0] = SET ? v : acc[r][0] + v;
+    }
+}
+
 // Add chunk c of R rows (already fetched into raw) to acc, activation digits
 // from LDS (tile starting at element k0).
 template <int SEM, int BM, int R>
@@ -509,16 +557,8 @@ MLLM_DEV void accumulate(const raw_chunk (&raw)[R], int c, const uint8_t *xl, co
 {
     chunk_codes k;
     if constexpr (BM == 1) {
-        // activation digits once per chunk, reused by the R rows
-        codes<SEM, true>(raw[0], c, k);
-        run_digits x0, x1;
-        load_run(xl, dg, k.x0 - k0, x0);
-        load_run(xl, dg, k.x1 - k0, x1);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (r) codes<SEM, true>(raw[r], c, k);
-            acc[r][0] += chunk_value<SEM>(k, x0, x1);
-        }
+        constexpr int CPB = sem_traits<SEM>::kChunksPerBlock;
+        accumulate_at<SEM, R>(raw, (int)((unsigned)c / CPB), (int)((unsigned)c % CPB), xl, dg, k0, acc);
     } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -952,8 +992,18 @@ __global__ __launch_bounds__((64 * gemv_p_waves<SEM, Q8, BM, R, LPR, FUSE>())) v
         for (int r = 0; r < R; r++)
 #pragma unroll
             for (int b = 0; b < BM; b++) part[r][b] = 0.0f;
-        if constexpr (Q8) accumulate_q8<SEM, BM, R>(buf, c, xl, tstride, qstride, KT, 0, B, part);
-        else accumulate<SEM, BM, R>(buf, c, reinterpret_cast<const uint8_t *>(xl), dg, 0, B, part);
+        if constexpr (Q8) {
+            accumulate_q8<SEM, BM, R>(buf, c, xl, tstride, qstride, KT, 0, B, part);
+        } else if constexpr (BM == 1 && LPR % CPB == 0) {
+            // a lane's chunk within its block is the same at every step (sl % CPB) and
+            // its block advances by LPR / CPB: the digit addresses and the scale
+            // selection follow from the lane and the step (a lane past the row's
+            // end takes the last block and is discarded)
+            const int blk = min(it * (LPR / CPB) + sl / CPB, nb - 1);
+            accumulate_at<SEM, R, true, true>(buf, blk, sl % CPB, reinterpret_cast<const uint8_t *>(xl), dg, 0, part);
+        } else {
+            accumulate<SEM, BM, R>(buf, c, reinterpret_cast<const uint8_t *>(xl), dg, 0, B, part);
+        }
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll

@@ -782,7 +782,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported: the multi-GPU sharding "
-              "(row-sharded GEMV, expert-parallel MoE) is a design in DESIGN.md, not a run.", file=sys.stderr)
+              "(row-sharded GEMV, expert-parallel MoE) is designed, not built: every run here uses one GPU.",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"

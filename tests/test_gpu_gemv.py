@@ -299,6 +299,23 @@ def test_q4k_q8_path_full_shape(lib, orc):
     assert O.norm_err(got, orc.gemv(K.Q4_K_Q8, w, x, 5632, 2048, 1)[0]) < GEMV_TOL
 
 
+@pytest.mark.parametrize("sem,qt,C", [(K.Q4_K_GGML, 12, 9984), (K.MXFP4, 39, 9952), (K.Q8_0, 8, 9920),
+                                      (K.Q6_K_SEQ, 14, 9984)])
+def test_long_row_ring_vs_oracle(dev, orc, sem, qt, C):
+    """The batch-1 path for long rows (64 lanes per row, the four-step weight ring,
+    eight-wave workgroups, buffer-resource fetch): rows of 5-10 KB, 4100 of them, so
+    waves run one or two row groups of five ring steps, the last step with lanes
+    past the row's end, and the last row group ragged."""
+    import torch
+    rng = np.random.default_rng(qt + C)
+    R = 4100
+    w = W.gen_weights(rng, qt, R, C)
+    x = W.gen_x(rng, 1, C)
+    packed = dev.pack(sem, torch.from_numpy(w).cuda(), R, C)
+    got = dev.gemv(sem, packed, torch.from_numpy(x).cuda(), R, C).cpu().numpy()
+    assert O.norm_err(got, orc.gemv(sem, w, x, R, C, 1)) < GEMV_TOL, K.SEM_NAMES[sem]
+
+
 def test_gemv_linearity_full_shape(dev):
     """Size-independent property at the lm_head shape: W(a x + b y) = a Wx + b Wy."""
     import torch
